@@ -1,0 +1,265 @@
+#!/usr/bin/env python
+"""Headline benchmark: Llama-3-8B post-attention MLP (post_attn_mlp) on one MI355X.
+
+Workload: hidden [M, 4096], norm_w [4096], w_gate_up [28672, 4096],
+w_down [4096, 14336], fp16, eps 1e-5, residual fused; M = 1 (the `value`) and
+M = 8 (reported beside it). Weights are random-init with the configured
+distributions (no checkpoints); four independent weight sets (1.41 GB) are
+rotated so every step streams its 352 MB of weights from HBM, not from the
+256 MB Infinity Cache.
+
+A step is one post_attn_mlp call, replayed from a HIP graph (the way a decode
+loop runs it); W untimed warmup steps, then exactly K timed steps between HIP
+events, bracketed by synchronisation. `value` is microseconds per step at M=1
+(lower is better).
+
+roofline: the dominant kernel, the fused RMSNorm + gate/up GEMV + SwiGLU
+launch, timed alone with HIP events on the stream it is launched on;
+achieved = its algorithmic bytes / its average duration.
+
+cpu_baseline: the NumPy oracle of the same block at M=1 on the host cores
+(a bounded sample of calls), in the same unit.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "fused-decode_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+H, I = 4096, 14336
+EPS = 1e-5
+N_SETS = 4
+HBM_PEAK_GBS = 8000.0
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on the CPU baseline sample")
+    return ap.parse_args()
+
+
+def make_sets(torch, m: int, dtype, dev):
+    g = torch.Generator(device=dev).manual_seed(1234)
+    sets = []
+    for _ in range(N_SETS):
+        hidden = torch.randn(m, H, generator=g, device=dev, dtype=torch.float32).to(dtype)
+        norm_w = (1 + 0.1 * torch.randn(H, generator=g, device=dev, dtype=torch.float32)).to(dtype)
+        w_gu = (torch.randn(2 * I, H, generator=g, device=dev, dtype=torch.float32) * H ** -0.5).to(dtype)
+        w_d = (torch.randn(H, I, generator=g, device=dev, dtype=torch.float32) * I ** -0.5).to(dtype)
+        sets.append((hidden, norm_w, w_gu, w_d))
+    return sets
+
+
+def time_graph_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None) -> float:
+    """Microseconds per step: step s replays the captured MLP of weight set s % N_SETS."""
+    graphs, outs = [], []
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for st in sets:
+            fd.post_attn_mlp(*st, EPS, kind=kind)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    for st in sets:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            outs.append(fd.post_attn_mlp(*st, EPS, kind=kind))
+        graphs.append(gr)
+    for s in range(warmup):
+        graphs[s % N_SETS].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(steps):
+        graphs[s % N_SETS].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def time_eager_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None) -> float:
+    for s in range(warmup):
+        fd.post_attn_mlp(*sets[s % N_SETS], EPS, kind=kind)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(steps):
+        fd.post_attn_mlp(*sets[s % N_SETS], EPS, kind=kind)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def time_gate_up_kernel(torch, lib, sets, m: int, iters: int, kind_code: int) -> float:
+    """Average duration (us) of the fused norm + gate/up + SwiGLU launch alone."""
+    from fused_decode._lib import DTYPE_CODE, check
+
+    mids = [torch.empty(m, I, device=sets[0][0].device, dtype=sets[0][0].dtype) for _ in sets]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch(s):
+        hid, nw, wgu, _ = sets[s % N_SETS]
+        check("fd_mlp_gate_up", lib.fd_mlp_gate_up(
+            mids[s % N_SETS].data_ptr(), hid.data_ptr(), nw.data_ptr(), DTYPE_CODE[nw.dtype],
+            wgu.data_ptr(), m, H, I, EPS, kind_code, DTYPE_CODE[hid.dtype], stream))
+
+    for s in range(10):
+        launch(s)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for s in range(iters):
+        launch(s)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / iters
+
+
+def copy_roof_gbs(torch) -> float:
+    from fused_decode.kernels import launch_copy
+
+    n = 1 << 30  # 1 GiB source and destination: far above the Infinity Cache
+    src = torch.empty(n, dtype=torch.uint8, device="cuda")
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        launch_copy(dst, src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    iters = 20
+    start.record()
+    for _ in range(iters):
+        launch_copy(dst, src)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    del src, dst
+    return 2 * n / (us * 1e-6) / 1e9
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """NumPy oracle of the same block at M=1, fp16 semantics, bounded sample."""
+    import numpy as np
+
+    from oracle import decode_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((d.get("num_threads", 1) for d in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(7)
+    hid = O.round_to(rng.standard_normal((1, H), dtype=np.float32), "f16")
+    nw = O.round_to(1 + 0.1 * rng.standard_normal(H, dtype=np.float32), "f16")
+    wgu = O.round_to(rng.standard_normal((2 * I, H), dtype=np.float32) * np.float32(H ** -0.5), "f16")
+    wd = O.round_to(rng.standard_normal((H, I), dtype=np.float32) * np.float32(I ** -0.5), "f16")
+    O.post_attn_mlp(hid, nw, wgu, wd, EPS, "f16")  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        O.post_attn_mlp(hid, nw, wgu, wd, EPS, "f16")
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or calls >= 200:
+            break
+    return {
+        "value": el / calls * 1e6,
+        "unit": "us",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{calls} calls of the NumPy oracle post_attn_mlp at M=1, H=4096, I=14336 "
+                  f"(fp32 math, fp16 rounding points), {el:.1f} s",
+    }
+
+
+def main() -> None:
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only; --gpus must be 1 "
+                          "(the operator set has no multi-GPU path)", "n_gpus": args.gpus}))
+        sys.exit(2)
+    import torch
+
+    import fused_decode as fd
+    from fused_decode._lib import KIND_CODE, lib
+    from fused_decode.kernels import resolve_kind
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda:0")
+    dtype = torch.float16
+    kind = resolve_kind(None)
+    roof = copy_roof_gbs(torch)
+
+    results = {}
+    for m in (1, 8):
+        sets = make_sets(torch, m, dtype, dev)
+        results[m] = {
+            "graph_us": time_graph_steps(torch, fd, sets, args.steps, args.warmup, None),
+            "eager_us": time_eager_steps(torch, fd, sets, args.steps, args.warmup, None),
+        }
+        if m == 1:
+            gate_us = time_gate_up_kernel(torch, lib(), sets, m, max(args.steps, 50), KIND_CODE[kind])
+        del sets
+        torch.cuda.empty_cache()
+
+    us1 = results[1]["graph_us"]
+    weights = 3 * H * I * 2
+    mlp_bytes = (3 * H * I + 2 * 1 * H + H) * 2
+    gate_bytes = (2 * I * H + 1 * H + H + 1 * I) * 2  # weights, hidden, norm_w, mid write
+    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
+    line = {
+        "metric": "post_attn_mlp us @M=1 (Llama-3-8B widths); M=8 in m8_us",
+        "value": round(us1, 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(us1 / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: random-init weights ~N(0,1/sqrt(K)), hidden ~N(0,1), 4 rotating weight sets",
+        "config": {
+            "workload": "post_attn_mlp Llama-3-8B H=4096 I=14336 M=1, hipGraph replay, cold weights",
+            "kind": kind,
+            "m": 1,
+        },
+        "m8_us": round(results[8]["graph_us"], 3),
+        "eager_us": {"m1": round(results[1]["eager_us"], 3), "m8": round(results[8]["eager_us"], 3)},
+        "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
+        "copy_roof_gbs": round(roof, 1),
+        "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
+        "target_us": round(1.25 * weights / (roof * 1e9) * 1e6, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mlp_gate_up (RMSNorm + gate/up GEMV + SwiGLU), M=1",
+            "achieved": round(gate_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+            "avg_us": round(gate_us, 3),
+            "algorithmic_bytes": gate_bytes,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+// Device-side helpers shared by the gfx950 kernels: element types, 16-byte
+// vector loads/stores, float conversions, the row-layout index, and wave64
+// reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fused_decode.h"
+
+namespace fd {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// 8 activation elements = one 16-byte vector.
+template <typename T> struct Vec8;
+template <> struct Vec8<f16> { typedef f16x8 type; };
+template <> struct Vec8<bf16> { typedef bf16x8 type; };
+
+__device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+
+// Round-to-nearest-even float32 -> storage type (the same rounding as torch's .to()).
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+
+// Round-trip through the storage type: the value a stored-then-reloaded tensor holds.
+template <typename T> __device__ __forceinline__ float round_as(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+// 16-byte load of 8 activations (pointer must be 16-byte aligned).
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::type load8(const T* p) {
+  return *reinterpret_cast<const typename Vec8<T>::type*>(p);
+}
+template <typename T>
+__device__ __forceinline__ void store8(T* p, typename Vec8<T>::type v) {
+  *reinterpret_cast<typename Vec8<T>::type*>(p) = v;
+}
+
+// 8 consecutive values of any of the three dtypes, widened to float32.
+template <typename W>
+__device__ __forceinline__ void load8_f32(const W* p, float (&f)[8]) {
+  typename Vec8<W>::type v = load8<W>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = to_f32(v[i]);
+}
+template <>
+__device__ __forceinline__ void load8_f32<float>(const float* p, float (&f)[8]) {
+  f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = a[i];
+    f[i + 4] = b[i];
+  }
+}
+
+// Scalar load of element `i` of a buffer whose dtype is known only at run time.
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+  if (dtype == FD_F32) return static_cast<const float*>(p)[i];
+  if (dtype == FD_BF16) return to_f32(static_cast<const bf16*>(p)[i]);
+  return to_f32(static_cast<const f16*>(p)[i]);
+}
+
+// Row grid of fd_rows, as passed to a kernel (the row count is the grid size).
+struct RowIdx {
+  int64_t b, c;
+  int64_t sa, sb, sc;
+  int64_t col;
+};
+
+__host__ __device__ __forceinline__ RowIdx row_idx(const fd_rows& l) {
+  RowIdx r;
+  r.b = l.b;
+  r.c = l.c;
+  r.sa = l.sa;
+  r.sb = l.sb;
+  r.sc = l.sc;
+  r.col = l.col;
+  return r;
+}
+
+// Offset (elements) of the first element of linear row `row`.
+__device__ __forceinline__ int64_t row_base(const RowIdx& l, int64_t row) {
+  int64_t ci = row % l.c;
+  int64_t t = row / l.c;
+  int64_t bi = t % l.b;
+  int64_t ai = t / l.b;
+  return ai * l.sa + bi * l.sb + ci * l.sc;
+}
+
+// Dot product of 8 activation pairs accumulated into float32 with v_dot2
+// (each fp16/bf16 product is exact in float32).
+__device__ __forceinline__ float dot8(f16x8 a, f16x8 b, float acc) {
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 0, 1),
+                               __builtin_shufflevector(b, b, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3),
+                               __builtin_shufflevector(b, b, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5),
+                               __builtin_shufflevector(b, b, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7),
+                               __builtin_shufflevector(b, b, 6, 7), acc, false);
+  return acc;
+}
+__device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 0, 1),
+                                        __builtin_shufflevector(b, b, 0, 1), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2, 3),
+                                        __builtin_shufflevector(b, b, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 4, 5),
+                                        __builtin_shufflevector(b, b, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 6, 7),
+                                        __builtin_shufflevector(b, b, 6, 7), acc, false);
+  return acc;
+}
+
+// 16x16x32 MFMA: D[16x16] += A[16x32] * B[32x16], float32 accumulate.
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+// Transposing butterfly: V (a power of two <= 64) per-lane partial sums become
+// V wave-wide sums using V-1 exchanges instead of 6*V. Afterwards v[0] of lane
+// `l` holds the full sum of value index butterfly_index<V>(l).
+// One exchange step: COUNT live values, partner lane = lane ^ MASK. The lower
+// lane keeps the lower half of the values, the upper lane the upper half; each
+// adds the partner's copy of the half it keeps.
+template <int V, int COUNT, int MASK>
+struct Butterfly {
+  static __device__ __forceinline__ void run(float (&v)[V], int lane) {
+    constexpr int HALF = COUNT / 2;
+    const bool upper = (lane & MASK) != 0;
+#pragma unroll
+    for (int i = 0; i < HALF; ++i) {
+      const float send = upper ? v[i] : v[i + HALF];
+      const float keep = upper ? v[i + HALF] : v[i];
+      v[i] = keep + __shfl_xor(send, MASK, kWave);
+    }
+    Butterfly<V, HALF, MASK / 2>::run(v, lane);
+  }
+};
+// One value left: plain xor-reduction over the remaining lane bits.
+template <int V, int MASK>
+struct Butterfly<V, 1, MASK> {
+  static __device__ __forceinline__ void run(float (&v)[V], int lane) {
+    v[0] += __shfl_xor(v[0], MASK, kWave);
+    Butterfly<V, 1, MASK / 2>::run(v, lane);
+  }
+};
+template <int V, int COUNT>
+struct Butterfly<V, COUNT, 0> {
+  static __device__ __forceinline__ void run(float (&)[V], int) {}
+};
+template <int V>
+struct Butterfly<V, 1, 0> {
+  static __device__ __forceinline__ void run(float (&)[V], int) {}
+};
+
+template <int V>
+__device__ __forceinline__ void butterfly_sum(float (&v)[V], int lane) {
+  static_assert(V >= 1 && V <= 64 && (V & (V - 1)) == 0, "V must be a power of two <= 64");
+  Butterfly<V, V, 32>::run(v, lane);
+}
+
+// Value index whose wave-wide sum lane `lane` holds after butterfly_sum<V>.
+template <int V>
+__device__ __forceinline__ int butterfly_index(int lane) {
+  // The first log2(V) exchange masks are 32, 16, ...: lane bit (5 - s) selects the
+  // upper half at step s, contributing V >> (s + 1).
+  int idx = 0;
+  int count = V;
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) {
+    if (count > 1) {
+      if (lane & mask) idx += count >> 1;
+      count >>= 1;
+    }
+  }
+  return idx;
+}
+
+// Lanes that write a distinct value after butterfly_sum<V>: one per value index.
+template <int V>
+__device__ __forceinline__ bool butterfly_writer(int lane) {
+  // Value index bits come from the top log2(V) lane bits; the low bits are free.
+  constexpr int low = 64 / V;  // lanes sharing one value
+  return (lane & (low - 1)) == 0;
+}
+
+__device__ __forceinline__ float silu_stable(float g) {
+  // sigmoid(g) without overflow: exp of a non-positive argument only.
+  float e = __expf(-fabsf(g));
+  float sig = g >= 0.f ? 1.f / (1.f + e) : e / (1.f + e);
+  return g * sig;
+}
+
+}  // namespace fd

@@ -1,0 +1,665 @@
+// Small-M GEMV (M <= 16) and the fused Llama post-attention MLP for gfx950.
+//
+//   y[m,n] = round(sum_k x[m,k] * w[n,k] + bias[n] + row_add[m,n])
+//
+// At M <= 16 the product is weight streaming: every weight byte is read once
+// from HBM and used for M multiply-adds, so the kernels are built to keep many
+// 16-byte weight loads in flight and to touch every 128-byte line whole.
+//
+// SIMT kernel (gemv_simt_kernel, exact M): a workgroup owns R weight rows; its
+// waves split K into 512-element chunks (64 lanes x one 16-byte vector), each
+// lane streams its vector of every row and folds it against x with v_dot2
+// (fp16/bf16 pairs into float32). Per-lane partial sums are combined with a
+// transposing butterfly (V-1 exchanges for V sums) and then across waves in LDS.
+//
+// MFMA kernel (gemv_mfma_kernel, M padded to 16): a workgroup owns 16 weight
+// rows; waves split K into 128-element units of four v_mfma_f32_16x16x32 steps.
+// A = 16 weight rows x 32 k (lane l: row l%16, k-group l/16), B = x^T with the
+// same lane->k mapping, so padding rows m >= M are zero registers, not loads.
+//
+// Fused MLP: launch 1 computes the RMSNorm of hidden in a prologue (each
+// workgroup re-derives the row scale and stages the normalised activations in
+// LDS), streams matching gate row j and up row I+j, and writes only
+// mid = round(silu(round(g)) * round(u)). Launch 2 is the down GEMV with the
+// residual fused as row_add. Weights are read once; gate_up never exists in HBM.
+#include "fd_device.h"
+#include "fd_host.h"
+
+namespace fd {
+
+constexpr int kMaxWaves = 8;      // waves per workgroup (512 threads)
+constexpr int kChunk = 512;       // K elements one wave covers per SIMT step
+constexpr int kUnit = 128;        // K elements of one MFMA unit (4 steps of 32)
+
+constexpr int pow2_ceil(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+// Optional epilogue operands: bias[n] then row_add[m,n], added in float32 before
+// the single rounding of the output (kernels.py:657-672 order).
+struct Epi {
+  const void* bias;
+  int bias_dtype;
+  int64_t sb;
+  const void* row;
+  int row_dtype;
+  int64_t srm, srn;
+};
+
+__device__ __forceinline__ float epilogue(const Epi& e, float acc, int64_t m, int64_t n) {
+  if (e.bias) acc += load_any(e.bias, e.bias_dtype, n * e.sb);
+  if (e.row) acc += load_any(e.row, e.row_dtype, m * e.srm + n * e.srn);
+  return acc;
+}
+
+// Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
+// are R*M floats).
+template <int M> struct SimtRows { static constexpr int R = M <= 4 ? 8 : 4; };
+// Fused gate/up: R gate rows + R up rows.
+template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
+
+// ---------------------------------------------------------------------------
+// SIMT GEMV
+
+template <typename T, int M, int R>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
+    T* y, const T* x, const T* w, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
+    int64_t syn, Epi e) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(R * M);
+  __shared__ float part[kMaxWaves * V];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int64_t n0 = (int64_t)blockIdx.x * R;
+
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  const T* wr[R];
+  bool rok[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rok[r] = n0 + r < N;
+    wr[r] = w + (rok[r] ? n0 + r : 0) * swn;
+  }
+
+  for (int k = (wave * kWave + lane) * 8; k < K; k += nw * kChunk) {
+    V8 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[r] = rok[r] ? load8<T>(wr[r] + k) : V8{};
+    V8 xv[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) xv[m] = load8<T>(x + m * sxm + k);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(wv[r], xv[m], acc[r * M + m]);
+  }
+
+  butterfly_sum<V>(acc, lane);
+  if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+  __syncthreads();
+  for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+    const int r = t / M, m = t % M;
+    const int64_t n = n0 + r;
+    if (n < N) {
+      float s = 0.f;
+      for (int i = 0; i < nw; ++i) s += part[i * V + t];
+      y[m * sym + n * syn] = from_f32<T>(epilogue(e, s, m, n));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMV (M padded to 16)
+
+template <typename T>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_kernel(
+    T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
+    int64_t syn, Epi e) {
+  typedef typename Vec8<T>::type V8;
+  __shared__ f32x4 part[kMaxWaves * kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const bool wok = n0 + r < N;
+  const bool xok = r < M;
+  const T* wp = w + (wok ? n0 + r : 0) * swn + g * 8;
+  const T* xp = x + (xok ? r : 0) * sxm + g * 8;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int units = (K + kUnit - 1) / kUnit;
+  for (int u = wave; u < units; u += nw) {
+    V8 a[4], b[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int k = u * kUnit + s * 32;
+      const bool in = k + g * 8 < K;
+      a[s] = (wok && in) ? load8<T>(wp + k) : V8{};
+      b[s] = (xok && in) ? load8<T>(xp + k) : V8{};
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) acc = mfma16(a[s], b[s], acc);
+  }
+  part[wave * kWave + lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    f32x4 s = part[threadIdx.x];
+    for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
+    // D lane layout: lane t holds rows 4*(t/16)+i (weight rows), column t%16 (x row).
+    const int m = threadIdx.x & 15;
+    const int nb = (threadIdx.x >> 4) * 4;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + nb + i;
+        if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, s[i], m, n));
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Generic GEMV: any strides, any K. One workgroup per output column n.
+
+template <typename T>
+__global__ __launch_bounds__(256) void gemv_gen_kernel(T* y, const T* x, const T* w, int M,
+                                                       int64_t K, int64_t sxm, int64_t sxk,
+                                                       int64_t swn, int64_t swk, int64_t sym,
+                                                       int64_t syn, Epi e) {
+  __shared__ float red[4][16];
+  const int64_t n = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  float acc[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) acc[m] = 0.f;
+  for (int64_t k = threadIdx.x; k < K; k += 256) {
+    const float wv = to_f32(w[n * swn + k * swk]);
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      if (m < M) acc[m] += wv * to_f32(x[m * sxm + k * sxk]);
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    if (m < M) {
+      const float s = wave_sum(acc[m]);
+      if (lane == 0) red[wave][m] = s;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < M) {
+    const int m = threadIdx.x;
+    const float s = red[0][m] + red[1][m] + red[2][m] + red[3][m];
+    y[m * sym + n * syn] = from_f32<T>(epilogue(e, s, m, n));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Fused MLP, launch 1: RMSNorm prologue + gate/up GEMV + SwiGLU epilogue.
+
+// 8 consecutive norm-weight values of a run-time dtype (16-byte aligned).
+__device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k, float (&f)[8]) {
+  if (dtype == FD_F32)
+    load8_f32<float>(static_cast<const float*>(p) + k, f);
+  else if (dtype == FD_BF16)
+    load8_f32<bf16>(static_cast<const bf16*>(p) + k, f);
+  else
+    load8_f32<f16>(static_cast<const f16*>(p) + k, f);
+}
+
+// Stage round(hidden * rsqrt(mean(hidden^2) + eps) * norm_w) for all M rows in
+// LDS (xs, [M][H]). `scratch` needs kMaxWaves*16 + 16 floats.
+template <typename T, int MMAX>
+__device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hidden,
+                                             const void* nwp, int nw_dtype, int M, int H,
+                                             float eps) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int MP = pow2_ceil(MMAX);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int nt = blockDim.x, nwv = nt / kWave;
+  float ss[MP];
+#pragma unroll
+  for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+  for (int k = tid * 8; k < H; k += nt * 8) {
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m < M) {
+        V8 h = load8<T>(hidden + (int64_t)m * H + k);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss[m] += to_f32(h[i]) * to_f32(h[i]);
+      }
+    }
+  }
+  butterfly_sum<MP>(ss, lane);
+  float* inv = scratch + kMaxWaves * MP;
+  if (butterfly_writer<MP>(lane)) scratch[wave * MP + butterfly_index<MP>(lane)] = ss[0];
+  __syncthreads();
+  if (tid < M) {
+    float s = 0.f;
+    for (int i = 0; i < nwv; ++i) s += scratch[i * MP + tid];
+    inv[tid] = rsqrtf(s / (float)H + eps);
+  }
+  __syncthreads();
+  for (int k = tid * 8; k < H; k += nt * 8) {
+    float wf[8];
+    load8_norm_w(nwp, nw_dtype, k, wf);
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m < M) {
+        V8 h = load8<T>(hidden + (int64_t)m * H + k);
+        const float s = inv[m];
+        V8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(h[i]) * s * wf[i]);
+        store8<T>(xs + (int64_t)m * H + k, o);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+template <typename T>
+__device__ __forceinline__ T swiglu_out(float g, float u) {
+  return from_f32<T>(silu_stable(round_as<T>(g)) * round_as<T>(u));
+}
+
+constexpr int kNormScratch = kMaxWaves * 16 + 16;
+
+template <typename T, int M, int R>
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
+    T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int H, int I,
+    float eps, int tiles) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(2 * R * M);
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* xs = reinterpret_cast<T*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)M * H * sizeof(T));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+
+  stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t j0 = (int64_t)tile * R;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    const T* wg[R];
+    const T* wu[R];
+    bool rok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      rok[r] = j0 + r < I;
+      const int64_t j = rok[r] ? j0 + r : 0;
+      wg[r] = wgu + j * H;
+      wu[r] = wgu + (I + j) * H;
+    }
+    for (int k = (wave * kWave + lane) * 8; k < H; k += nw * kChunk) {
+      V8 gv[R], uv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        gv[r] = rok[r] ? load8<T>(wg[r] + k) : V8{};
+        uv[r] = rok[r] ? load8<T>(wu[r] + k) : V8{};
+      }
+      V8 xv[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * H + k);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          acc[r * M + m] = dot8(gv[r], xv[m], acc[r * M + m]);
+          acc[R * M + r * M + m] = dot8(uv[r], xv[m], acc[R * M + r * M + m]);
+        }
+    }
+    butterfly_sum<V>(acc, lane);
+    __syncthreads();  // previous tile's readers of `part` are done
+    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    __syncthreads();
+    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+      const int r = t / M, m = t % M;
+      const int64_t j = j0 + r;
+      if (j < I) {
+        float gs = 0.f, us = 0.f;
+        for (int i = 0; i < nw; ++i) {
+          gs += part[i * V + t];
+          us += part[i * V + R * M + t];
+        }
+        mid[m * (int64_t)I + j] = swiglu_out<T>(gs, us);
+      }
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
+    T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int M, int H, int I,
+    float eps, int tiles) {
+  typedef typename Vec8<T>::type V8;
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* xs = reinterpret_cast<T*>(smem);
+  f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)M * H * sizeof(T));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int r = lane & 15, g = lane >> 4;
+
+  stage_normed<T, 16>(xs, reinterpret_cast<float*>(part), hidden, nwp, nw_dtype, M, H, eps);
+
+  const bool xok = r < M;
+  const T* xp = xs + (xok ? r : 0) * H + g * 8;
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t j0 = (int64_t)tile * 16;
+    const bool wok = j0 + r < I;
+    const int64_t j = wok ? j0 + r : 0;
+    const T* gp = wgu + j * H + g * 8;
+    const T* up = wgu + (I + j) * H + g * 8;
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+    const int units = (H + kUnit - 1) / kUnit;
+    for (int u = wave; u < units; u += nw) {
+      V8 a[4], c[4], b[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = u * kUnit + s * 32;
+        const bool in = k + g * 8 < H;
+        a[s] = (wok && in) ? load8<T>(gp + k) : V8{};
+        c[s] = (wok && in) ? load8<T>(up + k) : V8{};
+        b[s] = (xok && in) ? load8<T>(xp + k) : V8{};
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        ag = mfma16(a[s], b[s], ag);
+        au = mfma16(c[s], b[s], au);
+      }
+    }
+    __syncthreads();  // previous tile's readers of `part` are done
+    part[wave * kWave + lane] = ag;
+    part[(kMaxWaves + wave) * kWave + lane] = au;
+    __syncthreads();
+    if (threadIdx.x < kWave) {
+      f32x4 sg = part[threadIdx.x], su = part[kMaxWaves * kWave + threadIdx.x];
+      for (int i = 1; i < nw; ++i) {
+        sg += part[i * kWave + threadIdx.x];
+        su += part[(kMaxWaves + i) * kWave + threadIdx.x];
+      }
+      const int m = threadIdx.x & 15;
+      const int nb = (threadIdx.x >> 4) * 4;
+      if (m < M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t jj = j0 + nb + i;
+          if (jj < I) mid[m * (int64_t)I + jj] = swiglu_out<T>(sg[i], su[i]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+
+namespace {
+
+constexpr int kMfmaMinM = 8;   // kind=dot uses MFMA from this M on
+constexpr size_t kMaxLds = 160 * 1024;
+
+// Waves per workgroup: enough to cover K with whole work items (512-element
+// chunks for SIMT, 128-element units for MFMA) in as even a split as possible.
+int pick_waves(int64_t items) {
+  if (items <= kMaxWaves) return (int)(items < 1 ? 1 : items);
+  for (int d = kMaxWaves; d >= 4; --d)
+    if (items % d == 0) return d;
+  return kMaxWaves;
+}
+
+template <typename T, int M>
+void launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                 int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+  constexpr int R = SimtRows<M>::R;
+  const int nw = pick_waves((K + kChunk - 1) / kChunk);
+  const unsigned blocks = (unsigned)((N + R - 1) / R);
+  hipLaunchKernelGGL((gemv_simt_kernel<T, M, R>), dim3(blocks), dim3(nw * kWave), 0, st,
+                     static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), N,
+                     K, sxm, swn, sym, syn, e);
+}
+
+template <typename T>
+void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
+                   int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: launch_simt<T, MM>(y, x, w, N, K, sxm, swn, sym, syn, e, st); break;
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+    FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
+    FD_CASE(16)
+#undef FD_CASE
+    default: break;
+  }
+}
+
+template <typename T>
+void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
+                 int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+  const int nw = pick_waves((K + kUnit - 1) / kUnit);
+  const unsigned blocks = (unsigned)((N + 15) / 16);
+  hipLaunchKernelGGL(gemv_mfma_kernel<T>, dim3(blocks), dim3(nw * kWave), 0, st,
+                     static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), M,
+                     N, K, sxm, swn, sym, syn, e);
+}
+
+// The dynamic-LDS limit of a kernel must be raised before a launch above 64 KiB.
+template <typename F>
+bool allow_lds(F kernel, size_t bytes) {
+  if (bytes <= 64 * 1024) return true;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes) == hipSuccess;
+}
+
+template <typename T, int M>
+int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype, const void* wgu,
+                    int H, int I, float eps, hipStream_t st) {
+  constexpr int R = MlpRows<M>::R;
+  constexpr int V = pow2_ceil(2 * R * M);
+  const size_t lds = (size_t)M * H * sizeof(T) +
+                     sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
+                                                                           : kNormScratch);
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  if (!allow_lds(mlp_gate_up_simt_kernel<T, M, R>, lds))
+    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  const int tiles = (I + R - 1) / R;
+  const int per = (tiles + 1023) / 1024;
+  const int grid = (tiles + per - 1) / per;
+  const int nwv = pick_waves((H + kChunk - 1) / kChunk);
+  hipLaunchKernelGGL((mlp_gate_up_simt_kernel<T, M, R>), dim3(grid), dim3(nwv * kWave), lds, st,
+                     static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
+                     static_cast<const T*>(wgu), H, I, eps, tiles);
+  return FD_OK;
+}
+
+template <typename T>
+int launch_mlp_simt_m(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
+                      const void* wgu, int H, int I, float eps, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return launch_mlp_simt<T, MM>(mid, hidden, nw, nw_dtype, wgu, H, I, eps, st);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+    FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
+    FD_CASE(16)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "M must be in [1, 16]");
+  }
+}
+
+template <typename T>
+int launch_mlp_mfma(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
+                    const void* wgu, int H, int I, float eps, hipStream_t st) {
+  const size_t lds = (size_t)M * H * sizeof(T) + sizeof(f32x4) * 2 * kMaxWaves * kWave;
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  if (!allow_lds(mlp_gate_up_mfma_kernel<T>, lds))
+    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  const int tiles = (I + 15) / 16;
+  const int per = (tiles + 1023) / 1024;
+  const int grid = (tiles + per - 1) / per;
+  const int nwv = pick_waves((H + kUnit - 1) / kUnit);
+  hipLaunchKernelGGL(mlp_gate_up_mfma_kernel<T>, dim3(grid), dim3(nwv * kWave), lds, st,
+                     static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
+                     static_cast<const T*>(wgu), M, H, I, eps, tiles);
+  return FD_OK;
+}
+
+// Launch the GEMV that fits the operands: the vector kernels need unit K
+// stride, K % 8 == 0 and 16-byte aligned rows; anything else takes the generic one.
+int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t M, int64_t N,
+                    int64_t K, int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sym,
+                    int64_t syn, int kind, int act_dtype, hipStream_t st) {
+  const bool fast = K % 8 == 0 && swk == 1 && sxk == 1 && aligned16(w) && aligned16(x) &&
+                    (N == 1 || swn % 8 == 0) && (M == 1 || sxm % 8 == 0) && N <= 0x7fffffffLL &&
+                    K <= 0x7fffffffLL;
+  if (!fast) {
+    if (N > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "N too large");
+    if (act_dtype == FD_F16)
+      hipLaunchKernelGGL(gemv_gen_kernel<f16>, dim3((unsigned)N), dim3(256), 0, st, (f16*)y,
+                         (const f16*)x, (const f16*)w, (int)M, K, sxm, sxk, swn, swk, sym, syn, e);
+    else
+      hipLaunchKernelGGL(gemv_gen_kernel<bf16>, dim3((unsigned)N), dim3(256), 0, st, (bf16*)y,
+                         (const bf16*)x, (const bf16*)w, (int)M, K, sxm, sxk, swn, swk, sym, syn,
+                         e);
+    return FD_OK;
+  }
+  const bool mfma = kind == FD_KIND_DOT && M >= kMfmaMinM;
+  if (act_dtype == FD_F16) {
+    if (mfma)
+      launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+    else
+      launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  } else {
+    if (mfma)
+      launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+    else
+      launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  }
+  return FD_OK;
+}
+
+}  // namespace
+}  // namespace fd
+
+using namespace fd;
+
+extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+                         const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+                         int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb,
+                         int64_t srm, int64_t srn, int64_t sym, int64_t syn, int kind,
+                         int act_dtype, void* stream) {
+  if (!check_act_dtype(act_dtype)) return FD_EINVAL;
+  if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
+    return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
+  if (M < 0 || N < 0 || K < 0) return set_error(FD_EINVAL, "negative size");
+  if (M > 16) return set_error(FD_EINVAL, "linear_out only covers M <= 16");
+  if (sxm < 0 || sxk < 0 || swn < 0 || swk < 0 || sb < 0 || srm < 0 || srn < 0 || sym < 0 ||
+      syn < 0)
+    return set_error(FD_EINVAL, "negative stride");
+  if (bias && bias_dtype != act_dtype && bias_dtype != FD_F32)
+    return set_error(FD_EINVAL, "bias must match x or be float32");
+  if (row_add && !check_any_dtype(row_dtype, "row_dtype")) return FD_EINVAL;
+  if (M == 0 || N == 0) return FD_OK;
+  if (!y || !w || (!x && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
+  Epi e;
+  e.bias = bias;
+  e.bias_dtype = bias_dtype;
+  e.sb = sb;
+  e.row = row_add;
+  e.row_dtype = row_dtype;
+  e.srm = srm;
+  e.srn = srn;
+  const int rc = linear_dispatch(y, x, w, e, M, N, K, sxm, sxk, swn, swk, sym, syn, kind,
+                                 act_dtype, static_cast<hipStream_t>(stream));
+  if (rc != FD_OK) return rc;
+  return check_launch();
+}
+
+namespace fd {
+namespace {
+
+int mlp_check(void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+              const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
+              int act_dtype) {
+  if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
+    return FD_EINVAL;
+  if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
+    return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
+  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
+  if (H <= 0 || I <= 0) return set_error(FD_EINVAL, "H and I must be positive");
+  if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
+  if (M == 0) return FD_OK;
+  if (!mid || !hidden || !norm_w || !w_gate_up) return set_error(FD_EINVAL, "null pointer argument");
+  if (H % 8 != 0 || I % 8 != 0)
+    return set_error(FD_EUNSUPPORTED, "H and I must be multiples of 8");
+  if (H > 0x7fffffffLL || 2 * I > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
+  if (!aligned16(mid) || !aligned16(hidden) || !aligned16(norm_w) || !aligned16(w_gate_up))
+    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  return FD_OK;
+}
+
+int mlp_gate_up(void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+                const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
+                int act_dtype, hipStream_t st) {
+  const bool mfma = kind == FD_KIND_DOT && M >= kMfmaMinM;
+  int rc;
+  if (act_dtype == FD_F16)
+    rc = mfma ? launch_mlp_mfma<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
+                                     (int)I, eps, st)
+              : launch_mlp_simt_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
+                                       (int)H, (int)I, eps, st);
+  else
+    rc = mfma ? launch_mlp_mfma<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
+                                      (int)H, (int)I, eps, st)
+              : launch_mlp_simt_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
+                                        (int)H, (int)I, eps, st);
+  if (rc != FD_OK) return rc;
+  return check_launch();
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_mlp_gate_up(void* mid, const void* hidden, const void* norm_w,
+                              int norm_w_dtype, const void* w_gate_up, int64_t M, int64_t H,
+                              int64_t I, float eps, int kind, int act_dtype, void* stream) {
+  int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
+  if (rc != FD_OK || M == 0) return rc;
+  return mlp_gate_up(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype,
+                     static_cast<hipStream_t>(stream));
+}
+
+extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
+                                int norm_w_dtype, const void* w_gate_up, const void* w_down,
+                                int64_t M, int64_t H, int64_t I, float eps, int kind,
+                                int act_dtype, void* stream) {
+  int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
+  if (rc != FD_OK || M == 0) return rc;
+  if (!y || !w_down) return set_error(FD_EINVAL, "null pointer argument");
+  if (!aligned16(y) || !aligned16(w_down))
+    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  rc = mlp_gate_up(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype, st);
+  if (rc != FD_OK) return rc;
+  Epi e;
+  e.bias = nullptr;
+  e.bias_dtype = act_dtype;
+  e.sb = 0;
+  e.row = hidden;
+  e.row_dtype = act_dtype;
+  e.srm = H;
+  e.srn = 1;
+  rc = linear_dispatch(y, mid, w_down, e, M, H, I, I, 1, I, 1, H, 1, kind, act_dtype, st);
+  if (rc != FD_OK) return rc;
+  return check_launch();
+}

@@ -1,0 +1,213 @@
+// Streaming elementwise kernels for gfx950: SwiGLU and rotate-half RoPE.
+//
+// Both run on the row grid of fd_rows (up to three leading dims with arbitrary
+// strides, including 0 for broadcast operands). The vector kernels move one
+// 16-byte vector per operand per thread; the generic kernels take any column
+// stride and any row length.
+#include "fd_device.h"
+#include "fd_host.h"
+
+namespace fd {
+
+constexpr int kPwThreads = 256;
+
+// ---------------------------------------------------------------------------
+// SwiGLU: y = round(silu(g) * u), float32 math (reference.py:33-35, stable sigmoid
+// as kernels.py:448-451).
+
+template <typename T>
+__global__ __launch_bounds__(kPwThreads) void swiglu_vec_kernel(T* y, const T* g, const T* u,
+                                                                RowIdx lg, RowIdx lu, RowIdx ly,
+                                                                uint32_t vpr, uint32_t total) {
+  const uint32_t v = blockIdx.x * kPwThreads + threadIdx.x;
+  if (v >= total) return;
+  const uint32_t row = v / vpr;
+  const uint32_t k = (v - row * vpr) * 8;
+  typename Vec8<T>::type a = load8<T>(g + row_base(lg, row) + k);
+  typename Vec8<T>::type b = load8<T>(u + row_base(lu, row) + k);
+  typename Vec8<T>::type o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(silu_stable(to_f32(a[i])) * to_f32(b[i]));
+  store8<T>(y + row_base(ly, row) + k, o);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPwThreads) void swiglu_gen_kernel(T* y, const T* g, const T* u,
+                                                                RowIdx lg, RowIdx lu, RowIdx ly,
+                                                                int64_t n, int64_t total) {
+  const int64_t e = (int64_t)blockIdx.x * kPwThreads + threadIdx.x;
+  if (e >= total) return;
+  const int64_t row = e / n;
+  const int64_t k = e - row * n;
+  const float a = to_f32(g[row_base(lg, row) + k * lg.col]);
+  const float b = to_f32(u[row_base(lu, row) + k * lu.col]);
+  y[row_base(ly, row) + k * ly.col] = from_f32<T>(silu_stable(a) * b);
+}
+
+// ---------------------------------------------------------------------------
+// RoPE, rotate-half pairing (reference.py:38-47):
+//   y[j]     = x[j] * c[j]     - x[j+h] * s[j]
+//   y[j + h] = x[j+h] * c[j+h] + x[j] * s[j+h]
+
+template <typename T, typename C>
+__global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, const C* cs,
+                                                              const C* sn, RowIdx lx, RowIdx lc,
+                                                              RowIdx ls, RowIdx ly, uint32_t h,
+                                                              uint32_t vpr, uint32_t total) {
+  const uint32_t v = blockIdx.x * kPwThreads + threadIdx.x;
+  if (v >= total) return;
+  const uint32_t row = v / vpr;
+  const uint32_t j = (v - row * vpr) * 8;
+  const T* xr = x + row_base(lx, row);
+  const C* cr = cs + row_base(lc, row);
+  const C* sr = sn + row_base(ls, row);
+  typename Vec8<T>::type x1 = load8<T>(xr + j);
+  typename Vec8<T>::type x2 = load8<T>(xr + j + h);
+  float c1[8], c2[8], s1[8], s2[8];
+  load8_f32<C>(cr + j, c1);
+  load8_f32<C>(cr + j + h, c2);
+  load8_f32<C>(sr + j, s1);
+  load8_f32<C>(sr + j + h, s2);
+  typename Vec8<T>::type o1, o2;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float a = to_f32(x1[i]), b = to_f32(x2[i]);
+    o1[i] = from_f32<T>(a * c1[i] - b * s1[i]);
+    o2[i] = from_f32<T>(b * c2[i] + a * s2[i]);
+  }
+  T* yr = y + row_base(ly, row);
+  store8<T>(yr + j, o1);
+  store8<T>(yr + j + h, o2);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPwThreads) void rope_gen_kernel(T* y, const T* x, const void* cs,
+                                                              const void* sn, int cs_dtype,
+                                                              RowIdx lx, RowIdx lc, RowIdx ls,
+                                                              RowIdx ly, int64_t h,
+                                                              int64_t total) {
+  const int64_t e = (int64_t)blockIdx.x * kPwThreads + threadIdx.x;
+  if (e >= total) return;
+  const int64_t row = e / h;
+  const int64_t j = e - row * h;
+  const T* xr = x + row_base(lx, row);
+  const int64_t cb = row_base(lc, row), sb = row_base(ls, row);
+  const float a = to_f32(xr[j * lx.col]);
+  const float b = to_f32(xr[(j + h) * lx.col]);
+  const float c1 = load_any(cs, cs_dtype, cb + j * lc.col);
+  const float c2 = load_any(cs, cs_dtype, cb + (j + h) * lc.col);
+  const float s1 = load_any(sn, cs_dtype, sb + j * ls.col);
+  const float s2 = load_any(sn, cs_dtype, sb + (j + h) * ls.col);
+  T* yr = y + row_base(ly, row);
+  yr[j * ly.col] = from_f32<T>(a * c1 - b * s1);
+  yr[(j + h) * ly.col] = from_f32<T>(b * c2 + a * s2);
+}
+
+namespace {
+
+inline unsigned blocks_for(int64_t work) {
+  return (unsigned)((work + kPwThreads - 1) / kPwThreads);
+}
+
+// Row layout with the last dim halved: the vector rope kernel addresses pairs
+// (j, j+h), so alignment is needed at both j and h.
+inline bool rope_rows_vec(const void* p, const fd_rows& l, int elem) {
+  fd_rows half = l;
+  half.n = l.n / 2;
+  return rows_vectorizable(p, half, elem);
+}
+
+}  // namespace
+}  // namespace fd
+
+using namespace fd;
+
+extern "C" int fd_swiglu(void* y, const void* gate, const void* up, const fd_rows* lg,
+                         const fd_rows* lu, const fd_rows* ly, int act_dtype, void* stream) {
+  if (!check_act_dtype(act_dtype)) return FD_EINVAL;
+  if (!y || !gate || !up || !lg || !lu || !ly) return set_error(FD_EINVAL, "null pointer argument");
+  if (!check_rows(*lg, "gate") || !check_rows(*lu, "up") || !check_rows(*ly, "out") ||
+      !same_grid(*lg, *lu, "up") || !same_grid(*lg, *ly, "out"))
+    return FD_EINVAL;
+  const int64_t rows = lg->a * lg->b * lg->c;
+  const int64_t total = rows * lg->n;
+  if (total == 0) return FD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool vec = rows_vectorizable(gate, *lg, 2) && rows_vectorizable(up, *lu, 2) &&
+                   rows_vectorizable(y, *ly, 2) && total / 8 < 0xffffffffLL - kPwThreads;
+  if (vec) {
+    const uint32_t vpr = (uint32_t)(lg->n / 8);
+    const uint32_t tv = (uint32_t)(total / 8);
+    if (act_dtype == FD_F16)
+      hipLaunchKernelGGL(swiglu_vec_kernel<f16>, dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,
+                         (f16*)y, (const f16*)gate, (const f16*)up, row_idx(*lg), row_idx(*lu),
+                         row_idx(*ly), vpr, tv);
+    else
+      hipLaunchKernelGGL(swiglu_vec_kernel<bf16>, dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,
+                         (bf16*)y, (const bf16*)gate, (const bf16*)up, row_idx(*lg),
+                         row_idx(*lu), row_idx(*ly), vpr, tv);
+  } else {
+    if (blocks_for(total) == 0 || total / kPwThreads > 0x7fffffffLL)
+      return set_error(FD_EUNSUPPORTED, "swiglu tensor too large");
+    if (act_dtype == FD_F16)
+      hipLaunchKernelGGL(swiglu_gen_kernel<f16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
+                         st, (f16*)y, (const f16*)gate, (const f16*)up, row_idx(*lg),
+                         row_idx(*lu), row_idx(*ly), lg->n, total);
+    else
+      hipLaunchKernelGGL(swiglu_gen_kernel<bf16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
+                         st, (bf16*)y, (const bf16*)gate, (const bf16*)up, row_idx(*lg),
+                         row_idx(*lu), row_idx(*ly), lg->n, total);
+  }
+  return check_launch();
+}
+
+extern "C" int fd_rope(void* y, const void* x, const void* cos, const void* sin, int cs_dtype,
+                       const fd_rows* lx, const fd_rows* lc, const fd_rows* ls,
+                       const fd_rows* ly, int act_dtype, void* stream) {
+  if (!check_act_dtype(act_dtype) || !check_any_dtype(cs_dtype, "cs_dtype")) return FD_EINVAL;
+  if (!y || !x || !cos || !sin || !lx || !lc || !ls || !ly)
+    return set_error(FD_EINVAL, "null pointer argument");
+  if (!check_rows(*lx, "x") || !check_rows(*lc, "cos") || !check_rows(*ls, "sin") ||
+      !check_rows(*ly, "out") || !same_grid(*lx, *lc, "cos") || !same_grid(*lx, *ls, "sin") ||
+      !same_grid(*lx, *ly, "out"))
+    return FD_EINVAL;
+  if (lx->n % 2 != 0) return set_error(FD_EINVAL, "rope last dimension must be even");
+  const int64_t rows = lx->a * lx->b * lx->c;
+  const int64_t h = lx->n / 2;
+  const int64_t total = rows * h;
+  if (total == 0) return FD_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int cse = cs_dtype == FD_F32 ? 4 : 2;
+  const bool vec = rope_rows_vec(x, *lx, 2) && rope_rows_vec(y, *ly, 2) &&
+                   rope_rows_vec(cos, *lc, cse) && rope_rows_vec(sin, *ls, cse) &&
+                   (cse == 2 || h % 4 == 0) && total / 8 < 0xffffffffLL - kPwThreads;
+  if (vec) {
+    const uint32_t vpr = (uint32_t)(h / 8);
+    const uint32_t tv = (uint32_t)(total / 8);
+#define FD_ROPE_VEC(T, C)                                                                     \
+  hipLaunchKernelGGL((rope_vec_kernel<T, C>), dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,  \
+                     (T*)y, (const T*)x, (const C*)cos, (const C*)sin, row_idx(*lx),          \
+                     row_idx(*lc), row_idx(*ls), row_idx(*ly), (uint32_t)h, vpr, tv)
+    if (act_dtype == FD_F16) {
+      if (cs_dtype == FD_F32) FD_ROPE_VEC(f16, float);
+      else if (cs_dtype == FD_BF16) FD_ROPE_VEC(f16, bf16);
+      else FD_ROPE_VEC(f16, f16);
+    } else {
+      if (cs_dtype == FD_F32) FD_ROPE_VEC(bf16, float);
+      else if (cs_dtype == FD_BF16) FD_ROPE_VEC(bf16, bf16);
+      else FD_ROPE_VEC(bf16, f16);
+    }
+#undef FD_ROPE_VEC
+  } else {
+    if (total / kPwThreads > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "rope tensor too large");
+    if (act_dtype == FD_F16)
+      hipLaunchKernelGGL(rope_gen_kernel<f16>, dim3(blocks_for(total)), dim3(kPwThreads), 0, st,
+                         (f16*)y, (const f16*)x, cos, sin, cs_dtype, row_idx(*lx), row_idx(*lc),
+                         row_idx(*ls), row_idx(*ly), h, total);
+    else
+      hipLaunchKernelGGL(rope_gen_kernel<bf16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
+                         st, (bf16*)y, (const bf16*)x, cos, sin, cs_dtype, row_idx(*lx),
+                         row_idx(*lc), row_idx(*ls), row_idx(*ly), h, total);
+  }
+  return check_launch();
+}

@@ -1,0 +1,109 @@
+"""ctypes binding of libfused_decode_hip.so (the C ABI in include/fused_decode.h).
+
+The shared library is loaded after torch, so its dependency on
+``libamdhip64.so.7`` resolves to the HIP runtime torch already loaded: streams
+and graph captures are shared with torch. There is no fallback: if the library
+is missing, every operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime before ours)
+
+LIB_NAME = "libfused_decode_hip.so"
+LIB_PATH = Path(os.environ.get("FUSED_DECODE_LIB", Path(__file__).with_name(LIB_NAME)))
+
+FD_F16, FD_BF16, FD_F32 = 0, 1, 2
+FD_KIND_DOT, FD_KIND_SIMT = 0, 1
+FD_OK, FD_EINVAL, FD_EUNSUPPORTED, FD_ELAUNCH = 0, 1, 2, 3
+
+DTYPE_CODE = {torch.float16: FD_F16, torch.bfloat16: FD_BF16, torch.float32: FD_F32}
+KIND_CODE = {"dot": FD_KIND_DOT, "simt": FD_KIND_SIMT}
+
+
+class FdRows(ctypes.Structure):
+    """``fd_rows``: a*b*c rows of n elements; row (i,j,l) at i*sa+j*sb+l*sc."""
+
+    _fields_ = [
+        ("a", ctypes.c_int64),
+        ("b", ctypes.c_int64),
+        ("c", ctypes.c_int64),
+        ("sa", ctypes.c_int64),
+        ("sb", ctypes.c_int64),
+        ("sc", ctypes.c_int64),
+        ("col", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+    ]
+
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_l = ctypes.c_int64
+_f = ctypes.c_float
+_rows = ctypes.POINTER(FdRows)
+
+# name -> argument types; every entry point returns an int status.
+SIGNATURES: dict[str, list] = {
+    "fd_version": [],
+    "fd_runtime_version": [ctypes.POINTER(ctypes.c_int)],
+    "fd_rms_norm": [_p, _p, _p, _i, _l, _rows, _rows, _f, _i, _p],
+    "fd_add_rms_norm": [_p, _p, _p, _p, _p, _i, _l, _rows, _rows, _rows, _rows, _f, _i, _p],
+    "fd_swiglu": [_p, _p, _p, _rows, _rows, _rows, _i, _p],
+    "fd_rope": [_p, _p, _p, _p, _i, _rows, _rows, _rows, _rows, _i, _p],
+    "fd_linear": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _i, _p],
+    "fd_post_attn_mlp": [_p, _p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p],
+    "fd_mlp_gate_up": [_p, _p, _p, _i, _p, _l, _l, _l, _f, _i, _i, _p],
+    "fd_copy": [_p, _p, _l, _p],
+    "fd_triad": [_p, _p, _p, _f, _l, _i, _p],
+}
+
+_LIB: ctypes.CDLL | None = None
+
+
+class FusedDecodeError(RuntimeError):
+    """A non-OK status from the HIP library."""
+
+    def __init__(self, func: str, status: int, message: str):
+        super().__init__(f"{func} failed (status {status}): {message}")
+        self.status = status
+
+
+def lib() -> ctypes.CDLL:
+    """Load the library once; raise if it has not been built."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: run `python fused-decode_amd/build.py` "
+                "(or __graft_entry__.build()) first"
+            )
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        handle.fd_last_error.argtypes = []
+        handle.fd_last_error.restype = ctypes.c_char_p
+        _LIB = handle
+    return _LIB
+
+
+def check(func: str, status: int) -> None:
+    if status != FD_OK:
+        msg = lib().fd_last_error().decode(errors="replace")
+        raise FusedDecodeError(func, status, msg)
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """Handle of torch's current stream on the tensor's device."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def runtime_version() -> int:
+    v = ctypes.c_int(0)
+    check("fd_runtime_version", lib().fd_runtime_version(ctypes.byref(v)))
+    return v.value

@@ -1,0 +1,236 @@
+"""Launchers: Python-side calls into the gfx950 HIP library.
+
+Same launcher boundary as the reference's src/fused_decode/kernels.py
+(``rms_out``, ``swiglu_out``, ``rope_out``, ``linear_out``, ``resolve_kind``,
+``linear_config``, ``launch_copy``, ``launch_triad``), but every launch goes
+through the C ABI of libfused_decode_hip.so on torch's current stream. The
+launchers write into caller-provided tensors and never synchronise, so they can
+be captured into a HIP graph.
+"""
+
+from __future__ import annotations
+
+import os
+import warnings
+
+import torch
+
+from . import _lib
+from ._layout import finish, joint_layout
+from ._lib import DTYPE_CODE, KIND_CODE, check, lib, stream_of
+
+_warned: set[str] = set()
+
+
+def _warn_once(key: str, msg: str) -> None:
+    if key not in _warned:
+        _warned.add(key)
+        warnings.warn(msg, RuntimeWarning, stacklevel=3)
+
+
+def _rms_env() -> None:
+    """The reference's Triton tile knobs (kernels.py:91-108) have no meaning for
+    the HIP kernels. FUSED_DECODE_RMS_BLOCK keeps its power-of-two validation;
+    both are otherwise ignored with a one-time warning."""
+    block = os.environ.get("FUSED_DECODE_RMS_BLOCK")
+    if block:
+        b = int(block)
+        if b & (b - 1):
+            raise ValueError("FUSED_DECODE_RMS_BLOCK must be a power of 2")
+        _warn_once("rms_block", "FUSED_DECODE_RMS_BLOCK is a Triton tile knob; the HIP RMSNorm ignores it")
+    if os.environ.get("FUSED_DECODE_RMS_WARPS"):
+        _warn_once("rms_warps", "FUSED_DECODE_RMS_WARPS is a Triton knob; the HIP RMSNorm ignores it")
+
+
+def rms_out(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    eps: float,
+    out: torch.Tensor,
+    residual: torch.Tensor | None = None,
+    residual_out: torch.Tensor | None = None,
+) -> None:
+    """RMSNorm (and fused residual add) into ``out``; mirrors kernels.py:343-414."""
+    _rms_env()
+    add = residual is not None
+    if add and residual_out is None:
+        raise ValueError("residual requires residual_out")
+    ins = [x, residual] if add else [x]
+    outs = [out, residual_out] if add else [out]
+    for t, what in zip(ins[1:] + outs, (["residual"] if add else []) + ["out"] + (["residual_out"] if add else [])):
+        if tuple(t.shape) != tuple(x.shape):
+            raise ValueError(f"{what} cannot be indexed with the same row grid as the input")
+    if x.numel() == 0:
+        return
+    li, lo = joint_layout(ins, outs)
+    act = DTYPE_CODE[x.dtype]
+    w_code = DTYPE_CODE[weight.dtype]
+    st = stream_of(x)
+    if add:
+        status = lib().fd_add_rms_norm(
+            lo[0].tensor.data_ptr(), lo[1].tensor.data_ptr(), li[0].tensor.data_ptr(),
+            li[1].tensor.data_ptr(), weight.data_ptr(), w_code, int(weight.stride(0)),
+            li[0].rows, li[1].rows, lo[0].rows, lo[1].rows, float(eps), act, st,
+        )
+        check("fd_add_rms_norm", status)
+    else:
+        status = lib().fd_rms_norm(
+            lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), weight.data_ptr(), w_code,
+            int(weight.stride(0)), li[0].rows, lo[0].rows, float(eps), act, st,
+        )
+        check("fd_rms_norm", status)
+    finish(lo)
+
+
+def swiglu_out(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:
+    """``out = silu(gate) * up``; mirrors kernels.py:456-487."""
+    if gate.numel() == 0:
+        return
+    li, lo = joint_layout([gate, up], [out])
+    status = lib().fd_swiglu(
+        lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), li[1].tensor.data_ptr(),
+        li[0].rows, li[1].rows, lo[0].rows, DTYPE_CODE[gate.dtype], stream_of(gate),
+    )
+    check("fd_swiglu", status)
+    finish(lo)
+
+
+def rope_out(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, out: torch.Tensor) -> None:
+    """Rotate-half RoPE; ``cos``/``sin`` already expanded to ``x.shape``
+    (stride-0 broadcast dims). Mirrors kernels.py:541-578."""
+    if x.numel() == 0:
+        return
+    if cos.dtype != sin.dtype:
+        # one dtype code per launch: widen both (exact for fp16/bf16 -> fp32)
+        cos, sin = cos.float(), sin.float()
+    li, lo = joint_layout([x, cos, sin], [out])
+    status = lib().fd_rope(
+        lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), li[1].tensor.data_ptr(),
+        li[2].tensor.data_ptr(), DTYPE_CODE[cos.dtype], li[0].rows, li[1].rows, li[2].rows,
+        lo[0].rows, DTYPE_CODE[x.dtype], stream_of(x),
+    )
+    check("fd_rope", status)
+    finish(lo)
+
+
+def resolve_kind(kind: str | None) -> str:
+    """``kind`` or ``FUSED_DECODE_LINEAR_KIND`` (default "dot"); mirrors kernels.py:581-586."""
+    if kind is None:
+        kind = os.environ.get("FUSED_DECODE_LINEAR_KIND", "dot")
+    if kind not in ("dot", "simt"):
+        raise ValueError("kind must be 'dot' or 'simt'")
+    return kind
+
+
+def linear_config(kind: str, n: int, k: int) -> tuple[int, int, int]:
+    """Tiling the HIP GEMV picks for ``[N, K]``: (rows per workgroup, K elements per
+    wave step, waves per workgroup). The reference's ``FUSED_DECODE_LINEAR``
+    (block_n,block_k,warps,stages; kernels.py:589-603) is a Triton knob and is
+    ignored with a warning."""
+    if os.environ.get("FUSED_DECODE_LINEAR"):
+        _warn_once("linear", "FUSED_DECODE_LINEAR is a Triton tile knob; the HIP GEMV picks its own tiling")
+    if kind == "dot":
+        items = -(-k // 128)
+        return 16, 128, _waves(items)
+    items = -(-k // 512)
+    return 8, 512, _waves(items)
+
+
+def _waves(items: int) -> int:
+    if items <= 8:
+        return max(1, items)
+    for d in range(8, 3, -1):
+        if items % d == 0:
+            return d
+    return 8
+
+
+def linear_out(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    y: torch.Tensor,
+    *,
+    bias: torch.Tensor | None = None,
+    row_add: torch.Tensor | None = None,
+    kind: str | None = None,
+) -> None:
+    """``y = x @ weight.T [+ bias] [+ row_add]`` for x ``[M, K]``, M <= 16.
+    ``row_add`` is ``[M, N]``, ``[1, N]``, ``[M, 1]`` or ``[1, 1]`` (size-1 dims
+    broadcast). Mirrors kernels.py:741-830."""
+    kind = resolve_kind(kind)
+    m, k = x.shape
+    n, k_w = weight.shape
+    if k != k_w:
+        raise ValueError(f"K mismatch: x has {k}, weight has {k_w}")
+    if tuple(y.shape) != (m, n):
+        raise ValueError(f"y shape {tuple(y.shape)} != {(m, n)}")
+    if m > 16:
+        raise ValueError("linear_out only covers M <= 16")
+    if m == 0 or n == 0:
+        return
+    if any(s < 0 for s in x.stride()):
+        x = x.contiguous()
+    if any(s < 0 for s in weight.stride()):
+        weight = weight.contiguous()
+    bias_ptr, bias_code, sb = 0, DTYPE_CODE[x.dtype], 0
+    if bias is not None:
+        if bias.stride(0) < 0:
+            bias = bias.contiguous()
+        bias_ptr, bias_code, sb = bias.data_ptr(), DTYPE_CODE[bias.dtype], int(bias.stride(0))
+    row_ptr, row_code, srm, srn = 0, DTYPE_CODE[x.dtype], 0, 0
+    if row_add is not None:
+        if any(s < 0 for s in row_add.stride()):
+            row_add = row_add.contiguous()
+        row_ptr, row_code = row_add.data_ptr(), DTYPE_CODE[row_add.dtype]
+        srm = 0 if row_add.shape[0] == 1 else int(row_add.stride(0))
+        srn = 0 if row_add.shape[1] == 1 else int(row_add.stride(1))
+    status = lib().fd_linear(
+        y.data_ptr(), x.data_ptr(), weight.data_ptr(), bias_ptr, bias_code, row_ptr, row_code,
+        m, n, k, int(x.stride(0)), int(x.stride(1)), int(weight.stride(0)), int(weight.stride(1)),
+        sb, srm, srn, int(y.stride(0)), int(y.stride(1)), KIND_CODE[kind], DTYPE_CODE[x.dtype],
+        stream_of(x),
+    )
+    check("fd_linear", status)
+
+
+def post_attn_mlp_out(
+    hidden: torch.Tensor,
+    norm_weight: torch.Tensor,
+    w_gate_up: torch.Tensor,
+    w_down: torch.Tensor,
+    eps: float,
+    out: torch.Tensor,
+    mid: torch.Tensor,
+    kind: str,
+) -> int:
+    """Fused MLP for contiguous ``hidden [M, H]`` (M <= 16): two launches. ``mid``
+    is ``[M, I]`` scratch. Returns the library status (FD_EUNSUPPORTED lets the
+    caller fall back to the composed operators)."""
+    m, h = hidden.shape
+    i = w_down.shape[1]
+    status = lib().fd_post_attn_mlp(
+        out.data_ptr(), mid.data_ptr(), hidden.data_ptr(), norm_weight.data_ptr(),
+        DTYPE_CODE[norm_weight.dtype], w_gate_up.data_ptr(), w_down.data_ptr(), m, h, i,
+        float(eps), KIND_CODE[kind], DTYPE_CODE[hidden.dtype], stream_of(hidden),
+    )
+    if status == _lib.FD_EUNSUPPORTED:
+        return status
+    check("fd_post_attn_mlp", status)
+    return status
+
+
+def launch_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """Bandwidth-roof copy of ``src`` into ``dst`` (same byte size, contiguous)."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("copy needs equal byte sizes")
+    check("fd_copy", lib().fd_copy(dst.data_ptr(), src.data_ptr(), nbytes, stream_of(src)))
+
+
+def launch_triad(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: float = 1.0) -> None:
+    """``c = a + b * scale`` over contiguous tensors of one dtype."""
+    status = lib().fd_triad(
+        c.data_ptr(), a.data_ptr(), b.data_ptr(), float(scale), a.numel(), DTYPE_CODE[a.dtype],
+        stream_of(a),
+    )
+    check("fd_triad", status)

@@ -1,0 +1,160 @@
+/*
+ * fused_decode.h - C ABI of libfused_decode_hip.so, the gfx950 (MI355X) kernels
+ * behind the Python package `fused_decode`.
+ *
+ * The reference has no C or FFI layer: its operators are Python functions in
+ * src/fused_decode/ops.py that call Triton launchers in src/fused_decode/kernels.py.
+ * Each entry point below replaces one of those launchers (cited per function) and
+ * keeps the launcher's contract:
+ *   - the caller owns every buffer; nothing here allocates device memory;
+ *   - work is enqueued on the given stream (a hipStream_t passed as void*; NULL is
+ *     the legacy default stream) and nothing synchronises, so a caller may capture
+ *     the calls into a hipGraph;
+ *   - inputs are read-only, except that residual_out may alias residual, and an
+ *     output may alias the input it is computed from element-for-element (in-place
+ *     norm, rope, swiglu);
+ *   - arguments are checked before any HIP call: a bad argument returns
+ *     FD_EINVAL and launches nothing. fd_last_error() gives the reason.
+ *
+ * Activations are float16 or bfloat16 (act_dtype), arithmetic is float32 with one
+ * rounding per stored tensor. Strides and sizes are in elements, not bytes.
+ */
+#ifndef FUSED_DECODE_H
+#define FUSED_DECODE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+enum { FD_F16 = 0, FD_BF16 = 1, FD_F32 = 2 };
+
+/* GEMV kinds: the names of kernels.py:581-586 (`resolve_kind`). */
+enum { FD_KIND_DOT = 0, FD_KIND_SIMT = 1 };
+
+/* status codes */
+enum {
+  FD_OK = 0,
+  FD_EINVAL = 1,      /* bad argument; nothing was launched */
+  FD_EUNSUPPORTED = 2, /* valid, but outside what this build handles (e.g. LDS budget) */
+  FD_ELAUNCH = 3      /* the HIP launch itself failed */
+};
+
+/*
+ * A row layout: the tensor is a grid of a*b*c rows of n elements. Row (i,j,l)
+ * starts at i*sa + j*sb + l*sc and element t of a row sits at t*col further on.
+ * Any stride may be 0 (broadcast). Mirrors RowLayout of kernels.py:26-70.
+ */
+typedef struct fd_rows {
+  int64_t a, b, c;
+  int64_t sa, sb, sc;
+  int64_t col;
+  int64_t n;
+} fd_rows;
+
+/* Version of this library (major*10000 + minor*100 + patch). */
+int fd_version(void);
+
+/* HIP runtime version the library is bound to (hipRuntimeGetVersion). */
+int fd_runtime_version(int* version);
+
+/* Human-readable reason for the last non-OK status returned on this thread. */
+const char* fd_last_error(void);
+
+/*
+ * y = x * rsqrt(mean(x^2) + eps) * w, per row, float32 reduction.
+ * Replaces kernels.py:343-414 (`rms_out` without residual), launched from
+ * ops.py:72-88 (`rms_norm`). w has n elements at stride w_stride, dtype w_dtype
+ * (FD_F16, FD_BF16 or FD_F32).
+ */
+int fd_rms_norm(void* y, const void* x, const void* w, int w_dtype, int64_t w_stride,
+                const fd_rows* lx, const fd_rows* ly, float eps, int act_dtype,
+                void* stream);
+
+/*
+ * s = x + residual in float32; residual_out = round(s);
+ * y = round(s * rsqrt(mean(s^2) + eps) * w) - the norm uses the float32 sum.
+ * Replaces kernels.py:343-414 (`rms_out` with residual and residual_out),
+ * launched from ops.py:91-119 (`add_rms_norm`). residual_out may alias residual.
+ */
+int fd_add_rms_norm(void* y, void* residual_out, const void* x, const void* residual,
+                    const void* w, int w_dtype, int64_t w_stride, const fd_rows* lx,
+                    const fd_rows* lr, const fd_rows* ly, const fd_rows* lro, float eps,
+                    int act_dtype, void* stream);
+
+/*
+ * y = round(silu(gate) * up), float32 math with a stable sigmoid.
+ * Replaces kernels.py:456-487 (`swiglu_out`), launched from ops.py:163-178.
+ */
+int fd_swiglu(void* y, const void* gate, const void* up, const fd_rows* lg,
+              const fd_rows* lu, const fd_rows* ly, int act_dtype, void* stream);
+
+/*
+ * Rotate-half RoPE over rows of even length n, h = n/2:
+ *   y[:h] = x1*c1 - x2*s1,  y[h:] = x2*c2 + x1*s2   (float32, one rounding).
+ * cos/sin rows (dtype cs_dtype: FD_F16, FD_BF16 or FD_F32) use their own layouts,
+ * typically with stride-0 broadcast dims.
+ * Replaces kernels.py:541-578 (`rope_out`), launched from ops.py:138-160.
+ */
+int fd_rope(void* y, const void* x, const void* cos, const void* sin, int cs_dtype,
+            const fd_rows* lx, const fd_rows* lc, const fd_rows* ls, const fd_rows* ly,
+            int act_dtype, void* stream);
+
+/*
+ * y[m,n] = round(sum_k x[m,k] * w[n,k] + bias[n] + row_add[m,n]) for M <= 16.
+ * w is [N,K] like F.linear. bias (optional, NULL for none) has dtype bias_dtype
+ * (act_dtype or FD_F32) and stride sb; row_add (optional) has dtype row_dtype
+ * (FD_F16/FD_BF16/FD_F32) and strides srm, srn (0 broadcasts). kind is
+ * FD_KIND_DOT or FD_KIND_SIMT.
+ * Replaces kernels.py:741-830 (`linear_out`, kernels `_linear_dot` :606-672 and
+ * `_linear_simt` :675-738), launched from ops.py:212-280 (`linear_decode`).
+ */
+int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+              const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+              int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb,
+              int64_t srm, int64_t srn, int64_t sym, int64_t syn, int kind, int act_dtype,
+              void* stream);
+
+/*
+ * Llama post-attention MLP for a contiguous hidden [M,H], M <= 16:
+ *   h   = round(rms_norm(hidden, norm_w, eps))
+ *   g,u = round(h @ w_gate_up[:I].T), round(h @ w_gate_up[I:].T)
+ *   mid = round(silu(g) * u)                      (written to `mid`, [M,I])
+ *   y   = round(mid @ w_down.T + hidden)
+ * w_gate_up is [2I,H] (gate rows above up rows), w_down is [H,I], both contiguous.
+ * `mid` is caller-owned scratch of M*I activation elements. Two launches.
+ * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
+ * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
+ */
+int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
+                     int norm_w_dtype, const void* w_gate_up, const void* w_down,
+                     int64_t M, int64_t H, int64_t I, float eps, int kind, int act_dtype,
+                     void* stream);
+
+/*
+ * Launch 1 of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u)) with
+ * g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
+ * rules as fd_post_attn_mlp. For callers that run their own down projection, and
+ * for timing the dominant kernel of the block on its own.
+ * Replaces ops.py:312-314 (rms_norm, the gate/up linear_decode and swiglu).
+ */
+int fd_mlp_gate_up(void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+                   const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps,
+                   int kind, int act_dtype, void* stream);
+
+/*
+ * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned
+ * pointers take the vector path). c = a + b*scale over n elements of dtype.
+ * Replace kernels.py:833-858 (`launch_copy`, `launch_triad`).
+ */
+int fd_copy(void* dst, const void* src, int64_t bytes, void* stream);
+int fd_triad(void* c, const void* a, const void* b, float scale, int64_t n, int dtype,
+             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FUSED_DECODE_H */

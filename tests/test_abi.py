@@ -1,0 +1,104 @@
+"""The C ABI library loads, exports every entry point include/fused_decode.h
+declares, and rejects bad arguments before any HIP call (CPU only)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "fused_decode.h"
+
+
+def declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(fd_\w+)\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from fused_decode import _lib
+
+    return _lib
+
+
+def test_header_declares_the_operator_set():
+    names = declared()
+    for n in ("fd_rms_norm", "fd_add_rms_norm", "fd_swiglu", "fd_rope", "fd_linear",
+              "fd_post_attn_mlp", "fd_copy", "fd_triad", "fd_last_error", "fd_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(L):
+    lib = L.lib()
+    for name in declared():
+        assert hasattr(lib, name), name
+    assert set(declared()) - {"fd_last_error"} == set(L.SIGNATURES)
+
+
+def test_version_and_error_string(L):
+    lib = L.lib()
+    assert lib.fd_version() == 100
+    assert lib.fd_copy(None, None, -1, None) == L.FD_EINVAL
+    assert b"bytes" in lib.fd_last_error()
+    assert lib.fd_copy(None, None, 0, None) == L.FD_OK  # empty copy: nothing to do
+
+
+# Argument checks below return before any HIP call; the pointers are never
+# dereferenced. Skipped where a GPU is present so no launch can ever see them.
+nogpu = pytest.mark.skipif(torch.cuda.is_available(), reason="host-only argument checks")
+FAKE = 0x1000
+
+
+def rows(a=1, b=1, c=4, n=64, col=1, L=None):
+    from fused_decode._lib import FdRows
+
+    return FdRows(a, b, c, 0, 0, n, col, n)
+
+
+@nogpu
+def test_linear_rejects(L):
+    lib = L.lib()
+    args = dict(bias=None, bd=0, row=None, rd=0, M=4, N=8, K=16, sxm=16, sxk=1, swn=16, swk=1,
+                sb=0, srm=0, srn=0, sym=8, syn=1, kind=0, act=0)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.fd_linear(FAKE, FAKE, FAKE, a["bias"], a["bd"], a["row"], a["rd"], a["M"], a["N"],
+                             a["K"], a["sxm"], a["sxk"], a["swn"], a["swk"], a["sb"], a["srm"], a["srn"],
+                             a["sym"], a["syn"], a["kind"], a["act"], None)
+
+    assert call(M=17) == L.FD_EINVAL and b"M <= 16" in lib.fd_last_error()
+    assert call(kind=7) == L.FD_EINVAL and b"kind" in lib.fd_last_error()
+    assert call(act=2) == L.FD_EINVAL and b"act_dtype" in lib.fd_last_error()
+    assert call(bias=FAKE, bd=1) == L.FD_EINVAL and b"bias" in lib.fd_last_error()
+    assert call(sxm=-1) == L.FD_EINVAL and b"stride" in lib.fd_last_error()
+    assert call(M=0) == L.FD_OK  # empty: no launch
+
+
+@nogpu
+def test_row_ops_reject(L):
+    lib = L.lib()
+    r = rows()
+    odd = rows(n=63)
+    assert lib.fd_rope(FAKE, FAKE, FAKE, FAKE, 0, odd, odd, odd, odd, 0, None) == L.FD_EINVAL
+    assert b"even" in lib.fd_last_error()
+    assert lib.fd_rms_norm(FAKE, FAKE, FAKE, 5, 1, r, r, 1e-6, 0, None) == L.FD_EINVAL
+    assert lib.fd_rms_norm(FAKE, FAKE, FAKE, 0, 1, r, rows(n=32), 1e-6, 0, None) == L.FD_EINVAL
+    assert b"row grid" in lib.fd_last_error()
+    assert lib.fd_rms_norm(FAKE, FAKE, FAKE, 0, 1, r, r, float("nan"), 0, None) == L.FD_EINVAL
+    assert lib.fd_swiglu(FAKE, FAKE, FAKE, r, r, rows(c=5), 1, None) == L.FD_EINVAL
+    assert lib.fd_swiglu(None, FAKE, FAKE, r, r, r, 1, None) == L.FD_EINVAL
+
+
+@nogpu
+def test_mlp_rejects(L):
+    lib = L.lib()
+    assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 17, 64, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
+    assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 0, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
+    assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 60, 128, 1e-6, 0, 0, None) == L.FD_EUNSUPPORTED
+    assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, 64, 128, 1e-6, 0, 0, None) == L.FD_OK
