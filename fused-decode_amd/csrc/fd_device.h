@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fd_fastdiv.h"
 #include "fused_decode.h"
 
 namespace fd {
@@ -77,31 +78,46 @@ __device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
   return to_f32(static_cast<const f16*>(p)[i]);
 }
 
-// Row grid of fd_rows, as passed to a kernel (the row count is the grid size).
-struct RowIdx {
-  int64_t b, c;
-  int64_t sa, sb, sc;
-  int64_t col;
+// Row grid shared by every operand of a launch: linear row r is (a, b, c) with
+// c = r % C, b = (r / C) % B, a = r / (C * B). Divisions by the launch-fixed
+// C and B use FastDiv (multiply-high + shift), computed once per thread.
+struct RowGrid {
+  FastDiv c, b;
+};
+// Per-operand strides (elements) of the three row dims and of the columns.
+struct RowStrides {
+  int64_t sa, sb, sc, col;
+};
+struct RowPos {
+  uint32_t a, b, c;
 };
 
-__host__ __device__ __forceinline__ RowIdx row_idx(const fd_rows& l) {
-  RowIdx r;
-  r.b = l.b;
-  r.c = l.c;
-  r.sa = l.sa;
-  r.sb = l.sb;
-  r.sc = l.sc;
-  r.col = l.col;
-  return r;
+inline RowGrid row_grid(const fd_rows& l) {
+  RowGrid g;
+  g.c = FastDiv((uint32_t)l.c);
+  g.b = FastDiv((uint32_t)l.b);
+  return g;
 }
 
-// Offset (elements) of the first element of linear row `row`.
-__device__ __forceinline__ int64_t row_base(const RowIdx& l, int64_t row) {
-  int64_t ci = row % l.c;
-  int64_t t = row / l.c;
-  int64_t bi = t % l.b;
-  int64_t ai = t / l.b;
-  return ai * l.sa + bi * l.sb + ci * l.sc;
+inline RowStrides row_strides(const fd_rows& l) {
+  RowStrides s;
+  s.sa = l.sa;
+  s.sb = l.sb;
+  s.sc = l.sc;
+  s.col = l.col;
+  return s;
+}
+
+__device__ __forceinline__ RowPos row_pos(const RowGrid& g, uint32_t row) {
+  RowPos p;
+  const uint32_t t = g.c.divmod(row, p.c);
+  p.a = g.b.divmod(t, p.b);
+  return p;
+}
+
+// Offset (elements) of the first element of the row at `p`.
+__device__ __forceinline__ int64_t row_off(const RowStrides& s, const RowPos& p) {
+  return (int64_t)p.a * s.sa + (int64_t)p.b * s.sb + (int64_t)p.c * s.sc;
 }
 
 // Dot product of 8 activation pairs accumulated into float32 with v_dot2

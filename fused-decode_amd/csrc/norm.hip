@@ -37,13 +37,14 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // T: activation type; W: weight type; VPT: 8-element vectors per thread.
 template <typename T, typename W, int NT, int VPT, bool ADD>
 __global__ __launch_bounds__(NT) void rms_vec_kernel(T* y, T* ro, const T* x, const T* r,
-                                                     const W* __restrict__ w, RowIdx lx,
-                                                     RowIdx lr, RowIdx ly, RowIdx lro,
-                                                     int n, float eps) {
+                                                     const W* __restrict__ w, RowGrid grid,
+                                                     RowStrides lx, RowStrides lr,
+                                                     RowStrides ly, RowStrides lro, int n,
+                                                     float eps) {
   __shared__ float red[NT / kWave];
-  const int64_t row = blockIdx.x;
-  const T* xr = x + row_base(lx, row);
-  const T* rr = ADD ? r + row_base(lr, row) : nullptr;
+  const RowPos p = row_pos(grid, blockIdx.x);
+  const T* xr = x + row_off(lx, p);
+  const T* rr = ADD ? r + row_off(lr, p) : nullptr;
   float v[VPT][8];
   float ss = 0.f;
 #pragma unroll
@@ -65,8 +66,8 @@ __global__ __launch_bounds__(NT) void rms_vec_kernel(T* y, T* ro, const T* x, co
   }
   ss = block_sum<NT>(ss, red);
   const float inv = rsqrtf(ss / (float)n + eps);
-  T* yr = y + row_base(ly, row);
-  T* ror = ADD ? ro + row_base(lro, row) : nullptr;
+  T* yr = y + row_off(ly, p);
+  T* ror = ADD ? ro + row_off(lro, p) : nullptr;
 #pragma unroll
   for (int j = 0; j < VPT; ++j) {
     const int k = (j * NT + threadIdx.x) * 8;
@@ -90,13 +91,14 @@ __global__ __launch_bounds__(NT) void rms_vec_kernel(T* y, T* ro, const T* x, co
 template <typename T, bool ADD>
 __global__ __launch_bounds__(256) void rms_gen_kernel(T* y, T* ro, const T* x, const T* r,
                                                       const void* __restrict__ w, int w_dtype,
-                                                      int64_t w_stride, RowIdx lx, RowIdx lr,
-                                                      RowIdx ly, RowIdx lro, int64_t n,
+                                                      int64_t w_stride, RowGrid grid,
+                                                      RowStrides lx, RowStrides lr,
+                                                      RowStrides ly, RowStrides lro, int64_t n,
                                                       float eps) {
   __shared__ float red[4];
-  const int64_t row = blockIdx.x;
-  const T* xr = x + row_base(lx, row);
-  const T* rr = ADD ? r + row_base(lr, row) : nullptr;
+  const RowPos p = row_pos(grid, blockIdx.x);
+  const T* xr = x + row_off(lx, p);
+  const T* rr = ADD ? r + row_off(lr, p) : nullptr;
   float ss = 0.f;
   for (int64_t k = threadIdx.x; k < n; k += 256) {
     float s = to_f32(xr[k * lx.col]);
@@ -105,8 +107,8 @@ __global__ __launch_bounds__(256) void rms_gen_kernel(T* y, T* ro, const T* x, c
   }
   ss = block_sum<256>(ss, red);
   const float inv = rsqrtf(ss / (float)n + eps);
-  T* yr = y + row_base(ly, row);
-  T* ror = ADD ? ro + row_base(lro, row) : nullptr;
+  T* yr = y + row_off(ly, p);
+  T* ror = ADD ? ro + row_off(lro, p) : nullptr;
   for (int64_t k = threadIdx.x; k < n; k += 256) {
     float s = to_f32(xr[k * lx.col]);
     if (ADD) {
@@ -126,8 +128,9 @@ void launch_vec(void* y, void* ro, const void* x, const void* r, const void* w,
   constexpr int NT = 256;
   hipLaunchKernelGGL((rms_vec_kernel<T, W, NT, VPT, ADD>), dim3((unsigned)rows), dim3(NT), 0,
                      st, static_cast<T*>(y), static_cast<T*>(ro), static_cast<const T*>(x),
-                     static_cast<const T*>(r), static_cast<const W*>(w), row_idx(lx),
-                     row_idx(lr), row_idx(ly), row_idx(lro), (int)lx.n, eps);
+                     static_cast<const T*>(r), static_cast<const W*>(w), row_grid(lx),
+                     row_strides(lx), row_strides(lr), row_strides(ly), row_strides(lro),
+                     (int)lx.n, eps);
 }
 
 template <typename T, typename W, bool ADD>
@@ -177,7 +180,7 @@ int rms_common(bool add, void* y, void* ro, const void* x, const void* r, const 
   if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
   const int64_t rows = lx->a * lx->b * lx->c;
   if (rows == 0 || lx->n == 0) return FD_OK;
-  if (rows > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too many rows");
+  if (rows > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too many rows (>= 2^31)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const fd_rows& LR = add ? *lr : *lx;
   const fd_rows& LRO = add ? *lro : *ly;
@@ -202,8 +205,9 @@ int rms_common(bool add, void* y, void* ro, const void* x, const void* r, const 
 #define FD_RMS_GEN(T, A)                                                                     \
   hipLaunchKernelGGL((rms_gen_kernel<T, A>), dim3((unsigned)rows), dim3(256), 0, st,         \
                      static_cast<T*>(y), static_cast<T*>(ro), static_cast<const T*>(x),      \
-                     static_cast<const T*>(r), w, w_dtype, w_stride, row_idx(*lx),           \
-                     row_idx(LR), row_idx(*ly), row_idx(LRO), lx->n, eps)
+                     static_cast<const T*>(r), w, w_dtype, w_stride, row_grid(*lx),          \
+                     row_strides(*lx), row_strides(LR), row_strides(*ly), row_strides(LRO),   \
+                     lx->n, eps)
     if (act_dtype == FD_F16) {
       if (add) FD_RMS_GEN(f16, true); else FD_RMS_GEN(f16, false);
     } else {

@@ -17,31 +17,36 @@ constexpr int kPwThreads = 256;
 
 template <typename T>
 __global__ __launch_bounds__(kPwThreads) void swiglu_vec_kernel(T* y, const T* g, const T* u,
-                                                                RowIdx lg, RowIdx lu, RowIdx ly,
-                                                                uint32_t vpr, uint32_t total) {
+                                                                RowGrid grid, FastDiv vpr,
+                                                                RowStrides sg, RowStrides su,
+                                                                RowStrides sy, uint32_t total) {
   const uint32_t v = blockIdx.x * kPwThreads + threadIdx.x;
   if (v >= total) return;
-  const uint32_t row = v / vpr;
-  const uint32_t k = (v - row * vpr) * 8;
-  typename Vec8<T>::type a = load8<T>(g + row_base(lg, row) + k);
-  typename Vec8<T>::type b = load8<T>(u + row_base(lu, row) + k);
+  uint32_t cv;
+  const uint32_t row = vpr.divmod(v, cv);
+  const uint32_t k = cv * 8;
+  const RowPos p = row_pos(grid, row);
+  typename Vec8<T>::type a = load8<T>(g + row_off(sg, p) + k);
+  typename Vec8<T>::type b = load8<T>(u + row_off(su, p) + k);
   typename Vec8<T>::type o;
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(silu_stable(to_f32(a[i])) * to_f32(b[i]));
-  store8<T>(y + row_base(ly, row) + k, o);
+  store8<T>(y + row_off(sy, p) + k, o);
 }
 
 template <typename T>
 __global__ __launch_bounds__(kPwThreads) void swiglu_gen_kernel(T* y, const T* g, const T* u,
-                                                                RowIdx lg, RowIdx lu, RowIdx ly,
-                                                                int64_t n, int64_t total) {
-  const int64_t e = (int64_t)blockIdx.x * kPwThreads + threadIdx.x;
+                                                                RowGrid grid, FastDiv n,
+                                                                RowStrides sg, RowStrides su,
+                                                                RowStrides sy, uint32_t total) {
+  const uint32_t e = blockIdx.x * kPwThreads + threadIdx.x;
   if (e >= total) return;
-  const int64_t row = e / n;
-  const int64_t k = e - row * n;
-  const float a = to_f32(g[row_base(lg, row) + k * lg.col]);
-  const float b = to_f32(u[row_base(lu, row) + k * lu.col]);
-  y[row_base(ly, row) + k * ly.col] = from_f32<T>(silu_stable(a) * b);
+  uint32_t k;
+  const uint32_t row = n.divmod(e, k);
+  const RowPos p = row_pos(grid, row);
+  const float a = to_f32(g[row_off(sg, p) + (int64_t)k * sg.col]);
+  const float b = to_f32(u[row_off(su, p) + (int64_t)k * su.col]);
+  y[row_off(sy, p) + (int64_t)k * sy.col] = from_f32<T>(silu_stable(a) * b);
 }
 
 // ---------------------------------------------------------------------------
@@ -51,16 +56,20 @@ __global__ __launch_bounds__(kPwThreads) void swiglu_gen_kernel(T* y, const T* g
 
 template <typename T, typename C>
 __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, const C* cs,
-                                                              const C* sn, RowIdx lx, RowIdx lc,
-                                                              RowIdx ls, RowIdx ly, uint32_t h,
-                                                              uint32_t vpr, uint32_t total) {
+                                                              const C* sn, RowGrid grid,
+                                                              FastDiv vpr, RowStrides sx,
+                                                              RowStrides sc, RowStrides ss,
+                                                              RowStrides sy, uint32_t h,
+                                                              uint32_t total) {
   const uint32_t v = blockIdx.x * kPwThreads + threadIdx.x;
   if (v >= total) return;
-  const uint32_t row = v / vpr;
-  const uint32_t j = (v - row * vpr) * 8;
-  const T* xr = x + row_base(lx, row);
-  const C* cr = cs + row_base(lc, row);
-  const C* sr = sn + row_base(ls, row);
+  uint32_t jv;
+  const uint32_t row = vpr.divmod(v, jv);
+  const uint32_t j = jv * 8;
+  const RowPos p = row_pos(grid, row);
+  const T* xr = x + row_off(sx, p);
+  const C* cr = cs + row_off(sc, p);
+  const C* sr = sn + row_off(ss, p);
   typename Vec8<T>::type x1 = load8<T>(xr + j);
   typename Vec8<T>::type x2 = load8<T>(xr + j + h);
   float c1[8], c2[8], s1[8], s2[8];
@@ -75,7 +84,7 @@ __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, 
     o1[i] = from_f32<T>(a * c1[i] - b * s1[i]);
     o2[i] = from_f32<T>(b * c2[i] + a * s2[i]);
   }
-  T* yr = y + row_base(ly, row);
+  T* yr = y + row_off(sy, p);
   store8<T>(yr + j, o1);
   store8<T>(yr + j + h, o2);
 }
@@ -83,27 +92,33 @@ __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, 
 template <typename T>
 __global__ __launch_bounds__(kPwThreads) void rope_gen_kernel(T* y, const T* x, const void* cs,
                                                               const void* sn, int cs_dtype,
-                                                              RowIdx lx, RowIdx lc, RowIdx ls,
-                                                              RowIdx ly, int64_t h,
-                                                              int64_t total) {
-  const int64_t e = (int64_t)blockIdx.x * kPwThreads + threadIdx.x;
+                                                              RowGrid grid, FastDiv hd,
+                                                              RowStrides sx, RowStrides sc,
+                                                              RowStrides ss, RowStrides sy,
+                                                              uint32_t total) {
+  const uint32_t e = blockIdx.x * kPwThreads + threadIdx.x;
   if (e >= total) return;
-  const int64_t row = e / h;
-  const int64_t j = e - row * h;
-  const T* xr = x + row_base(lx, row);
-  const int64_t cb = row_base(lc, row), sb = row_base(ls, row);
-  const float a = to_f32(xr[j * lx.col]);
-  const float b = to_f32(xr[(j + h) * lx.col]);
-  const float c1 = load_any(cs, cs_dtype, cb + j * lc.col);
-  const float c2 = load_any(cs, cs_dtype, cb + (j + h) * lc.col);
-  const float s1 = load_any(sn, cs_dtype, sb + j * ls.col);
-  const float s2 = load_any(sn, cs_dtype, sb + (j + h) * ls.col);
-  T* yr = y + row_base(ly, row);
-  yr[j * ly.col] = from_f32<T>(a * c1 - b * s1);
-  yr[(j + h) * ly.col] = from_f32<T>(b * c2 + a * s2);
+  uint32_t j;
+  const uint32_t row = hd.divmod(e, j);
+  const int64_t h = hd.d;
+  const RowPos p = row_pos(grid, row);
+  const T* xr = x + row_off(sx, p);
+  const int64_t cb = row_off(sc, p), sb = row_off(ss, p);
+  const float a = to_f32(xr[j * sx.col]);
+  const float b = to_f32(xr[(j + h) * sx.col]);
+  const float c1 = load_any(cs, cs_dtype, cb + j * sc.col);
+  const float c2 = load_any(cs, cs_dtype, cb + (j + h) * sc.col);
+  const float s1 = load_any(sn, cs_dtype, sb + j * ss.col);
+  const float s2 = load_any(sn, cs_dtype, sb + (j + h) * ss.col);
+  T* yr = y + row_off(sy, p);
+  yr[j * sy.col] = from_f32<T>(a * c1 - b * s1);
+  yr[(j + h) * sy.col] = from_f32<T>(b * c2 + a * s2);
 }
 
 namespace {
+
+// Work items (vectors, elements or pairs) of one launch are counted in 32 bits.
+constexpr int64_t kMaxPwWork = 0xffffffffLL - kPwThreads;
 
 inline unsigned blocks_for(int64_t work) {
   return (unsigned)((work + kPwThreads - 1) / kPwThreads);
@@ -132,31 +147,28 @@ extern "C" int fd_swiglu(void* y, const void* gate, const void* up, const fd_row
   const int64_t rows = lg->a * lg->b * lg->c;
   const int64_t total = rows * lg->n;
   if (total == 0) return FD_OK;
+  if (total > kMaxPwWork) return set_error(FD_EUNSUPPORTED, "swiglu tensor too large (>= 2^32 elements)");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const RowGrid grid = row_grid(*lg);
   const bool vec = rows_vectorizable(gate, *lg, 2) && rows_vectorizable(up, *lu, 2) &&
-                   rows_vectorizable(y, *ly, 2) && total / 8 < 0xffffffffLL - kPwThreads;
+                   rows_vectorizable(y, *ly, 2);
   if (vec) {
-    const uint32_t vpr = (uint32_t)(lg->n / 8);
     const uint32_t tv = (uint32_t)(total / 8);
-    if (act_dtype == FD_F16)
-      hipLaunchKernelGGL(swiglu_vec_kernel<f16>, dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,
-                         (f16*)y, (const f16*)gate, (const f16*)up, row_idx(*lg), row_idx(*lu),
-                         row_idx(*ly), vpr, tv);
-    else
-      hipLaunchKernelGGL(swiglu_vec_kernel<bf16>, dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,
-                         (bf16*)y, (const bf16*)gate, (const bf16*)up, row_idx(*lg),
-                         row_idx(*lu), row_idx(*ly), vpr, tv);
+    const FastDiv vpr((uint32_t)(lg->n / 8));
+#define FD_SWIGLU_VEC(T)                                                                       \
+  hipLaunchKernelGGL(swiglu_vec_kernel<T>, dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,      \
+                     (T*)y, (const T*)gate, (const T*)up, grid, vpr, row_strides(*lg),         \
+                     row_strides(*lu), row_strides(*ly), tv)
+    if (act_dtype == FD_F16) FD_SWIGLU_VEC(f16); else FD_SWIGLU_VEC(bf16);
+#undef FD_SWIGLU_VEC
   } else {
-    if (blocks_for(total) == 0 || total / kPwThreads > 0x7fffffffLL)
-      return set_error(FD_EUNSUPPORTED, "swiglu tensor too large");
-    if (act_dtype == FD_F16)
-      hipLaunchKernelGGL(swiglu_gen_kernel<f16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
-                         st, (f16*)y, (const f16*)gate, (const f16*)up, row_idx(*lg),
-                         row_idx(*lu), row_idx(*ly), lg->n, total);
-    else
-      hipLaunchKernelGGL(swiglu_gen_kernel<bf16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
-                         st, (bf16*)y, (const bf16*)gate, (const bf16*)up, row_idx(*lg),
-                         row_idx(*lu), row_idx(*ly), lg->n, total);
+    const FastDiv nd((uint32_t)lg->n);
+#define FD_SWIGLU_GEN(T)                                                                       \
+  hipLaunchKernelGGL(swiglu_gen_kernel<T>, dim3(blocks_for(total)), dim3(kPwThreads), 0, st,   \
+                     (T*)y, (const T*)gate, (const T*)up, grid, nd, row_strides(*lg),          \
+                     row_strides(*lu), row_strides(*ly), (uint32_t)total)
+    if (act_dtype == FD_F16) FD_SWIGLU_GEN(f16); else FD_SWIGLU_GEN(bf16);
+#undef FD_SWIGLU_GEN
   }
   return check_launch();
 }
@@ -176,18 +188,20 @@ extern "C" int fd_rope(void* y, const void* x, const void* cos, const void* sin,
   const int64_t h = lx->n / 2;
   const int64_t total = rows * h;
   if (total == 0) return FD_OK;
+  if (total > kMaxPwWork) return set_error(FD_EUNSUPPORTED, "rope tensor too large (>= 2^32 pairs)");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const RowGrid grid = row_grid(*lx);
   const int cse = cs_dtype == FD_F32 ? 4 : 2;
   const bool vec = rope_rows_vec(x, *lx, 2) && rope_rows_vec(y, *ly, 2) &&
-                   rope_rows_vec(cos, *lc, cse) && rope_rows_vec(sin, *ls, cse) &&
-                   (cse == 2 || h % 4 == 0) && total / 8 < 0xffffffffLL - kPwThreads;
+                   rope_rows_vec(cos, *lc, cse) && rope_rows_vec(sin, *ls, cse);
   if (vec) {
-    const uint32_t vpr = (uint32_t)(h / 8);
     const uint32_t tv = (uint32_t)(total / 8);
+    const FastDiv vpr((uint32_t)(h / 8));
 #define FD_ROPE_VEC(T, C)                                                                     \
   hipLaunchKernelGGL((rope_vec_kernel<T, C>), dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,  \
-                     (T*)y, (const T*)x, (const C*)cos, (const C*)sin, row_idx(*lx),          \
-                     row_idx(*lc), row_idx(*ls), row_idx(*ly), (uint32_t)h, vpr, tv)
+                     (T*)y, (const T*)x, (const C*)cos, (const C*)sin, grid, vpr,             \
+                     row_strides(*lx), row_strides(*lc), row_strides(*ls), row_strides(*ly),  \
+                     (uint32_t)h, tv)
     if (act_dtype == FD_F16) {
       if (cs_dtype == FD_F32) FD_ROPE_VEC(f16, float);
       else if (cs_dtype == FD_BF16) FD_ROPE_VEC(f16, bf16);
@@ -199,15 +213,13 @@ extern "C" int fd_rope(void* y, const void* x, const void* cos, const void* sin,
     }
 #undef FD_ROPE_VEC
   } else {
-    if (total / kPwThreads > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "rope tensor too large");
-    if (act_dtype == FD_F16)
-      hipLaunchKernelGGL(rope_gen_kernel<f16>, dim3(blocks_for(total)), dim3(kPwThreads), 0, st,
-                         (f16*)y, (const f16*)x, cos, sin, cs_dtype, row_idx(*lx), row_idx(*lc),
-                         row_idx(*ls), row_idx(*ly), h, total);
-    else
-      hipLaunchKernelGGL(rope_gen_kernel<bf16>, dim3(blocks_for(total)), dim3(kPwThreads), 0,
-                         st, (bf16*)y, (const bf16*)x, cos, sin, cs_dtype, row_idx(*lx),
-                         row_idx(*lc), row_idx(*ls), row_idx(*ly), h, total);
+    const FastDiv hd((uint32_t)h);
+#define FD_ROPE_GEN(T)                                                                         \
+  hipLaunchKernelGGL(rope_gen_kernel<T>, dim3(blocks_for(total)), dim3(kPwThreads), 0, st,     \
+                     (T*)y, (const T*)x, cos, sin, cs_dtype, grid, hd, row_strides(*lx),       \
+                     row_strides(*lc), row_strides(*ls), row_strides(*ly), (uint32_t)total)
+    if (act_dtype == FD_F16) FD_ROPE_GEN(f16); else FD_ROPE_GEN(bf16);
+#undef FD_ROPE_GEN
   }
   return check_launch();
 }

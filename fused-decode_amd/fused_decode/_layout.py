@@ -6,12 +6,13 @@ the contract of RowLayout in the reference (src/fused_decode/kernels.py:26-70).
 
 Unlike the reference, the operands of one launch are laid out *jointly*: size-1
 dims are dropped and adjacent leading dims are merged only where every operand
-allows it, so all operands always share one row grid. Layouts that cannot be
-expressed (negative strides, more than three unmergeable leading dims) are
-handled explicitly: an input is copied to a contiguous tensor, and an output is
-computed into a contiguous temporary that is then copied back into the caller's
-tensor. The reference's ``.contiguous()`` on such an ``out`` would silently drop
-the write (kernels.py:47-51).
+allows it, so all operands always share one row grid. A layout that cannot be
+expressed (more than three unmergeable leading dims) is handled explicitly: an
+input is copied to a contiguous tensor, and an output is computed into a
+contiguous temporary that is then copied back into the caller's tensor. The
+reference's ``.contiguous()`` on such an ``out`` would silently drop the write
+(kernels.py:47-51). PyTorch tensors never carry negative strides, so the
+reference's negative-stride branch has no counterpart here.
 """
 
 from __future__ import annotations
@@ -57,24 +58,18 @@ def _rows_from(dims, k: int, col: int, n: int) -> FdRows:
 
 def joint_layout(inputs: list[torch.Tensor], outputs: list[torch.Tensor]) -> tuple[list[Operand], list[Operand]]:
     """Row layouts for operands of one shape (broadcast inputs already expanded)."""
-    shape = tuple(inputs[0].shape)
+    shape = inputs[0].shape
     if len(shape) == 0:
         raise ValueError("expected a tensor with a last dimension")
+    n = shape[-1]
+    if n and all(t.is_contiguous() for t in inputs) and all(t.is_contiguous() for t in outputs):
+        # every operand is the same dense [rows, n] block: one shared layout
+        rows = FdRows(1, 1, inputs[0].numel() // n, 0, 0, n, 1, n)
+        return [Operand(t, None, rows) for t in inputs], [Operand(t, None, rows) for t in outputs]
+    shape = tuple(shape)
     ins = list(inputs)
     outs: list[torch.Tensor] = list(outputs)
     targets: list[torch.Tensor | None] = [None] * len(outs)
-
-    def fix_negative():
-        for i, t in enumerate(ins):
-            if any(s < 0 for s in t.stride()):
-                ins[i] = t.contiguous()
-        for i, t in enumerate(outs):
-            if any(s < 0 for s in t.stride()):
-                targets[i] = t
-                outs[i] = torch.empty(shape, dtype=t.dtype, device=t.device)
-
-    fix_negative()
-    n = shape[-1]
     allt = ins + outs
     dims = _plan(shape, [tuple(t.stride()) for t in allt])
     if len(dims) > 3:

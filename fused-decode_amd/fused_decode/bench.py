@@ -1,0 +1,339 @@
+"""Per-operator roofline and latency bench on one MI355X.
+
+    python -m fused_decode.bench [--out results.json] [--quick] [--dtype fp16|bf16|both]
+
+Mirrors the reference's bench (src/fused_decode/bench.py): an in-process copy
+roof, HIP-event medians (10 warmup calls, then `rounds` rounds of back-to-back
+calls, median of per-call microseconds; reference bench.py:42-56), useful
+bytes counted as in the reference README (README.md:33-43), PyTorch eager on
+the GPU beside each op, and graph replay of the MLP. Added for MI355X:
+
+* cold-cache numbers: every op rotates through enough distinct input/weight
+  sets that the rotation exceeds 2x the 256 MB Infinity Cache, so each call
+  reads HBM; warm (same buffers every call) numbers are reported beside them;
+* the copy roof moves >= 1 GiB, and a read-only roof is reported as well;
+* % of the 8 TB/s datasheet peak next to % of the copy roof;
+* PyTorch eager on the host CPU (same dtype, same shapes, thread count stated)
+  as the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import statistics
+import time
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+from .kernels import launch_copy, launch_triad
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, rms_norm, rope, swiglu
+
+LLAMA_H = 4096
+LLAMA_I = 14336
+DATASHEET_GBS = 8000.0
+MALL_BYTES = 256 * 1024 * 1024
+ROTATE_TARGET = 2 * MALL_BYTES + 64 * 1024 * 1024
+
+
+def _sync() -> None:
+    torch.cuda.synchronize()
+
+
+def time_us(fn, iters: int, warmup: int = 10, rounds: int = 5) -> float:
+    """Median over rounds of per-call microseconds; fn(i) gets the call index."""
+    for i in range(warmup):
+        fn(i)
+    _sync()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    samples = []
+    for _ in range(rounds):
+        start.record()
+        for i in range(iters):
+            fn(i)
+        end.record()
+        _sync()
+        samples.append(start.elapsed_time(end) / iters * 1000.0)
+    return statistics.median(samples)
+
+
+def cpu_time_us(fn, budget_s: float = 2.0, max_iters: int = 50) -> float:
+    fn()
+    t0 = time.perf_counter()
+    n = 0
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= max_iters:
+            return el / n * 1e6
+
+
+def copies_for(working_set: int) -> int:
+    """Number of distinct buffer sets so a rotation exceeds 2x the Infinity Cache."""
+    return max(1, math.ceil(ROTATE_TARGET / max(1, working_set)))
+
+
+def bench_roofline() -> dict:
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    c = torch.empty_like(a)
+    copy_us = time_us(lambda i: launch_copy(c, a), iters=10, warmup=3)
+    del a, c
+    e = (1 << 30) // 2
+    x = torch.randn(e, device="cuda", dtype=torch.float16)
+    y = torch.randn(e, device="cuda", dtype=torch.float16)
+    z = torch.empty_like(x)
+    triad_us = time_us(lambda i: launch_triad(x, y, z, 1.25), iters=10, warmup=3)
+    del x, y, z
+    torch.cuda.empty_cache()
+    return {
+        "copy_bytes_each_way": n,
+        "copy_us": copy_us,
+        "copy_gbs": 2 * n / (copy_us * 1e-6) / 1e9,
+        "triad_us": triad_us,
+        "triad_gbs": 3 * e * 2 / (triad_us * 1e-6) / 1e9,
+        "datasheet_gbs": DATASHEET_GBS,
+    }
+
+
+def _row(name, nbytes, cold_us, warm_us, roof, **extra) -> dict:
+    gbs = nbytes / (cold_us * 1e-6) / 1e9
+    row = {
+        "name": name,
+        "bytes": nbytes,
+        "us": cold_us,
+        "us_warm": warm_us,
+        "gbs": gbs,
+        "gbs_warm": nbytes / (warm_us * 1e-6) / 1e9,
+        "pct_copy_roof": 100.0 * gbs / roof,
+        "pct_datasheet": 100.0 * gbs / DATASHEET_GBS,
+    }
+    row.update(extra)
+    return row
+
+
+def _print(row: dict) -> None:
+    parts = [f"{row['name']:<44}", f"{row['us']:9.2f} us", f"{row['gbs']:8.1f} GB/s",
+             f"{row['pct_copy_roof']:5.1f}% copy", f"warm {row['us_warm']:8.2f}"]
+    for k in ("eager_us", "cpu_eager_us", "graph_us", "hipblas_us"):
+        if row.get(k) is not None:
+            parts.append(f"{k} {row[k]:.2f}")
+    print("  ".join(parts), flush=True)
+
+
+def _gen(shape, dtype, g, scale=1.0, mean=0.0):
+    return (torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32) * scale + mean).to(dtype)
+
+
+def bench_pointwise(dtype, roof, quick, cpu) -> list[dict]:
+    rows = []
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(0)
+    norm_shapes = [(8192, LLAMA_H), (1, LLAMA_H)]
+    for r, h in norm_shapes:
+        ws = 4 * r * h * e
+        k = copies_for(ws)
+        xs = [_gen((r, h), dtype, g) for _ in range(k)]
+        rs = [_gen((r, h), dtype, g) for _ in range(k)]
+        w = _gen((h,), dtype, g, 0.1, 1.0)
+        outs = [torch.empty_like(xs[0]) for _ in range(k)]
+        cold = time_us(lambda i: rms_norm(xs[i % k], w, 1e-5, out=outs[i % k]), iters=max(20, 2 * k))
+        warm = time_us(lambda i: rms_norm(xs[0], w, 1e-5, out=outs[0]), iters=50)
+        eager = time_us(lambda i: F.rms_norm(xs[i % k], (h,), w, 1e-5), iters=max(20, 2 * k))
+        cpu_us = None
+        if cpu:
+            xc, wc = xs[0].cpu(), w.cpu()
+            cpu_us = cpu_time_us(lambda: F.rms_norm(xc, (h,), wc, 1e-5))
+        rows.append(_row(f"rms_norm {r}x{h} {dtype}", (2 * r * h + h) * e, cold, warm, roof,
+                         eager_us=eager, cpu_eager_us=cpu_us))
+        _print(rows[-1])
+        cold = time_us(lambda i: add_rms_norm(xs[i % k], rs[i % k], w, 1e-5, out=outs[i % k], residual_out=rs[i % k]),
+                       iters=max(20, 2 * k))
+        warm = time_us(lambda i: add_rms_norm(xs[0], rs[0], w, 1e-5, out=outs[0], residual_out=rs[0]), iters=50)
+        eager = time_us(lambda i: F.rms_norm(xs[i % k] + rs[i % k], (h,), w, 1e-5), iters=max(20, 2 * k))
+        cpu_us = None
+        if cpu:
+            xc, rc, wc = xs[0].cpu(), rs[0].cpu(), w.cpu()
+            cpu_us = cpu_time_us(lambda: F.rms_norm(xc + rc, (h,), wc, 1e-5))
+        rows.append(_row(f"add_rms_norm {r}x{h} {dtype}", (4 * r * h + h) * e, cold, warm, roof,
+                         eager_us=eager, cpu_eager_us=cpu_us))
+        _print(rows[-1])
+        del xs, rs, outs
+    for r in ([2048, 1] if not quick else [2048]):
+        n = LLAMA_I
+        k = copies_for(3 * r * n * e)
+        gs = [_gen((r, n), dtype, g, 2.0) for _ in range(k)]
+        us_ = [_gen((r, n), dtype, g, 2.0) for _ in range(k)]
+        outs = [torch.empty_like(gs[0]) for _ in range(k)]
+        cold = time_us(lambda i: swiglu(gs[i % k], us_[i % k], out=outs[i % k]), iters=max(20, 2 * k))
+        warm = time_us(lambda i: swiglu(gs[0], us_[0], out=outs[0]), iters=50)
+        eager = time_us(lambda i: F.silu(gs[i % k]) * us_[i % k], iters=max(20, 2 * k))
+        cpu_us = None
+        if cpu:
+            gc, uc = gs[0].cpu(), us_[0].cpu()
+            cpu_us = cpu_time_us(lambda: F.silu(gc) * uc)
+        rows.append(_row(f"swiglu {r}x{n} {dtype}", 3 * r * n * e, cold, warm, roof, eager_us=eager, cpu_eager_us=cpu_us))
+        _print(rows[-1])
+        del gs, us_, outs
+    # RoPE with Llama-3 tables (theta 500000) viewed [S, 1, 128]
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float64, device="cuda") / 128))
+    pos = torch.arange(2048, dtype=torch.float64, device="cuda")
+    emb = torch.cat([torch.outer(pos, inv)] * 2, -1)
+    cos_t, sin_t = emb.cos().to(dtype), emb.sin().to(dtype)
+    for xshape, cs in (((1, 2048, 32, 128), (cos_t.view(2048, 1, 128), sin_t.view(2048, 1, 128))),
+                       ((1, 1, 32, 128), (cos_t[1024].view(1, 1, 128), sin_t[1024].view(1, 1, 128)))):
+        numel = math.prod(xshape)
+        nbytes = 2 * numel * e + 2 * cs[0].numel() * e
+        k = copies_for(nbytes)
+        xs = [_gen(xshape, dtype, g) for _ in range(k)]
+        outs = [torch.empty_like(xs[0]) for _ in range(k)]
+        c, s = cs
+
+        def eager_rope(x, c=c, s=s):
+            cb, sb = c.expand_as(x), s.expand_as(x)
+            h = x.shape[-1] // 2
+            return torch.cat((x[..., :h] * cb[..., :h] - x[..., h:] * sb[..., :h],
+                              x[..., h:] * cb[..., h:] + x[..., :h] * sb[..., h:]), -1)
+
+        cold = time_us(lambda i: rope(xs[i % k], c, s, out=outs[i % k]), iters=max(20, 2 * k))
+        warm = time_us(lambda i: rope(xs[0], c, s, out=outs[0]), iters=50)
+        eager = time_us(lambda i: eager_rope(xs[i % k]), iters=max(20, 2 * k))
+        cpu_us = None
+        if cpu:
+            xc, cc, sc = xs[0].cpu(), c.cpu(), s.cpu()
+            cpu_us = cpu_time_us(lambda: eager_rope(xc, cc, sc))
+        rows.append(_row(f"rope {xshape} {dtype}", nbytes, cold, warm, roof, eager_us=eager, cpu_eager_us=cpu_us))
+        _print(rows[-1])
+        del xs, outs
+    torch.cuda.empty_cache()
+    return rows
+
+
+def bench_linear(dtype, roof, quick, cpu) -> list[dict]:
+    rows = []
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    shapes = [(4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)]
+    ms = [1, 8] if quick else [1, 2, 4, 8, 16]
+    for n, kk in shapes:
+        wbytes = n * kk * e
+        k = copies_for(wbytes)
+        ws = [_gen((n, kk), dtype, g, kk ** -0.5) for _ in range(k)]
+        for m in ms:
+            x = _gen((m, kk), dtype, g)
+            out = torch.empty(m, n, device="cuda", dtype=dtype)
+            nbytes = (m * kk + n * kk + m * n) * e
+            hip = time_us(lambda i: F.linear(x, ws[i % k]), iters=max(30, 2 * k))
+            cpu_us = None
+            if cpu and m in (1, 8):
+                xc, wc = x.cpu(), ws[0].cpu()
+                cpu_us = cpu_time_us(lambda: F.linear(xc, wc), budget_s=1.0, max_iters=10)
+            for kind in ("simt", "dot"):
+                cold = time_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), iters=max(30, 2 * k))
+                warm = time_us(lambda i: linear_decode(x, ws[0], out=out, kind=kind), iters=50)
+                rows.append(_row(f"linear M={m} N={n} K={kk} {kind} {dtype}", nbytes, cold, warm, roof,
+                                 hipblas_us=hip, cpu_eager_us=cpu_us))
+                _print(rows[-1])
+        del ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+def bench_mlp(dtype, roof, quick, cpu) -> list[dict]:
+    rows = []
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(2)
+    h, i_ = LLAMA_H, LLAMA_I
+    k = copies_for(3 * h * i_ * e)
+    sets = []
+    for _ in range(k):
+        sets.append((_gen((h,), dtype, g, 0.1, 1.0), _gen((2 * i_, h), dtype, g, h ** -0.5), _gen((h, i_), dtype, g, i_ ** -0.5)))
+    for m in ([1, 8] if not quick else [1]):
+        hid = _gen((m, h), dtype, g)
+
+        def eager(j, m=m):
+            nw, wgu, wd = sets[j % k]
+            hn = F.rms_norm(hid, (h,), nw, 1e-5)
+            gate, up = F.linear(hn, wgu).split(i_, dim=-1)
+            return F.linear(F.silu(gate) * up, wd) + hid
+
+        for kind in ("dot", "simt"):
+            cold = time_us(lambda j: post_attn_mlp(hid, *sets[j % k], 1e-5, kind=kind), iters=max(30, 2 * k))
+            warm = time_us(lambda j: post_attn_mlp(hid, *sets[0], 1e-5, kind=kind), iters=30)
+            graphs = []
+            for j in range(k):
+                post_attn_mlp(hid, *sets[j], 1e-5, kind=kind)
+                _sync()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    post_attn_mlp(hid, *sets[j], 1e-5, kind=kind)
+                graphs.append(gr)
+            graph_us = time_us(lambda j: graphs[j % k].replay(), iters=max(30, 2 * k))
+            eager_us = time_us(eager, iters=max(30, 2 * k))
+            cpu_us = None
+            if cpu and kind == "dot":
+                nw, wgu, wd = (t.cpu() for t in sets[0])
+                hc = hid.cpu()
+
+                def cpu_mlp():
+                    hn = F.rms_norm(hc, (h,), nw, 1e-5)
+                    gate, up = F.linear(hn, wgu).split(i_, dim=-1)
+                    return F.linear(F.silu(gate) * up, wd) + hc
+
+                cpu_us = cpu_time_us(cpu_mlp, budget_s=3.0, max_iters=10)
+            nbytes = (3 * h * i_ + 2 * m * h + h) * e
+            rows.append(_row(f"post_attn_mlp M={m} {kind} {dtype}", nbytes, cold, warm, roof,
+                             graph_us=graph_us, eager_us=eager_us, cpu_eager_us=cpu_us,
+                             target_us=1.25 * 3 * h * i_ * e / (roof * 1e9) * 1e6))
+            _print(rows[-1])
+            del graphs
+    del sets
+    torch.cuda.empty_cache()
+    return rows
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--quick", action="store_true")
+    ap.add_argument("--dtype", choices=["fp16", "bf16", "both"], default="fp16")
+    ap.add_argument("--no-cpu", action="store_true", help="skip PyTorch-eager-on-CPU timings")
+    ap.add_argument("--only", choices=["pointwise", "linear", "mlp"], default=None)
+    args = ap.parse_args()
+    _lib.lib()
+    torch.cuda.set_device(0)
+    payload = {
+        "gpu": torch.cuda.get_device_name(0),
+        "torch": torch.__version__,
+        "hip_runtime": _lib.runtime_version(),
+        "cpu": platform.processor() or platform.machine(),
+        "cpu_threads": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cache_note": f"cold = rotation over >= {ROTATE_TARGET >> 20} MiB of distinct buffers; warm = same buffers",
+    }
+    roof = bench_roofline()
+    payload["roofline"] = roof
+    print(f"copy roof {roof['copy_gbs']:.1f} GB/s  triad {roof['triad_gbs']:.1f} GB/s  (datasheet {DATASHEET_GBS:.0f})", flush=True)
+    dtypes = {"fp16": [torch.float16], "bf16": [torch.bfloat16], "both": [torch.float16, torch.bfloat16]}[args.dtype]
+    payload["rows"] = []
+    for dt in dtypes:
+        if args.only in (None, "pointwise"):
+            payload["rows"] += bench_pointwise(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
+        if args.only in (None, "linear"):
+            payload["rows"] += bench_linear(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
+        if args.only in (None, "mlp"):
+            payload["rows"] += bench_mlp(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
+        if args.out:
+            with open(args.out, "w") as f:
+                json.dump(payload, f, indent=1)
+
+
+if __name__ == "__main__":
+    main()
