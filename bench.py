@@ -8,10 +8,12 @@ distributions (no checkpoints); four independent weight sets (1.41 GB) are
 rotated so every step streams its 352 MB of weights from HBM, not from the
 256 MB Infinity Cache.
 
-A step is one post_attn_mlp call, replayed from a HIP graph (the way a decode
-loop runs it); W untimed warmup steps, then exactly K timed steps between HIP
-events, bracketed by synchronisation. `value` is microseconds per step at M=1
-(lower is better).
+A step is one post_attn_mlp call launched eagerly (the reference's method,
+bench.py:42-56: back-to-back calls between events); W untimed warmup steps,
+then exactly K timed steps between HIP events, bracketed by synchronisation.
+`value` is microseconds per step at M=1 (lower is better). The same steps
+replayed one HIP graph per call (`graph_us`) and the 32-layer decode step
+minus attention, graph-captured (`decode_step`), are reported beside it.
 
 roofline: the dominant kernel, the fused RMSNorm + gate/up GEMV + SwiGLU
 launch, timed alone with HIP events on the stream it is launched on;
@@ -48,6 +50,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-decode-step", action="store_true", help="skip the 32-layer decode step")
     return ap.parse_args()
 
 
@@ -173,7 +176,7 @@ def cpu_baseline(seconds: float) -> dict:
         O.post_attn_mlp(hid, nw, wgu, wd, EPS, "f16")
         calls += 1
         el = time.perf_counter() - t0
-        if el >= seconds or calls >= 200:
+        if el >= seconds or calls >= 5000:
             break
     return {
         "value": el / calls * 1e6,
@@ -215,7 +218,7 @@ def main() -> None:
         del sets
         torch.cuda.empty_cache()
 
-    us1 = results[1]["graph_us"]
+    us1 = results[1]["eager_us"]
     weights = 3 * H * I * 2
     mlp_bytes = (3 * H * I + 2 * 1 * H + H) * 2
     gate_bytes = (2 * I * H + 1 * H + H + 1 * I) * 2  # weights, hidden, norm_w, mid write
@@ -234,12 +237,12 @@ def main() -> None:
         "dtype": "fp16",
         "data": "synthetic: random-init weights ~N(0,1/sqrt(K)), hidden ~N(0,1), 4 rotating weight sets",
         "config": {
-            "workload": "post_attn_mlp Llama-3-8B H=4096 I=14336 M=1, hipGraph replay, cold weights",
+            "workload": "post_attn_mlp Llama-3-8B H=4096 I=14336 M=1, fp16, cold weights (4 rotating sets)",
             "kind": kind,
             "m": 1,
         },
-        "m8_us": round(results[8]["graph_us"], 3),
-        "eager_us": {"m1": round(results[1]["eager_us"], 3), "m8": round(results[8]["eager_us"], 3)},
+        "m8_us": round(results[8]["eager_us"], 3),
+        "graph_us": {"m1": round(results[1]["graph_us"], 3), "m8": round(results[8]["graph_us"], 3)},
         "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
         "copy_roof_gbs": round(roof, 1),
         "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
@@ -256,6 +259,18 @@ def main() -> None:
             "traffic": None,
         },
     }
+    if not args.no_decode_step:
+        from fused_decode.decode_step import DecodeStep, time_step
+
+        line["decode_step"] = {}
+        for m in (1, 8):
+            ds = DecodeStep(m=m, layers=32, dtype=dtype)
+            g_us = time_step(ds, 10, 2, graph=True)
+            line["decode_step"][f"m{m}_us"] = round(g_us, 1)
+            line["decode_step"][f"m{m}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
+            del ds
+            torch.cuda.empty_cache()
+        line["decode_step"]["workload"] = "32-layer Llama-3-8B decode step minus attention, hipGraph"
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -48,6 +48,21 @@ template <typename T>
 __device__ __forceinline__ typename Vec8<T>::type load8(const T* p) {
   return *reinterpret_cast<const typename Vec8<T>::type*>(p);
 }
+// 16-byte load that bypasses cache retention (nontemporal): for weight streams
+// read exactly once, so they do not evict operands that are reused.
+template <typename T>
+__device__ __forceinline__ typename Vec8<T>::type load8_nt(const T* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return __builtin_bit_cast(typename Vec8<T>::type, v);
+}
+// Weight load: nontemporal when NT.
+template <bool NT, typename T>
+__device__ __forceinline__ typename Vec8<T>::type load8w(const T* p) {
+  if constexpr (NT)
+    return load8_nt<T>(p);
+  else
+    return load8<T>(p);
+}
 template <typename T>
 __device__ __forceinline__ void store8(T* p, typename Vec8<T>::type v) {
   *reinterpret_cast<typename Vec8<T>::type*>(p) = v;

@@ -56,14 +56,14 @@ __device__ __forceinline__ float epilogue(const Epi& e, float acc, int64_t m, in
 
 // Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
 // are R*M floats).
-template <int M> struct SimtRows { static constexpr int R = M <= 4 ? 8 : 4; };
+template <int M> struct SimtRows { static constexpr int R = 4; };
 // Fused gate/up: R gate rows + R up rows.
 template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
 
 // ---------------------------------------------------------------------------
 // SIMT GEMV
 
-template <typename T, int M, int R>
+template <typename T, int M, int R, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
     T* y, const T* x, const T* w, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
     int64_t syn, Epi e) {
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
   for (int k = (wave * kWave + lane) * 8; k < K; k += nw * kChunk) {
     V8 wv[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) wv[r] = rok[r] ? load8<T>(wr[r] + k) : V8{};
+    for (int r = 0; r < R; ++r) wv[r] = rok[r] ? load8w<NTW, T>(wr[r] + k) : V8{};
     V8 xv[M];
 #pragma unroll
     for (int m = 0; m < M; ++m) xv[m] = load8<T>(x + m * sxm + k);
@@ -115,48 +115,71 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 
 // ---------------------------------------------------------------------------
 // MFMA GEMV (M padded to 16)
+//
+// A workgroup owns TILES row tiles of 16 weight rows. Its waves take 128-element
+// K units round-robin and process U of them per iteration, issuing all of the
+// iteration's weight and x loads before its MFMAs (U*4 16-byte weight loads per
+// lane per tile in flight). The x operand of a step is loaded once and feeds
+// the MFMA of every row tile, so x traffic per weight byte is (M/16)/TILES.
 
-template <typename T>
+template <typename T, int TILES, int U, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_kernel(
     T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
     int64_t syn, Epi e) {
   typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * kWave];
+  __shared__ f32x4 part[kMaxWaves * TILES * kWave];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const bool wok = n0 + r < N;
+  const int64_t n0 = (int64_t)blockIdx.x * 16 * TILES;
   const bool xok = r < M;
-  const T* wp = w + (wok ? n0 + r : 0) * swn + g * 8;
   const T* xp = x + (xok ? r : 0) * sxm + g * 8;
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int units = (K + kUnit - 1) / kUnit;
-  for (int u = wave; u < units; u += nw) {
-    V8 a[4], b[4];
+  const T* wp[TILES];
+  bool wok[TILES];
+  f32x4 acc[TILES];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int k = u * kUnit + s * 32;
-      const bool in = k + g * 8 < K;
-      a[s] = (wok && in) ? load8<T>(wp + k) : V8{};
-      b[s] = (xok && in) ? load8<T>(xp + k) : V8{};
+  for (int t = 0; t < TILES; ++t) {
+    const int64_t n = n0 + t * 16 + r;
+    wok[t] = n < N;
+    wp[t] = w + (wok[t] ? n : 0) * swn + g * 8;
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const int units = (K + kUnit - 1) / kUnit;
+  for (int u0 = wave; u0 < units; u0 += nw * U) {
+    V8 a[TILES][U * 4], b[U * 4];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+      const int u = u0 + j * nw;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int k = u * kUnit + s * 32;
+        const bool in = u < units && k + g * 8 < K;
+        b[j * 4 + s] = (xok && in) ? load8<T>(xp + k) : V8{};
+#pragma unroll
+        for (int t = 0; t < TILES; ++t)
+          a[t][j * 4 + s] = (wok[t] && in) ? load8w<NTW, T>(wp[t] + k) : V8{};
+      }
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) acc = mfma16(a[s], b[s], acc);
+    for (int i = 0; i < U * 4; ++i)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) acc[t] = mfma16(a[t][i], b[i], acc[t]);
   }
-  part[wave * kWave + lane] = acc;
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) part[(wave * TILES + t) * kWave + lane] = acc[t];
   __syncthreads();
-  if (threadIdx.x < kWave) {
-    f32x4 s = part[threadIdx.x];
-    for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
-    // D lane layout: lane t holds rows 4*(t/16)+i (weight rows), column t%16 (x row).
-    const int m = threadIdx.x & 15;
-    const int nb = (threadIdx.x >> 4) * 4;
+  // D lane layout: lane l holds rows 4*(l/16)+i (weight rows), column l%16 (x row).
+  for (int idx = threadIdx.x; idx < TILES * kWave; idx += blockDim.x) {
+    const int t = idx / kWave, l = idx % kWave;
+    f32x4 s = part[t * kWave + l];
+    for (int i = 1; i < nw; ++i) s += part[(i * TILES + t) * kWave + l];
+    const int m = l & 15;
+    const int nb = (l >> 4) * 4;
     if (m < M) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + nb + i;
+        const int64_t n = n0 + t * 16 + nb + i;
         if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, s[i], m, n));
       }
     }
@@ -270,7 +293,7 @@ __device__ __forceinline__ T swiglu_out(float g, float u) {
 
 constexpr int kNormScratch = kMaxWaves * 16 + 16;
 
-template <typename T, int M, int R>
+template <typename T, int M, int R, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int H, int I,
     float eps, int tiles) {
@@ -304,8 +327,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
       V8 gv[R], uv[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        gv[r] = rok[r] ? load8<T>(wg[r] + k) : V8{};
-        uv[r] = rok[r] ? load8<T>(wu[r] + k) : V8{};
+        gv[r] = rok[r] ? load8w<NTW, T>(wg[r] + k) : V8{};
+        uv[r] = rok[r] ? load8w<NTW, T>(wu[r] + k) : V8{};
       }
       V8 xv[M];
 #pragma unroll
@@ -337,7 +360,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   }
 }
 
-template <typename T>
+template <typename T, int U, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
     T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int M, int H, int I,
     float eps, int tiles) {
@@ -354,6 +377,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
 
   const bool xok = r < M;
   const T* xp = xs + (xok ? r : 0) * H + g * 8;
+  const int units = (H + kUnit - 1) / kUnit;
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t j0 = (int64_t)tile * 16;
     const bool wok = j0 + r < I;
@@ -361,21 +385,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
     const T* gp = wgu + j * H + g * 8;
     const T* up = wgu + (I + j) * H + g * 8;
     f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    const int units = (H + kUnit - 1) / kUnit;
-    for (int u = wave; u < units; u += nw) {
-      V8 a[4], c[4], b[4];
+    for (int u0 = wave; u0 < units; u0 += nw * U) {
+      V8 a[U * 4], c[U * 4], b[U * 4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = u * kUnit + s * 32;
-        const bool in = k + g * 8 < H;
-        a[s] = (wok && in) ? load8<T>(gp + k) : V8{};
-        c[s] = (wok && in) ? load8<T>(up + k) : V8{};
-        b[s] = (xok && in) ? load8<T>(xp + k) : V8{};
+      for (int jj = 0; jj < U; ++jj) {
+        const int u = u0 + jj * nw;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int k = u * kUnit + s * 32;
+          const bool in = u < units && k + g * 8 < H;
+          a[jj * 4 + s] = (wok && in) ? load8w<NTW, T>(gp + k) : V8{};
+          c[jj * 4 + s] = (wok && in) ? load8w<NTW, T>(up + k) : V8{};
+          b[jj * 4 + s] = (xok && in) ? load8<T>(xp + k) : V8{};
+        }
       }
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        ag = mfma16(a[s], b[s], ag);
-        au = mfma16(c[s], b[s], au);
+      for (int i = 0; i < U * 4; ++i) {
+        ag = mfma16(a[i], b[i], ag);
+        au = mfma16(c[i], b[i], au);
       }
     }
     __syncthreads();  // previous tile's readers of `part` are done
@@ -407,6 +434,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
 namespace {
 
 constexpr int kMfmaMinM = 8;   // kind=dot uses MFMA from this M on
+// Weight streams use nontemporal loads in the SIMT kernels (measured +10-20% at
+// M <= 4). The MFMA kernels read each 128-byte line in two 64-byte halves from
+// consecutive instructions and lose when the first half is not retained.
+constexpr bool kNtWeights = true;
+constexpr bool kNtWeightsMfma = false;
 constexpr size_t kMaxLds = 160 * 1024;
 
 // Waves per workgroup: enough to cover K with whole work items (512-element
@@ -424,7 +456,7 @@ void launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sx
   constexpr int R = SimtRows<M>::R;
   const int nw = pick_waves((K + kChunk - 1) / kChunk);
   const unsigned blocks = (unsigned)((N + R - 1) / R);
-  hipLaunchKernelGGL((gemv_simt_kernel<T, M, R>), dim3(blocks), dim3(nw * kWave), 0, st,
+  hipLaunchKernelGGL((gemv_simt_kernel<T, M, R, kNtWeights>), dim3(blocks), dim3(nw * kWave), 0, st,
                      static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), N,
                      K, sxm, swn, sym, syn, e);
 }
@@ -443,14 +475,18 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
   }
 }
 
+constexpr int kMfmaU = 1;  // K units per MFMA iteration
+
 template <typename T>
 void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
   const int nw = pick_waves((K + kUnit - 1) / kUnit);
+  // One 16-row tile per workgroup: two tiles (shared x operand) measured slower
+  // at every decode shape, the grid is too small to fill 256 CUs.
   const unsigned blocks = (unsigned)((N + 15) / 16);
-  hipLaunchKernelGGL(gemv_mfma_kernel<T>, dim3(blocks), dim3(nw * kWave), 0, st,
-                     static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), M,
-                     N, K, sxm, swn, sym, syn, e);
+  hipLaunchKernelGGL((gemv_mfma_kernel<T, 1, kMfmaU, kNtWeightsMfma>), dim3(blocks),
+                     dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x),
+                     static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
 }
 
 // The dynamic-LDS limit of a kernel must be raised before a launch above 64 KiB.
@@ -462,6 +498,31 @@ bool allow_lds(F kernel, size_t bytes) {
                              (int)bytes) == hipSuccess;
 }
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+// Workgroups of the fused kernel: each stages the normalised activations in LDS
+// once and then loops over weight tiles, so the grid is what can be resident at
+// once (LDS-limited at larger M); more would restage x for nothing.
+int fused_grid(int tiles, size_t lds, int cap_small) {
+  const int per_cu = (int)(kMaxLds / (lds ? lds : 1));
+  const int cap = lds <= 16 * 1024 ? cap_small : device_cus() * (per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu);
+  const int per = (tiles + cap - 1) / cap;
+  return (tiles + per - 1) / per;
+}
+
 template <typename T, int M>
 int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype, const void* wgu,
                     int H, int I, float eps, hipStream_t st) {
@@ -471,13 +532,13 @@ int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype,
                      sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
                                                                            : kNormScratch);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  if (!allow_lds(mlp_gate_up_simt_kernel<T, M, R>, lds))
+  if (!allow_lds(mlp_gate_up_simt_kernel<T, M, R, kNtWeights>, lds))
     return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   const int tiles = (I + R - 1) / R;
-  const int per = (tiles + 1023) / 1024;
-  const int grid = (tiles + per - 1) / per;
-  const int nwv = pick_waves((H + kChunk - 1) / kChunk);
-  hipLaunchKernelGGL((mlp_gate_up_simt_kernel<T, M, R>), dim3(grid), dim3(nwv * kWave), lds, st,
+  const int grid = fused_grid(tiles, lds, 2048);
+  // Four waves: each covers two 512-element K chunks per row at H=4096.
+  const int nwv = pick_waves((H + kChunk - 1) / kChunk) > 4 ? 4 : pick_waves((H + kChunk - 1) / kChunk);
+  hipLaunchKernelGGL((mlp_gate_up_simt_kernel<T, M, R, kNtWeights>), dim3(grid), dim3(nwv * kWave), lds, st,
                      static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
                      static_cast<const T*>(wgu), H, I, eps, tiles);
   return FD_OK;
@@ -502,13 +563,12 @@ int launch_mlp_mfma(int M, void* mid, const void* hidden, const void* nw, int nw
                     const void* wgu, int H, int I, float eps, hipStream_t st) {
   const size_t lds = (size_t)M * H * sizeof(T) + sizeof(f32x4) * 2 * kMaxWaves * kWave;
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  if (!allow_lds(mlp_gate_up_mfma_kernel<T>, lds))
+  if (!allow_lds(mlp_gate_up_mfma_kernel<T, kMfmaU, kNtWeightsMfma>, lds))
     return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   const int tiles = (I + 15) / 16;
-  const int per = (tiles + 1023) / 1024;
-  const int grid = (tiles + per - 1) / per;
+  const int grid = fused_grid(tiles, lds, 1024);
   const int nwv = pick_waves((H + kUnit - 1) / kUnit);
-  hipLaunchKernelGGL(mlp_gate_up_mfma_kernel<T>, dim3(grid), dim3(nwv * kWave), lds, st,
+  hipLaunchKernelGGL((mlp_gate_up_mfma_kernel<T, kMfmaU, kNtWeightsMfma>), dim3(grid), dim3(nwv * kWave), lds, st,
                      static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
                      static_cast<const T*>(wgu), M, H, I, eps, tiles);
   return FD_OK;

@@ -5,11 +5,12 @@
 //   add_rms: s = x + r (float32); ro = round(s); y = round(s * rsqrt(mean(s^2) + eps) * w)
 // The norm always sees the float32 sum, never the rounded residual.
 //
-// Two kernels:
-//   rms_vec_kernel  - unit column stride, n % 8 == 0, 16-byte aligned rows, n small
-//                     enough that the row lives in registers (<= 256 threads x 8
-//                     vectors x 8 = 16384 elements). One workgroup per row, one HBM
-//                     pass: every byte is read once and written once.
+// Three kernels:
+//   rms_wave_kernel - unit column stride, n % 8 == 0, 16-byte aligned rows,
+//                     n <= 8192: one wave per row, the row in registers.
+//   rms_vec_kernel  - the same layouts for 8192 < n <= 16384: one 256-thread
+//                     workgroup per row. Both make one HBM pass: every byte is read
+//                     once and written once.
 //   rms_gen_kernel  - any strides and any n: two passes over the row (the second
 //                     pass re-reads through L2).
 // Reduction: wave64 shuffles, then one LDS exchange across the workgroup's waves.
@@ -88,6 +89,67 @@ __global__ __launch_bounds__(NT) void rms_vec_kernel(T* y, T* ro, const T* x, co
   }
 }
 
+// One wave per row, several rows per workgroup: the reduction is wave shuffles
+// only (no LDS, no workgroup barrier), and each lane keeps VPL vectors of its
+// row in registers. Activations stream through nontemporal loads and stores
+// (read and written exactly once).
+template <typename T, typename W, int VPL, bool ADD>
+__global__ __launch_bounds__(256) void rms_wave_kernel(T* y, T* ro, const T* x, const T* r,
+                                                      const W* __restrict__ w, RowGrid grid,
+                                                      RowStrides lx, RowStrides lr,
+                                                      RowStrides ly, RowStrides lro, int n,
+                                                      uint32_t rows, float eps) {
+  typedef typename Vec8<T>::type V8;
+  const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (row >= rows) return;
+  const int lane = threadIdx.x & (kWave - 1);
+  const RowPos p = row_pos(grid, row);
+  const T* xr = x + row_off(lx, p);
+  const T* rr = ADD ? r + row_off(lr, p) : nullptr;
+  V8 a[VPL], b[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int k = (j * kWave + lane) * 8;
+    if (k < n) {
+      a[j] = load8_nt<T>(xr + k);
+      if (ADD) b[j] = load8_nt<T>(rr + k);
+    }
+  }
+  float v[VPL][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int k = (j * kWave + lane) * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[j][i] = k < n ? (ADD ? to_f32(a[j][i]) + to_f32(b[j][i]) : to_f32(a[j][i])) : 0.f;
+      ss += v[j][i] * v[j][i];
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = rsqrtf(ss / (float)n + eps);
+  T* yr = y + row_off(ly, p);
+  T* ror = ADD ? ro + row_off(lro, p) : nullptr;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int k = (j * kWave + lane) * 8;
+    if (k < n) {
+      float wf[8];
+      load8_f32<W>(w + k, wf);
+      V8 o;
+      if (ADD) {
+        V8 s;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s[i] = from_f32<T>(v[j][i]);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s), reinterpret_cast<u32x4*>(ror + k));
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(v[j][i] * inv * wf[i]);
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(yr + k));
+    }
+  }
+}
+
 template <typename T, bool ADD>
 __global__ __launch_bounds__(256) void rms_gen_kernel(T* y, T* ro, const T* x, const T* r,
                                                       const void* __restrict__ w, int w_dtype,
@@ -133,10 +195,39 @@ void launch_vec(void* y, void* ro, const void* x, const void* r, const void* w,
                      (int)lx.n, eps);
 }
 
+template <typename T, typename W, int VPL, bool ADD>
+void launch_wave(void* y, void* ro, const void* x, const void* r, const void* w,
+                 const fd_rows& lx, const fd_rows& lr, const fd_rows& ly, const fd_rows& lro,
+                 int64_t rows, float eps, hipStream_t st) {
+  hipLaunchKernelGGL((rms_wave_kernel<T, W, VPL, ADD>), dim3((unsigned)((rows + 3) / 4)),
+                     dim3(256), 0, st, static_cast<T*>(y), static_cast<T*>(ro),
+                     static_cast<const T*>(x), static_cast<const T*>(r),
+                     static_cast<const W*>(w), row_grid(lx), row_strides(lx), row_strides(lr),
+                     row_strides(ly), row_strides(lro), (int)lx.n, (uint32_t)rows, eps);
+}
+
 template <typename T, typename W, bool ADD>
 void pick_vpt(void* y, void* ro, const void* x, const void* r, const void* w,
               const fd_rows& lx, const fd_rows& lr, const fd_rows& ly, const fd_rows& lro,
               int64_t rows, float eps, hipStream_t st) {
+  // Rows up to 8192 elements: one wave per row (VPL vectors per lane).
+  const int64_t lanes_vecs = (lx.n + 8 * kWave - 1) / (8 * kWave);
+  if (lanes_vecs <= 2) {
+    launch_wave<T, W, 2, ADD>(y, ro, x, r, w, lx, lr, ly, lro, rows, eps, st);
+    return;
+  }
+  if (lanes_vecs <= 4) {
+    launch_wave<T, W, 4, ADD>(y, ro, x, r, w, lx, lr, ly, lro, rows, eps, st);
+    return;
+  }
+  if (lanes_vecs <= 8) {
+    launch_wave<T, W, 8, ADD>(y, ro, x, r, w, lx, lr, ly, lro, rows, eps, st);
+    return;
+  }
+  if (lanes_vecs <= 16) {
+    launch_wave<T, W, 16, ADD>(y, ro, x, r, w, lx, lr, ly, lro, rows, eps, st);
+    return;
+  }
   const int64_t vecs = (lx.n + 8 * 256 - 1) / (8 * 256);
   if (vecs <= 1)
     launch_vec<T, W, 1, ADD>(y, ro, x, r, w, lx, lr, ly, lro, rows, eps, st);

@@ -10,7 +10,9 @@ constexpr int kRoofThreads = 256;
 constexpr int kRoofUnroll = 4;
 
 // Each thread moves kRoofUnroll vectors, strided by the block so every load
-// instruction of a wave covers 1 KiB of contiguous memory.
+// instruction of a wave covers 1 KiB of contiguous memory. Nontemporal loads and
+// stores: the fastest copy measured on MI355X (6.1 TB/s over 2 GiB, against
+// 5.7 TB/s with ordinary ones), so the roof is not understated.
 __global__ __launch_bounds__(kRoofThreads) void copy_vec_kernel(u32x4* dst, const u32x4* src,
                                                                 int64_t nvec) {
   const int64_t base = (int64_t)blockIdx.x * (kRoofThreads * kRoofUnroll) + threadIdx.x;
@@ -18,12 +20,12 @@ __global__ __launch_bounds__(kRoofThreads) void copy_vec_kernel(u32x4* dst, cons
 #pragma unroll
   for (int i = 0; i < kRoofUnroll; ++i) {
     const int64_t e = base + i * kRoofThreads;
-    if (e < nvec) v[i] = src[e];
+    if (e < nvec) v[i] = __builtin_nontemporal_load(src + e);
   }
 #pragma unroll
   for (int i = 0; i < kRoofUnroll; ++i) {
     const int64_t e = base + i * kRoofThreads;
-    if (e < nvec) dst[e] = v[i];
+    if (e < nvec) __builtin_nontemporal_store(v[i], dst + e);
   }
 }
 

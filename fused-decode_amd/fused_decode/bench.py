@@ -76,8 +76,33 @@ def cpu_time_us(fn, budget_s: float = 2.0, max_iters: int = 50) -> float:
 
 
 def copies_for(working_set: int) -> int:
-    """Number of distinct buffer sets so a rotation exceeds 2x the Infinity Cache."""
-    return max(1, math.ceil(ROTATE_TARGET / max(1, working_set)))
+    """Number of distinct buffer sets so a rotation exceeds 2x the Infinity Cache
+    (capped at 64: below ~10 MB per call an op is launch-bound, not HBM-bound)."""
+    return min(64, max(1, math.ceil(ROTATE_TARGET / max(1, working_set))))
+
+
+def graph_us(fn, k: int, replays: int = 20) -> float | None:
+    """Device time per call: one HIP graph holding fn(0..k-1) (every buffer set
+    once), replayed; excludes the Python launch path."""
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(k):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        _sync()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(k):
+                fn(i)
+        reps = max(replays, math.ceil(200 / k))
+        us = time_us(lambda i: g.replay(), iters=reps, warmup=3, rounds=3) / k
+        del g
+        return us
+    except Exception as exc:  # pragma: no cover
+        print("graph capture failed:", exc)
+        return None
 
 
 def bench_roofline() -> dict:
@@ -103,14 +128,20 @@ def bench_roofline() -> dict:
     }
 
 
-def _row(name, nbytes, cold_us, warm_us, roof, **extra) -> dict:
-    gbs = nbytes / (cold_us * 1e-6) / 1e9
+def _row(name, nbytes, cold_us, warm_us, roof, dev_us=None, **extra) -> dict:
+    """`us`: eager launches back to back (the reference's method); `dev_us`: the
+    same calls replayed from a HIP graph (device time). GB/s and % of roof use
+    the device time when there is one."""
+    t = dev_us if dev_us else cold_us
+    gbs = nbytes / (t * 1e-6) / 1e9
     row = {
         "name": name,
         "bytes": nbytes,
         "us": cold_us,
+        "dev_us": dev_us,
         "us_warm": warm_us,
         "gbs": gbs,
+        "gbs_eager": nbytes / (cold_us * 1e-6) / 1e9,
         "gbs_warm": nbytes / (warm_us * 1e-6) / 1e9,
         "pct_copy_roof": 100.0 * gbs / roof,
         "pct_datasheet": 100.0 * gbs / DATASHEET_GBS,
@@ -120,7 +151,8 @@ def _row(name, nbytes, cold_us, warm_us, roof, **extra) -> dict:
 
 
 def _print(row: dict) -> None:
-    parts = [f"{row['name']:<44}", f"{row['us']:9.2f} us", f"{row['gbs']:8.1f} GB/s",
+    dev = f"dev {row['dev_us']:8.2f}" if row.get("dev_us") else "dev      n/a"
+    parts = [f"{row['name']:<44}", f"{row['us']:9.2f} us", dev, f"{row['gbs']:8.1f} GB/s",
              f"{row['pct_copy_roof']:5.1f}% copy", f"warm {row['us_warm']:8.2f}"]
     for k in ("eager_us", "cpu_eager_us", "graph_us", "hipblas_us"):
         if row.get(k) is not None:
@@ -145,24 +177,26 @@ def bench_pointwise(dtype, roof, quick, cpu) -> list[dict]:
         w = _gen((h,), dtype, g, 0.1, 1.0)
         outs = [torch.empty_like(xs[0]) for _ in range(k)]
         cold = time_us(lambda i: rms_norm(xs[i % k], w, 1e-5, out=outs[i % k]), iters=max(20, 2 * k))
+        dev = graph_us(lambda i: rms_norm(xs[i % k], w, 1e-5, out=outs[i % k]), k)
         warm = time_us(lambda i: rms_norm(xs[0], w, 1e-5, out=outs[0]), iters=50)
         eager = time_us(lambda i: F.rms_norm(xs[i % k], (h,), w, 1e-5), iters=max(20, 2 * k))
         cpu_us = None
         if cpu:
             xc, wc = xs[0].cpu(), w.cpu()
             cpu_us = cpu_time_us(lambda: F.rms_norm(xc, (h,), wc, 1e-5))
-        rows.append(_row(f"rms_norm {r}x{h} {dtype}", (2 * r * h + h) * e, cold, warm, roof,
+        rows.append(_row(f"rms_norm {r}x{h} {dtype}", (2 * r * h + h) * e, cold, warm, roof, dev,
                          eager_us=eager, cpu_eager_us=cpu_us))
         _print(rows[-1])
         cold = time_us(lambda i: add_rms_norm(xs[i % k], rs[i % k], w, 1e-5, out=outs[i % k], residual_out=rs[i % k]),
                        iters=max(20, 2 * k))
+        dev = graph_us(lambda i: add_rms_norm(xs[i % k], rs[i % k], w, 1e-5, out=outs[i % k], residual_out=rs[i % k]), k)
         warm = time_us(lambda i: add_rms_norm(xs[0], rs[0], w, 1e-5, out=outs[0], residual_out=rs[0]), iters=50)
         eager = time_us(lambda i: F.rms_norm(xs[i % k] + rs[i % k], (h,), w, 1e-5), iters=max(20, 2 * k))
         cpu_us = None
         if cpu:
             xc, rc, wc = xs[0].cpu(), rs[0].cpu(), w.cpu()
             cpu_us = cpu_time_us(lambda: F.rms_norm(xc + rc, (h,), wc, 1e-5))
-        rows.append(_row(f"add_rms_norm {r}x{h} {dtype}", (4 * r * h + h) * e, cold, warm, roof,
+        rows.append(_row(f"add_rms_norm {r}x{h} {dtype}", (4 * r * h + h) * e, cold, warm, roof, dev,
                          eager_us=eager, cpu_eager_us=cpu_us))
         _print(rows[-1])
         del xs, rs, outs
@@ -173,13 +207,14 @@ def bench_pointwise(dtype, roof, quick, cpu) -> list[dict]:
         us_ = [_gen((r, n), dtype, g, 2.0) for _ in range(k)]
         outs = [torch.empty_like(gs[0]) for _ in range(k)]
         cold = time_us(lambda i: swiglu(gs[i % k], us_[i % k], out=outs[i % k]), iters=max(20, 2 * k))
+        dev = graph_us(lambda i: swiglu(gs[i % k], us_[i % k], out=outs[i % k]), k)
         warm = time_us(lambda i: swiglu(gs[0], us_[0], out=outs[0]), iters=50)
         eager = time_us(lambda i: F.silu(gs[i % k]) * us_[i % k], iters=max(20, 2 * k))
         cpu_us = None
         if cpu:
             gc, uc = gs[0].cpu(), us_[0].cpu()
             cpu_us = cpu_time_us(lambda: F.silu(gc) * uc)
-        rows.append(_row(f"swiglu {r}x{n} {dtype}", 3 * r * n * e, cold, warm, roof, eager_us=eager, cpu_eager_us=cpu_us))
+        rows.append(_row(f"swiglu {r}x{n} {dtype}", 3 * r * n * e, cold, warm, roof, dev, eager_us=eager, cpu_eager_us=cpu_us))
         _print(rows[-1])
         del gs, us_, outs
     # RoPE with Llama-3 tables (theta 500000) viewed [S, 1, 128]
@@ -203,13 +238,14 @@ def bench_pointwise(dtype, roof, quick, cpu) -> list[dict]:
                               x[..., h:] * cb[..., h:] + x[..., :h] * sb[..., h:]), -1)
 
         cold = time_us(lambda i: rope(xs[i % k], c, s, out=outs[i % k]), iters=max(20, 2 * k))
+        dev = graph_us(lambda i: rope(xs[i % k], c, s, out=outs[i % k]), k)
         warm = time_us(lambda i: rope(xs[0], c, s, out=outs[0]), iters=50)
         eager = time_us(lambda i: eager_rope(xs[i % k]), iters=max(20, 2 * k))
         cpu_us = None
         if cpu:
             xc, cc, sc = xs[0].cpu(), c.cpu(), s.cpu()
             cpu_us = cpu_time_us(lambda: eager_rope(xc, cc, sc))
-        rows.append(_row(f"rope {xshape} {dtype}", nbytes, cold, warm, roof, eager_us=eager, cpu_eager_us=cpu_us))
+        rows.append(_row(f"rope {xshape} {dtype}", nbytes, cold, warm, roof, dev, eager_us=eager, cpu_eager_us=cpu_us))
         _print(rows[-1])
         del xs, outs
     torch.cuda.empty_cache()
@@ -231,15 +267,17 @@ def bench_linear(dtype, roof, quick, cpu) -> list[dict]:
             out = torch.empty(m, n, device="cuda", dtype=dtype)
             nbytes = (m * kk + n * kk + m * n) * e
             hip = time_us(lambda i: F.linear(x, ws[i % k]), iters=max(30, 2 * k))
+            hip_dev = graph_us(lambda i: F.linear(x, ws[i % k]), k)
             cpu_us = None
             if cpu and m in (1, 8):
                 xc, wc = x.cpu(), ws[0].cpu()
                 cpu_us = cpu_time_us(lambda: F.linear(xc, wc), budget_s=1.0, max_iters=10)
             for kind in ("simt", "dot"):
                 cold = time_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), iters=max(30, 2 * k))
+                dev = graph_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), k)
                 warm = time_us(lambda i: linear_decode(x, ws[0], out=out, kind=kind), iters=50)
-                rows.append(_row(f"linear M={m} N={n} K={kk} {kind} {dtype}", nbytes, cold, warm, roof,
-                                 hipblas_us=hip, cpu_eager_us=cpu_us))
+                rows.append(_row(f"linear M={m} N={n} K={kk} {kind} {dtype}", nbytes, cold, warm, roof, dev,
+                                 hipblas_us=hip, hipblas_dev_us=hip_dev, cpu_eager_us=cpu_us))
                 _print(rows[-1])
         del ws
         torch.cuda.empty_cache()
@@ -267,15 +305,7 @@ def bench_mlp(dtype, roof, quick, cpu) -> list[dict]:
         for kind in ("dot", "simt"):
             cold = time_us(lambda j: post_attn_mlp(hid, *sets[j % k], 1e-5, kind=kind), iters=max(30, 2 * k))
             warm = time_us(lambda j: post_attn_mlp(hid, *sets[0], 1e-5, kind=kind), iters=30)
-            graphs = []
-            for j in range(k):
-                post_attn_mlp(hid, *sets[j], 1e-5, kind=kind)
-                _sync()
-                gr = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(gr):
-                    post_attn_mlp(hid, *sets[j], 1e-5, kind=kind)
-                graphs.append(gr)
-            graph_us = time_us(lambda j: graphs[j % k].replay(), iters=max(30, 2 * k))
+            g_us = graph_us(lambda j: post_attn_mlp(hid, *sets[j % k], 1e-5, kind=kind), k)
             eager_us = time_us(eager, iters=max(30, 2 * k))
             cpu_us = None
             if cpu and kind == "dot":
@@ -289,11 +319,10 @@ def bench_mlp(dtype, roof, quick, cpu) -> list[dict]:
 
                 cpu_us = cpu_time_us(cpu_mlp, budget_s=3.0, max_iters=10)
             nbytes = (3 * h * i_ + 2 * m * h + h) * e
-            rows.append(_row(f"post_attn_mlp M={m} {kind} {dtype}", nbytes, cold, warm, roof,
-                             graph_us=graph_us, eager_us=eager_us, cpu_eager_us=cpu_us,
+            rows.append(_row(f"post_attn_mlp M={m} {kind} {dtype}", nbytes, cold, warm, roof, g_us,
+                             eager_us=eager_us, cpu_eager_us=cpu_us,
                              target_us=1.25 * 3 * h * i_ * e / (roof * 1e9) * 1e6))
             _print(rows[-1])
-            del graphs
     del sets
     torch.cuda.empty_cache()
     return rows

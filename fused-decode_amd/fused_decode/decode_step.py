@@ -1,0 +1,165 @@
+"""A random-init Llama-3-8B decode step minus attention, captured in a HIP graph.
+
+    python -m fused_decode.decode_step [--m 1] [--layers 32] [--dtype fp16] [--steps 20]
+
+Per layer (widths of Llama-3-8B: H=4096, 32 query / 8 KV heads of 128, I=14336):
+
+    normed, stream = add_rms_norm(x, zero, attn_norm_w)   # stream <- x, normed <- rms(x)
+    qkv  = linear_decode(normed, w_qkv)                  # [M, 6144]
+    q, k = rope(qkv[:, :5120] as [M, 40, 128])           # q and k heads in one launch, position 1024
+    attn = stand-in attention output                     # seeded random [M, 4096] per layer
+    h    = linear_decode(attn, w_o, row_add=stream)      # O-proj with the residual fused
+    x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
+
+post_attn_mlp returns the whole residual stream (its residual add is fused into
+the down projection), so the next layer's add_rms_norm receives that stream with
+a zero delta: it both normalises it and keeps the copy the O-proj residual reads.
+The whole step (7 launches per layer) is captured once and replayed.
+
+Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), random
+with the benchmark distributions (no checkpoint is loaded).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+
+import torch
+
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, rope
+
+H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
+QKV = (HEADS + 2 * KV_HEADS) * HEAD_DIM  # 6144
+
+
+def llama3_angles(position: int, dim: int = HEAD_DIM, theta: float = 500000.0, device="cuda"):
+    """cos/sin rows [1, 1, dim] for one position (rotate-half layout)."""
+    inv = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float64, device=device) / dim))
+    ang = position * inv
+    emb = torch.cat((ang, ang))
+    return emb.cos().view(1, 1, dim), emb.sin().view(1, 1, dim)
+
+
+class DecodeStep:
+    """Weights and buffers of an L-layer decode step; `step()` runs it eagerly,
+    `capture()` records it into a HIP graph and `replay()` runs that."""
+
+    def __init__(self, m: int = 1, layers: int = 32, dtype=torch.float16, device="cuda",
+                 seed: int = 0, h: int = H, i: int = I, kind: str | None = None, position: int = 1024):
+        self.m, self.layers, self.dtype, self.kind = m, layers, dtype, kind
+        self.h, self.i = h, i
+        heads = h // HEAD_DIM
+        kv = max(1, heads // 4)
+        self.qk_heads = heads + kv
+        self.qkv_n = (heads + 2 * kv) * HEAD_DIM
+        g = torch.Generator(device=device).manual_seed(seed)
+
+        def rnd(*shape, scale=1.0, mean=0.0):
+            t = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+            return (t * scale + mean).to(dtype)
+
+        self.w = []
+        for _ in range(layers):
+            self.w.append({
+                "attn_norm": rnd(h, scale=0.1, mean=1.0),
+                "qkv": rnd(self.qkv_n, h, scale=h ** -0.5),
+                "o": rnd(h, h, scale=h ** -0.5),
+                "mlp_norm": rnd(h, scale=0.1, mean=1.0),
+                "gate_up": rnd(2 * i, h, scale=h ** -0.5),
+                "down": rnd(h, i, scale=i ** -0.5),
+                "attn_out": rnd(m, h),  # stand-in for the attention output of this layer
+            })
+        cos, sin = llama3_angles(position, device=device)
+        self.cos, self.sin = cos.to(dtype), sin.to(dtype)
+        self.x_in = rnd(m, h)
+        self.zero = torch.zeros(m, h, device=device, dtype=dtype)
+        self.stream = torch.empty(m, h, device=device, dtype=dtype)
+        self.normed = torch.empty(m, h, device=device, dtype=dtype)
+        self.qkv = torch.empty(m, self.qkv_n, device=device, dtype=dtype)
+        self.hbuf = torch.empty(m, h, device=device, dtype=dtype)
+        self.out = torch.empty(m, h, device=device, dtype=dtype)
+        self.graph = None
+
+    @property
+    def weight_bytes(self) -> int:
+        e = torch.empty((), dtype=self.dtype).element_size()
+        per = (self.qkv_n * self.h + self.h * self.h + 3 * self.h * self.i + 2 * self.h) * e
+        return per * self.layers
+
+    def step(self) -> torch.Tensor:
+        x = self.x_in
+        qk = self.qkv[:, : self.qk_heads * HEAD_DIM].view(self.m, self.qk_heads, HEAD_DIM)
+        for w in self.w:
+            add_rms_norm(x, self.zero, w["attn_norm"], 1e-5, out=self.normed, residual_out=self.stream)
+            linear_decode(self.normed, w["qkv"], out=self.qkv, kind=self.kind)
+            rope(qk, self.cos, self.sin, out=qk)
+            linear_decode(w["attn_out"], w["o"], row_add=self.stream, out=self.hbuf, kind=self.kind)
+            x = post_attn_mlp(self.hbuf, w["mlp_norm"], w["gate_up"], w["down"], 1e-5, kind=self.kind)
+        self.out.copy_(x)
+        return self.out
+
+    def capture(self) -> None:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+
+    def replay(self) -> torch.Tensor:
+        if self.graph is None:
+            self.capture()
+        self.graph.replay()
+        return self.out
+
+
+def time_step(ds: DecodeStep, steps: int, warmup: int, graph: bool) -> float:
+    run = ds.replay if graph else ds.step
+    if graph and ds.graph is None:
+        ds.capture()
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1000.0 / steps
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--m", type=int, nargs="+", default=[1, 8])
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    args = ap.parse_args()
+    dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    for m in args.m:
+        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype)
+        eager = time_step(ds, args.steps, args.warmup, graph=False)
+        graph = time_step(ds, args.steps, args.warmup, graph=True)
+        wb = ds.weight_bytes
+        print(json.dumps({
+            "workload": f"decode step minus attention, {args.layers} layers, Llama-3-8B widths, M={m}, {args.dtype}",
+            "eager_us": round(eager, 2),
+            "graph_us": round(graph, 2),
+            "weight_bytes": wb,
+            "graph_gbs": round(wb / (graph * 1e-6) / 1e9, 1),
+            "launches_per_step": 7 * args.layers + 1,
+            "finite": bool(torch.isfinite(ds.out.float()).all().item()),
+        }), flush=True)
+        del ds
+        torch.cuda.empty_cache()
+
+
+if __name__ == "__main__":
+    main()

@@ -22,7 +22,7 @@ from .kernels import linear_out, post_attn_mlp_out, resolve_kind, rms_out, rope_
 # reference sets this per GPU from measurement (its RTX 4070 Laptop value is 1,
 # ops.py:16-19); for MI355X it is set from the GEMV-vs-hipBLASLt sweep of the
 # bench (python -m fused_decode.bench).
-DECODE_LINEAR_MAX_M = 16
+DECODE_LINEAR_MAX_M = 8
 _HAND_LIMIT = 16
 _ACTIVATION = (torch.float16, torch.bfloat16)
 _NORM_WEIGHT = (torch.float16, torch.bfloat16, torch.float32)

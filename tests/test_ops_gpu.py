@@ -442,3 +442,51 @@ def test_library_runtime_is_torchs():
 
     assert L.runtime_version() // 10_000_000 == int(torch.version.hip.split(".")[0])
     assert math.isfinite(float(L.runtime_version()))
+
+
+# ---------------------------------------------------------------- decode step
+
+
+def _oracle_decode_step(ds, tagd):
+    """The harness's layer sequence restated with the oracle's operators."""
+    n = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    x = n(ds.x_in)
+    cos, sin = n(ds.cos), n(ds.sin)
+    qk = ds.qk_heads * 128
+    for w in ds.w:
+        normed, stream = O.add_rms_norm(x, np.zeros_like(x), n(w["attn_norm"]), 1e-5, tagd)
+        qkv = O.linear(normed, n(w["qkv"]), dtype=tagd)
+        q = qkv[:, :qk].reshape(ds.m, ds.qk_heads, 128)
+        qkv[:, :qk] = O.rope(q, cos, sin, tagd).reshape(ds.m, qk)
+        h = O.linear(n(w["attn_out"]), n(w["o"]), row_add=stream, dtype=tagd)
+        x = O.post_attn_mlp(h, n(w["mlp_norm"]), n(w["gate_up"]), n(w["down"]), 1e-5, tagd)
+    return x, qkv
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_decode_step_small_matches_oracle_and_graph(m):
+    from fused_decode.decode_step import DecodeStep
+
+    ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=5)
+    eager = ds.step().clone()
+    ref, ref_qkv = _oracle_decode_step(ds, "f16")
+    check(eager, ref, torch.float16, "linear")
+    check(ds.qkv, ref_qkv, torch.float16, "linear")  # last layer's q/k after RoPE, and v
+    ds.capture()
+    for _ in range(3):
+        ds.out.zero_()
+        out = ds.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, rtol=0, atol=0)
+
+
+def test_decode_step_llama3_8b_two_layers_finite():
+    from fused_decode.decode_step import DecodeStep
+
+    ds = DecodeStep(m=1, layers=2, seed=6)
+    a = ds.step().clone()
+    b = ds.replay().clone()
+    torch.cuda.synchronize()
+    assert torch.isfinite(a.float()).all()
+    torch.testing.assert_close(a, b, rtol=0, atol=0)
+    assert ds.weight_bytes == 2 * 436_207_616 + 2 * 2 * 4096 * 2
