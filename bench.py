@@ -153,6 +153,18 @@ def copy_roof_gbs(torch) -> float:
     return 2 * n / (us * 1e-6) / 1e9
 
 
+def pmc_traffic() -> int | None:
+    """HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes (profiles/mlp_gate_up_m1_pmc.md), or None."""
+    path = ROOT / "profiles" / "mlp_gate_up_m1_pmc.md"
+    try:
+        text = path.read_text()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        return int(json.loads(block)["traffic_bytes"])
+    except Exception:
+        return None
+
+
 def cpu_baseline(seconds: float) -> dict:
     """NumPy oracle of the same block at M=1, fp16 semantics, bounded sample."""
     import numpy as np
@@ -256,7 +268,8 @@ def main() -> None:
             "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
             "avg_us": round(gate_us, 3),
             "algorithmic_bytes": gate_bytes,
-            "traffic": None,
+            "traffic": pmc_traffic(),
+            "traffic_source": "profiles/mlp_gate_up_m1_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE, copy-calibrated)",
         },
     }
     if not args.no_decode_step:
