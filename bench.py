@@ -116,7 +116,7 @@ def time_gate_up_kernel(torch, lib, sets, m: int, iters: int, kind_code: int) ->
     def launch(s):
         hid, nw, wgu, _ = sets[s % N_SETS]
         check("fd_mlp_gate_up", lib.fd_mlp_gate_up(
-            mids[s % N_SETS].data_ptr(), hid.data_ptr(), nw.data_ptr(), DTYPE_CODE[nw.dtype],
+            mids[s % N_SETS].data_ptr(), None, hid.data_ptr(), nw.data_ptr(), DTYPE_CODE[nw.dtype],
             wgu.data_ptr(), m, H, I, EPS, kind_code, DTYPE_CODE[hid.dtype], stream))
 
     for s in range(10):

@@ -24,6 +24,7 @@
 // residual fused as row_add. Weights are read once; gate_up never exists in HBM.
 #include "fd_device.h"
 #include "fd_host.h"
+#include "fd_internal.h"
 
 namespace fd {
 
@@ -114,72 +115,94 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// MFMA GEMV (M padded to 16)
+// MFMA GEMV with row-contiguous weight loads (M padded to 16)
 //
-// A workgroup owns TILES row tiles of 16 weight rows. Its waves take 128-element
-// K units round-robin and process U of them per iteration, issuing all of the
-// iteration's weight and x loads before its MFMAs (U*4 16-byte weight loads per
-// lane per tile in flight). The x operand of a step is loaded once and feeds
-// the MFMA of every row tile, so x traffic per weight byte is (M/16)/TILES.
-
-template <typename T, int TILES, int U, bool NTW>
-__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_kernel(
+// The MFMA A operand wants lane l to hold row l%16, so loading it directly
+// makes every load instruction touch 16 rows x 64 bytes: 16 half-used cache
+// lines (measured: a pure read in that pattern reaches 5.7 TB/s against 6.9 TB/s
+// for row-contiguous 16-byte loads). Here each wave loads its 16 x 128 tile as 4
+// instructions of 4 rows x 256 contiguous bytes (lane l: row 4i + l/16, chunk
+// l%16), stores it to a wave-private 4 KiB LDS buffer with the 16-byte chunk
+// index XOR-swizzled by the row (conflict-free on both sides), and reads it back
+// in MFMA layout. Waves split K in 128-element units, U units per iteration.
+template <typename T, int U, bool NTW>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
     T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
     int64_t syn, Epi e) {
   typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * TILES * kWave];
+  __shared__ f32x4 part[kMaxWaves * kWave];
+  __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16 * TILES;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
   const bool xok = r < M;
   const T* xp = x + (xok ? r : 0) * sxm + g * 8;
-  const T* wp[TILES];
-  bool wok[TILES];
-  f32x4 acc[TILES];
+  // load side: lane -> (row 4i + lane/16, chunk lane%16) for instruction i
+  const int lrow = lane >> 4, lchunk = lane & 15;
+  const T* wl[4];
+  bool lok[4];
 #pragma unroll
-  for (int t = 0; t < TILES; ++t) {
-    const int64_t n = n0 + t * 16 + r;
-    wok[t] = n < N;
-    wp[t] = w + (wok[t] ? n : 0) * swn + g * 8;
-    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + 4 * i + lrow;
+    lok[i] = n < N;
+    wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 8;
   }
+  u32x4* tile = tiles[wave];
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
   for (int u0 = wave; u0 < units; u0 += nw * U) {
-    V8 a[TILES][U * 4], b[U * 4];
+    u32x4 v[U][4];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       const int u = u0 + j * nw;
+      const int k = u * kUnit + lchunk * 8;
+      const bool in = u < units && k < K;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int k = u * kUnit + s * 32;
-        const bool in = u < units && k + g * 8 < K;
-        b[j * 4 + s] = (xok && in) ? load8<T>(xp + k) : V8{};
-#pragma unroll
-        for (int t = 0; t < TILES; ++t)
-          a[t][j * 4 + s] = (wok[t] && in) ? load8w<NTW, T>(wp[t] + k) : V8{};
+      for (int i = 0; i < 4; ++i) {
+        const u32x4* q = reinterpret_cast<const u32x4*>(wl[i] + u * kUnit);
+        v[j][i] = (lok[i] && in) ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
       }
     }
 #pragma unroll
-    for (int i = 0; i < U * 4; ++i)
+    for (int j = 0; j < U; ++j) {
+      const int u = u0 + j * nw;
+      // stage: row 4i+lrow, chunk lchunk -> slot row*16 + (chunk ^ row)
 #pragma unroll
-      for (int t = 0; t < TILES; ++t) acc[t] = mfma16(a[t][i], b[i], acc[t]);
+      for (int i = 0; i < 4; ++i) {
+        const int row = 4 * i + lrow;
+        tile[row * 16 + (lchunk ^ row)] = v[j][i];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      V8 a[4], b[4];
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int chunk = s2 * 4 + g;
+        a[s2] = __builtin_bit_cast(V8, tile[r * 16 + (chunk ^ r)]);
+        const int k = u * kUnit + chunk * 8;
+        b[s2] = (xok && u < units && k < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
+    }
   }
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) part[(wave * TILES + t) * kWave + lane] = acc[t];
+  part[wave * kWave + lane] = acc;
   __syncthreads();
-  // D lane layout: lane l holds rows 4*(l/16)+i (weight rows), column l%16 (x row).
-  for (int idx = threadIdx.x; idx < TILES * kWave; idx += blockDim.x) {
-    const int t = idx / kWave, l = idx % kWave;
-    f32x4 s = part[t * kWave + l];
-    for (int i = 1; i < nw; ++i) s += part[(i * TILES + t) * kWave + l];
-    const int m = l & 15;
-    const int nb = (l >> 4) * 4;
+  if (threadIdx.x < kWave) {
+    f32x4 s = part[threadIdx.x];
+    for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
+    const int m = threadIdx.x & 15;
+    const int nb = (threadIdx.x >> 4) * 4;
     if (m < M) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + t * 16 + nb + i;
+        const int64_t n = n0 + nb + i;
         if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, s[i], m, n));
       }
     }
@@ -235,12 +258,17 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
     load8_f32<f16>(static_cast<const f16*>(p) + k, f);
 }
 
+// LDS row stride of the staged activations: H plus 16 bytes, so the 16 rows an
+// MFMA B operand reads at one k land in different LDS banks.
+__host__ __device__ __forceinline__ int xs_stride(int H) { return H + 8; }
+
 // Stage round(hidden * rsqrt(mean(hidden^2) + eps) * norm_w) for all M rows in
-// LDS (xs, [M][H]). `scratch` needs kMaxWaves*16 + 16 floats.
+// LDS (xs, [M][xs_stride(H)]). `scratch` needs kMaxWaves*16 + 16 floats.
 template <typename T, int MMAX>
 __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hidden,
                                              const void* nwp, int nw_dtype, int M, int H,
                                              float eps) {
+  const int XS = xs_stride(H);
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -279,7 +307,7 @@ __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hid
         V8 o;
 #pragma unroll
         for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(h[i]) * s * wf[i]);
-        store8<T>(xs + (int64_t)m * H + k, o);
+        store8<T>(xs + (int64_t)m * XS + k, o);
       }
     }
   }
@@ -300,8 +328,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   typedef typename Vec8<T>::type V8;
   constexpr int V = pow2_ceil(2 * R * M);
   extern __shared__ __align__(16) unsigned char smem[];
+  const int XS = xs_stride(H);
   T* xs = reinterpret_cast<T*>(smem);
-  float* part = reinterpret_cast<float*>(smem + (size_t)M * H * sizeof(T));
+  float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
@@ -332,7 +361,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
       }
       V8 xv[M];
 #pragma unroll
-      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * H + k);
+      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -360,69 +389,108 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   }
 }
 
+// MFMA form of the gate/up launch for M >= 8 (M padded to 16): the RMSNorm of
+// hidden is written by a separate row kernel (into the caller's output buffer,
+// which the down projection overwrites last), and this kernel streams a tile of
+// 16 gate rows and the matching 16 up rows per workgroup with the row-contiguous
+// load + LDS relayout of gemv_mfma_relayout_kernel. B operand: the normalised
+// activations from global memory (L2-resident, [M, H]).
 template <typename T, int U, bool NTW>
-__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
-    T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int M, int H, int I,
-    float eps, int tiles) {
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel(
+    T* mid, const T* x, const T* wgu, int M, int H, int I) {
   typedef typename Vec8<T>::type V8;
-  extern __shared__ __align__(16) unsigned char smem[];
-  T* xs = reinterpret_cast<T*>(smem);
-  f32x4* part = reinterpret_cast<f32x4*>(smem + (size_t)M * H * sizeof(T));
+  __shared__ f32x4 part[kMaxWaves * kWave];
+  __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-
-  stage_normed<T, 16>(xs, reinterpret_cast<float*>(part), hidden, nwp, nw_dtype, M, H, eps);
-
+  const int64_t j0 = (int64_t)blockIdx.x * 16;
   const bool xok = r < M;
-  const T* xp = xs + (xok ? r : 0) * H + g * 8;
+  const T* xp = x + (xok ? r : 0) * (int64_t)H + g * 8;
+  const int lrow = lane >> 4, lchunk = lane & 15;
+  const T* gl[4];
+  const T* ul[4];
+  bool lok[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t j = j0 + 4 * i + lrow;
+    lok[i] = j < I;
+    gl[i] = wgu + (lok[i] ? j : 0) * H + lchunk * 8;
+    ul[i] = wgu + (I + (lok[i] ? j : 0)) * H + lchunk * 8;
+  }
+  u32x4* tile = tiles[wave];
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const int64_t j0 = (int64_t)tile * 16;
-    const bool wok = j0 + r < I;
-    const int64_t j = wok ? j0 + r : 0;
-    const T* gp = wgu + j * H + g * 8;
-    const T* up = wgu + (I + j) * H + g * 8;
-    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-    for (int u0 = wave; u0 < units; u0 += nw * U) {
-      V8 a[U * 4], c[U * 4], b[U * 4];
+  for (int u0 = wave; u0 < units; u0 += nw * U) {
+    u32x4 vg[U][4], vu[U][4];
 #pragma unroll
-      for (int jj = 0; jj < U; ++jj) {
-        const int u = u0 + jj * nw;
+    for (int jj = 0; jj < U; ++jj) {
+      const int u = u0 + jj * nw;
+      const bool in = u < units && u * kUnit + lchunk * 8 < H;
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int k = u * kUnit + s * 32;
-          const bool in = u < units && k + g * 8 < H;
-          a[jj * 4 + s] = (wok && in) ? load8w<NTW, T>(gp + k) : V8{};
-          c[jj * 4 + s] = (wok && in) ? load8w<NTW, T>(up + k) : V8{};
-          b[jj * 4 + s] = (xok && in) ? load8<T>(xp + k) : V8{};
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < U * 4; ++i) {
-        ag = mfma16(a[i], b[i], ag);
-        au = mfma16(c[i], b[i], au);
+      for (int i = 0; i < 4; ++i) {
+        const u32x4* qg = reinterpret_cast<const u32x4*>(gl[i] + u * kUnit);
+        const u32x4* qu = reinterpret_cast<const u32x4*>(ul[i] + u * kUnit);
+        const bool ok = lok[i] && in;
+        vg[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qg) : *qg) : u32x4{0, 0, 0, 0};
+        vu[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qu) : *qu) : u32x4{0, 0, 0, 0};
       }
     }
-    __syncthreads();  // previous tile's readers of `part` are done
-    part[wave * kWave + lane] = ag;
-    part[(kMaxWaves + wave) * kWave + lane] = au;
-    __syncthreads();
-    if (threadIdx.x < kWave) {
-      f32x4 sg = part[threadIdx.x], su = part[kMaxWaves * kWave + threadIdx.x];
-      for (int i = 1; i < nw; ++i) {
-        sg += part[i * kWave + threadIdx.x];
-        su += part[(kMaxWaves + i) * kWave + threadIdx.x];
-      }
-      const int m = threadIdx.x & 15;
-      const int nb = (threadIdx.x >> 4) * 4;
-      if (m < M) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int64_t jj = j0 + nb + i;
-          if (jj < I) mid[m * (int64_t)I + jj] = swiglu_out<T>(sg[i], su[i]);
-        }
+    for (int jj = 0; jj < U; ++jj) {
+      const int u = u0 + jj * nw;
+      V8 a[4], c[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tile[(4 * i + lrow) * 16 + (lchunk ^ (4 * i + lrow))] = vg[jj][i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) a[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int i = 0; i < 4; ++i) tile[(4 * i + lrow) * 16 + (lchunk ^ (4 * i + lrow))] = vu[jj][i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        c[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
+        const int k = u * kUnit + s2 * 32 + g * 8;
+        b[s2] = (xok && u < units && k < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        ag = mfma16(a[s2], b[s2], ag);
+        au = mfma16(c[s2], b[s2], au);
+      }
+    }
+  }
+  // two-phase reduction through one buffer: gate sums, then up sums
+  part[wave * kWave + lane] = ag;
+  __syncthreads();
+  f32x4 sg = {0.f, 0.f, 0.f, 0.f};
+  if (threadIdx.x < kWave)
+    for (int i = 0; i < nw; ++i) sg += part[i * kWave + threadIdx.x];
+  __syncthreads();
+  part[wave * kWave + lane] = au;
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    f32x4 su = part[threadIdx.x];
+    for (int i = 1; i < nw; ++i) su += part[i * kWave + threadIdx.x];
+    const int m = threadIdx.x & 15;
+    const int nb = (threadIdx.x >> 4) * 4;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t jj = j0 + nb + i;
+        if (jj < I) mid[m * (int64_t)I + jj] = swiglu_out<T>(sg[i], su[i]);
       }
     }
   }
@@ -434,11 +502,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_mfma_kernel(
 namespace {
 
 constexpr int kMfmaMinM = 8;   // kind=dot uses MFMA from this M on
-// Weight streams use nontemporal loads in the SIMT kernels (measured +10-20% at
-// M <= 4). The MFMA kernels read each 128-byte line in two 64-byte halves from
-// consecutive instructions and lose when the first half is not retained.
+// Weight streams use nontemporal loads (measured +10-20% over ordinary loads).
 constexpr bool kNtWeights = true;
-constexpr bool kNtWeightsMfma = false;
 constexpr size_t kMaxLds = 160 * 1024;
 
 // Waves per workgroup: enough to cover K with whole work items (512-element
@@ -475,18 +540,21 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
   }
 }
 
-constexpr int kMfmaU = 1;  // K units per MFMA iteration
-
 template <typename T>
 void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
   const int nw = pick_waves((K + kUnit - 1) / kUnit);
-  // One 16-row tile per workgroup: two tiles (shared x operand) measured slower
-  // at every decode shape, the grid is too small to fill 256 CUs.
   const unsigned blocks = (unsigned)((N + 15) / 16);
-  hipLaunchKernelGGL((gemv_mfma_kernel<T, 1, kMfmaU, kNtWeightsMfma>), dim3(blocks),
-                     dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x),
-                     static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
+  // Two K units per iteration, except on the tallest weights where one unit per
+  // iteration leaves more waves resident (measured at N = 28672).
+  if (N >= 16384)
+    hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, 1, true>), dim3(blocks), dim3(nw * kWave),
+                       0, st, static_cast<T*>(y), static_cast<const T*>(x),
+                       static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
+  else
+    hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, 2, true>), dim3(blocks), dim3(nw * kWave),
+                       0, st, static_cast<T*>(y), static_cast<const T*>(x),
+                       static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
 }
 
 // The dynamic-LDS limit of a kernel must be raised before a launch above 64 KiB.
@@ -528,7 +596,7 @@ int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype,
                     int H, int I, float eps, hipStream_t st) {
   constexpr int R = MlpRows<M>::R;
   constexpr int V = pow2_ceil(2 * R * M);
-  const size_t lds = (size_t)M * H * sizeof(T) +
+  const size_t lds = (size_t)M * xs_stride(H) * sizeof(T) +
                      sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
                                                                            : kNormScratch);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
@@ -559,18 +627,12 @@ int launch_mlp_simt_m(int M, void* mid, const void* hidden, const void* nw, int 
 }
 
 template <typename T>
-int launch_mlp_mfma(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
-                    const void* wgu, int H, int I, float eps, hipStream_t st) {
-  const size_t lds = (size_t)M * H * sizeof(T) + sizeof(f32x4) * 2 * kMaxWaves * kWave;
-  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  if (!allow_lds(mlp_gate_up_mfma_kernel<T, kMfmaU, kNtWeightsMfma>, lds))
-    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
-  const int tiles = (I + 15) / 16;
-  const int grid = fused_grid(tiles, lds, 1024);
+int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, int H, int I,
+                        hipStream_t st) {
   const int nwv = pick_waves((H + kUnit - 1) / kUnit);
-  hipLaunchKernelGGL((mlp_gate_up_mfma_kernel<T, kMfmaU, kNtWeightsMfma>), dim3(grid), dim3(nwv * kWave), lds, st,
-                     static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
-                     static_cast<const T*>(wgu), M, H, I, eps, tiles);
+  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, 1, true>), dim3((unsigned)((I + 15) / 16)),
+                     dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
+                     static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I);
   return FD_OK;
 }
 
@@ -668,21 +730,27 @@ int mlp_check(void* mid, const void* hidden, const void* norm_w, int norm_w_dtyp
   return FD_OK;
 }
 
-int mlp_gate_up(void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+// Whether the gate/up launch of this call needs the [M, H] `normed` buffer
+// (the MFMA form normalises in a separate row kernel).
+bool mlp_needs_normed(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
+
+int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
                 const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
                 int act_dtype, hipStream_t st) {
-  const bool mfma = kind == FD_KIND_DOT && M >= kMfmaMinM;
   int rc;
-  if (act_dtype == FD_F16)
-    rc = mfma ? launch_mlp_mfma<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
-                                     (int)I, eps, st)
-              : launch_mlp_simt_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
-                                       (int)H, (int)I, eps, st);
-  else
-    rc = mfma ? launch_mlp_mfma<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
+  if (mlp_needs_normed(M, kind)) {
+    rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    if (rc != FD_OK) return rc;
+    rc = act_dtype == FD_F16
+             ? launch_mlp_relayout<f16>((int)M, mid, normed, w_gate_up, (int)H, (int)I, st)
+             : launch_mlp_relayout<bf16>((int)M, mid, normed, w_gate_up, (int)H, (int)I, st);
+  } else {
+    rc = act_dtype == FD_F16
+             ? launch_mlp_simt_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
                                       (int)H, (int)I, eps, st)
-              : launch_mlp_simt_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
-                                        (int)H, (int)I, eps, st);
+             : launch_mlp_simt_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up,
+                                       (int)H, (int)I, eps, st);
+  }
   if (rc != FD_OK) return rc;
   return check_launch();
 }
@@ -690,13 +758,17 @@ int mlp_gate_up(void* mid, const void* hidden, const void* norm_w, int norm_w_dt
 }  // namespace
 }  // namespace fd
 
-extern "C" int fd_mlp_gate_up(void* mid, const void* hidden, const void* norm_w,
+extern "C" int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w,
                               int norm_w_dtype, const void* w_gate_up, int64_t M, int64_t H,
                               int64_t I, float eps, int kind, int act_dtype, void* stream) {
   int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
   if (rc != FD_OK || M == 0) return rc;
-  return mlp_gate_up(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype,
-                     static_cast<hipStream_t>(stream));
+  if (mlp_needs_normed(M, kind)) {
+    if (!normed) return set_error(FD_EINVAL, "kind=dot with M >= 8 needs the normed buffer");
+    if (!aligned16(normed)) return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  }
+  return mlp_gate_up(mid, normed, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind,
+                     act_dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
@@ -709,7 +781,10 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   if (!aligned16(y) || !aligned16(w_down))
     return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
-  rc = mlp_gate_up(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype, st);
+  // y doubles as the normed buffer of the MFMA form: the down projection, which
+  // writes y, runs after the gate/up launch has consumed it.
+  rc = mlp_gate_up(mid, y, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind,
+                   act_dtype, st);
   if (rc != FD_OK) return rc;
   Epi e;
   e.bias = nullptr;

@@ -16,6 +16,7 @@
 // Reduction: wave64 shuffles, then one LDS exchange across the workgroup's waves.
 #include "fd_device.h"
 #include "fd_host.h"
+#include "fd_internal.h"
 
 namespace fd {
 
@@ -310,6 +311,22 @@ int rms_common(bool add, void* y, void* ro, const void* x, const void* r, const 
 }
 
 }  // namespace
+
+int rms_rows(void* y, const void* x, const void* w, int w_dtype, int64_t rows, int64_t n,
+             float eps, int act_dtype, hipStream_t st) {
+  fd_rows l;
+  l.a = 1;
+  l.b = 1;
+  l.c = rows;
+  l.sa = 0;
+  l.sb = 0;
+  l.sc = n;
+  l.col = 1;
+  l.n = n;
+  return rms_common(false, y, nullptr, x, nullptr, w, w_dtype, 1, &l, nullptr, &l, nullptr, eps,
+                    act_dtype, st);
+}
+
 }  // namespace fd
 
 extern "C" int fd_rms_norm(void* y, const void* x, const void* w, int w_dtype, int64_t w_stride,

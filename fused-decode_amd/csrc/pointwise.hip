@@ -54,7 +54,10 @@ __global__ __launch_bounds__(kPwThreads) void swiglu_gen_kernel(T* y, const T* g
 //   y[j]     = x[j] * c[j]     - x[j+h] * s[j]
 //   y[j + h] = x[j+h] * c[j+h] + x[j] * s[j+h]
 
-template <typename T, typename C>
+// HPT rows per thread: when cos/sin do not vary along the innermost row dim
+// (stride 0 there, e.g. one table row shared by all heads of a token), a thread
+// handles HPT consecutive rows of that dim and loads its cos/sin vectors once.
+template <typename T, typename C, int HPT>
 __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, const C* cs,
                                                               const C* sn, RowGrid grid,
                                                               FastDiv vpr, RowStrides sx,
@@ -64,29 +67,36 @@ __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, 
   const uint32_t v = blockIdx.x * kPwThreads + threadIdx.x;
   if (v >= total) return;
   uint32_t jv;
-  const uint32_t row = vpr.divmod(v, jv);
+  const uint32_t grp = vpr.divmod(v, jv);
   const uint32_t j = jv * 8;
-  const RowPos p = row_pos(grid, row);
-  const T* xr = x + row_off(sx, p);
+  const RowPos p = row_pos(grid, grp * HPT);
   const C* cr = cs + row_off(sc, p);
   const C* sr = sn + row_off(ss, p);
-  typename Vec8<T>::type x1 = load8<T>(xr + j);
-  typename Vec8<T>::type x2 = load8<T>(xr + j + h);
   float c1[8], c2[8], s1[8], s2[8];
   load8_f32<C>(cr + j, c1);
   load8_f32<C>(cr + j + h, c2);
   load8_f32<C>(sr + j, s1);
   load8_f32<C>(sr + j + h, s2);
-  typename Vec8<T>::type o1, o2;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float a = to_f32(x1[i]), b = to_f32(x2[i]);
-    o1[i] = from_f32<T>(a * c1[i] - b * s1[i]);
-    o2[i] = from_f32<T>(b * c2[i] + a * s2[i]);
-  }
+  const T* xr = x + row_off(sx, p);
   T* yr = y + row_off(sy, p);
-  store8<T>(yr + j, o1);
-  store8<T>(yr + j + h, o2);
+  typename Vec8<T>::type x1[HPT], x2[HPT];
+#pragma unroll
+  for (int t = 0; t < HPT; ++t) {
+    x1[t] = load8<T>(xr + t * sx.sc + j);
+    x2[t] = load8<T>(xr + t * sx.sc + j + h);
+  }
+#pragma unroll
+  for (int t = 0; t < HPT; ++t) {
+    typename Vec8<T>::type o1, o2;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float a = to_f32(x1[t][i]), b = to_f32(x2[t][i]);
+      o1[i] = from_f32<T>(a * c1[i] - b * s1[i]);
+      o2[i] = from_f32<T>(b * c2[i] + a * s2[i]);
+    }
+    store8<T>(yr + t * sy.sc + j, o1);
+    store8<T>(yr + t * sy.sc + j + h, o2);
+  }
 }
 
 template <typename T>
@@ -195,13 +205,23 @@ extern "C" int fd_rope(void* y, const void* x, const void* cos, const void* sin,
   const bool vec = rope_rows_vec(x, *lx, 2) && rope_rows_vec(y, *ly, 2) &&
                    rope_rows_vec(cos, *lc, cse) && rope_rows_vec(sin, *ls, cse);
   if (vec) {
-    const uint32_t tv = (uint32_t)(total / 8);
+    // rows sharing cos/sin along the innermost row dim are handled 4 per thread
+    const int hpt = (lc->sc == 0 && ls->sc == 0 && lx->c % 4 == 0) ? 4 : 1;
+    const uint32_t tv = (uint32_t)(total / 8 / hpt);
     const FastDiv vpr((uint32_t)(h / 8));
-#define FD_ROPE_VEC(T, C)                                                                     \
-  hipLaunchKernelGGL((rope_vec_kernel<T, C>), dim3(blocks_for(tv)), dim3(kPwThreads), 0, st,  \
-                     (T*)y, (const T*)x, (const C*)cos, (const C*)sin, grid, vpr,             \
-                     row_strides(*lx), row_strides(*lc), row_strides(*ls), row_strides(*ly),  \
-                     (uint32_t)h, tv)
+#define FD_ROPE_VEC(T, C)                                                                       \
+  do {                                                                                          \
+  if (hpt == 4)                                                                                 \
+    hipLaunchKernelGGL((rope_vec_kernel<T, C, 4>), dim3(blocks_for(tv)), dim3(kPwThreads), 0,   \
+                       st, (T*)y, (const T*)x, (const C*)cos, (const C*)sin, grid, vpr,         \
+                       row_strides(*lx), row_strides(*lc), row_strides(*ls), row_strides(*ly),  \
+                       (uint32_t)h, tv);                                                        \
+  else                                                                                          \
+    hipLaunchKernelGGL((rope_vec_kernel<T, C, 1>), dim3(blocks_for(tv)), dim3(kPwThreads), 0,   \
+                       st, (T*)y, (const T*)x, (const C*)cos, (const C*)sin, grid, vpr,         \
+                       row_strides(*lx), row_strides(*lc), row_strides(*ls), row_strides(*ly),  \
+                       (uint32_t)h, tv);                                                        \
+  } while (0)
     if (act_dtype == FD_F16) {
       if (cs_dtype == FD_F32) FD_ROPE_VEC(f16, float);
       else if (cs_dtype == FD_BF16) FD_ROPE_VEC(f16, bf16);

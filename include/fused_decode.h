@@ -124,7 +124,8 @@ int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_
  *   mid = round(silu(g) * u)                      (written to `mid`, [M,I])
  *   y   = round(mid @ w_down.T + hidden)
  * w_gate_up is [2I,H] (gate rows above up rows), w_down is [H,I], both contiguous.
- * `mid` is caller-owned scratch of M*I activation elements. Two launches.
+ * `mid` is caller-owned scratch of M*I activation elements. Two launches (three for
+ * kind FD_KIND_DOT at M >= 8, whose RMSNorm runs as its own row kernel into y).
  * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
  * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
  */
@@ -134,15 +135,18 @@ int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
                      void* stream);
 
 /*
- * Launch 1 of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u)) with
- * g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
- * rules as fd_post_attn_mlp. For callers that run their own down projection, and
- * for timing the dominant kernel of the block on its own.
+ * The gate/up half of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u))
+ * with g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
+ * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 8 the RMSNorm is
+ * written to `normed` ([M,H] activation scratch, 16-byte aligned) by a row kernel
+ * before the MFMA gate/up kernel reads it; otherwise `normed` is unused (may be
+ * NULL) and a single kernel normalises in its prologue. For callers that run their
+ * own down projection, and for timing the dominant kernel of the block on its own.
  * Replaces ops.py:312-314 (rms_norm, the gate/up linear_decode and swiglu).
  */
-int fd_mlp_gate_up(void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
-                   const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps,
-                   int kind, int act_dtype, void* stream);
+int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w,
+                   int norm_w_dtype, const void* w_gate_up, int64_t M, int64_t H, int64_t I,
+                   float eps, int kind, int act_dtype, void* stream);
 
 /*
  * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned

@@ -490,3 +490,30 @@ def test_decode_step_llama3_8b_two_layers_finite():
     assert torch.isfinite(a.float()).all()
     torch.testing.assert_close(a, b, rtol=0, atol=0)
     assert ds.weight_bytes == 2 * 436_207_616 + 2 * 2 * 4096 * 2
+
+
+@pytest.mark.parametrize("m,kind", [(1, "simt"), (3, "dot"), (8, "dot"), (16, "dot"), (8, "simt")])
+def test_mlp_gate_up_entry_point(m, kind):
+    """fd_mlp_gate_up through the C ABI: mid = round(silu(g) * u) of the normed input."""
+    from fused_decode import _lib as L
+
+    h, i = 512, 768
+    g = torch.Generator().manual_seed(300 + m)
+    hidden = randn(m, h, gen=g)
+    norm_w = randn(h, gen=g, scale=0.1, mean=1.0)
+    w_gu = randn(2 * i, h, gen=g, scale=h ** -0.5)
+    hn = O.rms_norm(npf(hidden), npf(norm_w), 1e-5, "f16")
+    gu = O.linear(hn, npf(w_gu), dtype="f16")
+    ref = O.swiglu(gu[:, :i], gu[:, i:], "f16")
+    hd, nwd, wgd = hidden.to(DEV), norm_w.to(DEV), w_gu.to(DEV)
+    mid = torch.empty(m, i, device=DEV, dtype=torch.float16)
+    normed = torch.empty(m, h, device=DEV, dtype=torch.float16)
+    st = torch.cuda.current_stream().cuda_stream
+    L.check("fd_mlp_gate_up", L.lib().fd_mlp_gate_up(
+        mid.data_ptr(), normed.data_ptr(), hd.data_ptr(), nwd.data_ptr(), L.FD_F16, wgd.data_ptr(),
+        m, h, i, 1e-5, L.KIND_CODE[kind], L.FD_F16, st))
+    check(mid, ref, torch.float16, "linear")
+    if kind == "dot" and m >= 8:
+        check(normed, hn, torch.float16)  # the row kernel's output is the staged input
+        assert L.lib().fd_mlp_gate_up(mid.data_ptr(), None, hd.data_ptr(), nwd.data_ptr(), L.FD_F16,
+                                      wgd.data_ptr(), m, h, i, 1e-5, L.FD_KIND_DOT, L.FD_F16, st) == L.FD_EINVAL
