@@ -63,6 +63,11 @@ __device__ __forceinline__ typename Vec8<T>::type load8w(const T* p) {
   else
     return load8<T>(p);
 }
+// 16-byte store that does not retain the line (for outputs written once).
+template <typename T>
+__device__ __forceinline__ void store8_nt(T* p, typename Vec8<T>::type v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(p));
+}
 template <typename T>
 __device__ __forceinline__ void store8(T* p, typename Vec8<T>::type v) {
   *reinterpret_cast<typename Vec8<T>::type*>(p) = v;
@@ -85,6 +90,22 @@ __device__ __forceinline__ void load8_f32<float>(const float* p, float (&f)[8]) 
     f[i + 4] = b[i];
   }
 }
+
+// 8 consecutive values of any of the three dtypes kept in their storage form
+// (4 VGPRs for fp16/bf16, 8 for fp32) and widened one element at a time.
+template <typename W> struct Raw8 {
+  typename Vec8<W>::type v;
+  __device__ __forceinline__ void load(const W* p) { v = load8<W>(p); }
+  __device__ __forceinline__ float operator[](int i) const { return to_f32(v[i]); }
+};
+template <> struct Raw8<float> {
+  f32x4 lo, hi;
+  __device__ __forceinline__ void load(const float* p) {
+    lo = *reinterpret_cast<const f32x4*>(p);
+    hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ float operator[](int i) const { return i < 4 ? lo[i] : hi[i - 4]; }
+};
 
 // Scalar load of element `i` of a buffer whose dtype is known only at run time.
 __device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {

@@ -108,6 +108,7 @@ __global__ __launch_bounds__(256) void rms_wave_kernel(T* y, T* ro, const T* x, 
   const T* xr = x + row_off(lx, p);
   const T* rr = ADD ? r + row_off(lr, p) : nullptr;
   V8 a[VPL], b[VPL];
+  Raw8<W> wv[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
@@ -116,15 +117,26 @@ __global__ __launch_bounds__(256) void rms_wave_kernel(T* y, T* ro, const T* x, 
       if (ADD) b[j] = load8_nt<T>(rr + k);
     }
   }
-  float v[VPL][8];
+  // the weight (L2-resident, shared by every row) is fetched before the
+  // reduction so its latency overlaps the activation loads
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int k = (j * kWave + lane) * 8;
+    if (k < n) wv[j].load(w + k);
+  }
+  // rms: the row stays packed and is widened again in the output pass;
+  // add_rms: the float32 sums are kept (recomputing them costs more registers)
+  float v[ADD ? VPL : 1][8];
+  auto val = [&](int j, int i) { return ADD ? v[ADD ? j : 0][i] : to_f32(a[j][i]); };
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      v[j][i] = k < n ? (ADD ? to_f32(a[j][i]) + to_f32(b[j][i]) : to_f32(a[j][i])) : 0.f;
-      ss += v[j][i] * v[j][i];
+      if constexpr (ADD) v[j][i] = k < n ? to_f32(a[j][i]) + to_f32(b[j][i]) : 0.f;
+      const float t = k < n ? val(j, i) : 0.f;
+      ss += t * t;
     }
   }
   ss = wave_sum(ss);
@@ -135,17 +147,15 @@ __global__ __launch_bounds__(256) void rms_wave_kernel(T* y, T* ro, const T* x, 
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
     if (k < n) {
-      float wf[8];
-      load8_f32<W>(w + k, wf);
       V8 o;
       if (ADD) {
         V8 s;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] = from_f32<T>(v[j][i]);
+        for (int i = 0; i < 8; ++i) s[i] = from_f32<T>(val(j, i));
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s), reinterpret_cast<u32x4*>(ror + k));
       }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(v[j][i] * inv * wf[i]);
+      for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(val(j, i) * inv * wv[j][i]);
       __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(yr + k));
     }
   }

@@ -2,8 +2,9 @@
 //
 // Both run on the row grid of fd_rows (up to three leading dims with arbitrary
 // strides, including 0 for broadcast operands). The vector kernels move one
-// 16-byte vector per operand per thread; the generic kernels take any column
-// stride and any row length.
+// 16-byte vector per operand per thread, with nontemporal loads and stores for
+// the activations (each byte is touched once); the generic kernels take any
+// column stride and any row length.
 #include "fd_device.h"
 #include "fd_host.h"
 
@@ -26,12 +27,12 @@ __global__ __launch_bounds__(kPwThreads) void swiglu_vec_kernel(T* y, const T* g
   const uint32_t row = vpr.divmod(v, cv);
   const uint32_t k = cv * 8;
   const RowPos p = row_pos(grid, row);
-  typename Vec8<T>::type a = load8<T>(g + row_off(sg, p) + k);
-  typename Vec8<T>::type b = load8<T>(u + row_off(su, p) + k);
+  typename Vec8<T>::type a = load8_nt<T>(g + row_off(sg, p) + k);
+  typename Vec8<T>::type b = load8_nt<T>(u + row_off(su, p) + k);
   typename Vec8<T>::type o;
 #pragma unroll
   for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(silu_stable(to_f32(a[i])) * to_f32(b[i]));
-  store8<T>(y + row_off(sy, p) + k, o);
+  store8_nt<T>(y + row_off(sy, p) + k, o);
 }
 
 template <typename T>
@@ -82,8 +83,8 @@ __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, 
   typename Vec8<T>::type x1[HPT], x2[HPT];
 #pragma unroll
   for (int t = 0; t < HPT; ++t) {
-    x1[t] = load8<T>(xr + t * sx.sc + j);
-    x2[t] = load8<T>(xr + t * sx.sc + j + h);
+    x1[t] = load8_nt<T>(xr + t * sx.sc + j);
+    x2[t] = load8_nt<T>(xr + t * sx.sc + j + h);
   }
 #pragma unroll
   for (int t = 0; t < HPT; ++t) {
@@ -94,8 +95,8 @@ __global__ __launch_bounds__(kPwThreads) void rope_vec_kernel(T* y, const T* x, 
       o1[i] = from_f32<T>(a * c1[i] - b * s1[i]);
       o2[i] = from_f32<T>(b * c2[i] + a * s2[i]);
     }
-    store8<T>(yr + t * sy.sc + j, o1);
-    store8<T>(yr + t * sy.sc + j + h, o2);
+    store8_nt<T>(yr + t * sy.sc + j, o1);
+    store8_nt<T>(yr + t * sy.sc + j + h, o2);
   }
 }
 
