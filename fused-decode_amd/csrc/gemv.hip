@@ -321,6 +321,26 @@ __device__ __forceinline__ T swiglu_out(float g, float u) {
 
 constexpr int kNormScratch = kMaxWaves * 16 + 16;
 
+// Weight loads of one K step of tile `tile` (R gate rows and the matching R up
+// rows); rows past I, steps past H and tiles past the last are zero registers.
+template <typename T, int R, bool NTW>
+__device__ __forceinline__ void load_gate_up(typename Vec8<T>::type (&g)[R],
+                                             typename Vec8<T>::type (&u)[R], const T* wgu,
+                                             int tile, int tiles, int k, int H, int I) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t j = (int64_t)tile * R + r;
+    const bool ok = tile < tiles && j < I && k < H;
+    g[r] = ok ? load8w<NTW, T>(wgu + j * H + k) : typename Vec8<T>::type{};
+    u[r] = ok ? load8w<NTW, T>(wgu + (I + j) * H + k) : typename Vec8<T>::type{};
+  }
+}
+
+// SIMT gate/up for M < 8. The weight stream is software-pipelined one K step
+// deep: the loads of the next step (which may belong to the workgroup's next
+// tile) are issued before the math of the current one, and the first step is
+// issued before the RMSNorm prologue, so HBM requests stay in flight across the
+// prologue, the cross-wave reduction and the SwiGLU epilogue.
 template <typename T, int M, int R, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int H, int I,
@@ -334,7 +354,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
+  const int step = nw * kChunk;
+  const int steps = (H + step - 1) / step;  // the same for every wave
+  const int kbase = (wave * kWave + lane) * 8;
 
+  V8 gv[R], uv[R];
+  load_gate_up<T, R, NTW>(gv, uv, wgu, blockIdx.x, tiles, kbase, H, I);
   stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
@@ -342,33 +367,29 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    const T* wg[R];
-    const T* wu[R];
-    bool rok[R];
+    for (int it = 0; it < steps; ++it) {
+      const bool last = it + 1 == steps;
+      V8 gn[R], un[R];
+      load_gate_up<T, R, NTW>(gn, un, wgu, last ? tile + (int)gridDim.x : tile, tiles,
+                              kbase + (last ? 0 : (it + 1) * step), H, I);
+      const int k = kbase + it * step;
+      if (k < H) {
+        V8 xv[M];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      rok[r] = j0 + r < I;
-      const int64_t j = rok[r] ? j0 + r : 0;
-      wg[r] = wgu + j * H;
-      wu[r] = wgu + (I + j) * H;
-    }
-    for (int k = (wave * kWave + lane) * 8; k < H; k += nw * kChunk) {
-      V8 gv[R], uv[R];
+        for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            acc[r * M + m] = dot8(gv[r], xv[m], acc[r * M + m]);
+            acc[R * M + r * M + m] = dot8(uv[r], xv[m], acc[R * M + r * M + m]);
+          }
+      }
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        gv[r] = rok[r] ? load8w<NTW, T>(wg[r] + k) : V8{};
-        uv[r] = rok[r] ? load8w<NTW, T>(wu[r] + k) : V8{};
+        gv[r] = gn[r];
+        uv[r] = un[r];
       }
-      V8 xv[M];
-#pragma unroll
-      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < M; ++m) {
-          acc[r * M + m] = dot8(gv[r], xv[m], acc[r * M + m]);
-          acc[R * M + r * M + m] = dot8(uv[r], xv[m], acc[R * M + r * M + m]);
-        }
     }
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
@@ -583,10 +604,11 @@ int device_cus() {
 
 // Workgroups of the fused kernel: each stages the normalised activations in LDS
 // once and then loops over weight tiles, so the grid is what can be resident at
-// once (LDS-limited at larger M); more would restage x for nothing.
-int fused_grid(int tiles, size_t lds, int cap_small) {
-  const int per_cu = (int)(kMaxLds / (lds ? lds : 1));
-  const int cap = lds <= 16 * 1024 ? cap_small : device_cus() * (per_cu < 1 ? 1 : per_cu > 8 ? 8 : per_cu);
+// once, at most `per_cu` per CU and fewer when the LDS stage is large; more would
+// restage x for nothing (measured at H=4096: two 8-wave workgroups per CU).
+int fused_grid(int tiles, size_t lds, int per_cu) {
+  const int fit = (int)(kMaxLds / (lds ? lds : 1));
+  const int cap = device_cus() * (fit < 1 ? 1 : fit < per_cu ? fit : per_cu);
   const int per = (tiles + cap - 1) / cap;
   return (tiles + per - 1) / per;
 }
@@ -603,9 +625,11 @@ int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype,
   if (!allow_lds(mlp_gate_up_simt_kernel<T, M, R, kNtWeights>, lds))
     return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   const int tiles = (I + R - 1) / R;
-  const int grid = fused_grid(tiles, lds, 2048);
-  // Four waves: each covers two 512-element K chunks per row at H=4096.
-  const int nwv = pick_waves((H + kChunk - 1) / kChunk) > 4 ? 4 : pick_waves((H + kChunk - 1) / kChunk);
+  const int grid = fused_grid(tiles, lds, 2);
+  // Eight waves (one 512-element K chunk per row each at H=4096) while the
+  // accumulators are small; four above M=4, where R*M sums per lane cost VGPRs.
+  const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
+  const int nwv = M > 4 && nwv0 > 4 ? 4 : nwv0;
   hipLaunchKernelGGL((mlp_gate_up_simt_kernel<T, M, R, kNtWeights>), dim3(grid), dim3(nwv * kWave), lds, st,
                      static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
                      static_cast<const T*>(wgu), H, I, eps, tiles);
