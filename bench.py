@@ -13,7 +13,8 @@ bench.py:42-56: back-to-back calls between events); W untimed warmup steps,
 then exactly K timed steps between HIP events, bracketed by synchronisation.
 `value` is microseconds per step at M=1 (lower is better). The same steps
 replayed one HIP graph per call (`graph_us`) and the 32-layer decode step
-minus attention, graph-captured (`decode_step`), are reported beside it.
+minus attention, graph-captured (`decode_step`: the fused form with
+pre_attn_qkv, and the reference's operators composed), are reported beside it.
 
 roofline: the dominant kernel, the fused RMSNorm + gate/up GEMV + SwiGLU
 launch, timed alone with HIP events on the stream it is launched on;
@@ -277,13 +278,18 @@ def main() -> None:
 
         line["decode_step"] = {}
         for m in (1, 8):
-            ds = DecodeStep(m=m, layers=32, dtype=dtype)
-            g_us = time_step(ds, 10, 2, graph=True)
-            line["decode_step"][f"m{m}_us"] = round(g_us, 1)
-            line["decode_step"][f"m{m}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
-            del ds
-            torch.cuda.empty_cache()
-        line["decode_step"]["workload"] = "32-layer Llama-3-8B decode step minus attention, hipGraph"
+            for fused in (True, False):
+                ds = DecodeStep(m=m, layers=32, dtype=dtype, fused=fused)
+                g_us = time_step(ds, 10, 2, graph=True)
+                key = f"m{m}" if fused else f"m{m}_unfused"
+                line["decode_step"][f"{key}_us"] = round(g_us, 1)
+                line["decode_step"][f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
+                line["decode_step"][f"{key}_launches_per_layer"] = ds.launches_per_layer
+                del ds
+                torch.cuda.empty_cache()
+        line["decode_step"]["workload"] = (
+            "32-layer Llama-3-8B decode step minus attention, hipGraph; fused = pre_attn_qkv + "
+            "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -55,6 +55,57 @@ __device__ __forceinline__ float epilogue(const Epi& e, float acc, int64_t m, in
   return acc;
 }
 
+// RoPE in the epilogue of a QKV projection (rotate-half, as the standalone
+// rope op): output columns below `cols` form heads of `dim` columns; column d of
+// a head pairs with d + dim/2. cos/sin row m sits at m * rs (rs = 0: one row for
+// every m), in `dtype`. `tiles` tiles of S rows cover the rotated columns.
+struct Rope {
+  const void* cos;
+  const void* sin;
+  int dtype;
+  int64_t rs;
+  int cols;
+  int dim;
+  int tiles;
+};
+
+// Row placement of a tile of S weight rows. A rotated tile holds S/2 adjacent
+// pairs of one head, slot s < S/2 at column q + s and slot s + S/2 at its
+// partner q + s + dim/2, so both halves of every pair end in one workgroup
+// (needs dim/2 % (S/2) == 0). Tiles past the rotated ones hold S consecutive rows.
+template <int S>
+struct TileRows {
+  int64_t base;  // first row of the head (rotated) or of the tile
+  int q;         // head column of slot 0 (rotated tiles)
+  int hh;        // dim/2, 0 for unrotated tiles
+  __device__ __forceinline__ TileRows(const Rope& rp, int tile) {
+    if (tile < rp.tiles) {
+      hh = rp.dim >> 1;
+      const int pp = tile * (S / 2);
+      const int b = pp / hh;
+      q = pp - b * hh;
+      base = (int64_t)b * rp.dim;
+    } else {
+      hh = 0;
+      q = 0;
+      base = (int64_t)rp.cols + (int64_t)(tile - rp.tiles) * S;
+    }
+  }
+  __device__ __forceinline__ bool rotated() const { return hh != 0; }
+  // head column of slot s (rotated tiles)
+  __device__ __forceinline__ int col(int s) const { return q + s % (S / 2) + (s / (S / 2)) * hh; }
+  __device__ __forceinline__ int64_t row(int s) const { return rotated() ? base + col(s) : base + s; }
+};
+
+// Rotate one pair in float32 from the rounded projection outputs x1 (first
+// half, head column d) and x2 (second half, column d + dim/2), as the rope op.
+__device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, float x1, float x2,
+                                          float& o1, float& o2) {
+  const int64_t c = m * rp.rs + d, h = rp.dim >> 1;
+  o1 = x1 * load_any(rp.cos, rp.dtype, c) - x2 * load_any(rp.sin, rp.dtype, c);
+  o2 = x2 * load_any(rp.cos, rp.dtype, c + h) + x1 * load_any(rp.sin, rp.dtype, c + h);
+}
+
 // Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
 // are R*M floats).
 template <int M> struct SimtRows { static constexpr int R = 4; };
@@ -125,10 +176,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 // l%16), stores it to a wave-private 4 KiB LDS buffer with the 16-byte chunk
 // index XOR-swizzled by the row (conflict-free on both sides), and reads it back
 // in MFMA layout. Waves split K in 128-element units, U units per iteration.
-template <typename T, int U, bool NTW>
+//
+// With ROPE the tile rows follow TileRows<16> and the epilogue rotates the
+// rounded outputs of rotated tiles: lanes 0-31 hold slots 0-7 and lanes 32-63
+// their partners 8-15 (same m), one lane-xor-32 exchange apart.
+template <typename T, int U, bool NTW, bool ROPE>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
     T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
-    int64_t syn, Epi e) {
+    int64_t syn, Epi e, Rope rp) {
   typedef typename Vec8<T>::type V8;
   __shared__ f32x4 part[kMaxWaves * kWave];
   __shared__ u32x4 tiles[kMaxWaves][256];
@@ -143,9 +198,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   const int lrow = lane >> 4, lchunk = lane & 15;
   const T* wl[4];
   bool lok[4];
+  const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t n = n0 + 4 * i + lrow;
+    const int64_t n = ROPE ? tr.row(4 * i + lrow) : n0 + 4 * i + lrow;
     lok[i] = n < N;
     wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 8;
   }
@@ -199,10 +255,27 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
     for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
     const int m = threadIdx.x & 15;
     const int nb = (threadIdx.x >> 4) * 4;
-    if (m < M) {
+    if (ROPE && tr.rotated()) {
+      float v[4], pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + nb + i;
+        v[i] = m < M ? round_as<T>(epilogue(e, s[i], m, tr.row(nb + i))) : 0.f;
+        pv[i] = __shfl_xor(v[i], 32, kWave);
+      }
+      if (m < M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool first = nb < 8;
+          float o1, o2;
+          rope_pair(rp, m, tr.col(first ? nb + i : nb + i - 8), first ? v[i] : pv[i],
+                    first ? pv[i] : v[i], o1, o2);
+          y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(first ? o1 : o2);
+        }
+      }
+    } else if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
         if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, s[i], m, n));
       }
     }
@@ -410,6 +483,102 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   }
 }
 
+// Pre-attention QKV for M < 8 (and kind=simt): the RMSNorm prologue of the
+// fused gate/up kernel, a pipelined stream of 4 weight rows per tile placed by
+// TileRows<4> (two rotate-half pairs per rotated tile), and an epilogue that
+// adds the bias, rounds, and rotates the rotated tiles' pairs.
+template <typename T, int R, bool NTW>
+__device__ __forceinline__ void load_tile_rows(typename Vec8<T>::type (&v)[R], const T* w,
+                                               const Rope& rp, int tile, int tiles, int k, int H,
+                                               int N) {
+  const TileRows<R> tr(rp, tile < tiles ? tile : 0);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = tr.row(r);
+    const bool ok = tile < tiles && n < N && k < H;
+    v[r] = ok ? load8w<NTW, T>(w + n * H + k) : typename Vec8<T>::type{};
+  }
+}
+
+template <typename T, int M, bool NTW>
+__global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
+    T* y, const T* hidden, const void* nwp, int nw_dtype, const T* w, int H, int N, float eps,
+    int tiles, Epi e, Rope rp) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int R = 4;
+  constexpr int V = pow2_ceil(R * M);
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int XS = xs_stride(H);
+  T* xs = reinterpret_cast<T*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int step = nw * kChunk;
+  const int steps = (H + step - 1) / step;
+  const int kbase = (wave * kWave + lane) * 8;
+
+  V8 wv[R];
+  load_tile_rows<T, R, NTW>(wv, w, rp, blockIdx.x, tiles, kbase, H, N);
+  stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int it = 0; it < steps; ++it) {
+      const bool last = it + 1 == steps;
+      V8 wn[R];
+      load_tile_rows<T, R, NTW>(wn, w, rp, last ? tile + (int)gridDim.x : tile, tiles,
+                                kbase + (last ? 0 : (it + 1) * step), H, N);
+      const int k = kbase + it * step;
+      if (k < H) {
+        V8 xv[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(wv[r], xv[m], acc[r * M + m]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[r] = wn[r];
+    }
+    butterfly_sum<V>(acc, lane);
+    __syncthreads();  // previous tile's readers of `part` are done
+    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    __syncthreads();
+    const TileRows<R> tr(rp, tile);
+    if (tr.rotated()) {
+      // thread (p, m): pair p of the tile, slots p and p + 2
+      for (int t = threadIdx.x; t < 2 * M; t += blockDim.x) {
+        const int p = t / M, m = t % M;
+        float s1 = 0.f, s2 = 0.f;
+        for (int i = 0; i < nw; ++i) {
+          s1 += part[i * V + p * M + m];
+          s2 += part[i * V + (p + 2) * M + m];
+        }
+        const int64_t n1 = tr.row(p), n2 = tr.row(p + 2);
+        float o1, o2;
+        rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, s1, m, n1)),
+                  round_as<T>(epilogue(e, s2, m, n2)), o1, o2);
+        y[m * (int64_t)N + n1] = from_f32<T>(o1);
+        y[m * (int64_t)N + n2] = from_f32<T>(o2);
+      }
+    } else {
+      for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+        const int r = t / M, m = t % M;
+        const int64_t n = tr.row(r);
+        if (n < N) {
+          float s = 0.f;
+          for (int i = 0; i < nw; ++i) s += part[i * V + t];
+          y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, s, m, n));
+        }
+      }
+    }
+  }
+}
+
 // MFMA form of the gate/up launch for M >= 8 (M padded to 16): the RMSNorm of
 // hidden is written by a separate row kernel (into the caller's output buffer,
 // which the down projection overwrites last), and this kernel streams a tile of
@@ -563,19 +732,25 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
 
 template <typename T>
 void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
-                 int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+                 int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
+                 const Rope* rp = nullptr) {
   const int nw = pick_waves((K + kUnit - 1) / kUnit);
-  const unsigned blocks = (unsigned)((N + 15) / 16);
+  Rope none{};
+  const unsigned blocks =
+      rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
+  const Rope& r = rp ? *rp : none;
   // Two K units per iteration, except on the tallest weights where one unit per
   // iteration leaves more waves resident (measured at N = 28672).
-  if (N >= 16384)
-    hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, 1, true>), dim3(blocks), dim3(nw * kWave),
-                       0, st, static_cast<T*>(y), static_cast<const T*>(x),
-                       static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
-  else
-    hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, 2, true>), dim3(blocks), dim3(nw * kWave),
-                       0, st, static_cast<T*>(y), static_cast<const T*>(x),
-                       static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e);
+#define FD_MFMA(UU, RR)                                                                    \
+  hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, UU, true, RR>), dim3(blocks),          \
+                     dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), \
+                     static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e, r)
+  if (rp) {
+    if (N >= 16384) FD_MFMA(1, true); else FD_MFMA(2, true);
+  } else {
+    if (N >= 16384) FD_MFMA(1, false); else FD_MFMA(2, false);
+  }
+#undef FD_MFMA
 }
 
 // The dynamic-LDS limit of a kernel must be raised before a launch above 64 KiB.
@@ -642,6 +817,41 @@ int launch_mlp_simt_m(int M, void* mid, const void* hidden, const void* nw, int 
   switch (M) {
 #define FD_CASE(MM) \
   case MM: return launch_mlp_simt<T, MM>(mid, hidden, nw, nw_dtype, wgu, H, I, eps, st);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+    FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
+    FD_CASE(16)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "M must be in [1, 16]");
+  }
+}
+
+template <typename T, int M>
+int launch_qkv_simt(void* y, const void* hidden, const void* nw, int nw_dtype, const void* w,
+                    int H, int N, float eps, const Epi& e, const Rope& rp, hipStream_t st) {
+  constexpr int V = pow2_ceil(4 * M);
+  const size_t lds = (size_t)M * xs_stride(H) * sizeof(T) +
+                     sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
+                                                                           : kNormScratch);
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  if (!allow_lds(qkv_simt_kernel<T, M, kNtWeights>, lds))
+    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
+  const int grid = fused_grid(tiles, lds, 2);
+  const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
+  const int nwv = M > 4 && nwv0 > 4 ? 4 : nwv0;
+  hipLaunchKernelGGL((qkv_simt_kernel<T, M, kNtWeights>), dim3(grid), dim3(nwv * kWave), lds, st,
+                     static_cast<T*>(y), static_cast<const T*>(hidden), nw, nw_dtype,
+                     static_cast<const T*>(w), H, N, eps, tiles, e, rp);
+  return FD_OK;
+}
+
+template <typename T>
+int launch_qkv_simt_m(int M, void* y, const void* hidden, const void* nw, int nw_dtype,
+                      const void* w, int H, int N, float eps, const Epi& e, const Rope& rp,
+                      hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return launch_qkv_simt<T, MM>(y, hidden, nw, nw_dtype, w, H, N, eps, e, rp, st);
     FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
     FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
     FD_CASE(16)
@@ -820,5 +1030,76 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   e.srn = 1;
   rc = linear_dispatch(y, mid, w_down, e, M, H, I, I, 1, I, 1, H, 1, kind, act_dtype, st);
   if (rc != FD_OK) return rc;
+  return check_launch();
+}
+
+extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_w,
+                               int norm_w_dtype, const void* w_qkv, const void* bias,
+                               int bias_dtype, const void* cos, const void* sin, int cs_dtype,
+                               int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
+                               int64_t rope_cols, int64_t head_dim, float eps, int kind,
+                               int act_dtype, void* stream) {
+  using namespace fd;
+  if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
+    return FD_EINVAL;
+  if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
+    return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
+  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
+  if (H <= 0 || N <= 0) return set_error(FD_EINVAL, "H and N must be positive");
+  if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
+  if (rope_cols < 0 || rope_cols > N) return set_error(FD_EINVAL, "rope_cols must be in [0, N]");
+  if (rope_cols > 0) {
+    if (head_dim <= 0 || head_dim % 2 != 0) return set_error(FD_EINVAL, "head_dim must be even");
+    if (rope_cols % head_dim != 0)
+      return set_error(FD_EINVAL, "rope_cols must be a multiple of head_dim");
+    if (!check_any_dtype(cs_dtype, "cs_dtype")) return FD_EINVAL;
+    if (cs_row_stride < 0) return set_error(FD_EINVAL, "cs_row_stride must be >= 0");
+    if (head_dim % 16 != 0 || head_dim > 0x7fffffffLL)
+      return set_error(FD_EUNSUPPORTED, "head_dim must be a multiple of 16");
+  }
+  if (bias && !check_any_dtype(bias_dtype, "bias_dtype")) return FD_EINVAL;
+  if (M == 0) return FD_OK;
+  if (!y || !hidden || !norm_w || !w_qkv || (rope_cols > 0 && (!cos || !sin)))
+    return set_error(FD_EINVAL, "null pointer argument");
+  if (H % 8 != 0) return set_error(FD_EUNSUPPORTED, "H must be a multiple of 8");
+  if (H > 0x7fffffffLL || N > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
+  if (!aligned16(hidden) || !aligned16(norm_w) || !aligned16(w_qkv))
+    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  const bool mfma = mlp_needs_normed(M, kind);
+  if (mfma && (!normed || !aligned16(normed)))
+    return set_error(FD_EINVAL, "kind=dot with M >= 8 needs a 16-byte aligned normed buffer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Epi e;
+  e.bias = bias;
+  e.bias_dtype = bias_dtype;
+  e.sb = 1;
+  e.row = nullptr;
+  e.row_dtype = act_dtype;
+  e.srm = e.srn = 0;
+  Rope rp;
+  rp.cos = cos;
+  rp.sin = sin;
+  rp.dtype = cs_dtype;
+  rp.rs = cs_row_stride;
+  rp.cols = (int)rope_cols;
+  rp.dim = rope_cols > 0 ? (int)head_dim : 2;
+  int rc;
+  if (mfma) {
+    rp.tiles = (int)(rope_cols / 16);
+    rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    if (rc != FD_OK) return rc;
+    if (act_dtype == FD_F16)
+      launch_mfma<f16>((int)M, y, normed, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp);
+    else
+      launch_mfma<bf16>((int)M, y, normed, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp);
+  } else {
+    rp.tiles = (int)(rope_cols / 4);
+    rc = act_dtype == FD_F16
+             ? launch_qkv_simt_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H,
+                                      (int)N, eps, e, rp, st)
+             : launch_qkv_simt_m<bf16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H,
+                                       (int)N, eps, e, rp, st);
+    if (rc != FD_OK) return rc;
+  }
   return check_launch();
 }

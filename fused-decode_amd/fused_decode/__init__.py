@@ -9,6 +9,7 @@ from .ops import (
     add_rms_norm,
     linear_decode,
     post_attn_mlp,
+    pre_attn_qkv,
     rms_norm,
     rope,
     swiglu,
@@ -21,6 +22,7 @@ __all__ = [
     "add_rms_norm",
     "linear_decode",
     "post_attn_mlp",
+    "pre_attn_qkv",
     "rms_norm",
     "rope",
     "swiglu",

@@ -32,7 +32,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .kernels import launch_copy, launch_triad
-from .ops import add_rms_norm, linear_decode, post_attn_mlp, rms_norm, rope, swiglu
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope, swiglu
 
 LLAMA_H = 4096
 LLAMA_I = 14336
@@ -154,7 +154,7 @@ def _print(row: dict) -> None:
     dev = f"dev {row['dev_us']:8.2f}" if row.get("dev_us") else "dev      n/a"
     parts = [f"{row['name']:<44}", f"{row['us']:9.2f} us", dev, f"{row['gbs']:8.1f} GB/s",
              f"{row['pct_copy_roof']:5.1f}% copy", f"warm {row['us_warm']:8.2f}"]
-    for k in ("eager_us", "cpu_eager_us", "graph_us", "hipblas_us"):
+    for k in ("eager_us", "cpu_eager_us", "graph_us", "hipblas_us", "composed_dev_us"):
         if row.get(k) is not None:
             parts.append(f"{k} {row[k]:.2f}")
     print("  ".join(parts), flush=True)
@@ -328,13 +328,65 @@ def bench_mlp(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
+def bench_qkv(dtype, roof, quick, cpu) -> list[dict]:
+    """pre_attn_qkv at Llama-3-8B widths (H=4096, N=6144, q+k heads 40 x 128 rotated),
+    beside the same work as three launches of this library (rms_norm,
+    linear_decode, rope) and PyTorch eager."""
+    rows = []
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    h, d = LLAMA_H, 128
+    n, rc = 48 * d, 40 * d
+    k = copies_for(n * h * e)
+    sets = [(_gen((h,), dtype, g, 0.1, 1.0), _gen((n, h), dtype, g, h ** -0.5)) for _ in range(k)]
+    ang = 1024 * (1.0 / (500000.0 ** (torch.arange(0, d, 2, device="cuda", dtype=torch.float64) / d)))
+    cos = torch.cat([ang, ang]).cos().to(dtype).view(1, d)
+    sin = torch.cat([ang, ang]).sin().to(dtype).view(1, d)
+    for m in ([1, 8] if not quick else [1]):
+        hid = _gen((m, h), dtype, g)
+        out = torch.empty(m, n, device="cuda", dtype=dtype)
+
+        def fused(j, m=m):
+            nw, w = sets[j % k]
+            return pre_attn_qkv(hid, nw, w, cos, sin, 1e-5, rope_cols=rc, out=out)
+
+        def composed(j, m=m):
+            nw, w = sets[j % k]
+            y = linear_decode(rms_norm(hid, nw, 1e-5), w, out=out)
+            heads = y[:, :rc].view(m, rc // d, d)
+            rope(heads, cos, sin, out=heads)
+            return y
+
+        def eager(j, m=m):
+            nw, w = sets[j % k]
+            y = F.linear(F.rms_norm(hid, (h,), nw, 1e-5), w)
+            x = y[:, :rc].view(m, rc // d, d).float()
+            x1, x2 = x[..., : d // 2], x[..., d // 2:]
+            c, s_ = cos.float(), sin.float()
+            rot = torch.cat([x1 * c[..., : d // 2] - x2 * s_[..., : d // 2], x2 * c[..., d // 2:] + x1 * s_[..., d // 2:]], -1)
+            return torch.cat([rot.to(dtype).view(m, rc), y[:, rc:]], -1)
+
+        cold = time_us(fused, iters=max(30, 2 * k))
+        warm = time_us(lambda j: fused(0), iters=30)
+        g_us = graph_us(fused, k)
+        comp_us = graph_us(composed, k)
+        eager_us = time_us(eager, iters=max(30, 2 * k))
+        nbytes = (n * h + m * h + h + m * n) * e + 2 * d * e
+        rows.append(_row(f"pre_attn_qkv M={m} {dtype}", nbytes, cold, warm, roof, g_us,
+                         composed_dev_us=comp_us, eager_us=eager_us))
+        _print(rows[-1])
+    del sets
+    torch.cuda.empty_cache()
+    return rows
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--out", default=None)
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--dtype", choices=["fp16", "bf16", "both"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true", help="skip PyTorch-eager-on-CPU timings")
-    ap.add_argument("--only", choices=["pointwise", "linear", "mlp"], default=None)
+    ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv"], default=None)
     args = ap.parse_args()
     _lib.lib()
     torch.cuda.set_device(0)
@@ -359,6 +411,8 @@ def main() -> None:
             payload["rows"] += bench_linear(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
         if args.only in (None, "mlp"):
             payload["rows"] += bench_mlp(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
+        if args.only in (None, "qkv"):
+            payload["rows"] += bench_qkv(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
         if args.out:
             with open(args.out, "w") as f:
                 json.dump(payload, f, indent=1)

@@ -1,20 +1,28 @@
 """A random-init Llama-3-8B decode step minus attention, captured in a HIP graph.
 
-    python -m fused_decode.decode_step [--m 1] [--layers 32] [--dtype fp16] [--steps 20]
+    python -m fused_decode.decode_step [--m 1] [--layers 32] [--dtype fp16] [--steps 20] [--unfused]
 
-Per layer (widths of Llama-3-8B: H=4096, 32 query / 8 KV heads of 128, I=14336):
+Per layer (widths of Llama-3-8B: H=4096, 32 query / 8 KV heads of 128, I=14336),
+fused form (the default):
+
+    qkv = pre_attn_qkv(x, attn_norm_w, w_qkv, cos, sin)   # RMSNorm + [M, 6144] GEMV + RoPE of q, k
+    attn = stand-in attention output                     # seeded random [M, 4096] per layer
+    h    = linear_decode(attn, w_o, row_add=x)           # O-proj with the residual fused
+    x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
+
+That is four launches per layer at M < 8 (six from 8 rows with kind "dot",
+where both RMSNorms run as row kernels ahead of MFMA GEMVs). The unfused form
+composes the reference's operators instead, six launches per layer (seven):
 
     normed, stream = add_rms_norm(x, zero, attn_norm_w)   # stream <- x, normed <- rms(x)
     qkv  = linear_decode(normed, w_qkv)                  # [M, 6144]
     q, k = rope(qkv[:, :5120] as [M, 40, 128])           # q and k heads in one launch, position 1024
-    attn = stand-in attention output                     # seeded random [M, 4096] per layer
-    h    = linear_decode(attn, w_o, row_add=stream)      # O-proj with the residual fused
+    h    = linear_decode(attn, w_o, row_add=stream)
     x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
 
 post_attn_mlp returns the whole residual stream (its residual add is fused into
-the down projection), so the next layer's add_rms_norm receives that stream with
-a zero delta: it both normalises it and keeps the copy the O-proj residual reads.
-The whole step (7 launches per layer) is captured once and replayed.
+the down projection). Both forms compute the same values with the same rounding
+points. The whole step is captured once and replayed.
 
 Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), random
 with the benchmark distributions (no checkpoint is loaded).
@@ -28,7 +36,7 @@ import math
 
 import torch
 
-from .ops import add_rms_norm, linear_decode, post_attn_mlp, rope
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rope
 
 H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
 QKV = (HEADS + 2 * KV_HEADS) * HEAD_DIM  # 6144
@@ -47,8 +55,9 @@ class DecodeStep:
     `capture()` records it into a HIP graph and `replay()` runs that."""
 
     def __init__(self, m: int = 1, layers: int = 32, dtype=torch.float16, device="cuda",
-                 seed: int = 0, h: int = H, i: int = I, kind: str | None = None, position: int = 1024):
-        self.m, self.layers, self.dtype, self.kind = m, layers, dtype, kind
+                 seed: int = 0, h: int = H, i: int = I, kind: str | None = None, position: int = 1024,
+                 fused: bool = True):
+        self.m, self.layers, self.dtype, self.kind, self.fused = m, layers, dtype, kind, fused
         self.h, self.i = h, i
         heads = h // HEAD_DIM
         kv = max(1, heads // 4)
@@ -89,6 +98,20 @@ class DecodeStep:
         return per * self.layers
 
     def step(self) -> torch.Tensor:
+        return self._step_fused() if self.fused else self._step_composed()
+
+    def _step_fused(self) -> torch.Tensor:
+        x = self.x_in
+        rope_cols = self.qk_heads * HEAD_DIM
+        for w in self.w:
+            pre_attn_qkv(x, w["attn_norm"], w["qkv"], self.cos, self.sin, 1e-5, rope_cols=rope_cols,
+                         out=self.qkv, kind=self.kind)
+            linear_decode(w["attn_out"], w["o"], row_add=x, out=self.hbuf, kind=self.kind)
+            x = post_attn_mlp(self.hbuf, w["mlp_norm"], w["gate_up"], w["down"], 1e-5, kind=self.kind)
+        self.out.copy_(x)
+        return self.out
+
+    def _step_composed(self) -> torch.Tensor:
         x = self.x_in
         qk = self.qkv[:, : self.qk_heads * HEAD_DIM].view(self.m, self.qk_heads, HEAD_DIM)
         for w in self.w:
@@ -99,6 +122,16 @@ class DecodeStep:
             x = post_attn_mlp(self.hbuf, w["mlp_norm"], w["gate_up"], w["down"], 1e-5, kind=self.kind)
         self.out.copy_(x)
         return self.out
+
+    @property
+    def launches_per_layer(self) -> int:
+        """HIP launches one layer issues (the MFMA forms at kind "dot" from 8 rows
+        add a row kernel for the RMSNorm)."""
+        mfma = (self.kind or "dot") == "dot" and self.m >= 8
+        mlp = 3 if mfma else 2
+        if self.fused:
+            return (2 if mfma else 1) + 1 + mlp
+        return 4 + mlp
 
     def capture(self) -> None:
         side = torch.cuda.Stream()
@@ -141,20 +174,22 @@ def main() -> None:
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 8)")
     args = ap.parse_args()
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     for m in args.m:
-        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype)
+        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused)
         eager = time_step(ds, args.steps, args.warmup, graph=False)
         graph = time_step(ds, args.steps, args.warmup, graph=True)
         wb = ds.weight_bytes
         print(json.dumps({
-            "workload": f"decode step minus attention, {args.layers} layers, Llama-3-8B widths, M={m}, {args.dtype}",
+            "workload": f"decode step minus attention, {args.layers} layers, Llama-3-8B widths, M={m}, {args.dtype}, "
+                        f"{'unfused' if args.unfused else 'fused'}",
             "eager_us": round(eager, 2),
             "graph_us": round(graph, 2),
             "weight_bytes": wb,
             "graph_gbs": round(wb / (graph * 1e-6) / 1e9, 1),
-            "launches_per_step": 7 * args.layers + 1,
+            "launches_per_step": ds.launches_per_layer * args.layers + 1,
             "finite": bool(torch.isfinite(ds.out.float()).all().item()),
         }), flush=True)
         del ds

@@ -219,6 +219,44 @@ def post_attn_mlp_out(
     return status
 
 
+def pre_attn_qkv_out(
+    hidden: torch.Tensor,
+    norm_weight: torch.Tensor,
+    w_qkv: torch.Tensor,
+    bias: torch.Tensor | None,
+    cos: torch.Tensor | None,
+    sin: torch.Tensor | None,
+    cs_row_stride: int,
+    rope_cols: int,
+    head_dim: int,
+    eps: float,
+    out: torch.Tensor,
+    normed: torch.Tensor | None,
+    kind: str,
+) -> int:
+    """Fused RMSNorm + QKV GEMV + RoPE for contiguous ``hidden [M, H]`` (M <= 16)
+    into contiguous ``out [M, N]``; ``cos``/``sin`` are contiguous rows of
+    ``head_dim`` (row stride ``cs_row_stride``, 0 = shared). ``normed`` is ``[M, H]``
+    scratch for kind=dot at M >= 8. Returns the library status (FD_EUNSUPPORTED
+    lets the caller compose the operators instead)."""
+    m, h = hidden.shape
+    n = w_qkv.shape[0]
+    status = lib().fd_pre_attn_qkv(
+        out.data_ptr(), normed.data_ptr() if normed is not None else None, hidden.data_ptr(),
+        norm_weight.data_ptr(), DTYPE_CODE[norm_weight.dtype], w_qkv.data_ptr(),
+        bias.data_ptr() if bias is not None else None,
+        DTYPE_CODE[bias.dtype] if bias is not None else DTYPE_CODE[hidden.dtype],
+        cos.data_ptr() if cos is not None else None, sin.data_ptr() if sin is not None else None,
+        DTYPE_CODE[cos.dtype] if cos is not None else DTYPE_CODE[torch.float32],
+        cs_row_stride, m, h, n, rope_cols, head_dim, float(eps), KIND_CODE[kind],
+        DTYPE_CODE[hidden.dtype], stream_of(hidden),
+    )
+    if status == _lib.FD_EUNSUPPORTED:
+        return status
+    check("fd_pre_attn_qkv", status)
+    return status
+
+
 def launch_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
     """Bandwidth-roof copy of ``src`` into ``dst`` (same byte size, contiguous)."""
     nbytes = src.numel() * src.element_size()

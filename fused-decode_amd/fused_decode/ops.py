@@ -16,7 +16,15 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .kernels import linear_out, post_attn_mlp_out, resolve_kind, rms_out, rope_out, swiglu_out
+from .kernels import (
+    linear_out,
+    post_attn_mlp_out,
+    pre_attn_qkv_out,
+    resolve_kind,
+    rms_out,
+    rope_out,
+    swiglu_out,
+)
 
 # Largest flattened batch the default dispatcher sends to the HIP GEMV. The
 # reference sets this per GPU from measurement (its RTX 4070 Laptop value is 1,
@@ -32,6 +40,7 @@ __all__ = [
     "add_rms_norm",
     "linear_decode",
     "post_attn_mlp",
+    "pre_attn_qkv",
     "rms_norm",
     "rope",
     "swiglu",
@@ -334,3 +343,125 @@ def post_attn_mlp(
     gate_up = linear_decode(normed, w_gate_up, kind=kind)
     gate, up = gate_up.split(i, dim=-1)
     return linear_decode(swiglu(gate, up), w_down, row_add=hidden, kind=kind)
+
+
+def _token_angles(src: torch.Tensor, lead: tuple, name: str) -> torch.Tensor:
+    """cos/sin of ``pre_attn_qkv`` as ``[1 or M, D]`` contiguous rows: ``src``
+    broadcasts to ``[*lead, D]`` (a size-1 heads axis before D is allowed)."""
+    if not isinstance(src, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if src.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"{name} must be float16, bfloat16, or float32")
+    d = src.shape[-1]
+    if src.ndim == len(lead) + 2 and src.shape[-2] == 1:
+        src = src.squeeze(-2)
+    if src.numel() == d:
+        return src.reshape(1, d).contiguous()
+    try:
+        full = src.expand(*lead, d)
+    except RuntimeError as exc:
+        raise ValueError(
+            f"cannot broadcast {name} shape {tuple(src.shape)} to {(*lead, d)}"
+        ) from exc
+    return full.reshape(-1, d).contiguous()
+
+
+def pre_attn_qkv(
+    hidden: torch.Tensor,
+    norm_weight: torch.Tensor,
+    w_qkv: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float = 1e-6,
+    *,
+    rope_cols: int,
+    bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    kind: str | None = None,
+) -> torch.Tensor:
+    """Pre-attention half of a Llama decode layer: RMSNorm, the fused QKV
+    projection and RoPE of the q and k heads.
+
+    ``hidden`` is ``[..., H]``, ``w_qkv`` is ``[N, H]`` (q, k, v rows stacked),
+    ``bias`` is ``[N]`` (hidden's dtype or float32) or None. The first
+    ``rope_cols`` output columns, viewed as heads of ``D = cos.shape[-1]``, get the
+    rotate-half RoPE of ``rope`` with one cos/sin row per token: ``cos``/``sin``
+    broadcast to ``[..., D]`` (``[D]`` or ``[1, D]`` for one position, ``[..., D]``
+    or ``[..., 1, D]`` per token). Returns ``[..., N]`` equal to
+    ``rope(linear_decode(rms_norm(hidden), w_qkv, bias)[..., :rope_cols])`` with
+    the reference's rounding after each step. Up to the GEMV row limit this is one
+    HIP launch (two for kind "dot" from 8 rows: the norm runs as a row kernel).
+    No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
+    :138-160.
+    """
+    _check_activation(hidden, "hidden")
+    if w_qkv.ndim != 2:
+        raise ValueError(f"w_qkv must have shape [N, H], got {tuple(w_qkv.shape)}")
+    n, h = w_qkv.shape
+    if hidden.shape[-1] != h:
+        raise ValueError(f"hidden last dim {hidden.shape[-1]} != w_qkv H {h}")
+    if w_qkv.dtype != hidden.dtype:
+        raise TypeError("w_qkv must match hidden dtype")
+    if w_qkv.device != hidden.device:
+        raise ValueError("w_qkv must be on the same device as hidden")
+    _check_norm_weight(norm_weight, hidden)
+    eps = _check_eps(eps)
+    for name, t in (("cos", cos), ("sin", sin)):
+        if isinstance(t, torch.Tensor) and t.device != hidden.device:
+            raise ValueError(f"{name} is on {t.device}, expected {hidden.device}")
+    rope_cols = int(rope_cols)
+    d = cos.shape[-1]
+    if sin.shape[-1] != d:
+        raise ValueError(f"sin last dim {sin.shape[-1]} != cos last dim {d}")
+    if d % 2 != 0:
+        raise ValueError("rope head dimension must be even")
+    if rope_cols < 0 or rope_cols > n or rope_cols % d != 0:
+        raise ValueError(f"rope_cols must be a multiple of {d} in [0, {n}], got {rope_cols}")
+    if bias is not None:
+        if bias.ndim != 1 or bias.shape[0] != n:
+            raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
+        if bias.device != hidden.device:
+            raise ValueError("bias must be on the same device as hidden")
+        if bias.dtype not in (hidden.dtype, torch.float32):
+            raise TypeError("bias must match hidden or be float32")
+    lead = tuple(hidden.shape[:-1])
+    cos_r = _token_angles(cos, lead, "cos")
+    sin_r = _token_angles(sin, lead, "sin")
+    if cos_r.dtype != sin_r.dtype:
+        cos_r, sin_r = cos_r.float(), sin_r.float()
+    expected = (*lead, n)
+    if out is None:
+        out = torch.empty(expected, device=hidden.device, dtype=hidden.dtype)
+    else:
+        if tuple(out.shape) != expected or out.dtype != hidden.dtype or out.device != hidden.device:
+            raise ValueError(f"out must be a contiguous {expected} tensor of dtype {hidden.dtype}")
+        if not out.is_contiguous():
+            raise ValueError("out must be contiguous")
+    m = hidden.numel() // h if h else 0
+    if m == 0 or n == 0:
+        return out
+    hand_limit = _HAND_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
+    kind_r = resolve_kind(kind)
+    if cos_r.shape[0] not in (1, m):
+        raise ValueError(f"cos/sin need 1 or {m} rows, got {cos_r.shape[0]}")
+    rs = 0 if cos_r.shape[0] == 1 else d
+    y2 = out.view(m, n)
+    if m <= hand_limit and w_qkv.is_contiguous():
+        h2 = hidden.reshape(m, h)
+        if not h2.is_contiguous():
+            h2 = h2.contiguous()
+        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
+        b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
+        normed = None
+        if kind_r == "dot" and m >= 8:
+            normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
+        status = pre_attn_qkv_out(h2, nw, w_qkv, b, cos_r, sin_r, rs, rope_cols, d, eps, y2,
+                                  normed, kind_r)
+        if status == _lib.FD_OK:
+            return out
+    normed = rms_norm(hidden, norm_weight, eps=eps)
+    linear_decode(normed, w_qkv, bias, out=out, kind=kind)
+    if rope_cols:
+        heads = y2[:, :rope_cols].unflatten(-1, (rope_cols // d, d))
+        rope(heads, cos_r.unsqueeze(1), sin_r.unsqueeze(1), out=heads)
+    return out

@@ -149,6 +149,31 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
                    float eps, int kind, int act_dtype, void* stream);
 
 /*
+ * Pre-attention QKV projection of a decode step in one launch (two for kind
+ * FD_KIND_DOT at M >= 8):
+ *   h   = round(rms_norm(hidden, norm_w, eps))                       [M,H]
+ *   qkv = round(h @ w_qkv.T + bias)                                  [M,N]
+ *   y   = qkv with rope(qkv[:, :rope_cols] viewed as heads of head_dim, cos, sin)
+ * rope is the rotate-half of fd_rope, applied to the rounded projection; cos/sin
+ * row m (head_dim values of cs_dtype, unit stride) sits at m * cs_row_stride, and
+ * cs_row_stride 0 shares one row across all M. hidden [M,H], w_qkv [N,H] and y
+ * [M,N] are contiguous; bias ([N], bias_dtype) may be NULL. rope_cols is a
+ * multiple of head_dim (0: no rotation); this build needs head_dim % 16 == 0 and
+ * H % 8 == 0 (FD_EUNSUPPORTED otherwise: compose fd_rms_norm, fd_linear, fd_rope).
+ * With kind FD_KIND_DOT and M >= 8 the RMSNorm goes to `normed` ([M,H], 16-byte
+ * aligned) first; otherwise `normed` is unused and may be NULL.
+ * No reference counterpart as one call: it fuses the composition a caller of the
+ * reference writes from rms_norm (ops.py:72-88), linear_decode (ops.py:212-280)
+ * and rope (ops.py:138-160) on the q and k heads, the first cross-op fusion the
+ * decode step names after the MLP block.
+ */
+int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_w,
+                    int norm_w_dtype, const void* w_qkv, const void* bias, int bias_dtype,
+                    const void* cos, const void* sin, int cs_dtype, int64_t cs_row_stride,
+                    int64_t M, int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim,
+                    float eps, int kind, int act_dtype, void* stream);
+
+/*
  * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned
  * pointers take the vector path). c = a + b*scale over n elements of dtype.
  * Replace kernels.py:833-858 (`launch_copy`, `launch_triad`).

@@ -113,6 +113,32 @@ def post_attn_mlp(hidden, norm_w, w_gate_up, w_down, eps: float, dtype: str) -> 
     return linear(mid, w_down, row_add=hidden, dtype=dtype)
 
 
+def pre_attn_qkv(hidden, norm_w, w_qkv, cos, sin, eps: float, rope_cols: int, bias=None,
+                 dtype: str = "f16") -> np.ndarray:
+    """The pre-attention composition a caller of the reference writes from its
+    operators: h = round(rms(hidden)) (reference.py:14-18), y = round(h @ Wqkv.T +
+    bias) (reference.py:50-63), then rotate-half RoPE (reference.py:38-47) of the
+    first rope_cols columns viewed as heads of D = cos.shape[-1], each row m with
+    cos/sin row m (one row broadcasts to all)."""
+    hidden = np.asarray(hidden, F32)
+    m = hidden.shape[0]
+    h = rms_norm(hidden, norm_w, eps, dtype)
+    y = linear(h, w_qkv, bias=bias, dtype=dtype)
+    if rope_cols:
+        d = np.shape(cos)[-1]
+        c = np.asarray(cos, F32).reshape(-1, 1, d)
+        s = np.asarray(sin, F32).reshape(-1, 1, d)
+        heads = y[:, :rope_cols].reshape(m, rope_cols // d, d)
+        y = y.copy()
+        y[:, :rope_cols] = rope(heads, c, s, dtype).reshape(m, rope_cols)
+    return y
+
+
+def bytes_qkv(m: int, h: int, n: int, head_dim: int, cs_rows: int, e: int = 2, ce: int = 2) -> int:
+    """Weights + hidden read + norm weight + output write + cos/sin rows."""
+    return (n * h + m * h + h + m * n) * e + 2 * cs_rows * head_dim * ce
+
+
 # Useful-byte accounting (reference README.md:33-43, bench.py:215-216, :247,
 # :274, :303-305): weights counted once, no cache reuse, e bytes per element.
 def bytes_rms(rows: int, n: int, e: int = 2) -> int:

@@ -29,7 +29,8 @@ def L():
 def test_header_declares_the_operator_set():
     names = declared()
     for n in ("fd_rms_norm", "fd_add_rms_norm", "fd_swiglu", "fd_rope", "fd_linear",
-              "fd_post_attn_mlp", "fd_copy", "fd_triad", "fd_last_error", "fd_version"):
+              "fd_post_attn_mlp", "fd_pre_attn_qkv", "fd_copy", "fd_triad", "fd_last_error",
+              "fd_version"):
         assert n in names
 
 
@@ -102,3 +103,24 @@ def test_mlp_rejects(L):
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 0, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 60, 128, 1e-6, 0, 0, None) == L.FD_EUNSUPPORTED
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, 64, 128, 1e-6, 0, 0, None) == L.FD_OK
+
+
+@nogpu
+def test_qkv_rejects(L):
+    lib = L.lib()
+
+    def call(m=2, h=64, n=96, rope_cols=64, head_dim=32, eps=1e-6, kind=0, normed=None, cs_rs=0):
+        return lib.fd_pre_attn_qkv(FAKE, normed, FAKE, FAKE, 0, FAKE, None, 0, FAKE, FAKE, 2, cs_rs,
+                                   m, h, n, rope_cols, head_dim, eps, kind, 0, None)
+
+    assert call(m=17) == L.FD_EINVAL
+    assert call(rope_cols=100) == L.FD_EINVAL            # above N
+    assert call(rope_cols=48) == L.FD_EINVAL             # not a multiple of head_dim
+    assert call(head_dim=31, rope_cols=62) == L.FD_EINVAL  # odd head_dim
+    assert call(head_dim=24, rope_cols=48) == L.FD_EUNSUPPORTED  # head_dim % 16
+    assert call(h=60) == L.FD_EUNSUPPORTED
+    assert call(eps=float("nan")) == L.FD_EINVAL
+    assert call(kind=5) == L.FD_EINVAL
+    assert call(cs_rs=-1) == L.FD_EINVAL
+    assert call(m=8, kind=0) == L.FD_EINVAL              # kind=dot at 8 rows needs `normed`
+    assert call(m=0) == L.FD_OK

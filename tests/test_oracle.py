@@ -219,6 +219,64 @@ def test_post_attn_mlp_matches_torch_formula():
     np.testing.assert_allclose(O.post_attn_mlp(hid, nw, wgu, wd, 1e-6, "f16"), lib, rtol=2e-3, atol=2e-3)
 
 
+# ---------------------------------------------------------------- pre-attention QKV
+
+
+def _qkv_case(m=3, h=32, d=16, heads=3, kv=1, seed=0):
+    r = np.random.default_rng(seed)
+    n = (heads + 2 * kv) * d
+    hid = r.standard_normal((m, h)).astype(np.float32)
+    nw = (1 + 0.1 * r.standard_normal(h)).astype(np.float32)
+    w = (r.standard_normal((n, h)) / np.sqrt(h)).astype(np.float32)
+    return hid, nw, w, (heads + kv) * d, d
+
+
+def test_pre_attn_qkv_quarter_turn_swaps_head_halves():
+    """cos = 0, sin = 1 turns every rotated head (x1, x2) into (-x2, x1) exactly and
+    leaves the v columns alone: pins the head split at D, the partner column
+    d + D/2 and the signs, against the same call with no rotation."""
+    hid, nw, w, rc, d = _qkv_case()
+    plain = O.pre_attn_qkv(hid, nw, w, np.ones(d), np.zeros(d), 1e-6, 0, dtype="f32")
+    turned = O.pre_attn_qkv(hid, nw, w, np.zeros(d), np.ones(d), 1e-6, rc, dtype="f32")
+    for head in range(rc // d):
+        a, b = plain[:, head * d: head * d + d // 2], plain[:, head * d + d // 2: (head + 1) * d]
+        np.testing.assert_array_equal(turned[:, head * d: head * d + d // 2], -b)
+        np.testing.assert_array_equal(turned[:, head * d + d // 2: (head + 1) * d], a)
+    np.testing.assert_array_equal(turned[:, rc:], plain[:, rc:])
+    # no rotation at all equals a zero rope_cols call
+    same = O.pre_attn_qkv(hid, nw, w, np.ones(d), np.zeros(d), 1e-6, rc, dtype="f32")
+    np.testing.assert_array_equal(same, plain)
+
+
+def test_pre_attn_qkv_matches_torch_composition_and_per_row_angles():
+    """Against torch CPU library routines (F.rms_norm, F.linear, complex rotation),
+    with one position per row: row m uses angle row m."""
+    hid, nw, w, rc, d = _qkv_case(m=4, seed=3)
+    pos = np.array([3.0, 17.0, 250.0, 1024.0])
+    inv = 500000.0 ** (-np.arange(0, d, 2) / d)
+    ang = pos[:, None] * inv[None]
+    cos = np.concatenate([np.cos(ang), np.cos(ang)], 1).astype(np.float32)
+    sin = np.concatenate([np.sin(ang), np.sin(ang)], 1).astype(np.float32)
+    bias = np.linspace(-1, 1, w.shape[0]).astype(np.float32)
+    got = O.pre_attn_qkv(hid, nw, w, cos, sin, 1e-5, rc, bias=bias, dtype="f32")
+    T = lambda a: torch.from_numpy(a).double()  # noqa: E731
+    hn = F.rms_norm(T(hid), (hid.shape[1],), T(nw), 1e-5)
+    y = F.linear(hn, T(w), T(bias)).numpy()
+    exp = y.copy()
+    for head in range(rc // d):
+        x1 = y[:, head * d: head * d + d // 2]
+        x2 = y[:, head * d + d // 2: (head + 1) * d]
+        z = (x1 + 1j * x2) * np.exp(1j * ang)
+        exp[:, head * d: head * d + d // 2] = z.real
+        exp[:, head * d + d // 2: (head + 1) * d] = z.imag
+    np.testing.assert_allclose(got, exp, rtol=1e-4, atol=1e-4)
+    # a per-row call equals four single-row calls with that row's angles (to the
+    # last bit of a float32 matmul, whose summation order depends on the row count)
+    for r in range(4):
+        one = O.pre_attn_qkv(hid[r:r + 1], nw, w, cos[r], sin[r], 1e-5, rc, bias=bias, dtype="f32")
+        np.testing.assert_allclose(one[0], got[r], rtol=1e-5, atol=1e-6)
+
+
 # ---------------------------------------------------------------- bytes
 
 
