@@ -387,6 +387,96 @@ __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hid
   __syncthreads();
 }
 
+// Register form of the same prologue for small M, split so the weight stream
+// can start in between: norm_load issues every global load the norm needs
+// (this thread's KIT 8-element slices of each hidden row and of the norm
+// weight) before the caller issues its first weight loads, so the norm's loads
+// are not queued behind them; norm_store reduces, rounds and stages in LDS
+// from registers. Usable when H <= KIT * blockDim.x * 8 (norm_in_regs); the
+// same summation order and rounding as stage_normed.
+template <typename T, int MMAX, int KIT>
+struct NormRegs {
+  typename Vec8<T>::type h[KIT][MMAX];
+  float w[KIT][8];
+};
+
+template <typename T, int MMAX, int KIT>
+__device__ __forceinline__ void norm_load(NormRegs<T, MMAX, KIT>& c, const T* hidden,
+                                          const void* nwp, int nw_dtype, int M, int H) {
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int k = (threadIdx.x + it * blockDim.x) * 8;
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m)
+      c.h[it][m] = (m < M && k < H) ? load8<T>(hidden + (int64_t)m * H + k)
+                                    : typename Vec8<T>::type{};
+    if (k < H) {
+      load8_norm_w(nwp, nw_dtype, k, c.w[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c.w[it][i] = 0.f;
+    }
+  }
+}
+
+template <typename T, int MMAX, int KIT>
+__device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* xs,
+                                           float* scratch, int M, int H, float eps) {
+  const int XS = xs_stride(H);
+  typedef typename Vec8<T>::type V8;
+  constexpr int MP = pow2_ceil(MMAX);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int nwv = blockDim.x / kWave;
+  float ss[MP];
+#pragma unroll
+  for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss[m] += to_f32(c.h[it][m][i]) * to_f32(c.h[it][m][i]);
+    }
+  }
+  butterfly_sum<MP>(ss, lane);
+  float* inv = scratch + kMaxWaves * MP;
+  if (butterfly_writer<MP>(lane)) scratch[wave * MP + butterfly_index<MP>(lane)] = ss[0];
+  __syncthreads();
+  if (tid < M) {
+    float s = 0.f;
+    for (int i = 0; i < nwv; ++i) s += scratch[i * MP + tid];
+    inv[tid] = rsqrtf(s / (float)H + eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < KIT; ++it) {
+    const int k = (tid + it * (int)blockDim.x) * 8;
+    if (k < H) {
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) {
+        if (m < M) {
+          const float s = inv[m];
+          V8 o;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(c.h[it][m][i]) * s * c.w[it][i]);
+          store8<T>(xs + (int64_t)m * XS + k, o);
+        }
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// The register prologue holds 2 slices of 8 per row and thread (H up to 16
+// values per thread) and is used up to 2 rows; beyond that its registers would
+// cost the weight loop occupancy, and the loop's longer math hides the prologue.
+// The host decides with norm_in_regs and launches the kernel's REGS form.
+constexpr int kNormRegMaxM = 2;
+constexpr int kNormRegRows(int m) { return m <= kNormRegMaxM ? 2 : 1; }
+__host__ __device__ __forceinline__ bool norm_in_regs(int M, int H, int threads) {
+  return M <= kNormRegMaxM && H <= kNormRegRows(M) * threads * 8;
+}
+
 template <typename T>
 __device__ __forceinline__ T swiglu_out(float g, float u) {
   return from_f32<T>(silu_stable(round_as<T>(g)) * round_as<T>(u));
@@ -414,7 +504,7 @@ __device__ __forceinline__ void load_gate_up(typename Vec8<T>::type (&g)[R],
 // tile) are issued before the math of the current one, and the first step is
 // issued before the RMSNorm prologue, so HBM requests stay in flight across the
 // prologue, the cross-wave reduction and the SwiGLU epilogue.
-template <typename T, int M, int R, bool NTW>
+template <typename T, int M, int R, bool NTW, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int H, int I,
     float eps, int tiles) {
@@ -431,9 +521,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   const int steps = (H + step - 1) / step;  // the same for every wave
   const int kbase = (wave * kWave + lane) * 8;
 
+  NormRegs<T, M, kNormRegRows(M)> nr;
+  if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
   V8 gv[R], uv[R];
   load_gate_up<T, R, NTW>(gv, uv, wgu, blockIdx.x, tiles, kbase, H, I);
-  stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+  if constexpr (REGS)
+    norm_store(nr, xs, part, M, H, eps);
+  else
+    stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     const int64_t j0 = (int64_t)tile * R;
@@ -500,7 +595,7 @@ __device__ __forceinline__ void load_tile_rows(typename Vec8<T>::type (&v)[R], c
   }
 }
 
-template <typename T, int M, bool NTW>
+template <typename T, int M, bool NTW, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
     T* y, const T* hidden, const void* nwp, int nw_dtype, const T* w, int H, int N, float eps,
     int tiles, Epi e, Rope rp) {
@@ -518,9 +613,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   const int steps = (H + step - 1) / step;
   const int kbase = (wave * kWave + lane) * 8;
 
+  NormRegs<T, M, kNormRegRows(M)> nr;
+  if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
   V8 wv[R];
   load_tile_rows<T, R, NTW>(wv, w, rp, blockIdx.x, tiles, kbase, H, N);
-  stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+  if constexpr (REGS)
+    norm_store(nr, xs, part, M, H, eps);
+  else
+    stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
   for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
     float acc[V];
@@ -777,6 +877,12 @@ int device_cus() {
   return cached[dev];
 }
 
+// Dynamic LDS of a fused kernel: the staged activations and the reduction scratch.
+size_t fused_lds(int M, int H, size_t elem, int V) {
+  return (size_t)M * xs_stride(H) * elem +
+         sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves : kNormScratch);
+}
+
 // Workgroups of the fused kernel: each stages the normalised activations in LDS
 // once and then loops over weight tiles, so the grid is what can be resident at
 // once, at most `per_cu` per CU and fewer when the LDS stage is large; more would
@@ -793,22 +899,28 @@ int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype,
                     int H, int I, float eps, hipStream_t st) {
   constexpr int R = MlpRows<M>::R;
   constexpr int V = pow2_ceil(2 * R * M);
-  const size_t lds = (size_t)M * xs_stride(H) * sizeof(T) +
-                     sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
-                                                                           : kNormScratch);
+  // Eight waves (one 512-element K chunk per row each at H=4096) up to M=2;
+  // four above, where R*M sums per lane cost VGPRs (at M=3..4 the kernel holds
+  // three 4-wave workgroups per CU where two 8-wave ones would not fit).
+  const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
+  const int nwv = M > kNormRegMaxM && nwv0 > 4 ? 4 : nwv0;
+  const size_t lds = fused_lds(M, H, sizeof(T), V);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  if (!allow_lds(mlp_gate_up_simt_kernel<T, M, R, kNtWeights>, lds))
-    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   const int tiles = (I + R - 1) / R;
   const int grid = fused_grid(tiles, lds, 2);
-  // Eight waves (one 512-element K chunk per row each at H=4096) while the
-  // accumulators are small; four above M=4, where R*M sums per lane cost VGPRs.
-  const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
-  const int nwv = M > 4 && nwv0 > 4 ? 4 : nwv0;
-  hipLaunchKernelGGL((mlp_gate_up_simt_kernel<T, M, R, kNtWeights>), dim3(grid), dim3(nwv * kWave), lds, st,
-                     static_cast<T*>(mid), static_cast<const T*>(hidden), nw, nw_dtype,
-                     static_cast<const T*>(wgu), H, I, eps, tiles);
-  return FD_OK;
+  auto launch = [&](auto kernel) {
+    if (!allow_lds(kernel, lds))
+      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
+                       static_cast<const T*>(hidden), nw, nw_dtype, static_cast<const T*>(wgu), H,
+                       I, eps, tiles);
+    return (int)FD_OK;
+  };
+  if constexpr (M <= kNormRegMaxM) {
+    if (norm_in_regs(M, H, nwv * kWave))
+      return launch(mlp_gate_up_simt_kernel<T, M, R, kNtWeights, true>);
+  }
+  return launch(mlp_gate_up_simt_kernel<T, M, R, kNtWeights, false>);
 }
 
 template <typename T>
@@ -829,20 +941,26 @@ template <typename T, int M>
 int launch_qkv_simt(void* y, const void* hidden, const void* nw, int nw_dtype, const void* w,
                     int H, int N, float eps, const Epi& e, const Rope& rp, hipStream_t st) {
   constexpr int V = pow2_ceil(4 * M);
-  const size_t lds = (size_t)M * xs_stride(H) * sizeof(T) +
-                     sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves
-                                                                           : kNormScratch);
-  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  if (!allow_lds(qkv_simt_kernel<T, M, kNtWeights>, lds))
-    return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
-  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
-  const int grid = fused_grid(tiles, lds, 2);
+  // Four waves and every tile resident at once (one tile per workgroup at
+  // N = 6144): the QKV weights are too few to amortise a persistent loop.
   const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
-  const int nwv = M > 4 && nwv0 > 4 ? 4 : nwv0;
-  hipLaunchKernelGGL((qkv_simt_kernel<T, M, kNtWeights>), dim3(grid), dim3(nwv * kWave), lds, st,
-                     static_cast<T*>(y), static_cast<const T*>(hidden), nw, nw_dtype,
-                     static_cast<const T*>(w), H, N, eps, tiles, e, rp);
-  return FD_OK;
+  const int nwv = nwv0 > 4 ? 4 : nwv0;
+  const size_t lds = fused_lds(M, H, sizeof(T), V);
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
+  const int grid = fused_grid(tiles, lds, 8);
+  auto launch = [&](auto kernel) {
+    if (!allow_lds(kernel, lds))
+      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(y),
+                       static_cast<const T*>(hidden), nw, nw_dtype, static_cast<const T*>(w), H, N,
+                       eps, tiles, e, rp);
+    return (int)FD_OK;
+  };
+  if constexpr (M <= kNormRegMaxM) {
+    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_simt_kernel<T, M, kNtWeights, true>);
+  }
+  return launch(qkv_simt_kernel<T, M, kNtWeights, false>);
 }
 
 template <typename T>
