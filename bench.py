@@ -201,6 +201,11 @@ def cpu_baseline(seconds: float) -> dict:
     }
 
 
+def progress(msg: str) -> None:
+    """One line per finished stage on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -228,6 +233,7 @@ def main() -> None:
         }
         if m == 1:
             gate_us = time_gate_up_kernel(torch, lib(), sets, m, max(args.steps, 50), KIND_CODE[kind])
+        progress(f"post_attn_mlp M={m}: eager {results[m]['eager_us']:.2f} us, graph {results[m]['graph_us']:.2f} us")
         del sets
         torch.cuda.empty_cache()
 
@@ -285,6 +291,7 @@ def main() -> None:
                 line["decode_step"][f"{key}_us"] = round(g_us, 1)
                 line["decode_step"][f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
                 line["decode_step"][f"{key}_launches_per_layer"] = ds.launches_per_layer
+                progress(f"decode step {key}: {g_us:.1f} us")
                 del ds
                 torch.cuda.empty_cache()
         line["decode_step"]["workload"] = (
@@ -292,6 +299,7 @@ def main() -> None:
             "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        progress("cpu baseline done")
     print(json.dumps(line), flush=True)
 
 
