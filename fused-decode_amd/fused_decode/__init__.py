@@ -1,7 +1,9 @@
 """MI355X (gfx950) decode operators: the non-attention half of a Llama decode step.
 
 Drop-in for the reference package ``fused_decode`` (src/fused_decode/__init__.py):
-same names and signatures, hand-written HIP kernels behind a C ABI.
+same names and signatures, hand-written HIP kernels behind a C ABI. The same
+operators are registered as torch custom ops, ``torch.ops.fused_decode.*``
+(``fused_decode.library``), for torch.compile / export callers.
 """
 
 from .ops import (
@@ -14,6 +16,8 @@ from .ops import (
     rope,
     swiglu,
 )
+
+from . import library  # registers torch.ops.fused_decode.* (custom ops with fake kernels)
 
 __version__ = "0.1.0"
 

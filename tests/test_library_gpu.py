@@ -1,0 +1,93 @@
+"""torch.library registration on the GPU: torch.library.opcheck of every custom op,
+a torch.compile(fullgraph) trace of a decode layer built from them against the
+eager operators (bit-exact: the same HIP launches run), and HIP-graph capture."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def fdl():
+    import fused_decode._lib as L
+    import fused_decode  # noqa: F401
+
+    L.lib()  # raises if the HIP library is missing
+    return torch.ops.fused_decode
+
+
+def rnd(*shape, seed, scale=1.0, mean=0.0, dtype=torch.float16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale + mean).to(dtype).to(DEV)
+
+
+def layer_inputs(m=2, h=256, i=512, heads=2, kv=1, d=64):
+    n = (heads + 2 * kv) * d
+    return dict(
+        x=rnd(m, h, seed=1), nw1=rnd(h, seed=2, scale=0.1, mean=1.0), wqkv=rnd(n, h, seed=3, scale=h ** -0.5),
+        cos=rnd(1, d, seed=4), sin=rnd(1, d, seed=5), attn=rnd(m, h, seed=6), wo=rnd(h, h, seed=7, scale=h ** -0.5),
+        nw2=rnd(h, seed=8, scale=0.1, mean=1.0), wgu=rnd(2 * i, h, seed=9, scale=h ** -0.5),
+        wd=rnd(h, i, seed=10, scale=i ** -0.5), rc=(heads + kv) * d)
+
+
+def test_opcheck_every_op(fdl):
+    t = layer_inputs()
+    x, nw = t["x"], t["nw1"]
+    q = rnd(1, 3, 4, 64, seed=11)
+    cs, sn = rnd(3, 1, 64, seed=12), rnd(3, 1, 64, seed=13)
+    cases = [
+        (fdl.rms_norm, (x, nw, 1e-5)),
+        (fdl.add_rms_norm, (x, t["attn"], nw, 1e-5)),
+        (fdl.rope, (q, cs, sn)),
+        (fdl.swiglu, (x, t["attn"])),
+        (fdl.linear_decode, (x, t["wo"], None, t["attn"], "simt")),
+        (fdl.post_attn_mlp, (x, nw, t["wgu"], t["wd"], 1e-5, None)),
+        (fdl.pre_attn_qkv, (x, nw, t["wqkv"], t["cos"], t["sin"], 1e-5, t["rc"], None, "dot")),
+    ]
+    for op, args in cases:
+        torch.library.opcheck(op, args)
+
+
+def test_compiled_layer_matches_eager_operators(fdl):
+    import fused_decode as fd
+
+    t = layer_inputs()
+
+    def layer_ops(x):
+        qkv = fdl.pre_attn_qkv(x, t["nw1"], t["wqkv"], t["cos"], t["sin"], 1e-5, t["rc"])
+        h = fdl.linear_decode(t["attn"], t["wo"], None, x)
+        return fdl.post_attn_mlp(h, t["nw2"], t["wgu"], t["wd"], 1e-5), qkv
+
+    def layer_eager(x):
+        qkv = fd.pre_attn_qkv(x, t["nw1"], t["wqkv"], t["cos"], t["sin"], 1e-5, rope_cols=t["rc"])
+        h = fd.linear_decode(t["attn"], t["wo"], row_add=x)
+        return fd.post_attn_mlp(h, t["nw2"], t["wgu"], t["wd"], 1e-5), qkv
+
+    compiled = torch.compile(layer_ops, backend="aot_eager", fullgraph=True)
+    y_c, qkv_c = compiled(t["x"])
+    y_e, qkv_e = layer_eager(t["x"])
+    torch.testing.assert_close(y_c, y_e, rtol=0, atol=0)
+    torch.testing.assert_close(qkv_c, qkv_e, rtol=0, atol=0)
+
+
+def test_custom_ops_capture_in_a_hip_graph(fdl):
+    t = layer_inputs(m=1)
+    x = t["x"]
+    ref = fdl.post_attn_mlp(x, t["nw2"], t["wgu"], t["wd"], 1e-5).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fdl.post_attn_mlp(x, t["nw2"], t["wgu"], t["wd"], 1e-5)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = fdl.post_attn_mlp(x, t["nw2"], t["wgu"], t["wd"], 1e-5)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, ref, rtol=0, atol=0)
