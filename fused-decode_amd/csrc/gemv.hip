@@ -805,23 +805,44 @@ int pick_waves(int64_t items) {
   return kMaxWaves;
 }
 
-template <typename T, int M>
-void launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
-                 int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
-  constexpr int R = SimtRows<M>::R;
-  const int nw = pick_waves((K + kChunk - 1) / kChunk);
+// Tiling of one GEMV launch; 0 = the default for the kernel that runs.
+struct Tile {
+  int rows;    // weight rows per workgroup (SIMT 2, 4, 8; MFMA 16)
+  int waves;   // waves per workgroup, 1..8
+  int stages;  // MFMA K units per wave and iteration (1, 2); SIMT 1
+};
+
+template <typename T, int M, int R>
+void launch_simt_r(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                   int64_t sym, int64_t syn, const Epi& e, int nw, hipStream_t st) {
   const unsigned blocks = (unsigned)((N + R - 1) / R);
   hipLaunchKernelGGL((gemv_simt_kernel<T, M, R, kNtWeights>), dim3(blocks), dim3(nw * kWave), 0, st,
                      static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), N,
                      K, sxm, swn, sym, syn, e);
 }
 
+// Default: 4 rows, waves = the largest divisor of the K chunks up to 8. Rows 8
+// exist up to M = 8 (R*M accumulators per lane).
+template <typename T, int M>
+void launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                 int64_t sym, int64_t syn, const Epi& e, const Tile& t, hipStream_t st) {
+  const int nw = t.waves ? t.waves : pick_waves((K + kChunk - 1) / kChunk);
+  const int rows = t.rows ? t.rows : SimtRows<M>::R;
+  if (rows == 2)
+    launch_simt_r<T, M, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
+  else if (rows == 8 && M <= 8)
+    launch_simt_r<T, M, (M <= 8 ? 8 : 4)>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
+  else
+    launch_simt_r<T, M, 4>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
+}
+
 template <typename T>
 void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
-                   int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+                   int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Tile& t,
+                   hipStream_t st) {
   switch (M) {
 #define FD_CASE(MM) \
-  case MM: launch_simt<T, MM>(y, x, w, N, K, sxm, swn, sym, syn, e, st); break;
+  case MM: launch_simt<T, MM>(y, x, w, N, K, sxm, swn, sym, syn, e, t, st); break;
     FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
     FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
     FD_CASE(16)
@@ -833,8 +854,9 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
 template <typename T>
 void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
-                 const Rope* rp = nullptr) {
-  const int nw = pick_waves((K + kUnit - 1) / kUnit);
+                 const Rope* rp = nullptr, const Tile* t = nullptr) {
+  const int nw = t && t->waves ? t->waves : pick_waves((K + kUnit - 1) / kUnit);
+  const int stages = t && t->stages ? t->stages : (N >= 16384 ? 1 : 2);
   Rope none{};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
@@ -846,9 +868,9 @@ void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int
                      dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), \
                      static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e, r)
   if (rp) {
-    if (N >= 16384) FD_MFMA(1, true); else FD_MFMA(2, true);
+    if (stages == 1) FD_MFMA(1, true); else FD_MFMA(2, true);
   } else {
-    if (N >= 16384) FD_MFMA(1, false); else FD_MFMA(2, false);
+    if (stages == 1) FD_MFMA(1, false); else FD_MFMA(2, false);
   }
 #undef FD_MFMA
 }
@@ -988,11 +1010,28 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   return FD_OK;
 }
 
+bool linear_uses_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
+
+// Tile values the kernel that will run accepts (0 = default).
+int check_tile(const Tile& t, int64_t M, int kind) {
+  if (t.waves < 0 || t.waves > kMaxWaves) return set_error(FD_EINVAL, "waves must be in [0, 8]");
+  if (linear_uses_mfma(M, kind)) {
+    if (t.rows != 0 && t.rows != 16) return set_error(FD_EINVAL, "the MFMA GEMV has 16 rows per workgroup");
+    if (t.stages < 0 || t.stages > 2) return set_error(FD_EINVAL, "MFMA stages must be 0, 1 or 2");
+  } else {
+    if (t.rows != 0 && t.rows != 2 && t.rows != 4 && t.rows != 8)
+      return set_error(FD_EINVAL, "SIMT rows per workgroup must be 2, 4 or 8");
+    if (t.rows == 8 && M > 8) return set_error(FD_EINVAL, "8 SIMT rows per workgroup need M <= 8");
+    if (t.stages < 0 || t.stages > 1) return set_error(FD_EINVAL, "SIMT stages must be 0 or 1");
+  }
+  return FD_OK;
+}
+
 // Launch the GEMV that fits the operands: the vector kernels need unit K
 // stride, K % 8 == 0 and 16-byte aligned rows; anything else takes the generic one.
 int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t M, int64_t N,
                     int64_t K, int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sym,
-                    int64_t syn, int kind, int act_dtype, hipStream_t st) {
+                    int64_t syn, int kind, int act_dtype, hipStream_t st, const Tile& t = Tile{}) {
   const bool fast = K % 8 == 0 && swk == 1 && sxk == 1 && aligned16(w) && aligned16(x) &&
                     (N == 1 || swn % 8 == 0) && (M == 1 || sxm % 8 == 0) && N <= 0x7fffffffLL &&
                     K <= 0x7fffffffLL;
@@ -1007,17 +1046,17 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
                          e);
     return FD_OK;
   }
-  const bool mfma = kind == FD_KIND_DOT && M >= kMfmaMinM;
+  const bool mfma = linear_uses_mfma(M, kind);
   if (act_dtype == FD_F16) {
     if (mfma)
-      launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+      launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
     else
-      launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+      launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   } else {
     if (mfma)
-      launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+      launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
     else
-      launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+      launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   }
   return FD_OK;
 }
@@ -1027,11 +1066,12 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
 
 using namespace fd;
 
-extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
-                         const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
-                         int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb,
-                         int64_t srm, int64_t srn, int64_t sym, int64_t syn, int kind,
-                         int act_dtype, void* stream) {
+extern "C" int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias,
+                               int bias_dtype, const void* row_add, int row_dtype, int64_t M,
+                               int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swn,
+                               int64_t swk, int64_t sb, int64_t srm, int64_t srn, int64_t sym,
+                               int64_t syn, const fd_tile* tile, int kind, int act_dtype,
+                               void* stream) {
   if (!check_act_dtype(act_dtype)) return FD_EINVAL;
   if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
     return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
@@ -1043,6 +1083,14 @@ extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias
   if (bias && bias_dtype != act_dtype && bias_dtype != FD_F32)
     return set_error(FD_EINVAL, "bias must match x or be float32");
   if (row_add && !check_any_dtype(row_dtype, "row_dtype")) return FD_EINVAL;
+  Tile t{0, 0, 0};
+  if (tile) {
+    t.rows = tile->rows;
+    t.waves = tile->waves;
+    t.stages = tile->stages;
+    const int rc = check_tile(t, M, kind);
+    if (rc != FD_OK) return rc;
+  }
   if (M == 0 || N == 0) return FD_OK;
   if (!y || !w || (!x && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
   Epi e;
@@ -1054,9 +1102,18 @@ extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias
   e.srm = srm;
   e.srn = srn;
   const int rc = linear_dispatch(y, x, w, e, M, N, K, sxm, sxk, swn, swk, sym, syn, kind,
-                                 act_dtype, static_cast<hipStream_t>(stream));
+                                 act_dtype, static_cast<hipStream_t>(stream), t);
   if (rc != FD_OK) return rc;
   return check_launch();
+}
+
+extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+                         const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+                         int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb,
+                         int64_t srm, int64_t srn, int64_t sym, int64_t syn, int kind,
+                         int act_dtype, void* stream) {
+  return fd_linear_tiled(y, x, w, bias, bias_dtype, row_add, row_dtype, M, N, K, sxm, sxk, swn,
+                         swk, sb, srm, srn, sym, syn, nullptr, kind, act_dtype, stream);
 }
 
 namespace fd {

@@ -25,6 +25,13 @@ DTYPE_CODE = {torch.float16: FD_F16, torch.bfloat16: FD_BF16, torch.float32: FD_
 KIND_CODE = {"dot": FD_KIND_DOT, "simt": FD_KIND_SIMT}
 
 
+class FdTile(ctypes.Structure):
+    """``fd_tile``: weight rows per workgroup, waves per workgroup, MFMA K units in
+    flight per wave (0 = the library default for that field)."""
+
+    _fields_ = [("rows", ctypes.c_int), ("waves", ctypes.c_int), ("stages", ctypes.c_int)]
+
+
 class FdRows(ctypes.Structure):
     """``fd_rows``: a*b*c rows of n elements; row (i,j,l) at i*sa+j*sb+l*sc."""
 
@@ -55,6 +62,8 @@ SIGNATURES: dict[str, list] = {
     "fd_swiglu": [_p, _p, _p, _rows, _rows, _rows, _i, _p],
     "fd_rope": [_p, _p, _p, _p, _i, _rows, _rows, _rows, _rows, _i, _p],
     "fd_linear": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _i, _p],
+    "fd_linear_tiled": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l,
+                        ctypes.POINTER(FdTile), _i, _i, _p],
     "fd_post_attn_mlp": [_p, _p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p],
     "fd_mlp_gate_up": [_p, _p, _p, _p, _i, _p, _l, _l, _l, _f, _i, _i, _p],
     "fd_pre_attn_qkv": [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i,

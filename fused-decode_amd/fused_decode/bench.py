@@ -1,6 +1,6 @@
 """Per-operator roofline and latency bench on one MI355X.
 
-    python -m fused_decode.bench [--out results.json] [--quick] [--dtype fp16|bf16|both]
+    python -m fused_decode.bench [--out results.json] [--quick] [--dtype fp16|bf16|both] [--tune [--tune-out tiles.json]]
 
 Mirrors the reference's bench (src/fused_decode/bench.py): an in-process copy
 roof, HIP-event medians (10 warmup calls, then `rounds` rounds of back-to-back
@@ -30,7 +30,7 @@ import time
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, kernels
 from .kernels import launch_copy, launch_triad
 from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope, swiglu
 
@@ -380,6 +380,76 @@ def bench_qkv(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
+TIE_BAND = 1.05  # per-shape slack of the cutoff rule
+
+
+def tune(dtype, out_path: str | None = None) -> dict:
+    """Tile search for the HIP GEMV on this GPU (replaces the reference's Triton
+    tile sweep, bench.py:475-517): for every decode weight shape and M = 1..16,
+    each kernel that can run (SIMT; MFMA for kind "dot" from 8 rows) is timed
+    over its tiles (graph-replayed device time, cold weights) next to F.linear.
+    Returns and optionally writes the table ``linear_config`` reads: the best
+    tile per (kernel, N, K, M) where it beats the default by 3% or more, and
+    the value for DECODE_LINEAR_MAX_M: the largest M up to which, at every row
+    count, the default kind's best tiles run a decode layer's four GEMVs faster
+    in sum than F.linear with no shape more than 5% slower (``strict_max_m``:
+    every shape faster)."""
+    g = torch.Generator(device="cuda").manual_seed(4)
+    e = torch.empty((), dtype=dtype).element_size()
+    shapes = [(4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)]
+    entries, best_us, default_us, hip_us = {}, {}, {}, {}
+    for n, kk in shapes:
+        k = copies_for(n * kk * e)
+        ws = [_gen((n, kk), dtype, g, kk ** -0.5) for _ in range(k)]
+        for m in range(1, 17):
+            x = _gen((m, kk), dtype, g)
+            out = torch.empty(m, n, device="cuda", dtype=dtype)
+            hip_us[f"{n}x{kk}:m{m}"] = graph_us(lambda i: F.linear(x, ws[i % k]), k)
+            for kern in ("simt", "dot"):
+                if kern == "dot" and m < 8:
+                    continue
+                dflt = kernels.default_tile(kern, n, kk)
+                if kern == "dot":
+                    cands = {(16, w, st) for w in (4, 8, dflt[1]) for st in (1, 2)}
+                else:
+                    cands = {(r, w, 1) for r in (2, 4, 8) if r * m <= 64 for w in (4, 8, dflt[1])}
+                cands.add(dflt)
+                times = {}
+                for t in sorted(cands):
+                    us = graph_us(lambda i, t=t: kernels.linear_out(x, ws[i % k], out, kind=kern, tile=t), k)
+                    if us is not None:
+                        times[t] = us
+                key = f"{kern}:{n}x{kk}:m{m}"
+                best = min(times, key=times.get)
+                best_us[key], default_us[key] = times[best], times[dflt]
+                if best != dflt and times[best] <= 0.97 * times[dflt]:
+                    entries[key] = list(best)
+                print(f"{key:<24} default {dflt} {times[dflt]:8.2f} us  best {best} {times[best]:8.2f} us  "
+                      f"F.linear {hip_us[f'{n}x{kk}:m{m}']:8.2f} us", flush=True)
+        del ws
+        torch.cuda.empty_cache()
+    max_m = strict_m = 0
+    for m in range(1, 17):
+        kern = "dot" if m >= 8 else "simt"
+        ours = [best_us[f"{kern}:{n}x{kk}:m{m}"] for n, kk in shapes]
+        theirs = [hip_us[f"{n}x{kk}:m{m}"] for n, kk in shapes]
+        if strict_m == m - 1 and all(a <= b for a, b in zip(ours, theirs)):
+            strict_m = m
+        if max_m == m - 1 and sum(ours) < sum(theirs) and all(a <= TIE_BAND * b for a, b in zip(ours, theirs)):
+            max_m = m
+    table = {"arch": torch.cuda.get_device_properties(0).gcnArchName.split(":")[0],
+             "dtype": str(dtype).replace("torch.", ""), "entries": entries,
+             "best_us": best_us, "default_us": default_us, "hipblas_us": hip_us,
+             "decode_linear_max_m": max_m, "strict_max_m": strict_m}
+    print(f"DECODE_LINEAR_MAX_M: {max_m} (a layer's four GEMVs faster in sum, none more than "
+          f"{100 * (TIE_BAND - 1):.0f}% slower than F.linear); every shape faster up to M={strict_m}; "
+          f"{len(entries)} tiles beat the default by >= 3%", flush=True)
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump(table, f, indent=1, sort_keys=True)
+    return table
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--out", default=None)
@@ -387,9 +457,14 @@ def main() -> None:
     ap.add_argument("--dtype", choices=["fp16", "bf16", "both"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true", help="skip PyTorch-eager-on-CPU timings")
     ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv"], default=None)
+    ap.add_argument("--tune", action="store_true", help="GEMV tile search (writes --tune-out if given)")
+    ap.add_argument("--tune-out", default=None)
     args = ap.parse_args()
     _lib.lib()
     torch.cuda.set_device(0)
+    if args.tune:
+        tune(torch.float16 if args.dtype != "bf16" else torch.bfloat16, args.tune_out)
+        return
     payload = {
         "gpu": torch.cuda.get_device_name(0),
         "torch": torch.__version__,

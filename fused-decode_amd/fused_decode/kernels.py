@@ -10,6 +10,8 @@ be captured into a HIP graph.
 
 from __future__ import annotations
 
+import ctypes
+import json
 import os
 import warnings
 
@@ -17,7 +19,7 @@ import torch
 
 from . import _lib
 from ._layout import finish, joint_layout
-from ._lib import DTYPE_CODE, KIND_CODE, check, lib, stream_of
+from ._lib import DTYPE_CODE, KIND_CODE, FdTile, check, lib, stream_of
 
 _warned: set[str] = set()
 
@@ -122,18 +124,70 @@ def resolve_kind(kind: str | None) -> str:
     return kind
 
 
-def linear_config(kind: str, n: int, k: int) -> tuple[int, int, int]:
-    """Tiling the HIP GEMV picks for ``[N, K]``: (rows per workgroup, K elements per
-    wave step, waves per workgroup). The reference's ``FUSED_DECODE_LINEAR``
-    (block_n,block_k,warps,stages; kernels.py:589-603) is a Triton knob and is
-    ignored with a warning."""
-    if os.environ.get("FUSED_DECODE_LINEAR"):
-        _warn_once("linear", "FUSED_DECODE_LINEAR is a Triton tile knob; the HIP GEMV picks its own tiling")
-    if kind == "dot":
-        items = -(-k // 128)
-        return 16, 128, _waves(items)
-    items = -(-k // 512)
-    return 8, 512, _waves(items)
+# K elements per wave step of each GEMV kernel (a fixed property of the kernel).
+_BLOCK_K = {"simt": 512, "dot": 128}
+_MFMA_MIN_M = 8  # kind "dot" runs the MFMA kernel from this many rows on
+_TILE_TABLE: dict | None = None
+TILE_TABLE_FILE = os.path.join(os.path.dirname(__file__), "tiles_gfx950.json")
+
+
+def _tile_table() -> dict:
+    """Measured tiles per (kind, N, K, M), written by ``python -m fused_decode.bench
+    --tune``; empty when the file is absent."""
+    global _TILE_TABLE
+    if _TILE_TABLE is None:
+        try:
+            with open(TILE_TABLE_FILE) as f:
+                _TILE_TABLE = json.load(f).get("entries", {})
+        except (OSError, ValueError):
+            _TILE_TABLE = {}
+    return _TILE_TABLE
+
+
+def _kernel_of(kind: str, m: int | None) -> str:
+    return "dot" if kind == "dot" and (m is None or m >= _MFMA_MIN_M) else "simt"
+
+
+def tile_key(kind: str, n: int, k: int, m: int) -> str:
+    return f"{_kernel_of(kind, m)}:{n}x{k}:m{m}"
+
+
+def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int, int, int, int]:
+    """Tiling of the HIP GEMV for ``[N, K]`` weights and ``m`` rows: (rows per
+    workgroup, K elements per wave step, waves per workgroup, MFMA K units in
+    flight per wave). The kernel is the MFMA one for kind "dot" from 8 rows (or
+    when ``m`` is None), the SIMT one otherwise.
+
+    ``FUSED_DECODE_LINEAR=block_n,block_k,warps,stages`` overrides it as in the
+    reference (kernels.py:589-603): block_n = rows per workgroup (SIMT 2, 4 or 8;
+    MFMA 16), block_k must be the kernel's step (SIMT 512, MFMA 128), warps =
+    waves (1-8), stages = MFMA K units (1 or 2; SIMT 1). Otherwise the measured
+    table (``tiles_gfx950.json``) decides for its shapes, and the library's
+    defaults for the rest."""
+    kern = _kernel_of(kind, m)
+    forced = os.environ.get("FUSED_DECODE_LINEAR")
+    if forced:
+        try:
+            block_n, block_k, warps, stages = (int(part) for part in forced.split(","))
+        except ValueError as exc:
+            raise ValueError("FUSED_DECODE_LINEAR must be block_n,block_k,warps,stages") from exc
+        if block_k != _BLOCK_K[kern]:
+            raise ValueError(f"FUSED_DECODE_LINEAR block_k must be {_BLOCK_K[kern]} for the {kern} GEMV")
+        return block_n, block_k, warps, stages
+    if m is not None:
+        hit = _tile_table().get(tile_key(kind, n, k, m))
+        if hit:
+            rows, waves, stages = hit
+            return rows, _BLOCK_K[kern], waves, stages
+    rows, waves, stages = default_tile(kern, n, k)
+    return rows, _BLOCK_K[kern], waves, stages
+
+
+def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
+    """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot")."""
+    if kern == "dot":
+        return 16, _waves(-(-k // 128)), 1 if n >= 16384 else 2
+    return 4, _waves(-(-k // 512)), 1
 
 
 def _waves(items: int) -> int:
@@ -153,10 +207,12 @@ def linear_out(
     bias: torch.Tensor | None = None,
     row_add: torch.Tensor | None = None,
     kind: str | None = None,
+    tile: tuple[int, int, int] | None = None,
 ) -> None:
     """``y = x @ weight.T [+ bias] [+ row_add]`` for x ``[M, K]``, M <= 16.
     ``row_add`` is ``[M, N]``, ``[1, N]``, ``[M, 1]`` or ``[1, 1]`` (size-1 dims
-    broadcast). Mirrors kernels.py:741-830."""
+    broadcast). ``tile`` = (rows, waves, stages) overrides ``linear_config``.
+    Mirrors kernels.py:741-830."""
     kind = resolve_kind(kind)
     m, k = x.shape
     n, k_w = weight.shape
@@ -184,13 +240,16 @@ def linear_out(
         row_ptr, row_code = row_add.data_ptr(), DTYPE_CODE[row_add.dtype]
         srm = 0 if row_add.shape[0] == 1 else int(row_add.stride(0))
         srn = 0 if row_add.shape[1] == 1 else int(row_add.stride(1))
-    status = lib().fd_linear(
+    if tile is None:
+        rows, _, waves, stages = linear_config(kind, n, k, m)
+        tile = (rows, waves, stages)
+    status = lib().fd_linear_tiled(
         y.data_ptr(), x.data_ptr(), weight.data_ptr(), bias_ptr, bias_code, row_ptr, row_code,
         m, n, k, int(x.stride(0)), int(x.stride(1)), int(weight.stride(0)), int(weight.stride(1)),
-        sb, srm, srn, int(y.stride(0)), int(y.stride(1)), KIND_CODE[kind], DTYPE_CODE[x.dtype],
-        stream_of(x),
+        sb, srm, srn, int(y.stride(0)), int(y.stride(1)), ctypes.byref(FdTile(*tile)),
+        KIND_CODE[kind], DTYPE_CODE[x.dtype], stream_of(x),
     )
-    check("fd_linear", status)
+    check("fd_linear_tiled", status)
 
 
 def post_attn_mlp_out(

@@ -28,9 +28,11 @@ from .kernels import (
 
 # Largest flattened batch the default dispatcher sends to the HIP GEMV. The
 # reference sets this per GPU from measurement (its RTX 4070 Laptop value is 1,
-# ops.py:16-19); for MI355X it is set from the GEMV-vs-hipBLASLt sweep of the
-# bench (python -m fused_decode.bench).
-DECODE_LINEAR_MAX_M = 8
+# ops.py:16-19); for MI355X it is the `decode_linear_max_m` of the tile search
+# (python -m fused_decode.bench --tune, table in tiles_gfx950.json): up to 10 rows
+# the four GEMVs of a Llama-3-8B layer run faster in sum than hipBLASLt's
+# F.linear, none of them more than 5% slower.
+DECODE_LINEAR_MAX_M = 10
 _HAND_LIMIT = 16
 _ACTIVATION = (torch.float16, torch.bfloat16)
 _NORM_WEIGHT = (torch.float16, torch.bfloat16, torch.float32)

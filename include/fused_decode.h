@@ -118,6 +118,32 @@ int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_
               void* stream);
 
 /*
+ * GEMV tiling: weight rows per workgroup (SIMT kernel 2, 4 or 8 with 8 only up to
+ * M = 8; MFMA kernel 16), waves per workgroup (1..8) and, for the MFMA kernel, K
+ * units of 128 in flight per wave and iteration (1 or 2). 0 = the library's
+ * default for that field. Which kernel runs is decided as in fd_linear (MFMA for
+ * kind FD_KIND_DOT from M = 8).
+ */
+typedef struct fd_tile {
+  int rows;
+  int waves;
+  int stages;
+} fd_tile;
+
+/*
+ * fd_linear with an explicit tiling (`tile` may be NULL: the defaults). A tile
+ * the running kernel does not accept is FD_EINVAL. Replaces the tile override of
+ * kernels.py:589-603 (`linear_config` reading FUSED_DECODE_LINEAR), which the
+ * Python layer maps onto this call, and serves the tile search that replaces
+ * bench.py:475-517 (`tune`).
+ */
+int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+                    const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+                    int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb,
+                    int64_t srm, int64_t srn, int64_t sym, int64_t syn, const fd_tile* tile,
+                    int kind, int act_dtype, void* stream);
+
+/*
  * Llama post-attention MLP for a contiguous hidden [M,H], M <= 16:
  *   h   = round(rms_norm(hidden, norm_w, eps))
  *   g,u = round(h @ w_gate_up[:I].T), round(h @ w_gate_up[I:].T)

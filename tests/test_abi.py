@@ -124,3 +124,22 @@ def test_qkv_rejects(L):
     assert call(cs_rs=-1) == L.FD_EINVAL
     assert call(m=8, kind=0) == L.FD_EINVAL              # kind=dot at 8 rows needs `normed`
     assert call(m=0) == L.FD_OK
+
+
+@nogpu
+def test_tiled_linear_rejects_tiles_the_kernel_cannot_run(L):
+    lib = L.lib()
+
+    def call(m, kind, rows=0, waves=0, stages=0):
+        t = L.FdTile(rows, waves, stages)
+        return lib.fd_linear_tiled(FAKE, FAKE, FAKE, None, 0, None, 0, m, 64, 64, 64, 1, 64, 1, 0, 0, 0,
+                                   64, 1, ctypes.byref(t), kind, 0, None)
+
+    assert call(1, 1, rows=3) == L.FD_EINVAL          # SIMT rows are 2, 4 or 8
+    assert call(9, 1, rows=8) == L.FD_EINVAL          # 8 rows only up to M = 8
+    assert call(1, 1, stages=2) == L.FD_EINVAL        # SIMT has one stage
+    assert call(8, 0, rows=4) == L.FD_EINVAL          # the MFMA kernel has 16 rows
+    assert call(8, 0, stages=3) == L.FD_EINVAL
+    assert call(1, 0, waves=9) == L.FD_EINVAL
+    assert lib.fd_linear_tiled(FAKE, FAKE, FAKE, None, 0, None, 0, 0, 64, 64, 64, 1, 64, 1, 0, 0, 0,
+                               64, 1, None, 1, 0, None) == L.FD_OK   # M = 0, default tile

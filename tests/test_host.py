@@ -82,10 +82,26 @@ def test_rms_block_env_validation(monkeypatch):
         kernels._rms_env()
 
 
-def test_linear_config_tiling():
-    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 8)
-    assert kernels.linear_config("simt", 4096, 14336) == (8, 512, 7)
-    assert kernels.linear_config("simt", 64, 100) == (8, 512, 1)
+def test_linear_config_tiling(monkeypatch):
+    monkeypatch.delenv("FUSED_DECODE_LINEAR", raising=False)
+    monkeypatch.setattr(kernels, "_TILE_TABLE", {})
+    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 8, 2)        # MFMA kernel
+    assert kernels.linear_config("dot", 28672, 4096, 8) == (16, 128, 8, 1)
+    assert kernels.linear_config("dot", 4096, 4096, 1) == (4, 512, 8, 1)      # dot below 8 rows: SIMT
+    assert kernels.linear_config("simt", 4096, 14336) == (4, 512, 7, 1)
+    assert kernels.linear_config("simt", 64, 100) == (4, 512, 1, 1)
+    # a measured table entry wins for its exact shape and row count
+    monkeypatch.setattr(kernels, "_TILE_TABLE", {"simt:4096x4096:m1": [2, 8, 1]})
+    assert kernels.linear_config("simt", 4096, 4096, 1) == (2, 512, 8, 1)
+    assert kernels.linear_config("simt", 4096, 4096, 2) == (4, 512, 8, 1)
+    # the reference's override variable, with this build's meaning of the fields
+    monkeypatch.setenv("FUSED_DECODE_LINEAR", "8,512,4,1")
+    assert kernels.linear_config("simt", 4096, 4096, 1) == (8, 512, 4, 1)
+    with pytest.raises(ValueError, match="block_k must be 128"):
+        kernels.linear_config("dot", 4096, 4096, 8)
+    monkeypatch.setenv("FUSED_DECODE_LINEAR", "64,64,4")
+    with pytest.raises(ValueError, match="block_n,block_k,warps,stages"):
+        kernels.linear_config("simt", 4096, 4096, 1)
 
 
 def test_cpu_tensors_are_rejected_like_the_reference():
@@ -106,3 +122,23 @@ def test_exports_match_reference_surface():
                  "rms_norm", "rope", "swiglu"):
         assert hasattr(fused_decode, name)
     assert 1 <= fused_decode.DECODE_LINEAR_MAX_M <= 16
+
+
+def test_tile_table_matches_the_dispatch_constants():
+    """The committed gfx950 tile table: its cutoff is DECODE_LINEAR_MAX_M, and every
+    entry is a tile the library accepts for its kernel and row count."""
+    import json
+
+    with open(kernels.TILE_TABLE_FILE) as f:
+        table = json.load(f)
+    assert table["arch"] == "gfx950"
+    assert table["decode_linear_max_m"] == ops.DECODE_LINEAR_MAX_M
+    assert 1 <= table["strict_max_m"] <= table["decode_linear_max_m"]
+    for key, (rows, waves, stages) in table["entries"].items():
+        kern, shape, m = key.split(":")
+        m = int(m[1:])
+        assert 1 <= waves <= 8
+        if kern == "dot":
+            assert rows == 16 and stages in (1, 2) and m >= 8
+        else:
+            assert rows in (2, 4, 8) and rows * m <= 64 and stages == 1
