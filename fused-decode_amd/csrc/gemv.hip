@@ -209,7 +209,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
   for (int u0 = wave; u0 < units; u0 += nw * U) {
+    // Issue the iteration's B (x) loads with its weight loads: x comes from L2,
+    // and loading it after the LDS stage put its latency in series with the
+    // weight stream's (measured: 26.5 -> 21.9 us at N=4096, K=14336, M=8).
     u32x4 v[U][4];
+    V8 b[U][4];
 #pragma unroll
     for (int j = 0; j < U; ++j) {
       const int u = u0 + j * nw;
@@ -220,10 +224,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
         const u32x4* q = reinterpret_cast<const u32x4*>(wl[i] + u * kUnit);
         v[j][i] = (lok[i] && in) ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
       }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int kb = u * kUnit + (s2 * 4 + g) * 8;
+        b[j][s2] = (xok && u < units && kb < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+      }
     }
 #pragma unroll
     for (int j = 0; j < U; ++j) {
-      const int u = u0 + j * nw;
       // stage: row 4i+lrow, chunk lchunk -> slot row*16 + (chunk ^ row)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -233,19 +241,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      V8 a[4], b[4];
+      V8 a[4];
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const int chunk = s2 * 4 + g;
         a[s2] = __builtin_bit_cast(V8, tile[r * 16 + (chunk ^ r)]);
-        const int k = u * kUnit + chunk * 8;
-        b[s2] = (xok && u < units && k < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
+      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[j][s2], acc);
     }
   }
   part[wave * kWave + lane] = acc;
@@ -679,7 +685,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   }
 }
 
-// MFMA form of the gate/up launch for M >= 8 (M padded to 16): the RMSNorm of
+// MFMA form of the gate/up launch for M >= kMfmaMinM (M padded to 16): the RMSNorm of
 // hidden is written by a separate row kernel (into the caller's output buffer,
 // which the down projection overwrites last), and this kernel streams a tile of
 // 16 gate rows and the matching 16 up rows per workgroup with the row-contiguous
@@ -714,6 +720,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
   const int units = (H + kUnit - 1) / kUnit;
   for (int u0 = wave; u0 < units; u0 += nw * U) {
     u32x4 vg[U][4], vu[U][4];
+    V8 b[U][4];  // B (normed x) loads issued with the weight loads, as in the GEMV
 #pragma unroll
     for (int jj = 0; jj < U; ++jj) {
       const int u = u0 + jj * nw;
@@ -726,11 +733,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
         vg[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qg) : *qg) : u32x4{0, 0, 0, 0};
         vu[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qu) : *qu) : u32x4{0, 0, 0, 0};
       }
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const int k = u * kUnit + s2 * 32 + g * 8;
+        b[jj][s2] = (xok && u < units && k < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+      }
     }
 #pragma unroll
     for (int jj = 0; jj < U; ++jj) {
-      const int u = u0 + jj * nw;
-      V8 a[4], c[4], b[4];
+      V8 a[4], c[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) tile[(4 * i + lrow) * 16 + (lchunk ^ (4 * i + lrow))] = vg[jj][i];
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -747,18 +758,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        c[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
-        const int k = u * kUnit + s2 * 32 + g * 8;
-        b[s2] = (xok && u < units && k < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
-      }
+      for (int s2 = 0; s2 < 4; ++s2) c[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
-        ag = mfma16(a[s2], b[s2], ag);
-        au = mfma16(c[s2], b[s2], au);
+        ag = mfma16(a[s2], b[jj][s2], ag);
+        au = mfma16(c[s2], b[jj][s2], au);
       }
     }
   }
@@ -791,7 +798,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
 
 namespace {
 
-constexpr int kMfmaMinM = 8;   // kind=dot uses MFMA from this M on
+constexpr int kMfmaMinM = 5;   // kind=dot uses MFMA from this M on (tile search: MFMA wins from 5 rows on every decode shape)
 // Weight streams use nontemporal loads (measured +10-20% over ordinary loads).
 constexpr bool kNtWeights = true;
 constexpr size_t kMaxLds = 160 * 1024;
@@ -856,13 +863,14 @@ void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
                  const Rope* rp = nullptr, const Tile* t = nullptr) {
   const int nw = t && t->waves ? t->waves : pick_waves((K + kUnit - 1) / kUnit);
-  const int stages = t && t->stages ? t->stages : (N >= 16384 ? 1 : 2);
+  const int stages = t && t->stages ? t->stages : 1;
   Rope none{};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
   const Rope& r = rp ? *rp : none;
-  // Two K units per iteration, except on the tallest weights where one unit per
-  // iteration leaves more waves resident (measured at N = 28672).
+  // One K unit per iteration by default: with the x loads issued alongside the
+  // weights, a second unit only costs registers (measured on the four decode
+  // shapes at M = 8 and 16).
 #define FD_MFMA(UU, RR)                                                                    \
   hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, UU, true, RR>), dim3(blocks),          \
                      dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), \
@@ -1010,17 +1018,24 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   return FD_OK;
 }
 
-bool linear_uses_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
+// The kernel a call runs: a tile's row count names it (16 = MFMA, which needs
+// kind=dot; 2, 4, 8 = SIMT); with no rows given, kind=dot runs MFMA from
+// kMfmaMinM rows and SIMT below.
+bool linear_uses_mfma(int64_t M, int kind, const Tile& t = Tile{}) {
+  if (t.rows) return t.rows == 16;
+  return kind == FD_KIND_DOT && M >= kMfmaMinM;
+}
 
 // Tile values the kernel that will run accepts (0 = default).
 int check_tile(const Tile& t, int64_t M, int kind) {
   if (t.waves < 0 || t.waves > kMaxWaves) return set_error(FD_EINVAL, "waves must be in [0, 8]");
-  if (linear_uses_mfma(M, kind)) {
-    if (t.rows != 0 && t.rows != 16) return set_error(FD_EINVAL, "the MFMA GEMV has 16 rows per workgroup");
+  if (t.rows == 16 && kind != FD_KIND_DOT)
+    return set_error(FD_EINVAL, "16 rows per workgroup is the MFMA GEMV (kind=dot only)");
+  if (linear_uses_mfma(M, kind, t)) {
     if (t.stages < 0 || t.stages > 2) return set_error(FD_EINVAL, "MFMA stages must be 0, 1 or 2");
   } else {
     if (t.rows != 0 && t.rows != 2 && t.rows != 4 && t.rows != 8)
-      return set_error(FD_EINVAL, "SIMT rows per workgroup must be 2, 4 or 8");
+      return set_error(FD_EINVAL, "rows per workgroup must be 2, 4 or 8 (SIMT) or 16 (MFMA)");
     if (t.rows == 8 && M > 8) return set_error(FD_EINVAL, "8 SIMT rows per workgroup need M <= 8");
     if (t.stages < 0 || t.stages > 1) return set_error(FD_EINVAL, "SIMT stages must be 0 or 1");
   }
@@ -1046,7 +1061,7 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
                          e);
     return FD_OK;
   }
-  const bool mfma = linear_uses_mfma(M, kind);
+  const bool mfma = linear_uses_mfma(M, kind, t);
   if (act_dtype == FD_F16) {
     if (mfma)
       launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
@@ -1173,7 +1188,7 @@ extern "C" int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const
   int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
   if (rc != FD_OK || M == 0) return rc;
   if (mlp_needs_normed(M, kind)) {
-    if (!normed) return set_error(FD_EINVAL, "kind=dot with M >= 8 needs the normed buffer");
+    if (!normed) return set_error(FD_EINVAL, "kind=dot with M >= 5 needs the normed buffer");
     if (!aligned16(normed)) return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   }
   return mlp_gate_up(mid, normed, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind,
@@ -1242,7 +1257,7 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
     return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   const bool mfma = mlp_needs_normed(M, kind);
   if (mfma && (!normed || !aligned16(normed)))
-    return set_error(FD_EINVAL, "kind=dot with M >= 8 needs a 16-byte aligned normed buffer");
+    return set_error(FD_EINVAL, "kind=dot with M >= 5 needs a 16-byte aligned normed buffer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   Epi e;
   e.bias = bias;

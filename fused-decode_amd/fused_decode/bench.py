@@ -386,10 +386,11 @@ TIE_BAND = 1.05  # per-shape slack of the cutoff rule
 def tune(dtype, out_path: str | None = None) -> dict:
     """Tile search for the HIP GEMV on this GPU (replaces the reference's Triton
     tile sweep, bench.py:475-517): for every decode weight shape and M = 1..16,
-    each kernel that can run (SIMT; MFMA for kind "dot" from 8 rows) is timed
-    over its tiles (graph-replayed device time, cold weights) next to F.linear.
-    Returns and optionally writes the table ``linear_config`` reads: the best
-    tile per (kernel, N, K, M) where it beats the default by 3% or more, and
+    each kind is timed over the tiles of the kernels it may run (kind "simt":
+    SIMT; kind "dot": SIMT, and MFMA from 2 rows; graph-replayed device time,
+    cold weights) next to F.linear. Returns and optionally writes the table
+    ``linear_config`` reads: the best tile per (kind, N, K, M) where it beats
+    the default by 3% or more (its row count names the kernel), and
     the value for DECODE_LINEAR_MAX_M: the largest M up to which, at every row
     count, the default kind's best tiles run a decode layer's four GEMVs faster
     in sum than F.linear with no shape more than 5% slower (``strict_max_m``:
@@ -405,21 +406,19 @@ def tune(dtype, out_path: str | None = None) -> dict:
             x = _gen((m, kk), dtype, g)
             out = torch.empty(m, n, device="cuda", dtype=dtype)
             hip_us[f"{n}x{kk}:m{m}"] = graph_us(lambda i: F.linear(x, ws[i % k]), k)
-            for kern in ("simt", "dot"):
-                if kern == "dot" and m < 8:
-                    continue
-                dflt = kernels.default_tile(kern, n, kk)
-                if kern == "dot":
-                    cands = {(16, w, st) for w in (4, 8, dflt[1]) for st in (1, 2)}
-                else:
-                    cands = {(r, w, 1) for r in (2, 4, 8) if r * m <= 64 for w in (4, 8, dflt[1])}
+            for kind in ("simt", "dot"):
+                dflt = kernels.default_tile(kernels._kernel_of(kind, m), n, kk)
+                cands = {(r, w, 1) for r in (2, 4, 8) if r * m <= 64 for w in (4, 8, dflt[1])}
+                if kind == "dot" and m >= 2:
+                    dw = kernels.default_tile("dot", n, kk)[1]
+                    cands |= {(16, w, st) for w in (4, 8, dw) for st in (1, 2)}
                 cands.add(dflt)
                 times = {}
                 for t in sorted(cands):
-                    us = graph_us(lambda i, t=t: kernels.linear_out(x, ws[i % k], out, kind=kern, tile=t), k)
+                    us = graph_us(lambda i, t=t: kernels.linear_out(x, ws[i % k], out, kind=kind, tile=t), k)
                     if us is not None:
                         times[t] = us
-                key = f"{kern}:{n}x{kk}:m{m}"
+                key = kernels.tile_key(kind, n, kk, m)
                 best = min(times, key=times.get)
                 best_us[key], default_us[key] = times[best], times[dflt]
                 if best != dflt and times[best] <= 0.97 * times[dflt]:
@@ -430,8 +429,7 @@ def tune(dtype, out_path: str | None = None) -> dict:
         torch.cuda.empty_cache()
     max_m = strict_m = 0
     for m in range(1, 17):
-        kern = "dot" if m >= 8 else "simt"
-        ours = [best_us[f"{kern}:{n}x{kk}:m{m}"] for n, kk in shapes]
+        ours = [best_us[kernels.tile_key("dot", n, kk, m)] for n, kk in shapes]
         theirs = [hip_us[f"{n}x{kk}:m{m}"] for n, kk in shapes]
         if strict_m == m - 1 and all(a <= b for a, b in zip(ours, theirs)):
             strict_m = m

@@ -10,7 +10,7 @@ fused form (the default):
     h    = linear_decode(attn, w_o, row_add=x)           # O-proj with the residual fused
     x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
 
-That is four launches per layer at M < 8 (six from 8 rows with kind "dot",
+That is four launches per layer at M < 5 (six from 5 rows with kind "dot",
 where both RMSNorms run as row kernels ahead of MFMA GEMVs). The unfused form
 composes the reference's operators instead, six launches per layer (seven):
 
@@ -36,6 +36,7 @@ import math
 
 import torch
 
+from .kernels import _MFMA_MIN_M
 from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rope
 
 H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
@@ -125,9 +126,9 @@ class DecodeStep:
 
     @property
     def launches_per_layer(self) -> int:
-        """HIP launches one layer issues (the MFMA forms at kind "dot" from 8 rows
+        """HIP launches one layer issues (the MFMA forms at kind "dot" from 5 rows
         add a row kernel for the RMSNorm)."""
-        mfma = (self.kind or "dot") == "dot" and self.m >= 8
+        mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
         mlp = 3 if mfma else 2
         if self.fused:
             return (2 if mfma else 1) + 1 + mlp

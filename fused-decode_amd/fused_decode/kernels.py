@@ -126,7 +126,7 @@ def resolve_kind(kind: str | None) -> str:
 
 # K elements per wave step of each GEMV kernel (a fixed property of the kernel).
 _BLOCK_K = {"simt": 512, "dot": 128}
-_MFMA_MIN_M = 8  # kind "dot" runs the MFMA kernel from this many rows on
+_MFMA_MIN_M = 5  # kind "dot" runs the MFMA kernel from this many rows on (kMfmaMinM in gemv.hip)
 _TILE_TABLE: dict | None = None
 TILE_TABLE_FILE = os.path.join(os.path.dirname(__file__), "tiles_gfx950.json")
 
@@ -145,40 +145,45 @@ def _tile_table() -> dict:
 
 
 def _kernel_of(kind: str, m: int | None) -> str:
+    """The kernel the library runs by default: MFMA ("dot") for kind "dot" from
+    5 rows (or when m is None), SIMT otherwise."""
     return "dot" if kind == "dot" and (m is None or m >= _MFMA_MIN_M) else "simt"
 
 
 def tile_key(kind: str, n: int, k: int, m: int) -> str:
-    return f"{_kernel_of(kind, m)}:{n}x{k}:m{m}"
+    return f"{kind}:{n}x{k}:m{m}"
 
 
 def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int, int, int, int]:
     """Tiling of the HIP GEMV for ``[N, K]`` weights and ``m`` rows: (rows per
     workgroup, K elements per wave step, waves per workgroup, MFMA K units in
-    flight per wave). The kernel is the MFMA one for kind "dot" from 8 rows (or
-    when ``m`` is None), the SIMT one otherwise.
+    flight per wave). 16 rows is the MFMA kernel (kind "dot" only), 2/4/8 the
+    SIMT kernel.
 
     ``FUSED_DECODE_LINEAR=block_n,block_k,warps,stages`` overrides it as in the
-    reference (kernels.py:589-603): block_n = rows per workgroup (SIMT 2, 4 or 8;
-    MFMA 16), block_k must be the kernel's step (SIMT 512, MFMA 128), warps =
-    waves (1-8), stages = MFMA K units (1 or 2; SIMT 1). Otherwise the measured
-    table (``tiles_gfx950.json``) decides for its shapes, and the library's
-    defaults for the rest."""
-    kern = _kernel_of(kind, m)
+    reference (kernels.py:589-603): block_n = rows per workgroup, block_k the
+    kernel's step (SIMT 512, MFMA 128), warps = waves (1-8), stages = MFMA K
+    units (1 or 2; SIMT 1). Otherwise the measured table
+    (``tiles_gfx950.json``, per kind, N, K and M) decides for its shapes, and
+    the library's defaults (MFMA for "dot" from 5 rows) for the rest."""
     forced = os.environ.get("FUSED_DECODE_LINEAR")
     if forced:
         try:
             block_n, block_k, warps, stages = (int(part) for part in forced.split(","))
         except ValueError as exc:
             raise ValueError("FUSED_DECODE_LINEAR must be block_n,block_k,warps,stages") from exc
+        kern = "dot" if block_n == 16 else "simt"
+        if kern == "dot" and kind != "dot":
+            raise ValueError("FUSED_DECODE_LINEAR block_n 16 is the MFMA GEMV, which needs kind 'dot'")
         if block_k != _BLOCK_K[kern]:
-            raise ValueError(f"FUSED_DECODE_LINEAR block_k must be {_BLOCK_K[kern]} for the {kern} GEMV")
+            raise ValueError(f"FUSED_DECODE_LINEAR block_k must be {_BLOCK_K[kern]} for block_n {block_n}")
         return block_n, block_k, warps, stages
     if m is not None:
         hit = _tile_table().get(tile_key(kind, n, k, m))
         if hit:
             rows, waves, stages = hit
-            return rows, _BLOCK_K[kern], waves, stages
+            return rows, _BLOCK_K["dot" if rows == 16 else "simt"], waves, stages
+    kern = _kernel_of(kind, m)
     rows, waves, stages = default_tile(kern, n, k)
     return rows, _BLOCK_K[kern], waves, stages
 
@@ -186,7 +191,7 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
 def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
     """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot")."""
     if kern == "dot":
-        return 16, _waves(-(-k // 128)), 1 if n >= 16384 else 2
+        return 16, _waves(-(-k // 128)), 1
     return 4, _waves(-(-k // 512)), 1
 
 
@@ -296,7 +301,7 @@ def pre_attn_qkv_out(
     """Fused RMSNorm + QKV GEMV + RoPE for contiguous ``hidden [M, H]`` (M <= 16)
     into contiguous ``out [M, N]``; ``cos``/``sin`` are contiguous rows of
     ``head_dim`` (row stride ``cs_row_stride``, 0 = shared). ``normed`` is ``[M, H]``
-    scratch for kind=dot at M >= 8. Returns the library status (FD_EUNSUPPORTED
+    scratch for kind=dot at M >= 5. Returns the library status (FD_EUNSUPPORTED
     lets the caller compose the operators instead)."""
     m, h = hidden.shape
     n = w_qkv.shape[0]

@@ -17,6 +17,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .kernels import (
+    _MFMA_MIN_M,
     linear_out,
     post_attn_mlp_out,
     pre_attn_qkv_out,
@@ -29,10 +30,11 @@ from .kernels import (
 # Largest flattened batch the default dispatcher sends to the HIP GEMV. The
 # reference sets this per GPU from measurement (its RTX 4070 Laptop value is 1,
 # ops.py:16-19); for MI355X it is the `decode_linear_max_m` of the tile search
-# (python -m fused_decode.bench --tune, table in tiles_gfx950.json): up to 10 rows
-# the four GEMVs of a Llama-3-8B layer run faster in sum than hipBLASLt's
-# F.linear, none of them more than 5% slower.
-DECODE_LINEAR_MAX_M = 10
+# (python -m fused_decode.bench --tune, table in tiles_gfx950.json): at every row
+# count up to 16 the four GEMVs of a Llama-3-8B layer run faster in sum than
+# hipBLASLt's F.linear, none of them more than 5% slower (each strictly faster
+# up to 14 rows), so the HIP GEMV is the default over the whole hand range.
+DECODE_LINEAR_MAX_M = 16
 _HAND_LIMIT = 16
 _ACTIVATION = (torch.float16, torch.bfloat16)
 _NORM_WEIGHT = (torch.float16, torch.bfloat16, torch.float32)
@@ -392,7 +394,7 @@ def pre_attn_qkv(
     or ``[..., 1, D]`` per token). Returns ``[..., N]`` equal to
     ``rope(linear_decode(rms_norm(hidden), w_qkv, bias)[..., :rope_cols])`` with
     the reference's rounding after each step. Up to the GEMV row limit this is one
-    HIP launch (two for kind "dot" from 8 rows: the norm runs as a row kernel).
+    HIP launch (two for kind "dot" from 5 rows: the norm runs as a row kernel).
     No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
     :138-160.
     """
@@ -455,7 +457,7 @@ def pre_attn_qkv(
         nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
         b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
         normed = None
-        if kind_r == "dot" and m >= 8:
+        if kind_r == "dot" and m >= _MFMA_MIN_M:
             normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
         status = pre_attn_qkv_out(h2, nw, w_qkv, b, cos_r, sin_r, rs, rope_cols, d, eps, y2,
                                   normed, kind_r)

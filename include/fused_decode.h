@@ -118,11 +118,12 @@ int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_
               void* stream);
 
 /*
- * GEMV tiling: weight rows per workgroup (SIMT kernel 2, 4 or 8 with 8 only up to
- * M = 8; MFMA kernel 16), waves per workgroup (1..8) and, for the MFMA kernel, K
- * units of 128 in flight per wave and iteration (1 or 2). 0 = the library's
- * default for that field. Which kernel runs is decided as in fd_linear (MFMA for
- * kind FD_KIND_DOT from M = 8).
+ * GEMV tiling: weight rows per workgroup, which also names the kernel (2, 4 or 8:
+ * the SIMT kernel, 8 only up to M = 8; 16: the MFMA kernel, kind FD_KIND_DOT
+ * only), waves per workgroup (1..8) and, for the MFMA kernel, K units of 128 in
+ * flight per wave and iteration (1 or 2). 0 = the library's default for that
+ * field; with rows 0 the kernel is chosen as in fd_linear (MFMA for kind
+ * FD_KIND_DOT from M = 5).
  */
 typedef struct fd_tile {
   int rows;
@@ -151,7 +152,7 @@ int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias, int
  *   y   = round(mid @ w_down.T + hidden)
  * w_gate_up is [2I,H] (gate rows above up rows), w_down is [H,I], both contiguous.
  * `mid` is caller-owned scratch of M*I activation elements. Two launches (three for
- * kind FD_KIND_DOT at M >= 8, whose RMSNorm runs as its own row kernel into y).
+ * kind FD_KIND_DOT at M >= 5, whose RMSNorm runs as its own row kernel into y).
  * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
  * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
  */
@@ -163,7 +164,7 @@ int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
 /*
  * The gate/up half of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u))
  * with g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
- * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 8 the RMSNorm is
+ * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 5 the RMSNorm is
  * written to `normed` ([M,H] activation scratch, 16-byte aligned) by a row kernel
  * before the MFMA gate/up kernel reads it; otherwise `normed` is unused (may be
  * NULL) and a single kernel normalises in its prologue. For callers that run their
@@ -176,7 +177,7 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
 
 /*
  * Pre-attention QKV projection of a decode step in one launch (two for kind
- * FD_KIND_DOT at M >= 8):
+ * FD_KIND_DOT at M >= 5):
  *   h   = round(rms_norm(hidden, norm_w, eps))                       [M,H]
  *   qkv = round(h @ w_qkv.T + bias)                                  [M,N]
  *   y   = qkv with rope(qkv[:, :rope_cols] viewed as heads of head_dim, cos, sin)
@@ -186,7 +187,7 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
  * [M,N] are contiguous; bias ([N], bias_dtype) may be NULL. rope_cols is a
  * multiple of head_dim (0: no rotation); this build needs head_dim % 16 == 0 and
  * H % 8 == 0 (FD_EUNSUPPORTED otherwise: compose fd_rms_norm, fd_linear, fd_rope).
- * With kind FD_KIND_DOT and M >= 8 the RMSNorm goes to `normed` ([M,H], 16-byte
+ * With kind FD_KIND_DOT and M >= 5 the RMSNorm goes to `normed` ([M,H], 16-byte
  * aligned) first; otherwise `normed` is unused and may be NULL.
  * No reference counterpart as one call: it fuses the composition a caller of the
  * reference writes from rms_norm (ops.py:72-88), linear_decode (ops.py:212-280)

@@ -103,6 +103,8 @@ def test_mlp_rejects(L):
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 0, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 60, 128, 1e-6, 0, 0, None) == L.FD_EUNSUPPORTED
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, 64, 128, 1e-6, 0, 0, None) == L.FD_OK
+    # kind=dot takes the MFMA route (RMSNorm row kernel into `normed`) from 5 rows
+    assert lib.fd_mlp_gate_up(FAKE, None, FAKE, FAKE, 0, FAKE, 5, 64, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
 
 
 @nogpu
@@ -138,7 +140,8 @@ def test_tiled_linear_rejects_tiles_the_kernel_cannot_run(L):
     assert call(1, 1, rows=3) == L.FD_EINVAL          # SIMT rows are 2, 4 or 8
     assert call(9, 1, rows=8) == L.FD_EINVAL          # 8 rows only up to M = 8
     assert call(1, 1, stages=2) == L.FD_EINVAL        # SIMT has one stage
-    assert call(8, 0, rows=4) == L.FD_EINVAL          # the MFMA kernel has 16 rows
+    assert call(1, 1, rows=16) == L.FD_EINVAL         # 16 rows = the MFMA kernel, kind dot only
+    assert call(8, 0, rows=5) == L.FD_EINVAL
     assert call(8, 0, stages=3) == L.FD_EINVAL
     assert call(1, 0, waves=9) == L.FD_EINVAL
     assert lib.fd_linear_tiled(FAKE, FAKE, FAKE, None, 0, None, 0, 0, 64, 64, 64, 1, 64, 1, 0, 0, 0,

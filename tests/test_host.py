@@ -85,9 +85,12 @@ def test_rms_block_env_validation(monkeypatch):
 def test_linear_config_tiling(monkeypatch):
     monkeypatch.delenv("FUSED_DECODE_LINEAR", raising=False)
     monkeypatch.setattr(kernels, "_TILE_TABLE", {})
-    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 8, 2)        # MFMA kernel
+    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 8, 1)        # MFMA kernel
     assert kernels.linear_config("dot", 28672, 4096, 8) == (16, 128, 8, 1)
     assert kernels.linear_config("dot", 4096, 4096, 1) == (4, 512, 8, 1)      # dot below 8 rows: SIMT
+    monkeypatch.setattr(kernels, "_TILE_TABLE", {"dot:4096x4096:m4": [16, 8, 1]})
+    assert kernels.linear_config("dot", 4096, 4096, 4) == (16, 128, 8, 1)     # the table picks MFMA
+    monkeypatch.setattr(kernels, "_TILE_TABLE", {})
     assert kernels.linear_config("simt", 4096, 14336) == (4, 512, 7, 1)
     assert kernels.linear_config("simt", 64, 100) == (4, 512, 1, 1)
     # a measured table entry wins for its exact shape and row count
@@ -98,7 +101,11 @@ def test_linear_config_tiling(monkeypatch):
     monkeypatch.setenv("FUSED_DECODE_LINEAR", "8,512,4,1")
     assert kernels.linear_config("simt", 4096, 4096, 1) == (8, 512, 4, 1)
     with pytest.raises(ValueError, match="block_k must be 128"):
+        monkeypatch.setenv("FUSED_DECODE_LINEAR", "16,512,8,1")
         kernels.linear_config("dot", 4096, 4096, 8)
+    monkeypatch.setenv("FUSED_DECODE_LINEAR", "16,128,8,1")
+    with pytest.raises(ValueError, match="kind 'dot'"):
+        kernels.linear_config("simt", 4096, 4096, 8)
     monkeypatch.setenv("FUSED_DECODE_LINEAR", "64,64,4")
     with pytest.raises(ValueError, match="block_n,block_k,warps,stages"):
         kernels.linear_config("simt", 4096, 4096, 1)
@@ -135,10 +142,10 @@ def test_tile_table_matches_the_dispatch_constants():
     assert table["decode_linear_max_m"] == ops.DECODE_LINEAR_MAX_M
     assert 1 <= table["strict_max_m"] <= table["decode_linear_max_m"]
     for key, (rows, waves, stages) in table["entries"].items():
-        kern, shape, m = key.split(":")
+        kind, shape, m = key.split(":")
         m = int(m[1:])
-        assert 1 <= waves <= 8
-        if kern == "dot":
-            assert rows == 16 and stages in (1, 2) and m >= 8
+        assert kind in ("dot", "simt") and 1 <= waves <= 8
+        if rows == 16:
+            assert kind == "dot" and stages in (1, 2)
         else:
             assert rows in (2, 4, 8) and rows * m <= 64 and stages == 1
