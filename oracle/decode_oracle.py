@@ -139,6 +139,82 @@ def bytes_qkv(m: int, h: int, n: int, head_dim: int, cs_rows: int, e: int = 2, c
     return (n * h + m * h + h + m * n) * e + 2 * cs_rows * head_dim * ce
 
 
+# ---------------------------------------------------------------- fp8 weights
+# OCP FP8 E4M3 ("e4m3fn"): 1 sign, 4 exponent bits (bias 7), 3 mantissa bits;
+# no infinities, 0x7f/0xff are NaN, largest finite 448, subnormals m * 2^-9.
+FP8_MAX = 448.0
+
+
+def fp8_decode(codes) -> np.ndarray:
+    """E4M3 byte codes -> float32 values (exact), from the format's definition."""
+    b = np.asarray(codes, np.uint8).astype(np.int32)
+    sign = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 0x7
+    val = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    val = np.where((b & 0x7F) == 0x7F, np.nan, val)
+    return (sign * val).astype(F32)
+
+
+def fp8_encode(values) -> np.ndarray:
+    """float32 -> E4M3 codes, round to nearest even, |v| > 448 saturated to 448
+    (the quantizer never produces NaN)."""
+    v = np.clip(np.asarray(values, np.float64), -FP8_MAX, FP8_MAX)
+    grid = fp8_decode(np.arange(0x7F, dtype=np.uint8)).astype(np.float64)  # 0 .. 448, ascending
+    mag = np.abs(v)
+    hi = np.clip(np.searchsorted(grid, mag, side="left"), 1, 0x7E)
+    lo = hi - 1
+    d_lo, d_hi = mag - grid[lo], grid[hi] - mag
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo)
+    code = np.where(mag <= grid[0], 0, code)
+    code = np.where(mag >= grid[0x7E], 0x7E, code)
+    return (code | np.where(v < 0, 0x80, 0)).astype(np.uint8)
+
+
+def fp8_quantize(w) -> tuple:
+    """Per-output-channel scaling: scale[n] = max|w[n,:]| / 448 (1 for an all-zero
+    row), codes = encode(w / scale)."""
+    w = np.asarray(w, F32)
+    amax = np.max(np.abs(w), axis=1)
+    scale = np.where(amax > 0, amax / F32(FP8_MAX), F32(1.0)).astype(F32)
+    return fp8_encode(w / scale[:, None]), scale
+
+
+def linear_fp8(x, codes, scale, bias=None, row_add=None, dtype: str = "f16") -> np.ndarray:
+    """round(scale[n] * sum_k decode(codes[n,k]) * x[m,k] + bias[n] + row_add[m,n]):
+    fp32 accumulation of the exact decoded weights, the channel scale applied to
+    the sum, then the reference's epilogue order (kernels.py:657-672)."""
+    acc = np.asarray(x, F32) @ fp8_decode(codes).T
+    y = acc * np.asarray(scale, F32)
+    if bias is not None:
+        y = y + np.asarray(bias, F32)
+    if row_add is not None:
+        ra = np.asarray(row_add, F32)
+        y = y + (ra.reshape(y.shape) if ra.size == y.size else ra)
+    return round_to(y.astype(F32), dtype)
+
+
+def post_attn_mlp_fp8(hidden, norm_w, gu_codes, gu_scale, d_codes, d_scale, eps: float,
+                      dtype: str) -> np.ndarray:
+    """post_attn_mlp (reference.py:66-79) with fp8 weights: the same four rounding
+    points, each projection as linear_fp8."""
+    i = np.shape(d_codes)[1]
+    h = rms_norm(hidden, norm_w, eps, dtype)
+    gu = linear_fp8(h, gu_codes, gu_scale, dtype=dtype)
+    mid = swiglu(gu[..., :i], gu[..., i:], dtype)
+    return linear_fp8(mid, d_codes, d_scale, row_add=hidden, dtype=dtype)
+
+
+def bytes_linear_fp8(m: int, n: int, k: int, e: int = 2) -> int:
+    """fp8 weights (1 byte each) + fp32 scales + activations in and out."""
+    return n * k + 4 * n + (m * k + m * n) * e
+
+
+def bytes_mlp_fp8(m: int, h: int, i: int, e: int = 2) -> int:
+    return 3 * h * i + 4 * (2 * i + h) + (2 * m * h + h) * e
+
+
 # Useful-byte accounting (reference README.md:33-43, bench.py:215-216, :247,
 # :274, :303-305): weights counted once, no cache reuse, e bytes per element.
 def bytes_rms(rows: int, n: int, e: int = 2) -> int:

@@ -277,6 +277,67 @@ def test_pre_attn_qkv_matches_torch_composition_and_per_row_angles():
         np.testing.assert_allclose(one[0], got[r], rtol=1e-5, atol=1e-6)
 
 
+# ---------------------------------------------------------------- fp8 weights
+
+
+def test_fp8_decode_matches_torch_for_every_code():
+    codes = np.arange(256, dtype=np.uint8)
+    ours = O.fp8_decode(codes)
+    lib = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    assert np.array_equal(np.isnan(ours), np.isnan(lib))
+    assert np.array_equal(ours[~np.isnan(ours)], lib[~np.isnan(lib)])
+    assert ours[0x7E] == 448.0 and ours[0x01] == 2.0 ** -9 and ours[0x08] == 2.0 ** -6
+
+
+def test_fp8_encode_matches_torch_rounding_and_saturates():
+    grid = O.fp8_decode(np.arange(0x7F, dtype=np.uint8))
+    ties = (grid[:-1] + grid[1:]) / 2  # every midpoint: round half to even
+    v = np.concatenate([RNG.standard_normal(20000).astype(np.float32) * 60, grid, ties, -ties]).astype(np.float32)
+    lib = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(O.fp8_encode(v), lib)
+    assert O.fp8_encode(np.array([1000.0, -1e9], np.float32)).tolist() == [0x7E, 0xFE]  # saturation, not NaN
+
+
+def test_fp8_quantize_scale_and_error_bound():
+    w = RNG.standard_normal((16, 256)).astype(np.float32) * np.linspace(0.01, 3, 16, dtype=np.float32)[:, None]
+    w[3] = 0.0
+    codes, scale = O.fp8_quantize(w)
+    deq = O.fp8_decode(codes) * scale[:, None]
+    assert scale[3] == 1.0 and not deq[3].any()
+    rows = [r for r in range(16) if r != 3]
+    assert np.allclose(np.abs(deq[rows]).max(1), np.abs(w[rows]).max(1), rtol=1e-6)  # amax maps to 448
+    # E4M3 keeps 3 mantissa bits: relative error <= 2^-4 in the normal range,
+    # absolute <= 2^-10 * scale in the subnormal range
+    err = np.abs(deq - w)
+    bound = np.maximum(np.abs(w) * 2.0 ** -4, scale[:, None] * 2.0 ** -10) * (1 + 1e-6)
+    assert (err <= bound).all()
+
+
+def test_linear_fp8_against_float64_and_the_dequantized_product():
+    x = as_dtype(RNG.standard_normal((3, 96)), "f16")
+    codes, scale = O.fp8_quantize(RNG.standard_normal((40, 96)).astype(np.float32) / 10)
+    bias = RNG.standard_normal(40).astype(np.float32)
+    got = O.linear_fp8(x, codes, scale, bias=bias, dtype="f32")
+    exp = (x.astype(np.float64) @ O.fp8_decode(codes).astype(np.float64).T) * scale + bias
+    np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-5)
+    deq = O.fp8_decode(codes) * scale[:, None]
+    np.testing.assert_allclose(got, O.linear(x, deq, bias=bias, dtype="f32"), rtol=1e-5, atol=1e-5)
+    # a planted mistake: scaling the weights' rows by the wrong channel's scale
+    bad = (x @ O.fp8_decode(codes).T) * scale[::-1] + bias
+    assert not np.allclose(bad, exp, rtol=1e-3)
+
+
+def test_post_attn_mlp_fp8_equals_mlp_of_dequantized_weights():
+    h, i, m = 64, 96, 2
+    hid = as_dtype(RNG.standard_normal((m, h)), "f16")
+    nw = as_dtype(1 + 0.1 * RNG.standard_normal(h), "f16")
+    gq, gs = O.fp8_quantize(RNG.standard_normal((2 * i, h)).astype(np.float32) / 8)
+    dq, ds = O.fp8_quantize(RNG.standard_normal((h, i)).astype(np.float32) / 10)
+    got = O.post_attn_mlp_fp8(hid, nw, gq, gs, dq, ds, 1e-6, "f16")
+    ref = O.post_attn_mlp(hid, nw, O.fp8_decode(gq) * gs[:, None], O.fp8_decode(dq) * ds[:, None], 1e-6, "f16")
+    np.testing.assert_allclose(got, ref, rtol=2e-3, atol=2e-3)
+
+
 # ---------------------------------------------------------------- bytes
 
 
