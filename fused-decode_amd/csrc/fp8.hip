@@ -1,0 +1,382 @@
+// GEMV and fused post-attention MLP with FP8 (OCP E4M3) weights for gfx950.
+//
+//   y[m,n] = round(scale[n] * sum_k e4m3(w[n,k]) * x[m,k] + bias[n] + row_add[m,n])
+//
+// Weights are one byte each with one float32 scale per output row (per-channel
+// quantisation), so a decode GEMV streams half the bytes of the fp16 one. The
+// activations stay fp16/bf16 and the arithmetic float32: weights are decoded
+// exactly, never the activations quantised.
+//
+// Decode: an E4M3 code s.eeee.mmm placed as s.0eeee.mmm0000000 is an fp16 whose
+// value is exactly 2^-8 times the E4M3 value (the exponent bias differs by 8;
+// E4M3 subnormals land on fp16 subnormals). One v_perm spreads two codes to the
+// high bytes of two 16-bit halves and two masked ops finish the pair, so four
+// codes cost five integer ops; the 2^8 goes into the channel scale. fp16
+// activations then use v_dot2 (two products per op into float32); for bf16 ones
+// the pair is re-packed as bf16 (exactly) for v_dot2 bf16.
+//
+// Layout per SIMT step: a lane streams 16 consecutive codes (16 bytes) of each of
+// its workgroup's R rows, so a wave covers 1024 K elements per step.
+#include "fd_gemv.h"
+#include "fd_internal.h"
+
+namespace fd {
+
+constexpr int kChunk8 = 1024;  // K elements one wave covers per fp8 step
+
+// Four E4M3 codes (byte 0 first) -> two fp16 pairs of value * 2^-8.
+__device__ __forceinline__ void fp8x4_to_h2(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  // bytes [0, c0, 0, c1] and [0, c2, 0, c3]: each code in the high byte of a half
+  const uint32_t a = __builtin_amdgcn_perm(0u, w, 0x010c000cu);
+  const uint32_t b = __builtin_amdgcn_perm(0u, w, 0x030c020cu);
+  lo = (a & 0x80008000u) | ((a >> 1) & 0x3f803f80u);
+  hi = (b & 0x80008000u) | ((b >> 1) & 0x3f803f80u);
+}
+
+// acc += sum over 16 elements of (e4m3 weight * 2^-8) * x, x given as two
+// 8-element vectors (elements 0-7, 8-15).
+template <typename T>
+__device__ __forceinline__ float dot_fp8x16(const u32x4& w, const typename Vec8<T>::type& xa,
+                                            const typename Vec8<T>::type& xb, float acc);
+
+template <>
+__device__ __forceinline__ float dot_fp8x16<f16>(const u32x4& w, const f16x8& xa, const f16x8& xb,
+                                                 float acc) {
+  const u32x4 xa2 = __builtin_bit_cast(u32x4, xa), xb2 = __builtin_bit_cast(u32x4, xb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t lo, hi;
+    fp8x4_to_h2(w[i], lo, hi);
+    const uint32_t x0 = i < 2 ? xa2[2 * i] : xb2[2 * i - 4];
+    const uint32_t x1 = i < 2 ? xa2[2 * i + 1] : xb2[2 * i - 3];
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, lo), __builtin_bit_cast(f16x2, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, hi), __builtin_bit_cast(f16x2, x1), acc, false);
+  }
+  return acc;
+}
+
+// bf16 activations: each fp16 pair is widened to float32 (exact) and the upper
+// halves packed as a bf16 pair, which is exact too (at most 4 significant bits),
+// so the products run as v_dot2 bf16 with the activations used as loaded.
+template <>
+__device__ __forceinline__ float dot_fp8x16<bf16>(const u32x4& w, const bf16x8& xa,
+                                                  const bf16x8& xb, float acc) {
+  const u32x4 xa2 = __builtin_bit_cast(u32x4, xa), xb2 = __builtin_bit_cast(u32x4, xb);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t lo, hi;
+    fp8x4_to_h2(w[i], lo, hi);
+    const f16x2 l = __builtin_bit_cast(f16x2, lo), h = __builtin_bit_cast(f16x2, hi);
+    const uint32_t p0 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)l[1]),
+                                              __builtin_bit_cast(uint32_t, (float)l[0]), 0x07060302u);
+    const uint32_t p1 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)h[1]),
+                                              __builtin_bit_cast(uint32_t, (float)h[0]), 0x07060302u);
+    const uint32_t x0 = i < 2 ? xa2[2 * i] : xb2[2 * i - 4];
+    const uint32_t x1 = i < 2 ? xa2[2 * i + 1] : xb2[2 * i - 3];
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p0), __builtin_bit_cast(bf16x2, x0), acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p1), __builtin_bit_cast(bf16x2, x1), acc, false);
+  }
+  return acc;
+}
+
+__device__ __forceinline__ u32x4 load16_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// SIMT fp8 GEMV: R rows per workgroup, waves split K in 1024-element chunks,
+// transposing butterfly + LDS across waves, then scale, bias, row_add, rounding.
+template <typename T, int M, int R>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
+    T* y, const T* x, const uint8_t* w, const float* wscale, int N, int K, int64_t sxm,
+    int64_t swn, int64_t sym, int64_t syn, Epi e) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(R * M);
+  __shared__ float part[kMaxWaves * V];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int64_t n0 = (int64_t)blockIdx.x * R;
+  float acc[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  const uint8_t* wr[R];
+  bool rok[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    rok[r] = n0 + r < N;
+    wr[r] = w + (rok[r] ? n0 + r : 0) * swn;
+  }
+  for (int k = (wave * kWave + lane) * 16; k < K; k += nw * kChunk8) {
+    u32x4 wv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wv[r] = rok[r] ? load16_nt(wr[r] + k) : u32x4{0, 0, 0, 0};
+    V8 xa[M], xb[M];
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      xa[m] = load8<T>(x + m * sxm + k);
+      xb[m] = load8<T>(x + m * sxm + k + 8);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(wv[r], xa[m], xb[m], acc[r * M + m]);
+  }
+  butterfly_sum<V>(acc, lane);
+  if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+  __syncthreads();
+  for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+    const int r = t / M, m = t % M;
+    const int64_t n = n0 + r;
+    if (n < N) {
+      float s = 0.f;
+      for (int i = 0; i < nw; ++i) s += part[i * V + t];
+      y[m * sym + n * syn] = from_f32<T>(epilogue(e, s * 256.f * wscale[n], m, n));
+    }
+  }
+}
+
+// Fused gate/up + SwiGLU with fp8 weights: the RMSNorm prologue of the fp16
+// kernel (normalised rows rounded into LDS), R gate rows and the matching R up
+// rows per tile streamed one K step ahead of the math, and
+// mid = round(silu(round(sg*g)) * round(su*u)).
+template <typename T, int R>
+__device__ __forceinline__ void load_gate_up8(u32x4 (&g)[R], u32x4 (&u)[R], const uint8_t* wgu,
+                                              int tile, int tiles, int k, int H, int I) {
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t j = (int64_t)tile * R + r;
+    const bool ok = tile < tiles && j < I && k < H;
+    g[r] = ok ? load16_nt(wgu + j * H + k) : u32x4{0, 0, 0, 0};
+    u[r] = ok ? load16_nt(wgu + (I + j) * H + k) : u32x4{0, 0, 0, 0};
+  }
+}
+
+template <typename T, int M, int R, bool REGS>
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
+    T* mid, const T* hidden, const void* nwp, int nw_dtype, const uint8_t* wgu,
+    const float* gu_scale, int H, int I, float eps, int tiles) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(2 * R * M);
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int XS = xs_stride(H);
+  T* xs = reinterpret_cast<T*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int step = nw * kChunk8;
+  const int steps = (H + step - 1) / step;
+  const int kbase = (wave * kWave + lane) * 16;
+
+  NormRegs<T, M, kNormRegRows(M)> nr;
+  if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
+  u32x4 gv[R], uv[R];
+  load_gate_up8<T, R>(gv, uv, wgu, blockIdx.x, tiles, kbase, H, I);
+  if constexpr (REGS)
+    norm_store(nr, xs, part, M, H, eps);
+  else
+    stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    const int64_t j0 = (int64_t)tile * R;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int it = 0; it < steps; ++it) {
+      const bool last = it + 1 == steps;
+      u32x4 gn[R], un[R];
+      load_gate_up8<T, R>(gn, un, wgu, last ? tile + (int)gridDim.x : tile, tiles,
+                          kbase + (last ? 0 : (it + 1) * step), H, I);
+      const int k = kbase + it * step;
+      if (k < H) {
+        V8 xa[M], xb[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          xa[m] = load8<T>(xs + m * XS + k);
+          xb[m] = load8<T>(xs + m * XS + k + 8);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            acc[r * M + m] = dot_fp8x16<T>(gv[r], xa[m], xb[m], acc[r * M + m]);
+            acc[R * M + r * M + m] = dot_fp8x16<T>(uv[r], xa[m], xb[m], acc[R * M + r * M + m]);
+          }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        gv[r] = gn[r];
+        uv[r] = un[r];
+      }
+    }
+    butterfly_sum<V>(acc, lane);
+    __syncthreads();  // previous tile's readers of `part` are done
+    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    __syncthreads();
+    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+      const int r = t / M, m = t % M;
+      const int64_t j = j0 + r;
+      if (j < I) {
+        float gs = 0.f, us = 0.f;
+        for (int i = 0; i < nw; ++i) {
+          gs += part[i * V + t];
+          us += part[i * V + R * M + t];
+        }
+        mid[m * (int64_t)I + j] =
+            swiglu_out<T>(gs * 256.f * gu_scale[j], us * 256.f * gu_scale[I + j]);
+      }
+    }
+  }
+}
+
+namespace {
+
+template <int M> struct Fp8Rows { static constexpr int R = M <= 8 ? 4 : 2; };
+template <int M> struct Fp8MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
+
+template <typename T, int M>
+void launch_gemv_fp8(void* y, const void* x, const uint8_t* w, const float* s, int N, int K,
+                     int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                     hipStream_t st) {
+  constexpr int R = Fp8Rows<M>::R;
+  const int nw = pick_waves((K + kChunk8 - 1) / kChunk8);
+  hipLaunchKernelGGL((gemv_fp8_kernel<T, M, R>), dim3((unsigned)((N + R - 1) / R)),
+                     dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), w, s,
+                     N, K, sxm, swn, sym, syn, e);
+}
+
+template <typename T>
+void launch_gemv_fp8_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
+                       int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                       hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: launch_gemv_fp8<T, MM>(y, x, w, s, N, K, sxm, swn, sym, syn, e, st); break;
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+    FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
+    FD_CASE(16)
+#undef FD_CASE
+    default: break;
+  }
+}
+
+template <typename T, int M>
+int launch_mlp_fp8(void* mid, const void* hidden, const void* nw, int nw_dtype,
+                   const uint8_t* wgu, const float* s, int H, int I, float eps, hipStream_t st) {
+  constexpr int R = Fp8MlpRows<M>::R;
+  constexpr int V = pow2_ceil(2 * R * M);
+  const int nwv0 = pick_waves((H + kChunk8 - 1) / kChunk8);
+  const int nwv = M > kNormRegMaxM && nwv0 > 4 ? 4 : nwv0;
+  const size_t lds = fused_lds(M, H, sizeof(T), V);
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  const int tiles = (I + R - 1) / R;
+  const int grid = fused_grid(tiles, lds, 2);
+  auto launch = [&](auto kernel) {
+    if (!allow_lds(kernel, lds))
+      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
+                       static_cast<const T*>(hidden), nw, nw_dtype, wgu, s, H, I, eps, tiles);
+    return (int)FD_OK;
+  };
+  if constexpr (M <= kNormRegMaxM) {
+    if (norm_in_regs(M, H, nwv * kWave)) return launch(mlp_gate_up_fp8_kernel<T, M, R, true>);
+  }
+  return launch(mlp_gate_up_fp8_kernel<T, M, R, false>);
+}
+
+template <typename T>
+int launch_mlp_fp8_m(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
+                     const uint8_t* wgu, const float* s, int H, int I, float eps, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return launch_mlp_fp8<T, MM>(mid, hidden, nw, nw_dtype, wgu, s, H, I, eps, st);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+    FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
+    FD_CASE(16)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "M must be in [1, 16]");
+  }
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
+                             const void* bias, int bias_dtype, const void* row_add, int row_dtype,
+                             int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn,
+                             int64_t sb, int64_t srm, int64_t srn, int64_t sym, int64_t syn,
+                             int act_dtype, void* stream) {
+  using namespace fd;
+  if (!check_act_dtype(act_dtype)) return FD_EINVAL;
+  if (M < 0 || N < 0 || K < 0) return set_error(FD_EINVAL, "negative size");
+  if (M > 16) return set_error(FD_EINVAL, "the fp8 GEMV covers M <= 16");
+  if (sxm < 0 || swn < 0 || sb < 0 || srm < 0 || srn < 0 || sym < 0 || syn < 0)
+    return set_error(FD_EINVAL, "negative stride");
+  if (bias && bias_dtype != act_dtype && bias_dtype != FD_F32)
+    return set_error(FD_EINVAL, "bias must match x or be float32");
+  if (row_add && !check_any_dtype(row_dtype, "row_dtype")) return FD_EINVAL;
+  if (M == 0 || N == 0) return FD_OK;
+  if (!y || !w8 || !w_scale || (!x && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
+  if (K % 16 != 0 || (N > 1 && swn % 16 != 0) || (M > 1 && sxm % 8 != 0))
+    return set_error(FD_EUNSUPPORTED, "the fp8 GEMV needs K %% 16 == 0 and 16-byte aligned rows");
+  if (!aligned16(x) || !aligned16(w8)) return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  if (N > 0x7fffffffLL || K > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
+  Epi e;
+  e.bias = bias;
+  e.bias_dtype = bias_dtype;
+  e.sb = sb;
+  e.row = row_add;
+  e.row_dtype = row_dtype;
+  e.srm = srm;
+  e.srn = srn;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint8_t* w = static_cast<const uint8_t*>(w8);
+  if (act_dtype == FD_F16)
+    launch_gemv_fp8_m<f16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  else
+    launch_gemv_fp8_m<bf16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  return check_launch();
+}
+
+extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* norm_w,
+                                    int norm_w_dtype, const void* w_gate_up8,
+                                    const float* gate_up_scale, const void* w_down8,
+                                    const float* down_scale, int64_t M, int64_t H, int64_t I,
+                                    float eps, int act_dtype, void* stream) {
+  using namespace fd;
+  if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
+    return FD_EINVAL;
+  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
+  if (H <= 0 || I <= 0) return set_error(FD_EINVAL, "H and I must be positive");
+  if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
+  if (M == 0) return FD_OK;
+  if (!y || !mid || !hidden || !norm_w || !w_gate_up8 || !gate_up_scale || !w_down8 || !down_scale)
+    return set_error(FD_EINVAL, "null pointer argument");
+  if (H % 16 != 0 || I % 16 != 0) return set_error(FD_EUNSUPPORTED, "H and I must be multiples of 16");
+  if (H > 0x7fffffffLL || 2 * I > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
+  if (!aligned16(y) || !aligned16(mid) || !aligned16(hidden) || !aligned16(norm_w) ||
+      !aligned16(w_gate_up8) || !aligned16(w_down8))
+    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint8_t* wgu = static_cast<const uint8_t*>(w_gate_up8);
+  int rc = act_dtype == FD_F16
+               ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
+                                       gate_up_scale, (int)H, (int)I, eps, st)
+               : launch_mlp_fp8_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
+                                        gate_up_scale, (int)H, (int)I, eps, st);
+  if (rc != FD_OK) return rc;
+  Epi e;
+  e.bias = nullptr;
+  e.bias_dtype = act_dtype;
+  e.sb = 0;
+  e.row = hidden;
+  e.row_dtype = act_dtype;
+  e.srm = H;
+  e.srn = 1;
+  const uint8_t* wd = static_cast<const uint8_t*>(w_down8);
+  if (act_dtype == FD_F16)
+    launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  else
+    launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  return check_launch();
+}

@@ -17,6 +17,7 @@ from .ops import (
     swiglu,
 )
 
+from .fp8 import dequantize_fp8, linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
 from . import library  # registers torch.ops.fused_decode.* (custom ops with fake kernels)
 
 __version__ = "0.1.0"
@@ -24,6 +25,10 @@ __version__ = "0.1.0"
 __all__ = [
     "DECODE_LINEAR_MAX_M",
     "add_rms_norm",
+    "dequantize_fp8",
+    "linear_decode_fp8",
+    "post_attn_mlp_fp8",
+    "quantize_fp8",
     "linear_decode",
     "post_attn_mlp",
     "pre_attn_qkv",

@@ -62,6 +62,8 @@ SIGNATURES: dict[str, list] = {
     "fd_swiglu": [_p, _p, _p, _rows, _rows, _rows, _i, _p],
     "fd_rope": [_p, _p, _p, _p, _i, _rows, _rows, _rows, _rows, _i, _p],
     "fd_linear": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _i, _p],
+    "fd_linear_fp8": [_p, _p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _p],
+    "fd_post_attn_mlp_fp8": [_p, _p, _p, _p, _i, _p, _p, _p, _p, _l, _l, _l, _f, _i, _p],
     "fd_linear_tiled": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l,
                         ctypes.POINTER(FdTile), _i, _i, _p],
     "fd_post_attn_mlp": [_p, _p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p],

@@ -201,6 +201,36 @@ int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_
                     float eps, int kind, int act_dtype, void* stream);
 
 /*
+ * GEMV with FP8 weights (OCP E4M3, one byte per weight, row stride swn in bytes)
+ * and one float32 scale per output row:
+ *   y[m,n] = round(w_scale[n] * sum_k e4m3(w8[n,k]) * x[m,k] + bias[n] + row_add[m,n])
+ * M <= 16; x [M,K] activations with unit K stride; K % 16 == 0 and 16-byte
+ * aligned rows (else FD_EUNSUPPORTED). bias/row_add as in fd_linear. The
+ * weights are decoded exactly and the arithmetic is float32: the activations
+ * are never quantised.
+ * No reference counterpart: the survey's last "next" item (low-precision weight
+ * formats), halving the bytes the decode GEMV streams.
+ */
+int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
+                  const void* bias, int bias_dtype, const void* row_add, int row_dtype,
+                  int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn, int64_t sb,
+                  int64_t srm, int64_t srn, int64_t sym, int64_t syn, int act_dtype,
+                  void* stream);
+
+/*
+ * fd_post_attn_mlp with FP8 weights: w_gate_up8 [2I,H] and w_down8 [H,I] E4M3
+ * codes (contiguous) with per-row float32 scales gate_up_scale [2I] and
+ * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
+ * rounding points as fd_post_attn_mlp. Two launches (fused RMSNorm + gate/up +
+ * SwiGLU, then down + residual); `mid` is caller scratch of M*I activations.
+ * H % 16 == 0 and I % 16 == 0. No reference counterpart (see fd_linear_fp8).
+ */
+int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* norm_w,
+                         int norm_w_dtype, const void* w_gate_up8, const float* gate_up_scale,
+                         const void* w_down8, const float* down_scale, int64_t M, int64_t H,
+                         int64_t I, float eps, int act_dtype, void* stream);
+
+/*
  * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned
  * pointers take the vector path). c = a + b*scale over n elements of dtype.
  * Replace kernels.py:833-858 (`launch_copy`, `launch_triad`).

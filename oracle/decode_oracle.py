@@ -173,11 +173,11 @@ def fp8_encode(values) -> np.ndarray:
 
 
 def fp8_quantize(w) -> tuple:
-    """Per-output-channel scaling: scale[n] = max|w[n,:]| / 448 (1 for an all-zero
-    row), codes = encode(w / scale)."""
+    """Per-output-channel scaling: scale[n] = max|w[n,:]| * float32(1/448) (1 for an
+    all-zero row), codes = encode(w / scale)."""
     w = np.asarray(w, F32)
     amax = np.max(np.abs(w), axis=1)
-    scale = np.where(amax > 0, amax / F32(FP8_MAX), F32(1.0)).astype(F32)
+    scale = np.where(amax > 0, amax * F32(1.0 / FP8_MAX), F32(1.0)).astype(F32)
     return fp8_encode(w / scale[:, None]), scale
 
 

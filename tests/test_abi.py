@@ -146,3 +146,22 @@ def test_tiled_linear_rejects_tiles_the_kernel_cannot_run(L):
     assert call(1, 0, waves=9) == L.FD_EINVAL
     assert lib.fd_linear_tiled(FAKE, FAKE, FAKE, None, 0, None, 0, 0, 64, 64, 64, 1, 64, 1, 0, 0, 0,
                                64, 1, None, 1, 0, None) == L.FD_OK   # M = 0, default tile
+
+
+@nogpu
+def test_fp8_entry_points_reject(L):
+    lib = L.lib()
+
+    def lin(m=1, k=64, swn=64, x=FAKE):
+        return lib.fd_linear_fp8(FAKE, x, FAKE, FAKE, None, 0, None, 0, m, 32, k, k, swn, 0, 0, 0, 32, 1, 0, None)
+
+    assert lin(m=17) == L.FD_EINVAL
+    assert lin(k=40, swn=40) == L.FD_EUNSUPPORTED     # K % 16
+    assert lin(x=FAKE + 2) == L.FD_EUNSUPPORTED       # misaligned activations
+    assert lib.fd_linear_fp8(FAKE, FAKE, FAKE, None, None, 0, None, 0, 1, 32, 64, 64, 64, 0, 0, 0, 32, 1, 0,
+                             None) == L.FD_EINVAL      # scale is required
+    mlp = lambda m, h, i: lib.fd_post_attn_mlp_fp8(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, FAKE, FAKE, m, h, i,  # noqa: E731
+                                                   1e-6, 0, None)
+    assert mlp(17, 64, 128) == L.FD_EINVAL
+    assert mlp(2, 72, 128) == L.FD_EUNSUPPORTED
+    assert mlp(0, 64, 128) == L.FD_OK

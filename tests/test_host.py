@@ -149,3 +149,17 @@ def test_tile_table_matches_the_dispatch_constants():
             assert kind == "dot" and stages in (1, 2)
         else:
             assert rows in (2, 4, 8) and rows * m <= 64 and stages == 1
+
+
+def test_quantize_fp8_on_cpu_matches_the_oracle():
+    import numpy as np
+
+    from fused_decode.fp8 import quantize_fp8
+    from oracle import decode_oracle as O
+
+    w = torch.randn(24, 96, generator=torch.Generator().manual_seed(3)) * 0.02
+    w[4] = 0
+    q, s = quantize_fp8(w)
+    oq, os_ = O.fp8_quantize(w.numpy())
+    assert q.dtype == torch.float8_e4m3fn and s.dtype == torch.float32
+    assert np.array_equal(q.view(torch.uint8).numpy(), oq) and np.array_equal(s.numpy(), os_)
