@@ -15,8 +15,12 @@
 // activations then use v_dot2 (two products per op into float32); for bf16 ones
 // the pair is re-packed as bf16 (exactly) for v_dot2 bf16.
 //
-// Layout per SIMT step: a lane streams 16 consecutive codes (16 bytes) of each of
-// its workgroup's R rows, so a wave covers 1024 K elements per step.
+// Layout per SIMT step (M < 5): a lane streams 16 consecutive codes (16 bytes) of
+// each of its workgroup's R rows, so a wave covers 1024 K elements per step.
+// From 5 rows the products run on MFMA: codes are decoded into the LDS tile of
+// the relayout GEMV (gemv.hip) and multiplied there.
+#include <type_traits>
+
 #include "fd_gemv.h"
 #include "fd_internal.h"
 
@@ -229,10 +233,225 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
   }
 }
 
+// MFMA form of the fp8 GEMV for M >= kFp8MfmaMinM (M padded to 16): the relayout
+// GEMV of gemv.hip with a decode step. A lane loads 16 codes (one 16-byte load)
+// of row lane/8 (+8 for the second load) at K chunk lane%8 of a 128-wide unit,
+// decodes them to two 8-element fp16 chunks (value * 2^-8) and stores those to
+// the wave's XOR-swizzled LDS tile exactly where the fp16 kernel stores a loaded
+// chunk; the A reads, B (x) loads and MFMAs are the fp16 kernel's. The 2^8 and
+// the channel scale are applied to the sums. bf16 activations store the decoded
+// weights as bf16 (exact) and run the bf16 MFMA.
+template <typename T>
+__device__ __forceinline__ void fp8x16_to_tile(const u32x4& w, u32x4& c0, u32x4& c1) {
+  uint32_t h[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fp8x4_to_h2(w[i], h[2 * i], h[2 * i + 1]);
+  if constexpr (std::is_same<T, bf16>::value) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f16x2 p = __builtin_bit_cast(f16x2, h[i]);
+      h[i] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)p[1]),
+                                   __builtin_bit_cast(uint32_t, (float)p[0]), 0x07060302u);
+    }
+  }
+  c0 = u32x4{h[0], h[1], h[2], h[3]};
+  c1 = u32x4{h[4], h[5], h[6], h[7]};
+}
+
+template <typename T>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
+    T* y, const T* x, const uint8_t* w, const float* wscale, int M, int N, int K, int64_t sxm,
+    int64_t swn, int64_t sym, int64_t syn, Epi e) {
+  typedef typename Vec8<T>::type V8;
+  __shared__ f32x4 part[kMaxWaves * kWave];
+  __shared__ u32x4 tiles[kMaxWaves][256];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t n0 = (int64_t)blockIdx.x * 16;
+  const bool xok = r < M;
+  const T* xp = x + (xok ? r : 0) * sxm + g * 8;
+  const int lrow = lane >> 3, lchunk = lane & 7;  // load side: row lrow (+8), 16 codes at chunk lchunk
+  const uint8_t* wl[2];
+  bool lok[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t n = n0 + 8 * i + lrow;
+    lok[i] = n < N;
+    wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 16;
+  }
+  u32x4* tile = tiles[wave];
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int units = (K + kUnit - 1) / kUnit;
+  for (int u = wave; u < units; u += nw) {
+    const bool in = u * kUnit + lchunk * 16 < K;
+    u32x4 v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) v[i] = (lok[i] && in) ? load16_nt(wl[i] + u * kUnit) : u32x4{0, 0, 0, 0};
+    V8 b[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int kb = u * kUnit + (s2 * 4 + g) * 8;
+      b[s2] = (xok && kb < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      u32x4 c0, c1;
+      fp8x16_to_tile<T>(v[i], c0, c1);
+      const int row = 8 * i + lrow;
+      tile[row * 16 + ((2 * lchunk) ^ row)] = c0;
+      tile[row * 16 + ((2 * lchunk + 1) ^ row)] = c1;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    V8 a[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int chunk = s2 * 4 + g;
+      a[s2] = __builtin_bit_cast(V8, tile[r * 16 + (chunk ^ r)]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
+  }
+  part[wave * kWave + lane] = acc;
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    f32x4 sm = part[threadIdx.x];
+    for (int i = 1; i < nw; ++i) sm += part[i * kWave + threadIdx.x];
+    const int m = threadIdx.x & 15;
+    const int nb = (threadIdx.x >> 4) * 4;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + nb + i;
+        if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, sm[i] * 256.f * wscale[n], m, n));
+      }
+    }
+  }
+}
+
+// Gate/up + SwiGLU in the same form: 16 gate and the matching 16 up rows per
+// workgroup, B = the normalised activations written by the row kernel.
+template <typename T>
+__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_kernel(
+    T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I) {
+  typedef typename Vec8<T>::type V8;
+  __shared__ f32x4 part[kMaxWaves * kWave];
+  __shared__ u32x4 tiles[kMaxWaves][256];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int r = lane & 15, g = lane >> 4;
+  const int64_t j0 = (int64_t)blockIdx.x * 16;
+  const bool xok = r < M;
+  const T* xp = x + (xok ? r : 0) * (int64_t)H + g * 8;
+  const int lrow = lane >> 3, lchunk = lane & 7;
+  const uint8_t* gl[2];
+  const uint8_t* ul[2];
+  bool lok[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int64_t j = j0 + 8 * i + lrow;
+    lok[i] = j < I;
+    gl[i] = wgu + (lok[i] ? j : 0) * H + lchunk * 16;
+    ul[i] = wgu + (I + (lok[i] ? j : 0)) * H + lchunk * 16;
+  }
+  u32x4* tile = tiles[wave];
+  f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+  const int units = (H + kUnit - 1) / kUnit;
+  for (int u = wave; u < units; u += nw) {
+    const bool in = u * kUnit + lchunk * 16 < H;
+    u32x4 vg[2], vu[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      vg[i] = (lok[i] && in) ? load16_nt(gl[i] + u * kUnit) : u32x4{0, 0, 0, 0};
+      vu[i] = (lok[i] && in) ? load16_nt(ul[i] + u * kUnit) : u32x4{0, 0, 0, 0};
+    }
+    V8 b[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int kb = u * kUnit + (s2 * 4 + g) * 8;
+      b[s2] = (xok && kb < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+    }
+    V8 a[4], c[4];
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        u32x4 c0, c1;
+        fp8x16_to_tile<T>(half ? vu[i] : vg[i], c0, c1);
+        const int row = 8 * i + lrow;
+        tile[row * 16 + ((2 * lchunk) ^ row)] = c0;
+        tile[row * 16 + ((2 * lchunk + 1) ^ row)] = c1;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const V8 t = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
+        if (half) c[s2] = t; else a[s2] = t;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      ag = mfma16(a[s2], b[s2], ag);
+      au = mfma16(c[s2], b[s2], au);
+    }
+  }
+  part[wave * kWave + lane] = ag;
+  __syncthreads();
+  f32x4 sg = {0.f, 0.f, 0.f, 0.f};
+  if (threadIdx.x < kWave)
+    for (int i = 0; i < nw; ++i) sg += part[i * kWave + threadIdx.x];
+  __syncthreads();
+  part[wave * kWave + lane] = au;
+  __syncthreads();
+  if (threadIdx.x < kWave) {
+    f32x4 su = part[threadIdx.x];
+    for (int i = 1; i < nw; ++i) su += part[i * kWave + threadIdx.x];
+    const int m = threadIdx.x & 15;
+    const int nb = (threadIdx.x >> 4) * 4;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t jj = j0 + nb + i;
+        if (jj < I)
+          mid[m * (int64_t)I + jj] =
+              swiglu_out<T>(sg[i] * 256.f * gu_scale[jj], su[i] * 256.f * gu_scale[I + jj]);
+      }
+    }
+  }
+}
+
 namespace {
 
 template <int M> struct Fp8Rows { static constexpr int R = M <= 8 ? 4 : 2; };
-template <int M> struct Fp8MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
+// Two gate + two up rows per tile at M <= 2 with four workgroups per CU (measured
+// at Llama-3-8B widths: 25.8 against 30.3 us for four rows at two per CU).
+template <int M> struct Fp8MlpRows { static constexpr int R = M <= 2 ? 2 : M <= 4 ? 4 : 2; };
+template <int M> struct Fp8MlpPerCu { static constexpr int P = M <= 2 ? 4 : 2; };
+
+// From this many rows the fp8 GEMV and MLP take the MFMA (relayout) forms.
+constexpr int kFp8MfmaMinM = 5;
+
+template <typename T>
+void launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
+                          int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                          hipStream_t st) {
+  const int nw = pick_waves((K + kUnit - 1) / kUnit);
+  hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T>), dim3((unsigned)((N + 15) / 16)), dim3(nw * kWave),
+                     0, st, static_cast<T*>(y), static_cast<const T*>(x), w, s, M, N, K, sxm, swn,
+                     sym, syn, e);
+}
 
 template <typename T, int M>
 void launch_gemv_fp8(void* y, const void* x, const uint8_t* w, const float* s, int N, int K,
@@ -249,6 +468,10 @@ template <typename T>
 void launch_gemv_fp8_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
                        int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
                        hipStream_t st) {
+  if (M >= kFp8MfmaMinM) {
+    launch_gemv_fp8_mfma<T>(M, y, x, w, s, N, K, sxm, swn, sym, syn, e, st);
+    return;
+  }
   switch (M) {
 #define FD_CASE(MM) \
   case MM: launch_gemv_fp8<T, MM>(y, x, w, s, N, K, sxm, swn, sym, syn, e, st); break;
@@ -270,7 +493,7 @@ int launch_mlp_fp8(void* mid, const void* hidden, const void* nw, int nw_dtype,
   const size_t lds = fused_lds(M, H, sizeof(T), V);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
   const int tiles = (I + R - 1) / R;
-  const int grid = fused_grid(tiles, lds, 2);
+  const int grid = fused_grid(tiles, lds, Fp8MlpPerCu<M>::P);
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds))
       return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
@@ -359,12 +582,28 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
     return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* wgu = static_cast<const uint8_t*>(w_gate_up8);
-  int rc = act_dtype == FD_F16
-               ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
-                                       gate_up_scale, (int)H, (int)I, eps, st)
-               : launch_mlp_fp8_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
-                                        gate_up_scale, (int)H, (int)I, eps, st);
-  if (rc != FD_OK) return rc;
+  int rc;
+  if (M >= kFp8MfmaMinM) {
+    // y doubles as the normed buffer: the down projection writes it last
+    rc = rms_rows(y, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    if (rc != FD_OK) return rc;
+    const int nwv = pick_waves((H + kUnit - 1) / kUnit);
+    if (act_dtype == FD_F16)
+      hipLaunchKernelGGL(mlp_gate_up_fp8_relayout_kernel<f16>, dim3((unsigned)((I + 15) / 16)),
+                         dim3(nwv * kWave), 0, st, static_cast<f16*>(mid),
+                         static_cast<const f16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I);
+    else
+      hipLaunchKernelGGL(mlp_gate_up_fp8_relayout_kernel<bf16>, dim3((unsigned)((I + 15) / 16)),
+                         dim3(nwv * kWave), 0, st, static_cast<bf16*>(mid),
+                         static_cast<const bf16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I);
+  } else {
+    rc = act_dtype == FD_F16
+             ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
+                                     gate_up_scale, (int)H, (int)I, eps, st)
+             : launch_mlp_fp8_m<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
+                                      gate_up_scale, (int)H, (int)I, eps, st);
+    if (rc != FD_OK) return rc;
+  }
   Epi e;
   e.bias = nullptr;
   e.bias_dtype = act_dtype;

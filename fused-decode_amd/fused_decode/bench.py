@@ -380,6 +380,49 @@ def bench_qkv(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
+def bench_fp8(dtype, roof, quick, cpu) -> list[dict]:
+    """FP8-weight GEMV (the four decode shapes, M = 1 and 8) and MLP (M = 1 and 8)
+    beside their fp16-weight counterparts; bytes count one byte per weight plus the
+    float32 scales."""
+    from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
+
+    rows = []
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    shapes = [(4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)]
+    for n, kk in shapes:
+        k = copies_for(n * kk)
+        ws = [quantize_fp8(_gen((n, kk), dtype, g, kk ** -0.5)) for _ in range(k)]
+        for m in ([1] if quick else [1, 8]):
+            x = _gen((m, kk), dtype, g)
+            out = torch.empty(m, n, device="cuda", dtype=dtype)
+            fn = lambda i: linear_decode_fp8(x, *ws[i % k], out=out)  # noqa: E731
+            cold = time_us(fn, iters=max(30, 2 * k))
+            dev = graph_us(fn, k)
+            warm = time_us(lambda i: linear_decode_fp8(x, *ws[0], out=out), iters=50)
+            nbytes = n * kk + 4 * n + (m * kk + m * n) * e
+            rows.append(_row(f"linear_fp8 M={m} N={n} K={kk} {dtype}", nbytes, cold, warm, roof, dev))
+            _print(rows[-1])
+        del ws
+        torch.cuda.empty_cache()
+    h, i_ = LLAMA_H, LLAMA_I
+    k = copies_for(3 * h * i_)
+    sets = [(_gen((h,), dtype, g, 0.1, 1.0),) + quantize_fp8(_gen((2 * i_, h), dtype, g, h ** -0.5))
+            + quantize_fp8(_gen((h, i_), dtype, g, i_ ** -0.5)) for _ in range(k)]
+    for m in ([1] if quick else [1, 8]):
+        hid = _gen((m, h), dtype, g)
+        fn = lambda j: post_attn_mlp_fp8(hid, *sets[j % k], 1e-5)  # noqa: E731
+        cold = time_us(fn, iters=max(30, 2 * k))
+        dev = graph_us(fn, k)
+        warm = time_us(lambda j: post_attn_mlp_fp8(hid, *sets[0], 1e-5), iters=30)
+        nbytes = 3 * h * i_ + 4 * (2 * i_ + h) + (2 * m * h + h) * e
+        rows.append(_row(f"post_attn_mlp_fp8 M={m} {dtype}", nbytes, cold, warm, roof, dev))
+        _print(rows[-1])
+    del sets
+    torch.cuda.empty_cache()
+    return rows
+
+
 TIE_BAND = 1.05  # per-shape slack of the cutoff rule
 
 
@@ -454,7 +497,7 @@ def main() -> None:
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--dtype", choices=["fp16", "bf16", "both"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true", help="skip PyTorch-eager-on-CPU timings")
-    ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv"], default=None)
+    ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv", "fp8"], default=None)
     ap.add_argument("--tune", action="store_true", help="GEMV tile search (writes --tune-out if given)")
     ap.add_argument("--tune-out", default=None)
     args = ap.parse_args()
@@ -486,6 +529,8 @@ def main() -> None:
             payload["rows"] += bench_mlp(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
         if args.only in (None, "qkv"):
             payload["rows"] += bench_qkv(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
+        if args.only in (None, "fp8"):
+            payload["rows"] += bench_fp8(dt, roof["copy_gbs"], args.quick, not args.no_cpu)
         if args.out:
             with open(args.out, "w") as f:
                 json.dump(payload, f, indent=1)
