@@ -284,10 +284,11 @@ def main() -> None:
 
         line["decode_step"] = {}
         for m in (1, 8):
-            for fused in (True, False):
-                ds = DecodeStep(m=m, layers=32, dtype=dtype, fused=fused)
+            for form in ("fused", "unfused", "fp8"):
+                ds = DecodeStep(m=m, layers=32, dtype=dtype, fused=form != "unfused",
+                                weights="fp8" if form == "fp8" else "fp16")
                 g_us = time_step(ds, 10, 2, graph=True)
-                key = f"m{m}" if fused else f"m{m}_unfused"
+                key = f"m{m}" if form == "fused" else f"m{m}_{form}"
                 line["decode_step"][f"{key}_us"] = round(g_us, 1)
                 line["decode_step"][f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
                 line["decode_step"][f"{key}_launches_per_layer"] = ds.launches_per_layer
@@ -296,7 +297,8 @@ def main() -> None:
                 torch.cuda.empty_cache()
         line["decode_step"]["workload"] = (
             "32-layer Llama-3-8B decode step minus attention, hipGraph; fused = pre_attn_qkv + "
-            "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed")
+            "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed, "
+            "fp8 = the fused layer with E4M3 projection weights (gbs over its own weight bytes)")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
         progress("cpu baseline done")

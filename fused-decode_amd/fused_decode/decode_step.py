@@ -24,8 +24,13 @@ post_attn_mlp returns the whole residual stream (its residual add is fused into
 the down projection). Both forms compute the same values with the same rounding
 points. The whole step is captured once and replayed.
 
-Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), random
-with the benchmark distributions (no checkpoint is loaded).
+With weights="fp8" the four projections hold E4M3 codes with per-row scales
+(quantize_fp8) and run as linear_decode_fp8 / post_attn_mlp_fp8, the QKV as
+rms_norm, fp8 GEMV and rope (six launches per layer at M < 5).
+
+Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), half that
+plus the scales in fp8, random with the benchmark distributions (no checkpoint
+is loaded).
 """
 
 from __future__ import annotations
@@ -37,7 +42,8 @@ import math
 import torch
 
 from .kernels import _MFMA_MIN_M
-from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rope
+from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope
 
 H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
 QKV = (HEADS + 2 * KV_HEADS) * HEAD_DIM  # 6144
@@ -57,8 +63,11 @@ class DecodeStep:
 
     def __init__(self, m: int = 1, layers: int = 32, dtype=torch.float16, device="cuda",
                  seed: int = 0, h: int = H, i: int = I, kind: str | None = None, position: int = 1024,
-                 fused: bool = True):
+                 fused: bool = True, weights: str = "fp16"):
+        if weights not in ("fp16", "fp8"):
+            raise ValueError("weights must be 'fp16' (the activation dtype) or 'fp8'")
         self.m, self.layers, self.dtype, self.kind, self.fused = m, layers, dtype, kind, fused
+        self.fp8 = weights == "fp8"
         self.h, self.i = h, i
         heads = h // HEAD_DIM
         kv = max(1, heads // 4)
@@ -70,15 +79,17 @@ class DecodeStep:
             t = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
             return (t * scale + mean).to(dtype)
 
+        # projections as activation-dtype weights, or as E4M3 codes + per-row scales
+        proj = (lambda *shape, scale: quantize_fp8(rnd(*shape, scale=scale))) if self.fp8 else rnd
         self.w = []
         for _ in range(layers):
             self.w.append({
                 "attn_norm": rnd(h, scale=0.1, mean=1.0),
-                "qkv": rnd(self.qkv_n, h, scale=h ** -0.5),
-                "o": rnd(h, h, scale=h ** -0.5),
+                "qkv": proj(self.qkv_n, h, scale=h ** -0.5),
+                "o": proj(h, h, scale=h ** -0.5),
                 "mlp_norm": rnd(h, scale=0.1, mean=1.0),
-                "gate_up": rnd(2 * i, h, scale=h ** -0.5),
-                "down": rnd(h, i, scale=i ** -0.5),
+                "gate_up": proj(2 * i, h, scale=h ** -0.5),
+                "down": proj(h, i, scale=i ** -0.5),
                 "attn_out": rnd(m, h),  # stand-in for the attention output of this layer
             })
         cos, sin = llama3_angles(position, device=device)
@@ -95,11 +106,31 @@ class DecodeStep:
     @property
     def weight_bytes(self) -> int:
         e = torch.empty((), dtype=self.dtype).element_size()
-        per = (self.qkv_n * self.h + self.h * self.h + 3 * self.h * self.i + 2 * self.h) * e
+        proj = self.qkv_n * self.h + self.h * self.h + 3 * self.h * self.i
+        if self.fp8:  # one byte per weight plus a float32 scale per row
+            per = proj + 4 * (self.qkv_n + self.h + 2 * self.i + self.h) + 2 * self.h * e
+        else:
+            per = proj * e + 2 * self.h * e
         return per * self.layers
 
     def step(self) -> torch.Tensor:
+        if self.fp8:
+            return self._step_fp8()
         return self._step_fused() if self.fused else self._step_composed()
+
+    def _step_fp8(self) -> torch.Tensor:
+        """The fused layer with E4M3 projections: RMSNorm, fp8 QKV GEMV and RoPE as
+        three launches, fp8 O-proj with the residual, fp8 post_attn_mlp."""
+        x = self.x_in
+        qk = self.qkv[:, : self.qk_heads * HEAD_DIM].view(self.m, self.qk_heads, HEAD_DIM)
+        for w in self.w:
+            rms_norm(x, w["attn_norm"], 1e-5, out=self.normed)
+            linear_decode_fp8(self.normed, *w["qkv"], out=self.qkv)
+            rope(qk, self.cos, self.sin, out=qk)
+            linear_decode_fp8(w["attn_out"], *w["o"], row_add=x, out=self.hbuf)
+            x = post_attn_mlp_fp8(self.hbuf, w["mlp_norm"], *w["gate_up"], *w["down"], 1e-5)
+        self.out.copy_(x)
+        return self.out
 
     def _step_fused(self) -> torch.Tensor:
         x = self.x_in
@@ -130,6 +161,8 @@ class DecodeStep:
         add a row kernel for the RMSNorm)."""
         mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
         mlp = 3 if mfma else 2
+        if self.fp8:
+            return 3 + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
         if self.fused:
             return (2 if mfma else 1) + 1 + mlp
         return 4 + mlp
@@ -175,17 +208,18 @@ def main() -> None:
     ap.add_argument("--dtype", choices=["fp16", "bf16"], default="fp16")
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 8)")
+    ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 5)")
+    ap.add_argument("--weights", choices=["fp16", "fp8"], default="fp16", help="projection weights (fp8: E4M3 + row scales)")
     args = ap.parse_args()
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     for m in args.m:
-        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused)
+        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused, weights=args.weights)
         eager = time_step(ds, args.steps, args.warmup, graph=False)
         graph = time_step(ds, args.steps, args.warmup, graph=True)
         wb = ds.weight_bytes
         print(json.dumps({
             "workload": f"decode step minus attention, {args.layers} layers, Llama-3-8B widths, M={m}, {args.dtype}, "
-                        f"{'unfused' if args.unfused else 'fused'}",
+                        f"{'unfused' if args.unfused else 'fused'}, {args.weights} weights",
             "eager_us": round(eager, 2),
             "graph_us": round(graph, 2),
             "weight_bytes": wb,

@@ -7,6 +7,8 @@
     torch.ops.fused_decode.linear_decode(x, weight, bias, row_add, kind)
     torch.ops.fused_decode.post_attn_mlp(hidden, norm_weight, w_gate_up, w_down, eps, kind)
     torch.ops.fused_decode.pre_attn_qkv(hidden, norm_weight, w_qkv, cos, sin, eps, rope_cols, bias, kind)
+    torch.ops.fused_decode.linear_decode_fp8(x, weight, scale, bias, row_add)
+    torch.ops.fused_decode.post_attn_mlp_fp8(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps)
 
 Each is the functional form (no ``out=``) of the operator of the same name in
 ``fused_decode.ops``, registered as a custom op with a fake (meta) kernel, so
@@ -25,7 +27,7 @@ from __future__ import annotations
 import torch
 from torch import Tensor
 
-from . import ops
+from . import fp8, ops
 
 _NS = "fused_decode"
 
@@ -109,4 +111,27 @@ def _pre_attn_qkv_fake(hidden, norm_weight, w_qkv, cos, sin, eps, rope_cols, bia
     return hidden.new_empty((*_lead(hidden), w_qkv.shape[0]))
 
 
-OPS = ("rms_norm", "add_rms_norm", "rope", "swiglu", "linear_decode", "post_attn_mlp", "pre_attn_qkv")
+@torch.library.custom_op(f"{_NS}::linear_decode_fp8", mutates_args=())
+def linear_decode_fp8(x: Tensor, weight: Tensor, scale: Tensor, bias: Tensor | None = None,
+                      row_add: Tensor | None = None) -> Tensor:
+    return fp8.linear_decode_fp8(x, weight, scale, bias, row_add=row_add)
+
+
+@linear_decode_fp8.register_fake
+def _linear_decode_fp8_fake(x, weight, scale, bias=None, row_add=None):
+    return x.new_empty((*_lead(x), weight.shape[0]))
+
+
+@torch.library.custom_op(f"{_NS}::post_attn_mlp_fp8", mutates_args=())
+def post_attn_mlp_fp8(hidden: Tensor, norm_weight: Tensor, w_gate_up: Tensor, gate_up_scale: Tensor,
+                      w_down: Tensor, down_scale: Tensor, eps: float = 1e-6) -> Tensor:
+    return fp8.post_attn_mlp_fp8(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps)
+
+
+@post_attn_mlp_fp8.register_fake
+def _post_attn_mlp_fp8_fake(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps=1e-6):
+    return hidden.new_empty(hidden.shape)
+
+
+OPS = ("rms_norm", "add_rms_norm", "rope", "swiglu", "linear_decode", "post_attn_mlp", "pre_attn_qkv",
+       "linear_decode_fp8", "post_attn_mlp_fp8")

@@ -167,3 +167,32 @@ def test_fp8_rejects():
         fd.linear_decode_fp8(x.cpu(), q, s)
     with pytest.raises(ValueError, match="K"):
         fd.linear_decode_fp8(x[:, :32], q, s)
+
+
+def test_decode_step_fp8_matches_oracle_and_graph():
+    from fused_decode.decode_step import HEAD_DIM, DecodeStep
+
+    m = 2
+    ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=5, weights="fp8")
+    eager = ds.step().clone()
+    codes = lambda q: q.cpu().view(torch.uint8).numpy()  # noqa: E731
+    x = npf(ds.x_in)
+    cos, sin = npf(ds.cos), npf(ds.sin)
+    qk = ds.qk_heads * HEAD_DIM
+    for w in ds.w:
+        normed = O.rms_norm(x, npf(w["attn_norm"]), 1e-5, "f16")
+        qkv = O.linear_fp8(normed, codes(w["qkv"][0]), npf(w["qkv"][1]), dtype="f16")
+        q = qkv[:, :qk].reshape(m, ds.qk_heads, HEAD_DIM)
+        qkv[:, :qk] = O.rope(q, cos, sin, "f16").reshape(m, qk)
+        h = O.linear_fp8(npf(w["attn_out"]), codes(w["o"][0]), npf(w["o"][1]), row_add=x, dtype="f16")
+        x = O.post_attn_mlp_fp8(h, npf(w["mlp_norm"]), codes(w["gate_up"][0]), npf(w["gate_up"][1]),
+                                codes(w["down"][0]), npf(w["down"][1]), 1e-5, "f16")
+    torch.testing.assert_close(eager.float().cpu(), torch.from_numpy(x), **tol(torch.float16))
+    torch.testing.assert_close(ds.qkv.float().cpu(), torch.from_numpy(qkv), **tol(torch.float16))
+    ds.capture()
+    for _ in range(3):
+        ds.out.zero_()
+        out = ds.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager, rtol=0, atol=0)
+    assert ds.launches_per_layer == 6

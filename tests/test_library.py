@@ -46,6 +46,13 @@ def test_fake_kernels_give_result_shapes(fdl):
         assert fdl.post_attn_mlp(x, w, wgu, wd, 1e-5).shape == x.shape
         cs = torch.empty(1, 16, **f16)
         assert fdl.pre_attn_qkv(x, w, wl, cs, cs, 1e-5, 32).shape == (2, 3, n)
+        q8 = torch.empty(n, h, device="cuda", dtype=torch.float8_e4m3fn)
+        s8 = torch.empty(n, device="cuda", dtype=torch.float32)
+        assert fdl.linear_decode_fp8(x, q8, s8).shape == (2, 3, n)
+        g8 = torch.empty(2 * i, h, device="cuda", dtype=torch.float8_e4m3fn)
+        d8 = torch.empty(h, i, device="cuda", dtype=torch.float8_e4m3fn)
+        sg, sd = torch.empty(2 * i, device="cuda"), torch.empty(h, device="cuda")
+        assert fdl.post_attn_mlp_fp8(x, w, g8, sg, d8, sd, 1e-5).shape == x.shape
 
 
 def test_real_cpu_inputs_reach_the_operator_checks(fdl):
