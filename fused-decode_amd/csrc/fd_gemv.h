@@ -204,13 +204,12 @@ constexpr size_t kMaxLds = 160 * 1024;       // LDS per CU on gfx950
 // ---------------------------------------------------------------------------
 // Host-side launch-shape helpers
 
-// Waves per workgroup: enough to cover K with whole work items (512-element
-// chunks for SIMT, 128-element units for MFMA) in as even a split as possible.
+// Waves per workgroup: one per work item (512-element chunk for SIMT, 128-element
+// unit for MFMA) up to eight. An uneven split (K = 14336: 28 chunks over 8 waves)
+// measured faster than an even one with fewer waves (7): more loads in flight.
 inline int pick_waves(int64_t items) {
-  if (items <= kMaxWaves) return (int)(items < 1 ? 1 : items);
-  for (int d = kMaxWaves; d >= 4; --d)
-    if (items % d == 0) return d;
-  return kMaxWaves;
+  if (items < 1) return 1;
+  return items < kMaxWaves ? (int)items : kMaxWaves;
 }
 
 // The dynamic-LDS limit of a kernel must be raised before a launch above 64 KiB.

@@ -196,12 +196,8 @@ def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
 
 
 def _waves(items: int) -> int:
-    if items <= 8:
-        return max(1, items)
-    for d in range(8, 3, -1):
-        if items % d == 0:
-            return d
-    return 8
+    """pick_waves of fd_gemv.h: one wave per work item, up to eight."""
+    return max(1, min(8, items))
 
 
 def linear_out(

@@ -91,7 +91,7 @@ def test_linear_config_tiling(monkeypatch):
     monkeypatch.setattr(kernels, "_TILE_TABLE", {"dot:4096x4096:m4": [16, 8, 1]})
     assert kernels.linear_config("dot", 4096, 4096, 4) == (16, 128, 8, 1)     # the table picks MFMA
     monkeypatch.setattr(kernels, "_TILE_TABLE", {})
-    assert kernels.linear_config("simt", 4096, 14336) == (4, 512, 7, 1)
+    assert kernels.linear_config("simt", 4096, 14336) == (4, 512, 8, 1)
     assert kernels.linear_config("simt", 64, 100) == (4, 512, 1, 1)
     # a measured table entry wins for its exact shape and row count
     monkeypatch.setattr(kernels, "_TILE_TABLE", {"simt:4096x4096:m1": [2, 8, 1]})
