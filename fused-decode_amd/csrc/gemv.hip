@@ -12,16 +12,24 @@
 // (fp16/bf16 pairs into float32). Per-lane partial sums are combined with a
 // transposing butterfly (V-1 exchanges for V sums) and then across waves in LDS.
 //
-// MFMA kernel (gemv_mfma_kernel, M padded to 16): a workgroup owns 16 weight
-// rows; waves split K into 128-element units of four v_mfma_f32_16x16x32 steps.
-// A = 16 weight rows x 32 k (lane l: row l%16, k-group l/16), B = x^T with the
-// same lane->k mapping, so padding rows m >= M are zero registers, not loads.
+// MFMA kernel (gemv_mfma_relayout_kernel, M padded to 16; kind=dot from 5 rows):
+// a workgroup owns 16 weight rows; waves split K into 128-element units of four
+// v_mfma_f32_16x16x32 steps. A = 16 weight rows x 32 k (lane l: row l%16,
+// k-group l/16), B = x^T with the same lane->k mapping, so padding rows m >= M
+// are zero registers, not loads. The weights are loaded row-contiguously and
+// relaid through LDS into the A layout (see the kernel).
 //
 // Fused MLP: launch 1 computes the RMSNorm of hidden in a prologue (each
 // workgroup re-derives the row scale and stages the normalised activations in
 // LDS), streams matching gate row j and up row I+j, and writes only
 // mid = round(silu(round(g)) * round(u)). Launch 2 is the down GEMV with the
 // residual fused as row_add. Weights are read once; gate_up never exists in HBM.
+// From 5 rows (kind=dot) the norm runs as a row kernel and both launches use
+// the MFMA form.
+//
+// Fused QKV (qkv_simt_kernel, and the MFMA kernel with ROPE): the same prologue
+// and weight stream with tiles placed so that both halves of every rotate-half
+// pair land in one workgroup, which applies RoPE in the epilogue.
 #include "fd_gemv.h"
 #include "fd_internal.h"
 
@@ -314,7 +322,7 @@ __device__ __forceinline__ void load_gate_up(typename Vec8<T>::type (&g)[R],
   }
 }
 
-// SIMT gate/up for M < 8. The weight stream is software-pipelined one K step
+// SIMT gate/up for M < 5 (any M with kind=simt). The weight stream is software-pipelined one K step
 // deep: the loads of the next step (which may belong to the workgroup's next
 // tile) are issued before the math of the current one, and the first step is
 // issued before the RMSNorm prologue, so HBM requests stay in flight across the
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   }
 }
 
-// Pre-attention QKV for M < 8 (and kind=simt): the RMSNorm prologue of the
+// Pre-attention QKV for M < 5 (and kind=simt): the RMSNorm prologue of the
 // fused gate/up kernel, a pipelined stream of 4 weight rows per tile placed by
 // TileRows<4> (two rotate-half pairs per rotated tile), and an epilogue that
 // adds the bias, rounds, and rotates the rotated tiles' pairs.
