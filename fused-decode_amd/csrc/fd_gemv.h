@@ -201,6 +201,143 @@ constexpr int kNormScratch = kMaxWaves * 16 + 16;
 constexpr bool kNtWeights = true;           // nontemporal weight loads (measured +10-20%)
 constexpr size_t kMaxLds = 160 * 1024;       // LDS per CU on gfx950
 
+// RoPE in the epilogue of a QKV projection (rotate-half, as the standalone
+// rope op): output columns below `cols` form heads of `dim` columns; column d of
+// a head pairs with d + dim/2. cos/sin row m sits at m * rs (rs = 0: one row for
+// every m), in `dtype`. `tiles` tiles of S rows cover the rotated columns.
+struct Rope {
+  const void* cos;
+  const void* sin;
+  int dtype;
+  int64_t rs;
+  int cols;
+  int dim;
+  int tiles;
+};
+
+// Row placement of a tile of S weight rows. A rotated tile holds S/2 adjacent
+// pairs of one head, slot s < S/2 at column q + s and slot s + S/2 at its
+// partner q + s + dim/2, so both halves of every pair end in one workgroup
+// (needs dim/2 % (S/2) == 0). Tiles past the rotated ones hold S consecutive rows.
+template <int S>
+struct TileRows {
+  int64_t base;  // first row of the head (rotated) or of the tile
+  int q;         // head column of slot 0 (rotated tiles)
+  int hh;        // dim/2, 0 for unrotated tiles
+  __device__ __forceinline__ TileRows(const Rope& rp, int tile) {
+    if (tile < rp.tiles) {
+      hh = rp.dim >> 1;
+      const int pp = tile * (S / 2);
+      const int b = pp / hh;
+      q = pp - b * hh;
+      base = (int64_t)b * rp.dim;
+    } else {
+      hh = 0;
+      q = 0;
+      base = (int64_t)rp.cols + (int64_t)(tile - rp.tiles) * S;
+    }
+  }
+  __device__ __forceinline__ bool rotated() const { return hh != 0; }
+  // head column of slot s (rotated tiles)
+  __device__ __forceinline__ int col(int s) const { return q + s % (S / 2) + (s / (S / 2)) * hh; }
+  __device__ __forceinline__ int64_t row(int s) const { return rotated() ? base + col(s) : base + s; }
+};
+
+// Rotate one pair in float32 from the rounded projection outputs x1 (first
+// half, head column d) and x2 (second half, column d + dim/2), as the rope op.
+__device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, float x1, float x2,
+                                          float& o1, float& o2) {
+  const int64_t c = m * rp.rs + d, h = rp.dim >> 1;
+  o1 = x1 * load_any(rp.cos, rp.dtype, c) - x2 * load_any(rp.sin, rp.dtype, c);
+  o2 = x2 * load_any(rp.cos, rp.dtype, c + h) + x1 * load_any(rp.sin, rp.dtype, c + h);
+}
+
+// Per-row factor applied to a GEMV sum before the epilogue: none for fp16/bf16
+// weights, 256 * scale[n] for E4M3 codes decoded as value * 2^-8.
+struct NoScale {
+  __device__ __forceinline__ float operator()(float s, int64_t) const { return s; }
+};
+struct RowScale {
+  const float* scale;
+  __device__ __forceinline__ float operator()(float s, int64_t n) const {
+    return s * 256.f * scale[n];
+  }
+};
+
+// Output of one 16-row MFMA tile, from the 64 lanes of one wave holding the
+// cross-wave sums: lane l has rows nb..nb+3 (nb = 4*(l/16)) of column m = l%16.
+// With ROPE the rows follow TileRows<16>, and a rotated tile rotates its rounded
+// outputs: lanes 0-31 hold slots 0-7 and lanes 32-63 their partners 8-15 (same
+// m), one lane-xor-32 exchange apart, so every lane of the wave must call this.
+template <typename T, bool ROPE, typename Scale>
+__device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, int64_t n0,
+                                              const TileRows<16>& tr, const Epi& e,
+                                              const Rope& rp, const Scale& sc, int M, int N,
+                                              int64_t sym, int64_t syn) {
+  const int m = lane & 15;
+  const int nb = (lane >> 4) * 4;
+  if (ROPE && tr.rotated()) {
+    float v[4], pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = tr.row(nb + i);
+      v[i] = m < M ? round_as<T>(epilogue(e, sc(s[i], n), m, n)) : 0.f;
+      pv[i] = __shfl_xor(v[i], 32, kWave);
+    }
+    if (m < M) {
+      const bool first = nb < 8;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float o1, o2;
+        rope_pair(rp, m, tr.col(first ? nb + i : nb + i - 8), first ? v[i] : pv[i],
+                  first ? pv[i] : v[i], o1, o2);
+        y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(first ? o1 : o2);
+      }
+    }
+  } else if (m < M) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
+      if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, sc(s[i], n), m, n));
+    }
+  }
+}
+
+// Output of one fused-QKV SIMT tile of 4 rows placed by TileRows<4>, from the
+// waves' partial sums (wave i, slot r*M + m at part[i*V + r*M + m]): bias,
+// rounding, and in rotated tiles the rotation of pairs (slot p, slot p + 2).
+template <typename T, int M, typename Scale>
+__device__ __forceinline__ void qkv_tile_out(T* y, const float* part, int V, int nw,
+                                             const TileRows<4>& tr, const Epi& e, const Rope& rp,
+                                             const Scale& sc, int N) {
+  if (tr.rotated()) {
+    for (int t = threadIdx.x; t < 2 * M; t += blockDim.x) {
+      const int p = t / M, m = t % M;
+      float s1 = 0.f, s2 = 0.f;
+      for (int i = 0; i < nw; ++i) {
+        s1 += part[i * V + p * M + m];
+        s2 += part[i * V + (p + 2) * M + m];
+      }
+      const int64_t n1 = tr.row(p), n2 = tr.row(p + 2);
+      float o1, o2;
+      rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, sc(s1, n1), m, n1)),
+                round_as<T>(epilogue(e, sc(s2, n2), m, n2)), o1, o2);
+      y[m * (int64_t)N + n1] = from_f32<T>(o1);
+      y[m * (int64_t)N + n2] = from_f32<T>(o2);
+    }
+  } else {
+    for (int t = threadIdx.x; t < 4 * M; t += blockDim.x) {
+      const int r = t / M, m = t % M;
+      const int64_t n = tr.row(r);
+      if (n < N) {
+        float s = 0.f;
+        for (int i = 0; i < nw; ++i) s += part[i * V + t];
+        y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, sc(s, n), m, n));
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host-side launch-shape helpers
 
@@ -251,6 +388,58 @@ inline int fused_grid(int tiles, size_t lds, int per_cu) {
   const int cap = device_cus() * (fit < 1 ? 1 : fit < per_cu ? fit : per_cu);
   const int per = (tiles + cap - 1) / cap;
   return (tiles + per - 1) / per;
+}
+
+// Argument checks and operand set-up shared by the fused QKV entry points
+// (fp16/bf16 and fp8 weights). `mfma`: the launch runs the RMSNorm as a row
+// kernel into `normed`. Sets `empty` (and returns FD_OK) for M = 0.
+inline int qkv_prepare(const void* y, const void* normed, const void* hidden, const void* norm_w,
+                       int norm_w_dtype, const void* w, const void* bias, int bias_dtype,
+                       const void* cos, const void* sin, int cs_dtype, int64_t cs_row_stride,
+                       int64_t M, int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim,
+                       float eps, int act_dtype, bool mfma, Epi& e, Rope& rp, bool& empty) {
+  empty = false;
+  if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
+    return FD_EINVAL;
+  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
+  if (H <= 0 || N <= 0) return set_error(FD_EINVAL, "H and N must be positive");
+  if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
+  if (rope_cols < 0 || rope_cols > N) return set_error(FD_EINVAL, "rope_cols must be in [0, N]");
+  if (rope_cols > 0) {
+    if (head_dim <= 0 || head_dim % 2 != 0) return set_error(FD_EINVAL, "head_dim must be even");
+    if (rope_cols % head_dim != 0)
+      return set_error(FD_EINVAL, "rope_cols must be a multiple of head_dim");
+    if (!check_any_dtype(cs_dtype, "cs_dtype")) return FD_EINVAL;
+    if (cs_row_stride < 0) return set_error(FD_EINVAL, "cs_row_stride must be >= 0");
+    if (head_dim % 16 != 0 || head_dim > 0x7fffffffLL)
+      return set_error(FD_EUNSUPPORTED, "head_dim must be a multiple of 16");
+  }
+  if (bias && !check_any_dtype(bias_dtype, "bias_dtype")) return FD_EINVAL;
+  if (M == 0) {
+    empty = true;
+    return FD_OK;
+  }
+  if (!y || !hidden || !norm_w || !w || (rope_cols > 0 && (!cos || !sin)))
+    return set_error(FD_EINVAL, "null pointer argument");
+  if (H > 0x7fffffffLL || N > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
+  if (!aligned16(hidden) || !aligned16(norm_w) || !aligned16(w))
+    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
+  if (mfma && (!normed || !aligned16(normed)))
+    return set_error(FD_EINVAL, "M >= 5 on the MFMA path needs a 16-byte aligned normed buffer");
+  e.bias = bias;
+  e.bias_dtype = bias_dtype;
+  e.sb = 1;
+  e.row = nullptr;
+  e.row_dtype = act_dtype;
+  e.srm = e.srn = 0;
+  rp.cos = cos;
+  rp.sin = sin;
+  rp.dtype = cs_dtype;
+  rp.rs = cs_row_stride;
+  rp.cols = (int)rope_cols;
+  rp.dim = rope_cols > 0 ? (int)head_dim : 2;
+  rp.tiles = 0;
+  return FD_OK;
 }
 
 }  // namespace fd

@@ -258,10 +258,10 @@ __device__ __forceinline__ void fp8x16_to_tile(const u32x4& w, u32x4& c0, u32x4&
   c1 = u32x4{h[4], h[5], h[6], h[7]};
 }
 
-template <typename T>
+template <typename T, bool ROPE>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
     T* y, const T* x, const uint8_t* w, const float* wscale, int M, int N, int K, int64_t sxm,
-    int64_t swn, int64_t sym, int64_t syn, Epi e) {
+    int64_t swn, int64_t sym, int64_t syn, Epi e, Rope rp) {
   typedef typename Vec8<T>::type V8;
   __shared__ f32x4 part[kMaxWaves * kWave];
   __shared__ u32x4 tiles[kMaxWaves][256];
@@ -275,9 +275,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   const int lrow = lane >> 3, lchunk = lane & 7;  // load side: row lrow (+8), 16 codes at chunk lchunk
   const uint8_t* wl[2];
   bool lok[2];
+  const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int64_t n = n0 + 8 * i + lrow;
+    const int64_t n = ROPE ? tr.row(8 * i + lrow) : n0 + 8 * i + lrow;
     lok[i] = n < N;
     wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 16;
   }
@@ -323,15 +324,83 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   if (threadIdx.x < kWave) {
     f32x4 sm = part[threadIdx.x];
     for (int i = 1; i < nw; ++i) sm += part[i * kWave + threadIdx.x];
-    const int m = threadIdx.x & 15;
-    const int nb = (threadIdx.x >> 4) * 4;
-    if (m < M) {
+    mfma_tile_out<T, ROPE>(y, sm, threadIdx.x, n0, tr, e, rp, RowScale{wscale}, M, N, sym, syn);
+  }
+}
+
+// Pre-attention QKV with fp8 weights for M < 5: the fp16 fused QKV kernel's
+// structure (RMSNorm prologue staged in LDS, 4 weight rows per tile placed by
+// TileRows<4>, the next tile's loads issued one K step ahead, RoPE of the
+// rotated tiles in the epilogue) with the fp8 GEMV's 16 codes per lane and step.
+template <int R>
+__device__ __forceinline__ void load_tile_rows8(u32x4 (&v)[R], const uint8_t* w, const Rope& rp,
+                                                int tile, int tiles, int k, int H, int N) {
+  const TileRows<R> tr(rp, tile < tiles ? tile : 0);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + nb + i;
-        if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, sm[i] * 256.f * wscale[n], m, n));
+  for (int r = 0; r < R; ++r) {
+    const int64_t n = tr.row(r);
+    const bool ok = tile < tiles && n < N && k < H;
+    v[r] = ok ? load16_nt(w + n * H + k) : u32x4{0, 0, 0, 0};
+  }
+}
+
+template <typename T, int M, bool REGS>
+__global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
+    T* y, const T* hidden, const void* nwp, int nw_dtype, const uint8_t* w, const float* wscale,
+    int H, int N, float eps, int tiles, Epi e, Rope rp) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int R = 4;
+  constexpr int V = pow2_ceil(R * M);
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int XS = xs_stride(H);
+  T* xs = reinterpret_cast<T*>(smem);
+  float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int step = nw * kChunk8;
+  const int steps = (H + step - 1) / step;
+  const int kbase = (wave * kWave + lane) * 16;
+
+  NormRegs<T, M, kNormRegRows(M)> nr;
+  if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
+  u32x4 wv[R];
+  load_tile_rows8<R>(wv, w, rp, blockIdx.x, tiles, kbase, H, N);
+  if constexpr (REGS)
+    norm_store(nr, xs, part, M, H, eps);
+  else
+    stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
+
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+    for (int it = 0; it < steps; ++it) {
+      const bool last = it + 1 == steps;
+      u32x4 wn[R];
+      load_tile_rows8<R>(wn, w, rp, last ? tile + (int)gridDim.x : tile, tiles,
+                         kbase + (last ? 0 : (it + 1) * step), H, N);
+      const int k = kbase + it * step;
+      if (k < H) {
+        V8 xa[M], xb[M];
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          xa[m] = load8<T>(xs + m * XS + k);
+          xb[m] = load8<T>(xs + m * XS + k + 8);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(wv[r], xa[m], xb[m], acc[r * M + m]);
       }
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[r] = wn[r];
     }
+    butterfly_sum<V>(acc, lane);
+    __syncthreads();  // previous tile's readers of `part` are done
+    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    __syncthreads();
+    qkv_tile_out<T, M>(y, part, V, nw, TileRows<R>(rp, tile), e, rp, RowScale{wscale}, N);
   }
 }
 
@@ -443,14 +512,19 @@ template <int M> struct Fp8MlpPerCu { static constexpr int P = M <= 2 ? 4 : 2; }
 // From this many rows the fp8 GEMV and MLP take the MFMA (relayout) forms.
 constexpr int kFp8MfmaMinM = 5;
 
+// `rp` (fused QKV): tiles placed by TileRows<16> with RoPE in the epilogue.
 template <typename T>
 void launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
                           int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-                          hipStream_t st) {
+                          hipStream_t st, const Rope* rp = nullptr) {
   const int nw = pick_waves((K + kUnit - 1) / kUnit);
-  hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T>), dim3((unsigned)((N + 15) / 16)), dim3(nw * kWave),
-                     0, st, static_cast<T*>(y), static_cast<const T*>(x), w, s, M, N, K, sxm, swn,
-                     sym, syn, e);
+  const dim3 grid((unsigned)((N + 15) / 16)), block(nw * kWave);
+  if (rp)
+    hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T, true>), grid, block, 0, st, static_cast<T*>(y),
+                       static_cast<const T*>(x), w, s, M, N, K, sxm, swn, sym, syn, e, *rp);
+  else
+    hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T, false>), grid, block, 0, st, static_cast<T*>(y),
+                       static_cast<const T*>(x), w, s, M, N, K, sxm, swn, sym, syn, e, Rope{});
 }
 
 template <typename T, int M>
@@ -518,6 +592,45 @@ int launch_mlp_fp8_m(int M, void* mid, const void* hidden, const void* nw, int n
     FD_CASE(16)
 #undef FD_CASE
     default: return set_error(FD_EINVAL, "M must be in [1, 16]");
+  }
+}
+
+// Fused QKV, M < kFp8MfmaMinM: up to four waves and every tile resident at once
+// (the fp16 QKV launch shape).
+template <typename T, int M>
+int launch_qkv_fp8(void* y, const void* hidden, const void* nw, int nw_dtype, const uint8_t* w,
+                   const float* s, int H, int N, float eps, const Epi& e, const Rope& rp,
+                   hipStream_t st) {
+  constexpr int V = pow2_ceil(4 * M);
+  const int nwv0 = pick_waves((H + kChunk8 - 1) / kChunk8);
+  const int nwv = nwv0 > 4 ? 4 : nwv0;
+  const size_t lds = fused_lds(M, H, sizeof(T), V);
+  if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
+  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
+  const int grid = fused_grid(tiles, lds, 8);
+  auto launch = [&](auto kernel) {
+    if (!allow_lds(kernel, lds))
+      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(y),
+                       static_cast<const T*>(hidden), nw, nw_dtype, w, s, H, N, eps, tiles, e, rp);
+    return (int)FD_OK;
+  };
+  if constexpr (M <= kNormRegMaxM) {
+    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_fp8_kernel<T, M, true>);
+  }
+  return launch(qkv_fp8_kernel<T, M, false>);
+}
+
+template <typename T>
+int launch_qkv_fp8_m(int M, void* y, const void* hidden, const void* nw, int nw_dtype,
+                     const uint8_t* w, const float* s, int H, int N, float eps, const Epi& e,
+                     const Rope& rp, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return launch_qkv_fp8<T, MM>(y, hidden, nw, nw_dtype, w, s, H, N, eps, e, rp, st);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "the SIMT fp8 QKV covers M < %d", kFp8MfmaMinM);
   }
 }
 
@@ -617,5 +730,44 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
     launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
   else
     launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  return check_launch();
+}
+
+extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* norm_w,
+                                   int norm_w_dtype, const void* w_qkv8, const float* w_scale,
+                                   const void* bias, int bias_dtype, const void* cos,
+                                   const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
+                                   int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim,
+                                   float eps, int act_dtype, void* stream) {
+  using namespace fd;
+  const bool mfma = M >= kFp8MfmaMinM;
+  Epi e;
+  Rope rp;
+  bool empty = false;
+  const int checked = qkv_prepare(y, normed, hidden, norm_w, norm_w_dtype, w_qkv8, bias,
+                                  bias_dtype, cos, sin, cs_dtype, cs_row_stride, M, H, N,
+                                  rope_cols, head_dim, eps, act_dtype, mfma, e, rp, empty);
+  if (checked != FD_OK || empty) return checked;
+  if (!w_scale) return set_error(FD_EINVAL, "null pointer argument");
+  if (H % 16 != 0) return set_error(FD_EUNSUPPORTED, "the fp8 QKV needs H %% 16 == 0");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint8_t* w = static_cast<const uint8_t*>(w_qkv8);
+  if (mfma) {
+    rp.tiles = (int)(rope_cols / 16);
+    const int rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    if (rc != FD_OK) return rc;
+    if (act_dtype == FD_F16)
+      launch_gemv_fp8_mfma<f16>((int)M, y, normed, w, w_scale, (int)N, (int)H, H, H, N, 1, e, st, &rp);
+    else
+      launch_gemv_fp8_mfma<bf16>((int)M, y, normed, w, w_scale, (int)N, (int)H, H, H, N, 1, e, st, &rp);
+  } else {
+    rp.tiles = (int)(rope_cols / 4);
+    const int rc = act_dtype == FD_F16
+                       ? launch_qkv_fp8_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w, w_scale,
+                                               (int)H, (int)N, eps, e, rp, st)
+                       : launch_qkv_fp8_m<bf16>((int)M, y, hidden, norm_w, norm_w_dtype, w,
+                                                w_scale, (int)H, (int)N, eps, e, rp, st);
+    if (rc != FD_OK) return rc;
+  }
   return check_launch();
 }

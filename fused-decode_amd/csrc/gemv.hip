@@ -35,57 +35,6 @@
 
 namespace fd {
 
-// RoPE in the epilogue of a QKV projection (rotate-half, as the standalone
-// rope op): output columns below `cols` form heads of `dim` columns; column d of
-// a head pairs with d + dim/2. cos/sin row m sits at m * rs (rs = 0: one row for
-// every m), in `dtype`. `tiles` tiles of S rows cover the rotated columns.
-struct Rope {
-  const void* cos;
-  const void* sin;
-  int dtype;
-  int64_t rs;
-  int cols;
-  int dim;
-  int tiles;
-};
-
-// Row placement of a tile of S weight rows. A rotated tile holds S/2 adjacent
-// pairs of one head, slot s < S/2 at column q + s and slot s + S/2 at its
-// partner q + s + dim/2, so both halves of every pair end in one workgroup
-// (needs dim/2 % (S/2) == 0). Tiles past the rotated ones hold S consecutive rows.
-template <int S>
-struct TileRows {
-  int64_t base;  // first row of the head (rotated) or of the tile
-  int q;         // head column of slot 0 (rotated tiles)
-  int hh;        // dim/2, 0 for unrotated tiles
-  __device__ __forceinline__ TileRows(const Rope& rp, int tile) {
-    if (tile < rp.tiles) {
-      hh = rp.dim >> 1;
-      const int pp = tile * (S / 2);
-      const int b = pp / hh;
-      q = pp - b * hh;
-      base = (int64_t)b * rp.dim;
-    } else {
-      hh = 0;
-      q = 0;
-      base = (int64_t)rp.cols + (int64_t)(tile - rp.tiles) * S;
-    }
-  }
-  __device__ __forceinline__ bool rotated() const { return hh != 0; }
-  // head column of slot s (rotated tiles)
-  __device__ __forceinline__ int col(int s) const { return q + s % (S / 2) + (s / (S / 2)) * hh; }
-  __device__ __forceinline__ int64_t row(int s) const { return rotated() ? base + col(s) : base + s; }
-};
-
-// Rotate one pair in float32 from the rounded projection outputs x1 (first
-// half, head column d) and x2 (second half, column d + dim/2), as the rope op.
-__device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, float x1, float x2,
-                                          float& o1, float& o2) {
-  const int64_t c = m * rp.rs + d, h = rp.dim >> 1;
-  o1 = x1 * load_any(rp.cos, rp.dtype, c) - x2 * load_any(rp.sin, rp.dtype, c);
-  o2 = x2 * load_any(rp.cos, rp.dtype, c + h) + x1 * load_any(rp.sin, rp.dtype, c + h);
-}
-
 // Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
 // are R*M floats).
 template <int M> struct SimtRows { static constexpr int R = 4; };
@@ -239,32 +188,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   if (threadIdx.x < kWave) {
     f32x4 s = part[threadIdx.x];
     for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
-    const int m = threadIdx.x & 15;
-    const int nb = (threadIdx.x >> 4) * 4;
-    if (ROPE && tr.rotated()) {
-      float v[4], pv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        v[i] = m < M ? round_as<T>(epilogue(e, s[i], m, tr.row(nb + i))) : 0.f;
-        pv[i] = __shfl_xor(v[i], 32, kWave);
-      }
-      if (m < M) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool first = nb < 8;
-          float o1, o2;
-          rope_pair(rp, m, tr.col(first ? nb + i : nb + i - 8), first ? v[i] : pv[i],
-                    first ? pv[i] : v[i], o1, o2);
-          y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(first ? o1 : o2);
-        }
-      }
-    } else if (m < M) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
-        if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, s[i], m, n));
-      }
-    }
+    mfma_tile_out<T, ROPE>(y, s, threadIdx.x, n0, tr, e, rp, NoScale{}, M, N, sym, syn);
   }
 }
 
@@ -471,34 +395,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    const TileRows<R> tr(rp, tile);
-    if (tr.rotated()) {
-      // thread (p, m): pair p of the tile, slots p and p + 2
-      for (int t = threadIdx.x; t < 2 * M; t += blockDim.x) {
-        const int p = t / M, m = t % M;
-        float s1 = 0.f, s2 = 0.f;
-        for (int i = 0; i < nw; ++i) {
-          s1 += part[i * V + p * M + m];
-          s2 += part[i * V + (p + 2) * M + m];
-        }
-        const int64_t n1 = tr.row(p), n2 = tr.row(p + 2);
-        float o1, o2;
-        rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, s1, m, n1)),
-                  round_as<T>(epilogue(e, s2, m, n2)), o1, o2);
-        y[m * (int64_t)N + n1] = from_f32<T>(o1);
-        y[m * (int64_t)N + n2] = from_f32<T>(o2);
-      }
-    } else {
-      for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
-        const int r = t / M, m = t % M;
-        const int64_t n = tr.row(r);
-        if (n < N) {
-          float s = 0.f;
-          for (int i = 0; i < nw; ++i) s += part[i * V + t];
-          y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, s, m, n));
-        }
-      }
-    }
+    qkv_tile_out<T, M>(y, part, V, nw, TileRows<R>(rp, tile), e, rp, NoScale{}, N);
   }
 }
 
@@ -994,49 +891,18 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
                                int64_t rope_cols, int64_t head_dim, float eps, int kind,
                                int act_dtype, void* stream) {
   using namespace fd;
-  if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
-    return FD_EINVAL;
   if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
     return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
-  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
-  if (H <= 0 || N <= 0) return set_error(FD_EINVAL, "H and N must be positive");
-  if (!(eps >= 0.f) || eps == INFINITY) return set_error(FD_EINVAL, "eps must be a finite value >= 0");
-  if (rope_cols < 0 || rope_cols > N) return set_error(FD_EINVAL, "rope_cols must be in [0, N]");
-  if (rope_cols > 0) {
-    if (head_dim <= 0 || head_dim % 2 != 0) return set_error(FD_EINVAL, "head_dim must be even");
-    if (rope_cols % head_dim != 0)
-      return set_error(FD_EINVAL, "rope_cols must be a multiple of head_dim");
-    if (!check_any_dtype(cs_dtype, "cs_dtype")) return FD_EINVAL;
-    if (cs_row_stride < 0) return set_error(FD_EINVAL, "cs_row_stride must be >= 0");
-    if (head_dim % 16 != 0 || head_dim > 0x7fffffffLL)
-      return set_error(FD_EUNSUPPORTED, "head_dim must be a multiple of 16");
-  }
-  if (bias && !check_any_dtype(bias_dtype, "bias_dtype")) return FD_EINVAL;
-  if (M == 0) return FD_OK;
-  if (!y || !hidden || !norm_w || !w_qkv || (rope_cols > 0 && (!cos || !sin)))
-    return set_error(FD_EINVAL, "null pointer argument");
-  if (H % 8 != 0) return set_error(FD_EUNSUPPORTED, "H must be a multiple of 8");
-  if (H > 0x7fffffffLL || N > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
-  if (!aligned16(hidden) || !aligned16(norm_w) || !aligned16(w_qkv))
-    return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   const bool mfma = mlp_needs_normed(M, kind);
-  if (mfma && (!normed || !aligned16(normed)))
-    return set_error(FD_EINVAL, "kind=dot with M >= 5 needs a 16-byte aligned normed buffer");
-  hipStream_t st = static_cast<hipStream_t>(stream);
   Epi e;
-  e.bias = bias;
-  e.bias_dtype = bias_dtype;
-  e.sb = 1;
-  e.row = nullptr;
-  e.row_dtype = act_dtype;
-  e.srm = e.srn = 0;
   Rope rp;
-  rp.cos = cos;
-  rp.sin = sin;
-  rp.dtype = cs_dtype;
-  rp.rs = cs_row_stride;
-  rp.cols = (int)rope_cols;
-  rp.dim = rope_cols > 0 ? (int)head_dim : 2;
+  bool empty = false;
+  const int checked = qkv_prepare(y, normed, hidden, norm_w, norm_w_dtype, w_qkv, bias, bias_dtype,
+                                  cos, sin, cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim,
+                                  eps, act_dtype, mfma, e, rp, empty);
+  if (checked != FD_OK || empty) return checked;
+  if (H % 8 != 0) return set_error(FD_EUNSUPPORTED, "H must be a multiple of 8");
+  hipStream_t st = static_cast<hipStream_t>(stream);
   int rc;
   if (mfma) {
     rp.tiles = (int)(rope_cols / 16);

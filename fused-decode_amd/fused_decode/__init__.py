@@ -17,7 +17,7 @@ from .ops import (
     swiglu,
 )
 
-from .fp8 import dequantize_fp8, linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
+from .fp8 import dequantize_fp8, linear_decode_fp8, post_attn_mlp_fp8, pre_attn_qkv_fp8, quantize_fp8
 from . import library  # registers torch.ops.fused_decode.* (custom ops with fake kernels)
 
 __version__ = "0.1.0"
@@ -28,6 +28,7 @@ __all__ = [
     "dequantize_fp8",
     "linear_decode_fp8",
     "post_attn_mlp_fp8",
+    "pre_attn_qkv_fp8",
     "quantize_fp8",
     "linear_decode",
     "post_attn_mlp",

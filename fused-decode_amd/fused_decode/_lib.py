@@ -70,6 +70,8 @@ SIGNATURES: dict[str, list] = {
     "fd_mlp_gate_up": [_p, _p, _p, _p, _i, _p, _l, _l, _l, _f, _i, _i, _p],
     "fd_pre_attn_qkv": [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i,
                         _i, _p],
+    "fd_pre_attn_qkv_fp8": [_p, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l,
+                            _l, _f, _i, _p],
     "fd_copy": [_p, _p, _l, _p],
     "fd_triad": [_p, _p, _p, _f, _l, _i, _p],
 }

@@ -381,10 +381,9 @@ def bench_qkv(dtype, roof, quick, cpu) -> list[dict]:
 
 
 def bench_fp8(dtype, roof, quick, cpu) -> list[dict]:
-    """FP8-weight GEMV (the four decode shapes, M = 1 and 8) and MLP (M = 1 and 8)
-    beside their fp16-weight counterparts; bytes count one byte per weight plus the
-    float32 scales."""
-    from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
+    """FP8-weight GEMV (the four decode shapes, M = 1 and 8), MLP and fused QKV
+    (M = 1 and 8); bytes count one byte per weight plus the float32 scales."""
+    from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, pre_attn_qkv_fp8, quantize_fp8
 
     rows = []
     e = torch.empty((), dtype=dtype).element_size()
@@ -419,6 +418,26 @@ def bench_fp8(dtype, roof, quick, cpu) -> list[dict]:
         rows.append(_row(f"post_attn_mlp_fp8 M={m} {dtype}", nbytes, cold, warm, roof, dev))
         _print(rows[-1])
     del sets
+    torch.cuda.empty_cache()
+    d = 128
+    n, rc = 48 * d, 40 * d
+    k = copies_for(n * h)
+    qsets = [(_gen((h,), dtype, g, 0.1, 1.0),) + quantize_fp8(_gen((n, h), dtype, g, h ** -0.5))
+             for _ in range(k)]
+    ang = 1024 * (1.0 / (500000.0 ** (torch.arange(0, d, 2, device="cuda", dtype=torch.float64) / d)))
+    cos = torch.cat([ang, ang]).cos().to(dtype).view(1, d)
+    sin = torch.cat([ang, ang]).sin().to(dtype).view(1, d)
+    for m in ([1] if quick else [1, 8]):
+        hid = _gen((m, h), dtype, g)
+        out = torch.empty(m, n, device="cuda", dtype=dtype)
+        fn = lambda j: pre_attn_qkv_fp8(hid, *qsets[j % k], cos, sin, 1e-5, rope_cols=rc, out=out)  # noqa: E731
+        cold = time_us(fn, iters=max(30, 2 * k))
+        dev = graph_us(fn, k)
+        warm = time_us(lambda j: fn(0), iters=30)
+        nbytes = n * h + 4 * n + (m * h + h + m * n) * e + 2 * d * e
+        rows.append(_row(f"pre_attn_qkv_fp8 M={m} {dtype}", nbytes, cold, warm, roof, dev))
+        _print(rows[-1])
+    del qsets
     torch.cuda.empty_cache()
     return rows
 

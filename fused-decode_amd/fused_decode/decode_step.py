@@ -25,8 +25,8 @@ the down projection). Both forms compute the same values with the same rounding
 points. The whole step is captured once and replayed.
 
 With weights="fp8" the four projections hold E4M3 codes with per-row scales
-(quantize_fp8) and run as linear_decode_fp8 / post_attn_mlp_fp8, the QKV as
-rms_norm, fp8 GEMV and rope (six launches per layer at M < 5).
+(quantize_fp8) and the layer runs as pre_attn_qkv_fp8, linear_decode_fp8 (O-proj
+with the residual) and post_attn_mlp_fp8: four launches per layer at M < 5.
 
 Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), half that
 plus the scales in fp8, random with the benchmark distributions (no checkpoint
@@ -37,13 +37,12 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 
 import torch
 
 from .kernels import _MFMA_MIN_M
-from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, quantize_fp8
-from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope
+from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, pre_attn_qkv_fp8, quantize_fp8
+from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rope
 
 H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
 QKV = (HEADS + 2 * KV_HEADS) * HEAD_DIM  # 6144
@@ -119,14 +118,13 @@ class DecodeStep:
         return self._step_fused() if self.fused else self._step_composed()
 
     def _step_fp8(self) -> torch.Tensor:
-        """The fused layer with E4M3 projections: RMSNorm, fp8 QKV GEMV and RoPE as
-        three launches, fp8 O-proj with the residual, fp8 post_attn_mlp."""
+        """The fused layer with E4M3 projections: pre_attn_qkv_fp8, fp8 O-proj with
+        the residual, post_attn_mlp_fp8."""
         x = self.x_in
-        qk = self.qkv[:, : self.qk_heads * HEAD_DIM].view(self.m, self.qk_heads, HEAD_DIM)
+        rope_cols = self.qk_heads * HEAD_DIM
         for w in self.w:
-            rms_norm(x, w["attn_norm"], 1e-5, out=self.normed)
-            linear_decode_fp8(self.normed, *w["qkv"], out=self.qkv)
-            rope(qk, self.cos, self.sin, out=qk)
+            pre_attn_qkv_fp8(x, w["attn_norm"], *w["qkv"], self.cos, self.sin, 1e-5, rope_cols=rope_cols,
+                             out=self.qkv)
             linear_decode_fp8(w["attn_out"], *w["o"], row_add=x, out=self.hbuf)
             x = post_attn_mlp_fp8(self.hbuf, w["mlp_norm"], *w["gate_up"], *w["down"], 1e-5)
         self.out.copy_(x)
@@ -161,8 +159,8 @@ class DecodeStep:
         add a row kernel for the RMSNorm)."""
         mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
         mlp = 3 if mfma else 2
-        if self.fp8:
-            return 3 + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
+        if self.fp8:  # the fp8 kernels take the MFMA forms from 5 rows whatever the kind
+            return (2 if self.m >= _MFMA_MIN_M else 1) + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
         if self.fused:
             return (2 if mfma else 1) + 1 + mlp
         return 4 + mlp

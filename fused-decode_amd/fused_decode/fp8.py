@@ -3,6 +3,7 @@
     q, scale = quantize_fp8(w)                        # [N, K] -> e4m3 codes + float32 [N]
     y = linear_decode_fp8(x, q, scale, bias, row_add=r)
     y = post_attn_mlp_fp8(hidden, norm_w, q_gu, s_gu, q_d, s_d, eps)
+    y = pre_attn_qkv_fp8(hidden, norm_w, q_qkv, s_qkv, cos, sin, eps, rope_cols=c)
 
 Per-output-channel quantisation: scale[n] = max|w[n, :]| * (1/448) and the codes are
 w / scale rounded to nearest-even E4M3 (torch's float8_e4m3fn cast). The HIP
@@ -22,11 +23,22 @@ import torch
 
 from . import _lib
 from ._lib import DTYPE_CODE, check, lib, stream_of
-from .ops import _as_mk, _as_row_add, _check_activation, _check_eps, _check_norm_weight, rms_norm, swiglu
+from .ops import (
+    _as_mk,
+    _as_row_add,
+    _check_activation,
+    _check_eps,
+    _check_norm_weight,
+    _qkv_args,
+    _rope_qkv_heads,
+    rms_norm,
+    swiglu,
+)
 
 FP8_MAX = 448.0
 FP8_DTYPE = torch.float8_e4m3fn
 _HAND_LIMIT = 16
+_FP8_MFMA_MIN_M = 5  # rows from which the fp8 kernels run on MFMA (fp8.hip)
 
 
 def quantize_fp8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -66,7 +78,7 @@ def _fp8_rows_ok(weight: torch.Tensor) -> bool:
         and weight.shape[1] % 16 == 0 and weight.data_ptr() % 16 == 0
 
 
-def _reference_path(x2, weight, scale, bias, ra, dtype):
+def _decoded_product(x2, weight, scale, bias, ra, dtype):
     """float32 product of the decoded weights, for shapes the HIP kernel does not take."""
     y = (x2.float() @ weight.float().t()) * scale
     if bias is not None:
@@ -119,7 +131,7 @@ def linear_decode_fp8(
         return out
     if m > _HAND_LIMIT or not _fp8_rows_ok(weight) or x2.stride(1) != 1 or \
             (m > 1 and x2.stride(0) % 8 != 0) or x2.data_ptr() % 16 != 0:
-        y2.copy_(_reference_path(x2, weight, scale, bias, ra, x.dtype))
+        y2.copy_(_decoded_product(x2, weight, scale, bias, ra, x.dtype))
         return out
     bias_ptr, bias_code, sb = None, DTYPE_CODE[x.dtype], 0
     if bias is not None:
@@ -188,4 +200,57 @@ def post_attn_mlp_fp8(
     return linear_decode_fp8(swiglu(gate, up), w_down, down_scale, row_add=hidden)
 
 
-__all__ = ["FP8_MAX", "dequantize_fp8", "linear_decode_fp8", "post_attn_mlp_fp8", "quantize_fp8"]
+def pre_attn_qkv_fp8(
+    hidden: torch.Tensor,
+    norm_weight: torch.Tensor,
+    w_qkv: torch.Tensor,
+    scale: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float = 1e-6,
+    *,
+    rope_cols: int,
+    bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``pre_attn_qkv`` with E4M3 ``w_qkv [N, H]`` and its float32 per-row
+    ``scale [N]``: RMSNorm, the projection as ``linear_decode_fp8``'s product (plus
+    ``bias``), rounding, then RoPE of the first ``rope_cols`` columns, with the
+    argument rules of ``pre_attn_qkv``. One HIP launch up to 4 rows, two up to 16
+    (the norm runs as a row kernel ahead of the MFMA form); otherwise, or for
+    shapes the kernels do not take, composed from the operators."""
+    _check_activation(hidden, "hidden")
+    _check_fp8_weight(w_qkv, scale, hidden, "w_qkv")
+    n, h = w_qkv.shape
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    out, m = a.out, a.m
+    if m == 0 or n == 0:
+        return out
+    if m <= _HAND_LIMIT and w_qkv.is_contiguous() and h % 16 == 0:
+        h2 = hidden.reshape(m, h)
+        if not h2.is_contiguous():
+            h2 = h2.contiguous()
+        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
+        b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
+        normed = None
+        if m >= _FP8_MFMA_MIN_M:
+            normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
+        status = lib().fd_pre_attn_qkv_fp8(
+            out.data_ptr(), normed.data_ptr() if normed is not None else None, h2.data_ptr(),
+            nw.data_ptr(), DTYPE_CODE[nw.dtype], w_qkv.data_ptr(), scale.contiguous().data_ptr(),
+            b.data_ptr() if b is not None else None,
+            DTYPE_CODE[b.dtype] if b is not None else DTYPE_CODE[hidden.dtype],
+            a.cos.data_ptr(), a.sin.data_ptr(), DTYPE_CODE[a.cos.dtype], a.cs_row_stride, m, h, n,
+            a.rope_cols, a.d, float(a.eps), DTYPE_CODE[hidden.dtype], stream_of(hidden),
+        )
+        if status != _lib.FD_EUNSUPPORTED:
+            check("fd_pre_attn_qkv_fp8", status)
+            return out
+    normed = rms_norm(hidden, norm_weight, eps=a.eps)
+    linear_decode_fp8(normed, w_qkv, scale, bias, out=out)
+    _rope_qkv_heads(a)
+    return out
+
+
+__all__ = ["FP8_MAX", "dequantize_fp8", "linear_decode_fp8", "post_attn_mlp_fp8", "pre_attn_qkv_fp8",
+           "quantize_fp8"]

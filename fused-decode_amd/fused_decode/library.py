@@ -9,6 +9,7 @@
     torch.ops.fused_decode.pre_attn_qkv(hidden, norm_weight, w_qkv, cos, sin, eps, rope_cols, bias, kind)
     torch.ops.fused_decode.linear_decode_fp8(x, weight, scale, bias, row_add)
     torch.ops.fused_decode.post_attn_mlp_fp8(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps)
+    torch.ops.fused_decode.pre_attn_qkv_fp8(hidden, norm_weight, w_qkv, scale, cos, sin, eps, rope_cols, bias)
 
 Each is the functional form (no ``out=``) of the operator of the same name in
 ``fused_decode.ops``, registered as a custom op with a fake (meta) kernel, so
@@ -133,5 +134,17 @@ def _post_attn_mlp_fp8_fake(hidden, norm_weight, w_gate_up, gate_up_scale, w_dow
     return hidden.new_empty(hidden.shape)
 
 
+@torch.library.custom_op(f"{_NS}::pre_attn_qkv_fp8", mutates_args=())
+def pre_attn_qkv_fp8(hidden: Tensor, norm_weight: Tensor, w_qkv: Tensor, scale: Tensor, cos: Tensor,
+                     sin: Tensor, eps: float, rope_cols: int, bias: Tensor | None = None) -> Tensor:
+    return fp8.pre_attn_qkv_fp8(hidden, norm_weight, w_qkv, scale, cos, sin, eps, rope_cols=rope_cols,
+                                bias=bias)
+
+
+@pre_attn_qkv_fp8.register_fake
+def _pre_attn_qkv_fp8_fake(hidden, norm_weight, w_qkv, scale, cos, sin, eps, rope_cols, bias=None):
+    return hidden.new_empty((*_lead(hidden), w_qkv.shape[0]))
+
+
 OPS = ("rms_norm", "add_rms_norm", "rope", "swiglu", "linear_decode", "post_attn_mlp", "pre_attn_qkv",
-       "linear_decode_fp8", "post_attn_mlp_fp8")
+       "linear_decode_fp8", "post_attn_mlp_fp8", "pre_attn_qkv_fp8")

@@ -11,6 +11,7 @@ passing ``kind`` forces the GEMV up to 16 rows, as in the reference.
 from __future__ import annotations
 
 import math
+from typing import NamedTuple
 
 import torch
 import torch.nn.functional as F
@@ -370,44 +371,24 @@ def _token_angles(src: torch.Tensor, lead: tuple, name: str) -> torch.Tensor:
     return full.reshape(-1, d).contiguous()
 
 
-def pre_attn_qkv(
-    hidden: torch.Tensor,
-    norm_weight: torch.Tensor,
-    w_qkv: torch.Tensor,
-    cos: torch.Tensor,
-    sin: torch.Tensor,
-    eps: float = 1e-6,
-    *,
-    rope_cols: int,
-    bias: torch.Tensor | None = None,
-    out: torch.Tensor | None = None,
-    kind: str | None = None,
-) -> torch.Tensor:
-    """Pre-attention half of a Llama decode layer: RMSNorm, the fused QKV
-    projection and RoPE of the q and k heads.
+class _QkvArgs(NamedTuple):
+    m: int
+    n: int
+    h: int
+    d: int
+    rope_cols: int
+    eps: float
+    cos: torch.Tensor  # [1 or m, d] contiguous rows
+    sin: torch.Tensor
+    cs_row_stride: int
+    out: torch.Tensor
 
-    ``hidden`` is ``[..., H]``, ``w_qkv`` is ``[N, H]`` (q, k, v rows stacked),
-    ``bias`` is ``[N]`` (hidden's dtype or float32) or None. The first
-    ``rope_cols`` output columns, viewed as heads of ``D = cos.shape[-1]``, get the
-    rotate-half RoPE of ``rope`` with one cos/sin row per token: ``cos``/``sin``
-    broadcast to ``[..., D]`` (``[D]`` or ``[1, D]`` for one position, ``[..., D]``
-    or ``[..., 1, D]`` per token). Returns ``[..., N]`` equal to
-    ``rope(linear_decode(rms_norm(hidden), w_qkv, bias)[..., :rope_cols])`` with
-    the reference's rounding after each step. Up to the GEMV row limit this is one
-    HIP launch (two for kind "dot" from 5 rows: the norm runs as a row kernel).
-    No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
-    :138-160.
-    """
-    _check_activation(hidden, "hidden")
-    if w_qkv.ndim != 2:
-        raise ValueError(f"w_qkv must have shape [N, H], got {tuple(w_qkv.shape)}")
-    n, h = w_qkv.shape
+
+def _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out) -> _QkvArgs:
+    """Checks and operands shared by ``pre_attn_qkv`` and its fp8 form, for a
+    projection of ``n`` rows over ``h`` (``hidden [..., h]``)."""
     if hidden.shape[-1] != h:
         raise ValueError(f"hidden last dim {hidden.shape[-1]} != w_qkv H {h}")
-    if w_qkv.dtype != hidden.dtype:
-        raise TypeError("w_qkv must match hidden dtype")
-    if w_qkv.device != hidden.device:
-        raise ValueError("w_qkv must be on the same device as hidden")
     _check_norm_weight(norm_weight, hidden)
     eps = _check_eps(eps)
     for name, t in (("cos", cos), ("sin", sin)):
@@ -442,14 +423,61 @@ def pre_attn_qkv(
         if not out.is_contiguous():
             raise ValueError("out must be contiguous")
     m = hidden.numel() // h if h else 0
+    if m and n and cos_r.shape[0] not in (1, m):
+        raise ValueError(f"cos/sin need 1 or {m} rows, got {cos_r.shape[0]}")
+    rs = 0 if cos_r.shape[0] == 1 else d
+    return _QkvArgs(m, n, h, d, rope_cols, eps, cos_r, sin_r, rs, out)
+
+
+def _rope_qkv_heads(a: _QkvArgs) -> None:
+    """RoPE of the first ``rope_cols`` columns of ``a.out`` in place (the composed path)."""
+    if a.rope_cols:
+        heads = a.out.view(a.m, a.n)[:, : a.rope_cols].unflatten(-1, (a.rope_cols // a.d, a.d))
+        rope(heads, a.cos.unsqueeze(1), a.sin.unsqueeze(1), out=heads)
+
+
+def pre_attn_qkv(
+    hidden: torch.Tensor,
+    norm_weight: torch.Tensor,
+    w_qkv: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    eps: float = 1e-6,
+    *,
+    rope_cols: int,
+    bias: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    kind: str | None = None,
+) -> torch.Tensor:
+    """Pre-attention half of a Llama decode layer: RMSNorm, the fused QKV
+    projection and RoPE of the q and k heads.
+
+    ``hidden`` is ``[..., H]``, ``w_qkv`` is ``[N, H]`` (q, k, v rows stacked),
+    ``bias`` is ``[N]`` (hidden's dtype or float32) or None. The first
+    ``rope_cols`` output columns, viewed as heads of ``D = cos.shape[-1]``, get the
+    rotate-half RoPE of ``rope`` with one cos/sin row per token: ``cos``/``sin``
+    broadcast to ``[..., D]`` (``[D]`` or ``[1, D]`` for one position, ``[..., D]``
+    or ``[..., 1, D]`` per token). Returns ``[..., N]`` equal to
+    ``rope(linear_decode(rms_norm(hidden), w_qkv, bias)[..., :rope_cols])`` with
+    the reference's rounding after each step. Up to the GEMV row limit this is one
+    HIP launch (two for kind "dot" from 5 rows: the norm runs as a row kernel).
+    No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
+    :138-160.
+    """
+    _check_activation(hidden, "hidden")
+    if w_qkv.ndim != 2:
+        raise ValueError(f"w_qkv must have shape [N, H], got {tuple(w_qkv.shape)}")
+    n, h = w_qkv.shape
+    if w_qkv.dtype != hidden.dtype:
+        raise TypeError("w_qkv must match hidden dtype")
+    if w_qkv.device != hidden.device:
+        raise ValueError("w_qkv must be on the same device as hidden")
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    out, m, eps = a.out, a.m, a.eps
     if m == 0 or n == 0:
         return out
     hand_limit = _HAND_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
     kind_r = resolve_kind(kind)
-    if cos_r.shape[0] not in (1, m):
-        raise ValueError(f"cos/sin need 1 or {m} rows, got {cos_r.shape[0]}")
-    rs = 0 if cos_r.shape[0] == 1 else d
-    y2 = out.view(m, n)
     if m <= hand_limit and w_qkv.is_contiguous():
         h2 = hidden.reshape(m, h)
         if not h2.is_contiguous():
@@ -459,13 +487,11 @@ def pre_attn_qkv(
         normed = None
         if kind_r == "dot" and m >= _MFMA_MIN_M:
             normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
-        status = pre_attn_qkv_out(h2, nw, w_qkv, b, cos_r, sin_r, rs, rope_cols, d, eps, y2,
-                                  normed, kind_r)
+        status = pre_attn_qkv_out(h2, nw, w_qkv, b, a.cos, a.sin, a.cs_row_stride, a.rope_cols,
+                                  a.d, eps, out.view(m, n), normed, kind_r)
         if status == _lib.FD_OK:
             return out
     normed = rms_norm(hidden, norm_weight, eps=eps)
     linear_decode(normed, w_qkv, bias, out=out, kind=kind)
-    if rope_cols:
-        heads = y2[:, :rope_cols].unflatten(-1, (rope_cols // d, d))
-        rope(heads, cos_r.unsqueeze(1), sin_r.unsqueeze(1), out=heads)
+    _rope_qkv_heads(a)
     return out

@@ -208,8 +208,8 @@ int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_
  * aligned rows (else FD_EUNSUPPORTED). bias/row_add as in fd_linear. The
  * weights are decoded exactly and the arithmetic is float32: the activations
  * are never quantised.
- * No reference counterpart: the survey's last "next" item (low-precision weight
- * formats), halving the bytes the decode GEMV streams.
+ * No reference counterpart (its weights are fp16/bf16 only): a low-precision
+ * weight format, halving the bytes the decode GEMV streams.
  */
 int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
                   const void* bias, int bias_dtype, const void* row_add, int row_dtype,
@@ -229,6 +229,23 @@ int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* nor
                          int norm_w_dtype, const void* w_gate_up8, const float* gate_up_scale,
                          const void* w_down8, const float* down_scale, int64_t M, int64_t H,
                          int64_t I, float eps, int act_dtype, void* stream);
+
+/*
+ * fd_pre_attn_qkv with FP8 weights: w_qkv8 [N,H] E4M3 codes (contiguous) with
+ * per-row float32 scales w_scale [N]; the projection is fd_linear_fp8's product
+ * and everything else (RMSNorm, bias, rounding, RoPE of the first rope_cols
+ * columns, cos/sin layout) is fd_pre_attn_qkv's. One launch up to M = 4; from
+ * M = 5 the RMSNorm runs first into `normed` ([M,H], 16-byte aligned; unused and
+ * may be NULL below that) and the products run on MFMA. H % 16 == 0 and
+ * head_dim % 16 == 0 (else FD_EUNSUPPORTED). No reference counterpart (see
+ * fd_linear_fp8 and fd_pre_attn_qkv).
+ */
+int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* norm_w,
+                        int norm_w_dtype, const void* w_qkv8, const float* w_scale,
+                        const void* bias, int bias_dtype, const void* cos, const void* sin,
+                        int cs_dtype, int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
+                        int64_t rope_cols, int64_t head_dim, float eps, int act_dtype,
+                        void* stream);
 
 /*
  * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned

@@ -120,17 +120,21 @@ def pre_attn_qkv(hidden, norm_w, w_qkv, cos, sin, eps: float, rope_cols: int, bi
     bias) (reference.py:50-63), then rotate-half RoPE (reference.py:38-47) of the
     first rope_cols columns viewed as heads of D = cos.shape[-1], each row m with
     cos/sin row m (one row broadcasts to all)."""
-    hidden = np.asarray(hidden, F32)
-    m = hidden.shape[0]
-    h = rms_norm(hidden, norm_w, eps, dtype)
-    y = linear(h, w_qkv, bias=bias, dtype=dtype)
-    if rope_cols:
-        d = np.shape(cos)[-1]
-        c = np.asarray(cos, F32).reshape(-1, 1, d)
-        s = np.asarray(sin, F32).reshape(-1, 1, d)
-        heads = y[:, :rope_cols].reshape(m, rope_cols // d, d)
-        y = y.copy()
-        y[:, :rope_cols] = rope(heads, c, s, dtype).reshape(m, rope_cols)
+    h = rms_norm(np.asarray(hidden, F32), norm_w, eps, dtype)
+    return _rope_leading_cols(linear(h, w_qkv, bias=bias, dtype=dtype), cos, sin, rope_cols, dtype)
+
+
+def _rope_leading_cols(y, cos, sin, rope_cols: int, dtype: str) -> np.ndarray:
+    """Rotate-half RoPE of y[:, :rope_cols] viewed as heads of D = cos.shape[-1]."""
+    if not rope_cols:
+        return y
+    m = y.shape[0]
+    d = np.shape(cos)[-1]
+    c = np.asarray(cos, F32).reshape(-1, 1, d)
+    s = np.asarray(sin, F32).reshape(-1, 1, d)
+    heads = y[:, :rope_cols].reshape(m, rope_cols // d, d)
+    y = y.copy()
+    y[:, :rope_cols] = rope(heads, c, s, dtype).reshape(m, rope_cols)
     return y
 
 
@@ -204,6 +208,20 @@ def post_attn_mlp_fp8(hidden, norm_w, gu_codes, gu_scale, d_codes, d_scale, eps:
     gu = linear_fp8(h, gu_codes, gu_scale, dtype=dtype)
     mid = swiglu(gu[..., :i], gu[..., i:], dtype)
     return linear_fp8(mid, d_codes, d_scale, row_add=hidden, dtype=dtype)
+
+
+def pre_attn_qkv_fp8(hidden, norm_w, codes, scale, cos, sin, eps: float, rope_cols: int,
+                     bias=None, dtype: str = "f16") -> np.ndarray:
+    """pre_attn_qkv with fp8 weights: the same rounding points, the projection as
+    linear_fp8."""
+    h = rms_norm(np.asarray(hidden, F32), norm_w, eps, dtype)
+    y = linear_fp8(h, codes, scale, bias=bias, dtype=dtype)
+    return _rope_leading_cols(y, cos, sin, rope_cols, dtype)
+
+
+def bytes_qkv_fp8(m: int, h: int, n: int, head_dim: int, cs_rows: int, e: int = 2, ce: int = 2) -> int:
+    """fp8 weights + fp32 scales + hidden read + norm weight + output write + cos/sin rows."""
+    return n * h + 4 * n + (m * h + h + m * n) * e + 2 * cs_rows * head_dim * ce
 
 
 def bytes_linear_fp8(m: int, n: int, k: int, e: int = 2) -> int:

@@ -165,3 +165,15 @@ def test_fp8_entry_points_reject(L):
     assert mlp(17, 64, 128) == L.FD_EINVAL
     assert mlp(2, 72, 128) == L.FD_EUNSUPPORTED
     assert mlp(0, 64, 128) == L.FD_OK
+
+    def qkv(m=2, h=64, rope_cols=64, head_dim=32, scale=FAKE, normed=None):
+        return lib.fd_pre_attn_qkv_fp8(FAKE, normed, FAKE, FAKE, 0, FAKE, scale, None, 0, FAKE, FAKE, 2, 0,
+                                       m, h, 96, rope_cols, head_dim, 1e-6, 0, None)
+
+    assert qkv(m=17) == L.FD_EINVAL
+    assert qkv(scale=None) == L.FD_EINVAL                  # scale is required
+    assert qkv(h=72) == L.FD_EUNSUPPORTED                  # H % 16
+    assert qkv(head_dim=24, rope_cols=48) == L.FD_EUNSUPPORTED
+    assert qkv(rope_cols=48) == L.FD_EINVAL                # not a multiple of head_dim
+    assert qkv(m=5) == L.FD_EINVAL                         # the MFMA form needs `normed`
+    assert qkv(m=0) == L.FD_OK

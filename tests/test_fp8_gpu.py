@@ -1,5 +1,6 @@
-"""GPU parity of the FP8-weight GEMV and MLP against the oracle's E4M3 products
-(oracle.linear_fp8 / post_attn_mlp_fp8 on the same codes and scales), at the
+"""GPU parity of the FP8-weight GEMV, MLP and fused QKV against the oracle's E4M3
+products (oracle.linear_fp8 / post_attn_mlp_fp8 / pre_attn_qkv_fp8 on the same
+codes and scales), at the
 reference's GEMV tolerance (tests/test_ops.py:27-35: fp16 2e-2, bf16 4e-2): the
 codes are decoded exactly on both sides, so only summation order differs."""
 
@@ -180,10 +181,8 @@ def test_decode_step_fp8_matches_oracle_and_graph():
     cos, sin = npf(ds.cos), npf(ds.sin)
     qk = ds.qk_heads * HEAD_DIM
     for w in ds.w:
-        normed = O.rms_norm(x, npf(w["attn_norm"]), 1e-5, "f16")
-        qkv = O.linear_fp8(normed, codes(w["qkv"][0]), npf(w["qkv"][1]), dtype="f16")
-        q = qkv[:, :qk].reshape(m, ds.qk_heads, HEAD_DIM)
-        qkv[:, :qk] = O.rope(q, cos, sin, "f16").reshape(m, qk)
+        qkv = O.pre_attn_qkv_fp8(x, npf(w["attn_norm"]), codes(w["qkv"][0]), npf(w["qkv"][1]), cos, sin,
+                                 1e-5, qk, dtype="f16")
         h = O.linear_fp8(npf(w["attn_out"]), codes(w["o"][0]), npf(w["o"][1]), row_add=x, dtype="f16")
         x = O.post_attn_mlp_fp8(h, npf(w["mlp_norm"]), codes(w["gate_up"][0]), npf(w["gate_up"][1]),
                                 codes(w["down"][0]), npf(w["down"][1]), 1e-5, "f16")
@@ -195,4 +194,123 @@ def test_decode_step_fp8_matches_oracle_and_graph():
         out = ds.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, rtol=0, atol=0)
-    assert ds.launches_per_layer == 6
+    assert ds.launches_per_layer == 4
+
+
+# ---------------------------------------------------------------- fused QKV
+
+
+def qkv_case(m, h, heads, kv, d, dtype, seed, bias=False, per_row=True, cs_dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    n = (heads + 2 * kv) * d
+    hidden = (torch.randn(m, h, generator=g)).to(dtype)
+    norm_w = (torch.randn(h, generator=g) * 0.1 + 1.0).to(dtype)
+    w = torch.randn(n, h, generator=g) * h ** -0.5
+    b = torch.randn(n, generator=g) * 0.5 if bias else None
+    rows = m if per_row else 1
+    inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    pos = torch.arange(900 + seed, 900 + seed + rows, dtype=torch.float64)
+    emb = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], dim=1)
+    q, s, qn, sn = quant(w)
+    return (hidden, norm_w, q, s, qn, sn, b, emb.cos().to(cs_dtype), emb.sin().to(cs_dtype),
+            (heads + kv) * d)
+
+
+def qkv_run(hidden, norm_w, q, s, b, cos, sin, rc, eps=1e-5, out=None):
+    import fused_decode as fd
+
+    dev = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    return fd.pre_attn_qkv_fp8(dev(hidden), dev(norm_w), q, s, dev(cos), dev(sin), eps, rope_cols=rc,
+                               bias=dev(b), out=out)
+
+
+def qkv_oracle(hidden, norm_w, qn, sn, b, cos, sin, rc, dtype, eps=1e-5):
+    return O.pre_attn_qkv_fp8(npf(hidden), npf(norm_w), qn, sn, npf(cos), npf(sin), eps, rc,
+                              bias=None if b is None else npf(b), dtype=tag(dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
+def test_pre_attn_qkv_fp8_matches_oracle(dtype, m):
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 512, 4, 2, 64, dtype, seed=m, bias=m % 2 == 1)
+    y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, dtype)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_pre_attn_qkv_fp8_shared_angles_and_rope_cols_edges(m):
+    """One cos/sin row for every token in each angle dtype; rope_cols 0 (norm +
+    GEMV only) and N (every column rotated)."""
+    for cs_dtype in (torch.float16, torch.bfloat16, torch.float32):
+        hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 256, 2, 1, 128, torch.float16, seed=30 + m,
+                                                             bias=True, per_row=False, cs_dtype=cs_dtype)
+        y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+        ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    n = q.shape[0]
+    for rc in (0, n):
+        y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+        ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
+def test_pre_attn_qkv_fp8_composes_where_the_kernel_declines():
+    """head_dim 72 and 24 rows: composed from rms_norm, linear_decode_fp8 and rope,
+    same values."""
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(2, 256, 2, 1, 72, torch.float16, seed=9)
+    y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(24, 256, 2, 1, 64, torch.bfloat16, seed=10)
+    y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.bfloat16)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 8])
+def test_pre_attn_qkv_fp8_llama3_8b(dtype, m):
+    """H=4096, 32 q + 8 kv heads of 128: the fused call against the library's own
+    composition (rms_norm, linear_decode_fp8, rope) and row 0 of the oracle."""
+    import fused_decode as fd
+
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 4096, 32, 8, 128, dtype, seed=20 + m)
+    hd, nwd, cd, sd = (t.to(DEV) for t in (hidden, nw, cos, sin))
+    y = fd.pre_attn_qkv_fp8(hd, nwd, q, s, cd, sd, 1e-5, rope_cols=rc)
+    comp = fd.linear_decode_fp8(fd.rms_norm(hd, nwd, eps=1e-5), q, s)
+    heads = comp[:, :rc].unflatten(-1, (rc // 128, 128))
+    fd.rope(heads, cd[:, None], sd[:, None], out=heads)
+    torch.testing.assert_close(y, comp, **tol(dtype))
+    ref = qkv_oracle(hidden[:1], nw, qn, sn, b, cos[:1], sin[:1], rc, dtype)
+    torch.testing.assert_close(y[:1].float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
+def test_pre_attn_qkv_fp8_entry_point_and_rejects():
+    """fd_pre_attn_qkv_fp8 through the C ABI: from 5 rows it needs `normed`, H not
+    a multiple of 16 is FD_EUNSUPPORTED; the Python checks of pre_attn_qkv hold."""
+    import fused_decode as fd
+    from fused_decode import _lib as L
+
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(8, 256, 2, 1, 64, torch.float16, seed=12)
+    hd, nwd, cd, sd = (t.to(DEV) for t in (hidden, nw, cos, sin))
+    n = q.shape[0]
+    y = torch.empty(8, n, device=DEV, dtype=torch.float16)
+    normed = torch.empty(8, 256, device=DEV, dtype=torch.float16)
+    st = torch.cuda.current_stream().cuda_stream
+    args = lambda nrm, hh: (  # noqa: E731
+        y.data_ptr(), nrm, hd.data_ptr(), nwd.data_ptr(), L.FD_F16, q.data_ptr(), s.data_ptr(), None,
+        L.FD_F16, cd.data_ptr(), sd.data_ptr(), L.FD_F32, 64, 8, hh, n, rc, 64, 1e-5, L.FD_F16, st)
+    assert L.lib().fd_pre_attn_qkv_fp8(*args(None, 256)) == L.FD_EINVAL
+    assert L.lib().fd_pre_attn_qkv_fp8(*args(normed.data_ptr(), 248)) == L.FD_EUNSUPPORTED
+    L.check("fd_pre_attn_qkv_fp8", L.lib().fd_pre_attn_qkv_fp8(*args(normed.data_ptr(), 256)))
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    with pytest.raises(TypeError, match="float8_e4m3fn"):
+        fd.pre_attn_qkv_fp8(hd, nwd, q.float(), s, cd, sd, rope_cols=rc)
+    with pytest.raises(ValueError, match="scale"):
+        fd.pre_attn_qkv_fp8(hd, nwd, q, s[:3], cd, sd, rope_cols=rc)
+    with pytest.raises(ValueError, match="rope_cols"):
+        fd.pre_attn_qkv_fp8(hd, nwd, q, s, cd, sd, rope_cols=rc + 3)
+    with pytest.raises(ValueError, match="CUDA"):
+        fd.pre_attn_qkv_fp8(hidden, nwd, q, s, cd, sd, rope_cols=rc)

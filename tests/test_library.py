@@ -53,6 +53,7 @@ def test_fake_kernels_give_result_shapes(fdl):
         d8 = torch.empty(h, i, device="cuda", dtype=torch.float8_e4m3fn)
         sg, sd = torch.empty(2 * i, device="cuda"), torch.empty(h, device="cuda")
         assert fdl.post_attn_mlp_fp8(x, w, g8, sg, d8, sd, 1e-5).shape == x.shape
+        assert fdl.pre_attn_qkv_fp8(x, w, q8, s8, cs, cs, 1e-5, 32).shape == (2, 3, n)
 
 
 def test_real_cpu_inputs_reach_the_operator_checks(fdl):

@@ -48,8 +48,23 @@ def test_opcheck_every_op(fdl):
         (fdl.post_attn_mlp, (x, nw, t["wgu"], t["wd"], 1e-5, None)),
         (fdl.pre_attn_qkv, (x, nw, t["wqkv"], t["cos"], t["sin"], 1e-5, t["rc"], None, "dot")),
     ]
+    import fused_decode as fd
+
+    q8, s8 = fd.quantize_fp8(t["wqkv"])
+    g8, sg = fd.quantize_fp8(t["wgu"])
+    d8, sd = fd.quantize_fp8(t["wd"])
+    o8, so = fd.quantize_fp8(t["wo"])
     for op, args in cases:
         torch.library.opcheck(op, args)
+    # The schema check compares inputs before and after with arithmetic torch does
+    # not implement for float8_e4m3fn tensors, so the fp8 ops run the other checks.
+    fp8_cases = [
+        (fdl.linear_decode_fp8, (t["attn"], o8, so, None, x)),
+        (fdl.post_attn_mlp_fp8, (x, nw, g8, sg, d8, sd, 1e-5)),
+        (fdl.pre_attn_qkv_fp8, (x, nw, q8, s8, t["cos"], t["sin"], 1e-5, t["rc"], None)),
+    ]
+    for op, args in fp8_cases:
+        torch.library.opcheck(op, args, test_utils=("test_faketensor", "test_aot_dispatch_dynamic"))
 
 
 def test_compiled_layer_matches_eager_operators(fdl):

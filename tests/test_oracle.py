@@ -338,10 +338,34 @@ def test_post_attn_mlp_fp8_equals_mlp_of_dequantized_weights():
     np.testing.assert_allclose(got, ref, rtol=2e-3, atol=2e-3)
 
 
+def test_pre_attn_qkv_fp8_equals_qkv_of_dequantized_weights_and_rotates():
+    """The fp8 QKV is the fp16 composition over the decoded weights (to float32
+    rounding of where the scale is applied), and its RoPE is the same rotation:
+    a quarter turn swaps head halves exactly. Reversed scales are caught."""
+    hid, nw, w, rc, d = _qkv_case(m=3, seed=5)
+    codes, scale = O.fp8_quantize(w)
+    deq = O.fp8_decode(codes) * scale[:, None]
+    bias = np.linspace(-0.5, 0.5, w.shape[0]).astype(np.float32)
+    cos = RNG.standard_normal(d).astype(np.float32)
+    sin = RNG.standard_normal(d).astype(np.float32)
+    got = O.pre_attn_qkv_fp8(hid, nw, codes, scale, cos, sin, 1e-5, rc, bias=bias, dtype="f32")
+    ref = O.pre_attn_qkv(hid, nw, deq, cos, sin, 1e-5, rc, bias=bias, dtype="f32")
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5)
+    bad = O.pre_attn_qkv_fp8(hid, nw, codes, scale[::-1].copy(), cos, sin, 1e-5, rc, bias=bias, dtype="f32")
+    assert not np.allclose(bad, ref, rtol=1e-3, atol=1e-3)
+    plain = O.pre_attn_qkv_fp8(hid, nw, codes, scale, np.ones(d), np.zeros(d), 1e-5, 0, dtype="f32")
+    turned = O.pre_attn_qkv_fp8(hid, nw, codes, scale, np.zeros(d), np.ones(d), 1e-5, rc, dtype="f32")
+    for head in range(rc // d):
+        a, b = plain[:, head * d: head * d + d // 2], plain[:, head * d + d // 2: (head + 1) * d]
+        np.testing.assert_array_equal(turned[:, head * d: head * d + d // 2], -b)
+        np.testing.assert_array_equal(turned[:, head * d + d // 2: (head + 1) * d], a)
+    np.testing.assert_array_equal(turned[:, rc:], plain[:, rc:])
+
+
 # ---------------------------------------------------------------- bytes
 
 
-def test_useful_bytes_match_survey_table():
+def test_useful_bytes_match_the_readme_byte_rules():
     assert O.bytes_add_rms(8192, 4096) == 268_443_648
     assert O.bytes_rms(8192, 4096) == 134_225_920
     assert O.bytes_swiglu(2048, 14336) == 176_160_768
