@@ -103,39 +103,64 @@ __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hid
 
 // Register form of the same prologue for small M, split so the weight stream
 // can start in between: norm_load issues every global load the norm needs
-// (this thread's KIT 8-element slices of each hidden row and of the norm
-// weight) before the caller issues its first weight loads, so the norm's loads
-// are not queued behind them; norm_store reduces, rounds and stages in LDS
-// from registers. Usable when H <= KIT * blockDim.x * 8 (norm_in_regs); the
-// same summation order and rounding as stage_normed.
+// (this thread's KIT 8-element slices of each hidden row and the raw bytes of
+// the norm weight) before the caller issues its first weight loads, and
+// norm_store reduces, converts, rounds and stages in LDS from registers. Every
+// load is unconditional (slices past H and rows past M read an in-bounds
+// address and are masked later): a load under a branch leaves the compiler
+// unsure how many loads are outstanding, and it then waits for all of them,
+// the weight loads included, before the norm's first use. Usable when
+// H <= KIT * blockDim.x * 8 (norm_in_regs); the same summation order and
+// rounding as stage_normed.
 template <typename T, int MMAX, int KIT>
 struct NormRegs {
   typename Vec8<T>::type h[KIT][MMAX];
-  float w[KIT][8];
+  u32x4 w0[KIT], w1[KIT];  // 8 norm-weight values: 16 bytes (fp16/bf16) or 32 (fp32)
 };
 
 template <typename T, int MMAX, int KIT>
 __device__ __forceinline__ void norm_load(NormRegs<T, MMAX, KIT>& c, const T* hidden,
                                           const void* nwp, int nw_dtype, int M, int H) {
+  const bool is32 = nw_dtype == FD_F32;
+  const int esz = is32 ? 4 : 2;
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
     const int k = (threadIdx.x + it * blockDim.x) * 8;
+    const int kc = k < H ? k : 0;
 #pragma unroll
     for (int m = 0; m < MMAX; ++m)
-      c.h[it][m] = (m < M && k < H) ? load8<T>(hidden + (int64_t)m * H + k)
-                                    : typename Vec8<T>::type{};
-    if (k < H) {
-      load8_norm_w(nwp, nw_dtype, k, c.w[it]);
-    } else {
+      c.h[it][m] = load8<T>(hidden + (int64_t)(m < M ? m : 0) * H + kc);
+    const char* pb = static_cast<const char*>(nwp) + (int64_t)kc * esz;
+    c.w0[it] = *reinterpret_cast<const u32x4*>(pb);
+    c.w1[it] = *reinterpret_cast<const u32x4*>(pb + (is32 ? 16 : 0));
+  }
+}
+
+// The 8 float32 norm-weight values of a norm_load slice.
+__device__ __forceinline__ void norm_w8(const u32x4& w0, const u32x4& w1, int dtype,
+                                        float (&f)[8]) {
+  if (dtype == FD_F32) {
+    const f32x4 a = __builtin_bit_cast(f32x4, w0), b = __builtin_bit_cast(f32x4, w1);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) c.w[it][i] = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      f[i] = a[i];
+      f[i + 4] = b[i];
     }
+  } else if (dtype == FD_BF16) {
+    const bf16x8 a = __builtin_bit_cast(bf16x8, w0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = to_f32(a[i]);
+  } else {
+    const f16x8 a = __builtin_bit_cast(f16x8, w0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = to_f32(a[i]);
   }
 }
 
 template <typename T, int MMAX, int KIT>
 __device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* xs,
-                                           float* scratch, int M, int H, float eps) {
+                                           float* scratch, int nw_dtype, int M, int H,
+                                           float eps) {
   const int XS = xs_stride(H);
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
@@ -146,10 +171,14 @@ __device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* x
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
+    const bool in = (tid + it * (int)blockDim.x) * 8 < H;
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss[m] += to_f32(c.h[it][m][i]) * to_f32(c.h[it][m][i]);
+      for (int i = 0; i < 8; ++i) {
+        const float v = in && m < M ? to_f32(c.h[it][m][i]) : 0.f;
+        ss[m] += v * v;
+      }
     }
   }
   butterfly_sum<MP>(ss, lane);
@@ -166,19 +195,63 @@ __device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* x
   for (int it = 0; it < KIT; ++it) {
     const int k = (tid + it * (int)blockDim.x) * 8;
     if (k < H) {
+      float wf[8];
+      norm_w8(c.w0[it], c.w1[it], nw_dtype, wf);
 #pragma unroll
       for (int m = 0; m < MMAX; ++m) {
         if (m < M) {
           const float s = inv[m];
           V8 o;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(c.h[it][m][i]) * s * c.w[it][i]);
+          for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(c.h[it][m][i]) * s * wf[i]);
           store8<T>(xs + (int64_t)m * XS + k, o);
         }
       }
     }
   }
   __syncthreads();
+}
+
+// The K steps a persistent workgroup streams: its tiles blockIdx.x,
+// blockIdx.x + gridDim.x, ... below `tiles`, each `steps` steps of `step`
+// elements, flattened to s = 0 .. total-1 (this thread's slice of step s starts
+// at k(s)).
+struct StepPlan {
+  int steps, step, kbase, total;
+  __device__ __forceinline__ StepPlan(int tiles, int H, int step_, int kbase_)
+      : steps((H + step_ - 1) / step_), step(step_), kbase(kbase_) {
+    const int g = (int)gridDim.x;
+    total = (tiles - (int)blockIdx.x + g - 1) / g * steps;
+  }
+  __device__ __forceinline__ int tile(int s) const { return (int)blockIdx.x + s / steps * (int)gridDim.x; }
+  __device__ __forceinline__ int k(int s) const { return kbase + s % steps * step; }
+  __device__ __forceinline__ bool last(int s) const { return s % steps == steps - 1; }
+};
+
+// Streams the plan's steps through two register buffers: the loads of step s+1
+// are in flight while step s is consumed (and its tile's epilogue runs).
+// issue(buf, s) loads step s (s < total) with every load unconditional -- lanes
+// or rows out of range read an in-bounds dummy address -- so that waiting for
+// one buffer never waits for the other; consume(buf, s) does the math of step s.
+// The caller issues step 0 into `a` first, so a prologue can overlap it. The
+// last one or two steps are peeled so no step past the plan is ever loaded.
+template <typename Buf, typename Issue, typename Consume>
+__device__ __forceinline__ void stream_steps(int total, Buf& a, Buf& b, Issue&& issue,
+                                             Consume&& consume) {
+  int s = 0;
+  for (; s + 2 < total; s += 2) {
+    issue(b, s + 1);
+    consume(a, s);
+    issue(a, s + 2);
+    consume(b, s + 1);
+  }
+  if (s + 1 < total) {
+    issue(b, s + 1);
+    consume(a, s);
+    consume(b, s + 1);
+  } else if (s < total) {
+    consume(a, s);
+  }
 }
 
 // The register prologue holds 2 slices of 8 per row and thread (H up to 16
@@ -303,22 +376,23 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
   }
 }
 
-// Output of one fused-QKV SIMT tile of 4 rows placed by TileRows<4>, from the
+// Output of one fused-QKV SIMT tile of R rows placed by TileRows<R>, from the
 // waves' partial sums (wave i, slot r*M + m at part[i*V + r*M + m]): bias,
-// rounding, and in rotated tiles the rotation of pairs (slot p, slot p + 2).
-template <typename T, int M, typename Scale>
+// rounding, and in rotated tiles the rotation of pairs (slot p, slot p + R/2).
+template <typename T, int M, int R, typename Scale>
 __device__ __forceinline__ void qkv_tile_out(T* y, const float* part, int V, int nw,
-                                             const TileRows<4>& tr, const Epi& e, const Rope& rp,
+                                             const TileRows<R>& tr, const Epi& e, const Rope& rp,
                                              const Scale& sc, int N) {
+  constexpr int P = R / 2;
   if (tr.rotated()) {
-    for (int t = threadIdx.x; t < 2 * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < P * M; t += blockDim.x) {
       const int p = t / M, m = t % M;
       float s1 = 0.f, s2 = 0.f;
       for (int i = 0; i < nw; ++i) {
         s1 += part[i * V + p * M + m];
-        s2 += part[i * V + (p + 2) * M + m];
+        s2 += part[i * V + (p + P) * M + m];
       }
-      const int64_t n1 = tr.row(p), n2 = tr.row(p + 2);
+      const int64_t n1 = tr.row(p), n2 = tr.row(p + P);
       float o1, o2;
       rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, sc(s1, n1), m, n1)),
                 round_as<T>(epilogue(e, sc(s2, n2), m, n2)), o1, o2);
@@ -326,7 +400,7 @@ __device__ __forceinline__ void qkv_tile_out(T* y, const float* part, int V, int
       y[m * (int64_t)N + n2] = from_f32<T>(o2);
     }
   } else {
-    for (int t = threadIdx.x; t < 4 * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
       const int r = t / M, m = t % M;
       const int64_t n = tr.row(r);
       if (n < N) {

@@ -143,15 +143,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
 // kernel (normalised rows rounded into LDS), R gate rows and the matching R up
 // rows per tile streamed one K step ahead of the math, and
 // mid = round(silu(round(sg*g)) * round(su*u)).
-template <typename T, int R>
-__device__ __forceinline__ void load_gate_up8(u32x4 (&g)[R], u32x4 (&u)[R], const uint8_t* wgu,
-                                              int tile, int tiles, int k, int H, int I) {
+template <int R>
+struct GateUp8Regs {
+  u32x4 g[R], u[R];
+};
+
+// Loads of step s of the plan; lanes past H and rows past I load the first 16
+// codes instead (never used), so every load is unconditional.
+template <int R>
+__device__ __forceinline__ void load_gate_up8(GateUp8Regs<R>& b, const uint8_t* wgu,
+                                              const StepPlan& p, int s, int H, int I) {
+  const int64_t j0 = (int64_t)p.tile(s) * R;
+  const int k = p.k(s);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t j = (int64_t)tile * R + r;
-    const bool ok = tile < tiles && j < I && k < H;
-    g[r] = ok ? load16_nt(wgu + j * H + k) : u32x4{0, 0, 0, 0};
-    u[r] = ok ? load16_nt(wgu + (I + j) * H + k) : u32x4{0, 0, 0, 0};
+    const int64_t j = j0 + r;
+    const bool ok = j < I && k < H;
+    b.g[r] = load16_nt(ok ? wgu + j * H + k : wgu);
+    b.u[r] = load16_nt(ok ? wgu + (I + j) * H + k : wgu);
   }
 }
 
@@ -168,55 +177,44 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
-  const int step = nw * kChunk8;
-  const int steps = (H + step - 1) / step;
-  const int kbase = (wave * kWave + lane) * 16;
+  const StepPlan p(tiles, H, nw * kChunk8, (wave * kWave + lane) * 16);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
   if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
-  u32x4 gv[R], uv[R];
-  load_gate_up8<T, R>(gv, uv, wgu, blockIdx.x, tiles, kbase, H, I);
+  GateUp8Regs<R> a, b;
+  load_gate_up8<R>(a, wgu, p, 0, H, I);
   if constexpr (REGS)
-    norm_store(nr, xs, part, M, H, eps);
+    norm_store(nr, xs, part, nw_dtype, M, H, eps);
   else
     stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const int64_t j0 = (int64_t)tile * R;
-    float acc[V];
+  float acc[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int it = 0; it < steps; ++it) {
-      const bool last = it + 1 == steps;
-      u32x4 gn[R], un[R];
-      load_gate_up8<T, R>(gn, un, wgu, last ? tile + (int)gridDim.x : tile, tiles,
-                          kbase + (last ? 0 : (it + 1) * step), H, I);
-      const int k = kbase + it * step;
-      if (k < H) {
-        V8 xa[M], xb[M];
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  auto issue = [&](GateUp8Regs<R>& buf, int s) { load_gate_up8<R>(buf, wgu, p, s, H, I); };
+  auto consume = [&](const GateUp8Regs<R>& buf, int s) {
+    const int k = p.k(s);
+    if (k < H) {
+      V8 xa[M], xb[M];
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        xa[m] = load8<T>(xs + m * XS + k);
+        xb[m] = load8<T>(xs + m * XS + k + 8);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-          xa[m] = load8<T>(xs + m * XS + k);
-          xb[m] = load8<T>(xs + m * XS + k + 8);
+          acc[r * M + m] = dot_fp8x16<T>(buf.g[r], xa[m], xb[m], acc[r * M + m]);
+          acc[R * M + r * M + m] = dot_fp8x16<T>(buf.u[r], xa[m], xb[m], acc[R * M + r * M + m]);
         }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int m = 0; m < M; ++m) {
-            acc[r * M + m] = dot_fp8x16<T>(gv[r], xa[m], xb[m], acc[r * M + m]);
-            acc[R * M + r * M + m] = dot_fp8x16<T>(uv[r], xa[m], xb[m], acc[R * M + r * M + m]);
-          }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        gv[r] = gn[r];
-        uv[r] = un[r];
-      }
     }
+    if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
+    const int64_t j0 = (int64_t)p.tile(s) * R;
     for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
       const int r = t / M, m = t % M;
       const int64_t j = j0 + r;
@@ -230,7 +228,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
             swiglu_out<T>(gs * 256.f * gu_scale[j], us * 256.f * gu_scale[I + j]);
       }
     }
-  }
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  };
+  stream_steps(p.total, a, b, issue, consume);
 }
 
 // MFMA form of the fp8 GEMV for M >= kFp8MfmaMinM (M padded to 16): the relayout
@@ -330,26 +331,31 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
 
 // Pre-attention QKV with fp8 weights for M < 5: the fp16 fused QKV kernel's
 // structure (RMSNorm prologue staged in LDS, 4 weight rows per tile placed by
-// TileRows<4>, the next tile's loads issued one K step ahead, RoPE of the
+// TileRows<4>, the step pipeline of stream_steps, RoPE of the
 // rotated tiles in the epilogue) with the fp8 GEMV's 16 codes per lane and step.
 template <int R>
-__device__ __forceinline__ void load_tile_rows8(u32x4 (&v)[R], const uint8_t* w, const Rope& rp,
-                                                int tile, int tiles, int k, int H, int N) {
-  const TileRows<R> tr(rp, tile < tiles ? tile : 0);
+struct Rows8Regs {
+  u32x4 v[R];
+};
+
+template <int R>
+__device__ __forceinline__ void load_tile_rows8(Rows8Regs<R>& b, const uint8_t* w, const Rope& rp,
+                                                const StepPlan& p, int s, int H, int N) {
+  const TileRows<R> tr(rp, p.tile(s));
+  const int k = p.k(s);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t n = tr.row(r);
-    const bool ok = tile < tiles && n < N && k < H;
-    v[r] = ok ? load16_nt(w + n * H + k) : u32x4{0, 0, 0, 0};
+    const bool ok = n < N && k < H;
+    b.v[r] = load16_nt(ok ? w + n * H + k : w);
   }
 }
 
-template <typename T, int M, bool REGS>
+template <typename T, int M, int R, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
     T* y, const T* hidden, const void* nwp, int nw_dtype, const uint8_t* w, const float* wscale,
     int H, int N, float eps, int tiles, Epi e, Rope rp) {
   typedef typename Vec8<T>::type V8;
-  constexpr int R = 4;
   constexpr int V = pow2_ceil(R * M);
   extern __shared__ __align__(16) unsigned char smem[];
   const int XS = xs_stride(H);
@@ -358,50 +364,45 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
-  const int step = nw * kChunk8;
-  const int steps = (H + step - 1) / step;
-  const int kbase = (wave * kWave + lane) * 16;
+  const StepPlan p(tiles, H, nw * kChunk8, (wave * kWave + lane) * 16);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
   if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
-  u32x4 wv[R];
-  load_tile_rows8<R>(wv, w, rp, blockIdx.x, tiles, kbase, H, N);
+  Rows8Regs<R> a, b;
+  load_tile_rows8<R>(a, w, rp, p, 0, H, N);
   if constexpr (REGS)
-    norm_store(nr, xs, part, M, H, eps);
+    norm_store(nr, xs, part, nw_dtype, M, H, eps);
   else
     stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    float acc[V];
+  float acc[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int it = 0; it < steps; ++it) {
-      const bool last = it + 1 == steps;
-      u32x4 wn[R];
-      load_tile_rows8<R>(wn, w, rp, last ? tile + (int)gridDim.x : tile, tiles,
-                         kbase + (last ? 0 : (it + 1) * step), H, N);
-      const int k = kbase + it * step;
-      if (k < H) {
-        V8 xa[M], xb[M];
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  auto issue = [&](Rows8Regs<R>& buf, int s) { load_tile_rows8<R>(buf, w, rp, p, s, H, N); };
+  auto consume = [&](const Rows8Regs<R>& buf, int s) {
+    const int k = p.k(s);
+    if (k < H) {
+      V8 xa[M], xb[M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-          xa[m] = load8<T>(xs + m * XS + k);
-          xb[m] = load8<T>(xs + m * XS + k + 8);
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(wv[r], xa[m], xb[m], acc[r * M + m]);
+      for (int m = 0; m < M; ++m) {
+        xa[m] = load8<T>(xs + m * XS + k);
+        xb[m] = load8<T>(xs + m * XS + k + 8);
       }
 #pragma unroll
-      for (int r = 0; r < R; ++r) wv[r] = wn[r];
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(buf.v[r], xa[m], xb[m], acc[r * M + m]);
     }
+    if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    qkv_tile_out<T, M>(y, part, V, nw, TileRows<R>(rp, tile), e, rp, RowScale{wscale}, N);
-  }
+    qkv_tile_out<T, M, R>(y, part, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, RowScale{wscale}, N);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  };
+  stream_steps(p.total, a, b, issue, consume);
 }
 
 // Gate/up + SwiGLU in the same form: 16 gate and the matching 16 up rows per
@@ -504,10 +505,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
 namespace {
 
 template <int M> struct Fp8Rows { static constexpr int R = M <= 8 ? 4 : 2; };
-// Two gate + two up rows per tile at M <= 2 with four workgroups per CU (measured
-// at Llama-3-8B widths: 25.8 against 30.3 us for four rows at two per CU).
-template <int M> struct Fp8MlpRows { static constexpr int R = M <= 2 ? 2 : M <= 4 ? 4 : 2; };
-template <int M> struct Fp8MlpPerCu { static constexpr int P = M <= 2 ? 4 : 2; };
+// Two gate + two up rows per tile with four workgroups per CU (measured at
+// Llama-3-8B widths: M=1 23.3 us against 24.1 for four rows at two per CU, M=3
+// 30.5 against 31.5).
+template <int M> struct Fp8MlpRows { static constexpr int R = 2; };
+template <int M> struct Fp8MlpPerCu { static constexpr int P = M <= 4 ? 4 : 2; };
+
+// Fused QKV: R rows per tile (R/2 rotate-half pairs in a rotated tile); eight
+// up to 2 rows (Llama-3-8B widths, M=1: 9.1 against 9.7 us for four).
+template <int M> struct Fp8QkvRows { static constexpr int R = M <= 2 ? 8 : 4; };
 
 // From this many rows the fp8 GEMV and MLP take the MFMA (relayout) forms.
 constexpr int kFp8MfmaMinM = 5;
@@ -599,14 +605,17 @@ int launch_mlp_fp8_m(int M, void* mid, const void* hidden, const void* nw, int n
 // (the fp16 QKV launch shape).
 template <typename T, int M>
 int launch_qkv_fp8(void* y, const void* hidden, const void* nw, int nw_dtype, const uint8_t* w,
-                   const float* s, int H, int N, float eps, const Epi& e, const Rope& rp,
+                   const float* s, int H, int N, float eps, const Epi& e, const Rope& rp_in,
                    hipStream_t st) {
-  constexpr int V = pow2_ceil(4 * M);
+  constexpr int R = Fp8QkvRows<M>::R;
+  constexpr int V = pow2_ceil(R * M);
   const int nwv0 = pick_waves((H + kChunk8 - 1) / kChunk8);
   const int nwv = nwv0 > 4 ? 4 : nwv0;
   const size_t lds = fused_lds(M, H, sizeof(T), V);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
+  Rope rp = rp_in;
+  rp.tiles = rp.cols / R;
+  const int tiles = rp.tiles + (N - rp.cols + R - 1) / R;
   const int grid = fused_grid(tiles, lds, 8);
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds))
@@ -616,9 +625,9 @@ int launch_qkv_fp8(void* y, const void* hidden, const void* nw, int nw_dtype, co
     return (int)FD_OK;
   };
   if constexpr (M <= kNormRegMaxM) {
-    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_fp8_kernel<T, M, true>);
+    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_fp8_kernel<T, M, R, true>);
   }
-  return launch(qkv_fp8_kernel<T, M, false>);
+  return launch(qkv_fp8_kernel<T, M, R, false>);
 }
 
 template <typename T>
@@ -761,7 +770,6 @@ extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, co
     else
       launch_gemv_fp8_mfma<bf16>((int)M, y, normed, w, w_scale, (int)N, (int)H, H, H, N, 1, e, st, &rp);
   } else {
-    rp.tiles = (int)(rope_cols / 4);
     const int rc = act_dtype == FD_F16
                        ? launch_qkv_fp8_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w, w_scale,
                                                (int)H, (int)N, eps, e, rp, st)

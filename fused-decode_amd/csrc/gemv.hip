@@ -40,6 +40,9 @@ namespace fd {
 template <int M> struct SimtRows { static constexpr int R = 4; };
 // Fused gate/up: R gate rows + R up rows.
 template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
+// Fused QKV: R rows per tile (R/2 rotate-half pairs in a rotated tile); eight
+// up to 2 rows (Llama-3-8B widths, M=1: 11.1 against 11.7 us for four).
+template <int M> struct QkvRows { static constexpr int R = M <= 2 ? 8 : 4; };
 
 // ---------------------------------------------------------------------------
 // SIMT GEMV
@@ -231,26 +234,35 @@ __global__ __launch_bounds__(256) void gemv_gen_kernel(T* y, const T* x, const T
 // ---------------------------------------------------------------------------
 // Fused MLP, launch 1: RMSNorm prologue + gate/up GEMV + SwiGLU epilogue.
 
-// Weight loads of one K step of tile `tile` (R gate rows and the matching R up
-// rows); rows past I, steps past H and tiles past the last are zero registers.
+// Weight registers of one K step: R gate rows and the matching R up rows.
+template <typename T, int R>
+struct GateUpRegs {
+  typename Vec8<T>::type g[R], u[R];
+};
+
+// Loads of step s of the plan. Lanes past H and rows past I load the matrix's
+// first 16 bytes instead (never used), so every load is unconditional (see
+// stream_steps).
 template <typename T, int R, bool NTW>
-__device__ __forceinline__ void load_gate_up(typename Vec8<T>::type (&g)[R],
-                                             typename Vec8<T>::type (&u)[R], const T* wgu,
-                                             int tile, int tiles, int k, int H, int I) {
+__device__ __forceinline__ void load_gate_up(GateUpRegs<T, R>& b, const T* wgu,
+                                             const StepPlan& p, int s, int H, int I) {
+  const int64_t j0 = (int64_t)p.tile(s) * R;
+  const int k = p.k(s);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const int64_t j = (int64_t)tile * R + r;
-    const bool ok = tile < tiles && j < I && k < H;
-    g[r] = ok ? load8w<NTW, T>(wgu + j * H + k) : typename Vec8<T>::type{};
-    u[r] = ok ? load8w<NTW, T>(wgu + (I + j) * H + k) : typename Vec8<T>::type{};
+    const int64_t j = j0 + r;
+    const bool ok = j < I && k < H;
+    b.g[r] = load8w<NTW, T>(ok ? wgu + j * H + k : wgu);
+    b.u[r] = load8w<NTW, T>(ok ? wgu + (I + j) * H + k : wgu);
   }
 }
 
-// SIMT gate/up for M < 5 (any M with kind=simt). The weight stream is software-pipelined one K step
-// deep: the loads of the next step (which may belong to the workgroup's next
-// tile) are issued before the math of the current one, and the first step is
-// issued before the RMSNorm prologue, so HBM requests stay in flight across the
-// prologue, the cross-wave reduction and the SwiGLU epilogue.
+// SIMT gate/up for M < 5 (any M with kind=simt). The weight stream is
+// software-pipelined one K step deep over the workgroup's whole sequence of
+// (tile, step) pairs: the loads of the next step (which may belong to the next
+// tile) are in flight during the math, cross-wave reduction and SwiGLU
+// epilogue of the current one, and the first step is issued before the RMSNorm
+// prologue's reduction.
 template <typename T, int M, int R, bool NTW, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     T* mid, const T* hidden, const void* nwp, int nw_dtype, const T* wgu, int H, int I,
@@ -264,52 +276,41 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
-  const int step = nw * kChunk;
-  const int steps = (H + step - 1) / step;  // the same for every wave
-  const int kbase = (wave * kWave + lane) * 8;
+  const StepPlan p(tiles, H, nw * kChunk, (wave * kWave + lane) * 8);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
   if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
-  V8 gv[R], uv[R];
-  load_gate_up<T, R, NTW>(gv, uv, wgu, blockIdx.x, tiles, kbase, H, I);
+  GateUpRegs<T, R> a, b;
+  load_gate_up<T, R, NTW>(a, wgu, p, 0, H, I);
   if constexpr (REGS)
-    norm_store(nr, xs, part, M, H, eps);
+    norm_store(nr, xs, part, nw_dtype, M, H, eps);
   else
     stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    const int64_t j0 = (int64_t)tile * R;
-    float acc[V];
+  float acc[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int it = 0; it < steps; ++it) {
-      const bool last = it + 1 == steps;
-      V8 gn[R], un[R];
-      load_gate_up<T, R, NTW>(gn, un, wgu, last ? tile + (int)gridDim.x : tile, tiles,
-                              kbase + (last ? 0 : (it + 1) * step), H, I);
-      const int k = kbase + it * step;
-      if (k < H) {
-        V8 xv[M];
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  auto issue = [&](GateUpRegs<T, R>& buf, int s) { load_gate_up<T, R, NTW>(buf, wgu, p, s, H, I); };
+  auto consume = [&](const GateUpRegs<T, R>& buf, int s) {
+    const int k = p.k(s);
+    if (k < H) {
+      V8 xv[M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
+      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int m = 0; m < M; ++m) {
-            acc[r * M + m] = dot8(gv[r], xv[m], acc[r * M + m]);
-            acc[R * M + r * M + m] = dot8(uv[r], xv[m], acc[R * M + r * M + m]);
-          }
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        gv[r] = gn[r];
-        uv[r] = un[r];
-      }
+        for (int m = 0; m < M; ++m) {
+          acc[r * M + m] = dot8(buf.g[r], xv[m], acc[r * M + m]);
+          acc[R * M + r * M + m] = dot8(buf.u[r], xv[m], acc[R * M + r * M + m]);
+        }
     }
+    if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
+    const int64_t j0 = (int64_t)p.tile(s) * R;
     for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
       const int r = t / M, m = t % M;
       const int64_t j = j0 + r;
@@ -322,32 +323,39 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
         mid[m * (int64_t)I + j] = swiglu_out<T>(gs, us);
       }
     }
-  }
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  };
+  stream_steps(p.total, a, b, issue, consume);
 }
 
-// Pre-attention QKV for M < 5 (and kind=simt): the RMSNorm prologue of the
-// fused gate/up kernel, a pipelined stream of 4 weight rows per tile placed by
+// Pre-attention QKV for M < 5 (and kind=simt): the RMSNorm prologue and step
+// pipeline of the fused gate/up kernel over 4 weight rows per tile placed by
 // TileRows<4> (two rotate-half pairs per rotated tile), and an epilogue that
 // adds the bias, rounds, and rotates the rotated tiles' pairs.
+template <typename T, int R>
+struct RowRegs {
+  typename Vec8<T>::type v[R];
+};
+
 template <typename T, int R, bool NTW>
-__device__ __forceinline__ void load_tile_rows(typename Vec8<T>::type (&v)[R], const T* w,
-                                               const Rope& rp, int tile, int tiles, int k, int H,
-                                               int N) {
-  const TileRows<R> tr(rp, tile < tiles ? tile : 0);
+__device__ __forceinline__ void load_tile_rows(RowRegs<T, R>& b, const T* w, const Rope& rp,
+                                               const StepPlan& p, int s, int H, int N) {
+  const TileRows<R> tr(rp, p.tile(s));
+  const int k = p.k(s);
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int64_t n = tr.row(r);
-    const bool ok = tile < tiles && n < N && k < H;
-    v[r] = ok ? load8w<NTW, T>(w + n * H + k) : typename Vec8<T>::type{};
+    const bool ok = n < N && k < H;
+    b.v[r] = load8w<NTW, T>(ok ? w + n * H + k : w);
   }
 }
 
-template <typename T, int M, bool NTW, bool REGS>
+template <typename T, int M, int R, bool NTW, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
     T* y, const T* hidden, const void* nwp, int nw_dtype, const T* w, int H, int N, float eps,
     int tiles, Epi e, Rope rp) {
   typedef typename Vec8<T>::type V8;
-  constexpr int R = 4;
   constexpr int V = pow2_ceil(R * M);
   extern __shared__ __align__(16) unsigned char smem[];
   const int XS = xs_stride(H);
@@ -356,47 +364,42 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = blockDim.x / kWave;
-  const int step = nw * kChunk;
-  const int steps = (H + step - 1) / step;
-  const int kbase = (wave * kWave + lane) * 8;
+  const StepPlan p(tiles, H, nw * kChunk, (wave * kWave + lane) * 8);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
   if constexpr (REGS) norm_load(nr, hidden, nwp, nw_dtype, M, H);
-  V8 wv[R];
-  load_tile_rows<T, R, NTW>(wv, w, rp, blockIdx.x, tiles, kbase, H, N);
+  RowRegs<T, R> a, b;
+  load_tile_rows<T, R, NTW>(a, w, rp, p, 0, H, N);
   if constexpr (REGS)
-    norm_store(nr, xs, part, M, H, eps);
+    norm_store(nr, xs, part, nw_dtype, M, H, eps);
   else
     stage_normed<T, M>(xs, part, hidden, nwp, nw_dtype, M, H, eps);
 
-  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
-    float acc[V];
+  float acc[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.f;
-    for (int it = 0; it < steps; ++it) {
-      const bool last = it + 1 == steps;
-      V8 wn[R];
-      load_tile_rows<T, R, NTW>(wn, w, rp, last ? tile + (int)gridDim.x : tile, tiles,
-                                kbase + (last ? 0 : (it + 1) * step), H, N);
-      const int k = kbase + it * step;
-      if (k < H) {
-        V8 xv[M];
+  for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  auto issue = [&](RowRegs<T, R>& buf, int s) { load_tile_rows<T, R, NTW>(buf, w, rp, p, s, H, N); };
+  auto consume = [&](const RowRegs<T, R>& buf, int s) {
+    const int k = p.k(s);
+    if (k < H) {
+      V8 xv[M];
 #pragma unroll
-        for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
+      for (int m = 0; m < M; ++m) xv[m] = load8<T>(xs + m * XS + k);
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(wv[r], xv[m], acc[r * M + m]);
-      }
-#pragma unroll
-      for (int r = 0; r < R; ++r) wv[r] = wn[r];
+        for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(buf.v[r], xv[m], acc[r * M + m]);
     }
+    if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    qkv_tile_out<T, M>(y, part, V, nw, TileRows<R>(rp, tile), e, rp, NoScale{}, N);
-  }
+    qkv_tile_out<T, M, R>(y, part, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, NoScale{}, N);
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+  };
+  stream_steps(p.total, a, b, issue, consume);
 }
 
 // MFMA form of the gate/up launch for M >= kMfmaMinM (M padded to 16): the RMSNorm of
@@ -630,15 +633,18 @@ int launch_mlp_simt_m(int M, void* mid, const void* hidden, const void* nw, int 
 
 template <typename T, int M>
 int launch_qkv_simt(void* y, const void* hidden, const void* nw, int nw_dtype, const void* w,
-                    int H, int N, float eps, const Epi& e, const Rope& rp, hipStream_t st) {
-  constexpr int V = pow2_ceil(4 * M);
+                    int H, int N, float eps, const Epi& e, const Rope& rp_in, hipStream_t st) {
+  constexpr int R = QkvRows<M>::R;
+  constexpr int V = pow2_ceil(R * M);
   // Four waves and every tile resident at once (one tile per workgroup at
   // N = 6144): the QKV weights are too few to amortise a persistent loop.
   const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
   const int nwv = nwv0 > 4 ? 4 : nwv0;
   const size_t lds = fused_lds(M, H, sizeof(T), V);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
-  const int tiles = rp.tiles + (N - rp.cols + 3) / 4;
+  Rope rp = rp_in;
+  rp.tiles = rp.cols / R;
+  const int tiles = rp.tiles + (N - rp.cols + R - 1) / R;
   const int grid = fused_grid(tiles, lds, 8);
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds))
@@ -649,9 +655,9 @@ int launch_qkv_simt(void* y, const void* hidden, const void* nw, int nw_dtype, c
     return (int)FD_OK;
   };
   if constexpr (M <= kNormRegMaxM) {
-    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_simt_kernel<T, M, kNtWeights, true>);
+    if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_simt_kernel<T, M, R, kNtWeights, true>);
   }
-  return launch(qkv_simt_kernel<T, M, kNtWeights, false>);
+  return launch(qkv_simt_kernel<T, M, R, kNtWeights, false>);
 }
 
 template <typename T>
@@ -913,7 +919,6 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
     else
       launch_mfma<bf16>((int)M, y, normed, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp);
   } else {
-    rp.tiles = (int)(rope_cols / 4);
     rc = act_dtype == FD_F16
              ? launch_qkv_simt_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H,
                                       (int)N, eps, e, rp, st)
