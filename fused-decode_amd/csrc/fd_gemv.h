@@ -254,6 +254,15 @@ __device__ __forceinline__ void stream_steps(int total, Buf& a, Buf& b, Issue&& 
   }
 }
 
+// B fragment s2 of MFMA unit u for lane group g (x[m][k .. k+8), k = u*128 +
+// (4*s2 + g)*8), zeroed past K; the MFMA forms load it unconditionally.
+__device__ __forceinline__ f16x8 unit_b(const f16x8& b, int u, int s2, int g, int K) {
+  return u * kUnit + (s2 * 4 + g) * 8 < K ? b : f16x8{};
+}
+__device__ __forceinline__ bf16x8 unit_b(const bf16x8& b, int u, int s2, int g, int K) {
+  return u * kUnit + (s2 * 4 + g) * 8 < K ? b : bf16x8{};
+}
+
 // The register prologue holds 2 slices of 8 per row and thread (H up to 16
 // values per thread) and is used up to 2 rows; beyond that its registers would
 // cost the weight loop occupancy, and the loop's longer math hides the prologue.

@@ -259,6 +259,56 @@ __device__ __forceinline__ void fp8x16_to_tile(const u32x4& w, u32x4& c0, u32x4&
   c1 = u32x4{h[4], h[5], h[6], h[7]};
 }
 
+// Registers of one 16x128 unit of the MFMA forms: S weight sets (gate/up: 2) of
+// two 16-byte code loads each, and the four B (x) fragments.
+template <typename T, int S>
+struct UnitRegs8 {
+  u32x4 v[S][2];
+  typename Vec8<T>::type b[4];
+};
+
+// Loads of unit u, all unconditional: a lane whose K chunk is past K reads
+// chunk 0 instead (masked when staged), and B fragments past K read x's first
+// fragment (masked in unit_b); rows past N were clamped by the caller.
+template <typename T, int S>
+__device__ __forceinline__ void load_unit8(UnitRegs8<T, S>& q, const uint8_t* const (&wl)[S][2],
+                                           const T* xp, int u, int lchunk, int g, int K) {
+  const int kc = u * kUnit + lchunk * 16 < K ? u * kUnit : 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) q.v[s][j] = load16_nt(wl[s][j] + kc);
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+    const int kb = u * kUnit + (s2 * 4 + g) * 8;
+    q.b[s2] = load8<T>(xp + (kb < K ? u * kUnit + s2 * 32 : 0));
+  }
+}
+// Decode a unit's codes (zeros past K) into the wave's LDS tile and read back
+// the MFMA A fragments.
+template <typename T>
+__device__ __forceinline__ void stage_unit8(const u32x4 (&v)[2], u32x4* tile, int lrow, int lchunk,
+                                            int u, int K, int r, int g,
+                                            typename Vec8<T>::type (&a)[4]) {
+  const bool in = u * kUnit + lchunk * 16 < K;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    u32x4 c0, c1;
+    fp8x16_to_tile<T>(in ? v[i] : u32x4{0, 0, 0, 0}, c0, c1);
+    const int row = 8 * i + lrow;
+    tile[row * 16 + ((2 * lchunk) ^ row)] = c0;
+    tile[row * 16 + ((2 * lchunk + 1) ^ row)] = c1;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) a[s2] = __builtin_bit_cast(typename Vec8<T>::type, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename T, bool ROPE>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
     T* y, const T* x, const uint8_t* w, const float* wscale, int M, int N, int K, int64_t sxm,
@@ -271,55 +321,30 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const bool xok = r < M;
-  const T* xp = x + (xok ? r : 0) * sxm + g * 8;
+  const T* xp = x + (r < M ? r : 0) * sxm + g * 8;  // rows past M: output columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;  // load side: row lrow (+8), 16 codes at chunk lchunk
-  const uint8_t* wl[2];
-  bool lok[2];
+  const uint8_t* wl[1][2];
   const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t n = ROPE ? tr.row(8 * i + lrow) : n0 + 8 * i + lrow;
-    lok[i] = n < N;
-    wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 16;
+    wl[0][i] = w + (n < N ? n : 0) * swn + lchunk * 16;
   }
   u32x4* tile = tiles[wave];
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
-  for (int u = wave; u < units; u += nw) {
-    const bool in = u * kUnit + lchunk * 16 < K;
-    u32x4 v[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) v[i] = (lok[i] && in) ? load16_nt(wl[i] + u * kUnit) : u32x4{0, 0, 0, 0};
-    V8 b[4];
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      const int kb = u * kUnit + (s2 * 4 + g) * 8;
-      b[s2] = (xok && kb < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
-    }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      u32x4 c0, c1;
-      fp8x16_to_tile<T>(v[i], c0, c1);
-      const int row = 8 * i + lrow;
-      tile[row * 16 + ((2 * lchunk) ^ row)] = c0;
-      tile[row * 16 + ((2 * lchunk + 1) ^ row)] = c1;
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
+  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xp, wave + i * nw, lchunk, g, K); };
+  auto consume = [&](const UnitRegs8<T, 1>& q, int i) {
+    const int u = wave + i * nw;
     V8 a[4];
+    stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, K, r, g, a);
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      const int chunk = s2 * 4 + g;
-      a[s2] = __builtin_bit_cast(V8, tile[r * 16 + (chunk ^ r)]);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
-  }
+    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], unit_b(q.b[s2], u, s2, g, K), acc);
+  };
+  UnitRegs8<T, 1> qa, qb;
+  if (mine > 0) issue(qa, 0);
+  stream_steps(mine, qa, qb, issue, consume);
   part[wave * kWave + lane] = acc;
   __syncthreads();
   if (threadIdx.x < kWave) {
@@ -418,65 +443,36 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const bool xok = r < M;
-  const T* xp = x + (xok ? r : 0) * (int64_t)H + g * 8;
+  const T* xp = x + (r < M ? r : 0) * (int64_t)H + g * 8;  // rows past M: columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;
-  const uint8_t* gl[2];
-  const uint8_t* ul[2];
-  bool lok[2];
+  const uint8_t* wl[2][2];  // [gate, up][row lrow, lrow + 8]
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t j = j0 + 8 * i + lrow;
-    lok[i] = j < I;
-    gl[i] = wgu + (lok[i] ? j : 0) * H + lchunk * 16;
-    ul[i] = wgu + (I + (lok[i] ? j : 0)) * H + lchunk * 16;
+    const int64_t jc = j < I ? j : 0;
+    wl[0][i] = wgu + jc * H + lchunk * 16;
+    wl[1][i] = wgu + (I + jc) * H + lchunk * 16;
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
-  for (int u = wave; u < units; u += nw) {
-    const bool in = u * kUnit + lchunk * 16 < H;
-    u32x4 vg[2], vu[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      vg[i] = (lok[i] && in) ? load16_nt(gl[i] + u * kUnit) : u32x4{0, 0, 0, 0};
-      vu[i] = (lok[i] && in) ? load16_nt(ul[i] + u * kUnit) : u32x4{0, 0, 0, 0};
-    }
-    V8 b[4];
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      const int kb = u * kUnit + (s2 * 4 + g) * 8;
-      b[s2] = (xok && kb < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
-    }
+  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
+  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xp, wave + i * nw, lchunk, g, H); };
+  auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
+    const int u = wave + i * nw;
     V8 a[4], c[4];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        u32x4 c0, c1;
-        fp8x16_to_tile<T>(half ? vu[i] : vg[i], c0, c1);
-        const int row = 8 * i + lrow;
-        tile[row * 16 + ((2 * lchunk) ^ row)] = c0;
-        tile[row * 16 + ((2 * lchunk + 1) ^ row)] = c1;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const V8 t = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
-        if (half) c[s2] = t; else a[s2] = t;
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
+    stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
+    stage_unit8<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
-      ag = mfma16(a[s2], b[s2], ag);
-      au = mfma16(c[s2], b[s2], au);
+      const V8 b = unit_b(q.b[s2], u, s2, g, H);
+      ag = mfma16(a[s2], b, ag);
+      au = mfma16(c[s2], b, au);
     }
-  }
+  };
+  UnitRegs8<T, 2> qa, qb;
+  if (mine > 0) issue(qa, 0);
+  stream_steps(mine, qa, qb, issue, consume);
   part[wave * kWave + lane] = ag;
   __syncthreads();
   f32x4 sg = {0.f, 0.f, 0.f, 0.f};
@@ -523,8 +519,13 @@ template <typename T>
 void launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
                           int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
                           hipStream_t st, const Rope* rp = nullptr) {
-  const int nw = pick_waves((K + kUnit - 1) / kUnit);
-  const dim3 grid((unsigned)((N + 15) / 16)), block(nw * kWave);
+  // Each wave keeps two units in flight; with four or more 16-row tiles per CU
+  // (N = 28672: 1792 tiles), 4-wave workgroups measured faster than 8 (29.7
+  // against 35.5 us at M=8), with fewer, 8-wave ones (N = 4096: 7.6 against 9.1).
+  const int tiles = (N + 15) / 16;
+  int nw = pick_waves((K + kUnit - 1) / kUnit);
+  if (tiles >= 4 * device_cus() && nw > 4) nw = 4;
+  const dim3 grid((unsigned)tiles), block(nw * kWave);
   if (rp)
     hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T, true>), grid, block, 0, st, static_cast<T*>(y),
                        static_cast<const T*>(x), w, s, M, N, K, sxm, swn, sym, syn, e, *rp);
@@ -709,7 +710,10 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
     // y doubles as the normed buffer: the down projection writes it last
     rc = rms_rows(y, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
     if (rc != FD_OK) return rc;
-    const int nwv = pick_waves((H + kUnit - 1) / kUnit);
+    // Two waves per workgroup: every workgroup resident at once (I = 14336: 896
+    // of them at 130 VGPRs), each wave with two of its 16 units in flight
+    // (M=8: 26.4 us against 29.5 for four waves and 32.5 for eight).
+    const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : 2;
     if (act_dtype == FD_F16)
       hipLaunchKernelGGL(mlp_gate_up_fp8_relayout_kernel<f16>, dim3((unsigned)((I + 15) / 16)),
                          dim3(nwv * kWave), 0, st, static_cast<f16*>(mid),

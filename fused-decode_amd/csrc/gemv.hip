@@ -107,11 +107,65 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 // instructions of 4 rows x 256 contiguous bytes (lane l: row 4i + l/16, chunk
 // l%16), stores it to a wave-private 4 KiB LDS buffer with the 16-byte chunk
 // index XOR-swizzled by the row (conflict-free on both sides), and reads it back
-// in MFMA layout. Waves split K in 128-element units, U units per iteration.
+// in MFMA layout. Waves split K in 128-element units; with U = 2 each wave keeps
+// its next unit's loads in flight while it stages and multiplies the current
+// one (stream_steps), with U = 1 one unit at a time.
 //
 // With ROPE the tile rows follow TileRows<16> and the epilogue rotates the
 // rounded outputs of rotated tiles: lanes 0-31 hold slots 0-7 and lanes 32-63
 // their partners 8-15 (same m), one lane-xor-32 exchange apart.
+// Registers of one 16x128 unit of the MFMA forms: S weight sets (gate/up: 2)
+// of four 16-byte row-chunk loads, and the four B (x) fragments.
+template <typename T, int S>
+struct UnitRegs16 {
+  u32x4 v[S][4];
+  typename Vec8<T>::type b[4];
+};
+
+// Loads of unit u, all unconditional: a lane whose K chunk is past K reads
+// chunk 0 instead (zeroed when staged), B fragments past K read x's first
+// fragment (zeroed by unit_b); rows past N were clamped by the caller.
+template <typename T, int S, bool NTW>
+__device__ __forceinline__ void load_unit16(UnitRegs16<T, S>& q, const T* const (&wl)[S][4],
+                                            const T* xp, int u, int lchunk, int g, int K) {
+  const int kc = u * kUnit + lchunk * 8 < K ? u * kUnit : 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(wl[s][i] + kc);
+      q.v[s][i] = NTW ? __builtin_nontemporal_load(p) : *p;
+    }
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+    const int kb = u * kUnit + (s2 * 4 + g) * 8;
+    q.b[s2] = load8<T>(xp + (kb < K ? u * kUnit + s2 * 32 : 0));
+  }
+}
+
+// Stage a unit's rows (zeros past K) in the wave's LDS tile, row 4i+lrow chunk
+// lchunk at slot row*16 + (chunk ^ row), and read back the MFMA A fragments.
+template <typename T>
+__device__ __forceinline__ void stage_unit16(const u32x4 (&v)[4], u32x4* tile, int lrow,
+                                             int lchunk, int u, int K, int r, int g,
+                                             typename Vec8<T>::type (&a)[4]) {
+  const bool in = u * kUnit + lchunk * 8 < K;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * i + lrow;
+    tile[row * 16 + (lchunk ^ row)] = in ? v[i] : u32x4{0, 0, 0, 0};
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2)
+    a[s2] = __builtin_bit_cast(typename Vec8<T>::type, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename T, int U, bool NTW, bool ROPE>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
     T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
@@ -124,67 +178,56 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const bool xok = r < M;
-  const T* xp = x + (xok ? r : 0) * sxm + g * 8;
+  const T* xp = x + (r < M ? r : 0) * sxm + g * 8;  // rows past M: columns never stored
   // load side: lane -> (row 4i + lane/16, chunk lane%16) for instruction i
   const int lrow = lane >> 4, lchunk = lane & 15;
-  const T* wl[4];
-  bool lok[4];
+  const T* wl[1][4];
   const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t n = ROPE ? tr.row(4 * i + lrow) : n0 + 4 * i + lrow;
-    lok[i] = n < N;
-    wl[i] = w + (lok[i] ? n : 0) * swn + lchunk * 8;
+    wl[0][i] = w + (n < N ? n : 0) * swn + lchunk * 8;  // rows past N: outputs never stored
   }
   u32x4* tile = tiles[wave];
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
-  for (int u0 = wave; u0 < units; u0 += nw * U) {
-    // Issue the iteration's B (x) loads with its weight loads: x comes from L2,
-    // and loading it after the LDS stage put its latency in series with the
-    // weight stream's (measured: 26.5 -> 21.9 us at N=4096, K=14336, M=8).
-    u32x4 v[U][4];
-    V8 b[U][4];
+  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
+  auto issue = [&](UnitRegs16<T, 1>& q, int i) {
+    load_unit16<T, 1, NTW>(q, wl, xp, wave + i * nw, lchunk, g, K);
+  };
+  auto consume = [&](const UnitRegs16<T, 1>& q, int i) {
+    const int u = wave + i * nw;
+    V8 a[4];
+    stage_unit16<T>(q.v[0], tile, lrow, lchunk, u, K, r, g, a);
 #pragma unroll
-    for (int j = 0; j < U; ++j) {
-      const int u = u0 + j * nw;
-      const int k = u * kUnit + lchunk * 8;
-      const bool in = u < units && k < K;
+    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], unit_b(q.b[s2], u, s2, g, K), acc);
+  };
+  if constexpr (U == 1) {
+    // one unit at a time; loads under a condition, which suits this form (the
+    // same loop with the pipeline's unconditional loads measured 30% slower)
+    for (int u = wave; u < units; u += nw) {
+      const bool in = u * kUnit + lchunk * 8 < K;
+      u32x4 v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(wl[i] + u * kUnit);
-        v[j][i] = (lok[i] && in) ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
+        const u32x4* q = reinterpret_cast<const u32x4*>(wl[0][i] + u * kUnit);
+        v[i] = in ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
       }
+      V8 b[4];
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const int kb = u * kUnit + (s2 * 4 + g) * 8;
-        b[j][s2] = (xok && u < units && kb < K) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+        b[s2] = kb < K ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
       }
-    }
-#pragma unroll
-    for (int j = 0; j < U; ++j) {
-      // stage: row 4i+lrow, chunk lchunk -> slot row*16 + (chunk ^ row)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 4 * i + lrow;
-        tile[row * 16 + (lchunk ^ row)] = v[j][i];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       V8 a[4];
+      stage_unit16<T>(v, tile, lrow, lchunk, u, K, r, g, a);
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int chunk = s2 * 4 + g;
-        a[s2] = __builtin_bit_cast(V8, tile[r * 16 + (chunk ^ r)]);
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[j][s2], acc);
+      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
     }
+  } else {
+    UnitRegs16<T, 1> qa, qb;
+    if (mine > 0) issue(qa, 0);
+    stream_steps(mine, qa, qb, issue, consume);
   }
   part[wave * kWave + lane] = acc;
   __syncthreads();
@@ -408,7 +451,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
 // 16 gate rows and the matching 16 up rows per workgroup with the row-contiguous
 // load + LDS relayout of gemv_mfma_relayout_kernel. B operand: the normalised
 // activations from global memory (L2-resident, [M, H]).
-template <typename T, int U, bool NTW>
+template <typename T, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel(
     T* mid, const T* x, const T* wgu, int M, int H, int I) {
   typedef typename Vec8<T>::type V8;
@@ -419,73 +462,38 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const bool xok = r < M;
-  const T* xp = x + (xok ? r : 0) * (int64_t)H + g * 8;
+  const T* xp = x + (r < M ? r : 0) * (int64_t)H + g * 8;  // rows past M: columns never stored
   const int lrow = lane >> 4, lchunk = lane & 15;
-  const T* gl[4];
-  const T* ul[4];
-  bool lok[4];
+  const T* wl[2][4];  // [gate, up][row 4i + lrow]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t j = j0 + 4 * i + lrow;
-    lok[i] = j < I;
-    gl[i] = wgu + (lok[i] ? j : 0) * H + lchunk * 8;
-    ul[i] = wgu + (I + (lok[i] ? j : 0)) * H + lchunk * 8;
+    const int64_t jc = j < I ? j : 0;
+    wl[0][i] = wgu + jc * H + lchunk * 8;
+    wl[1][i] = wgu + (I + jc) * H + lchunk * 8;
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
-  for (int u0 = wave; u0 < units; u0 += nw * U) {
-    u32x4 vg[U][4], vu[U][4];
-    V8 b[U][4];  // B (normed x) loads issued with the weight loads, as in the GEMV
+  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
+  auto issue = [&](UnitRegs16<T, 2>& q, int i) {
+    load_unit16<T, 2, NTW>(q, wl, xp, wave + i * nw, lchunk, g, H);
+  };
+  auto consume = [&](const UnitRegs16<T, 2>& q, int i) {
+    const int u = wave + i * nw;
+    V8 a[4], c[4];
+    stage_unit16<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
+    stage_unit16<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
 #pragma unroll
-    for (int jj = 0; jj < U; ++jj) {
-      const int u = u0 + jj * nw;
-      const bool in = u < units && u * kUnit + lchunk * 8 < H;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4* qg = reinterpret_cast<const u32x4*>(gl[i] + u * kUnit);
-        const u32x4* qu = reinterpret_cast<const u32x4*>(ul[i] + u * kUnit);
-        const bool ok = lok[i] && in;
-        vg[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qg) : *qg) : u32x4{0, 0, 0, 0};
-        vu[jj][i] = ok ? (NTW ? __builtin_nontemporal_load(qu) : *qu) : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int k = u * kUnit + s2 * 32 + g * 8;
-        b[jj][s2] = (xok && u < units && k < H) ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
-      }
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const V8 b = unit_b(q.b[s2], u, s2, g, H);
+      ag = mfma16(a[s2], b, ag);
+      au = mfma16(c[s2], b, au);
     }
-#pragma unroll
-    for (int jj = 0; jj < U; ++jj) {
-      V8 a[4], c[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tile[(4 * i + lrow) * 16 + (lchunk ^ (4 * i + lrow))] = vg[jj][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) a[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int i = 0; i < 4; ++i) tile[(4 * i + lrow) * 16 + (lchunk ^ (4 * i + lrow))] = vu[jj][i];
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) c[s2] = __builtin_bit_cast(V8, tile[r * 16 + ((s2 * 4 + g) ^ r)]);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        ag = mfma16(a[s2], b[jj][s2], ag);
-        au = mfma16(c[s2], b[jj][s2], au);
-      }
-    }
-  }
+  };
+  UnitRegs16<T, 2> qa, qb;
+  if (mine > 0) issue(qa, 0);
+  stream_steps(mine, qa, qb, issue, consume);
   // two-phase reduction through one buffer: gate sums, then up sums
   part[wave * kWave + lane] = ag;
   __syncthreads();
@@ -521,7 +529,7 @@ constexpr int kMfmaMinM = 5;   // kind=dot uses MFMA from this M on (tile search
 struct Tile {
   int rows;    // weight rows per workgroup (SIMT 2, 4, 8; MFMA 16)
   int waves;   // waves per workgroup, 1..8
-  int stages;  // MFMA K units per wave and iteration (1, 2); SIMT 1
+  int stages;  // MFMA K units in flight per wave (1, 2); SIMT 1
 };
 
 template <typename T, int M, int R>
@@ -568,14 +576,14 @@ void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
                  const Rope* rp = nullptr, const Tile* t = nullptr) {
   const int nw = t && t->waves ? t->waves : pick_waves((K + kUnit - 1) / kUnit);
-  const int stages = t && t->stages ? t->stages : 1;
+  // Two units in flight per wave by default: the pipelined form measured faster
+  // than one unit at a time on all four decode shapes at M = 5, 8 and 16
+  // (N = 4096, K = 14336, M = 8: 21.2 against 22.4 us).
+  const int stages = t && t->stages ? t->stages : 2;
   Rope none{};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
   const Rope& r = rp ? *rp : none;
-  // One K unit per iteration by default: with the x loads issued alongside the
-  // weights, a second unit only costs registers (measured on the four decode
-  // shapes at M = 8 and 16).
 #define FD_MFMA(UU, RR)                                                                    \
   hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, UU, true, RR>), dim3(blocks),          \
                      dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), \
@@ -678,8 +686,11 @@ int launch_qkv_simt_m(int M, void* y, const void* hidden, const void* nw, int nw
 template <typename T>
 int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, int H, int I,
                         hipStream_t st) {
-  const int nwv = pick_waves((H + kUnit - 1) / kUnit);
-  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, 1, true>), dim3((unsigned)((I + 15) / 16)),
+  // Four waves, each with two of its units in flight (M=8 at Llama-3-8B widths:
+  // 39.3 us against 41.2 for eight waves and 39.8 for the one-unit loop).
+  const int units = (H + kUnit - 1) / kUnit;
+  const int nwv = units < 4 ? units : 4;
+  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, true>), dim3((unsigned)((I + 15) / 16)),
                      dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
                      static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I);
   return FD_OK;

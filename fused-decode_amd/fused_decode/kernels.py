@@ -191,7 +191,7 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
 def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
     """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot")."""
     if kern == "dot":
-        return 16, _waves(-(-k // 128)), 1
+        return 16, _waves(-(-k // 128)), 2
     return 4, _waves(-(-k // 512)), 1
 
 
