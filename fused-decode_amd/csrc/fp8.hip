@@ -89,11 +89,19 @@ __device__ __forceinline__ u32x4 load16_nt(const uint8_t* p) {
 
 // SIMT fp8 GEMV: R rows per workgroup, waves split K in 1024-element chunks,
 // transposing butterfly + LDS across waves, then scale, bias, row_add, rounding.
+// A wave's K steps run through stream_steps with every load unconditional (a
+// lane past K reads chunk 0, masked in the math), so each wave has its next
+// step's codes and activations in flight while it multiplies the current one.
+template <typename T, int M, int R>
+struct Step8Regs {
+  u32x4 w[R];
+  typename Vec8<T>::type xa[M], xb[M];
+};
+
 template <typename T, int M, int R>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
     T* y, const T* x, const uint8_t* w, const float* wscale, int N, int K, int64_t sxm,
     int64_t swn, int64_t sym, int64_t syn, Epi e) {
-  typedef typename Vec8<T>::type V8;
   constexpr int V = pow2_ceil(R * M);
   __shared__ float part[kMaxWaves * V];
   const int lane = threadIdx.x & (kWave - 1);
@@ -104,27 +112,32 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
 #pragma unroll
   for (int i = 0; i < V; ++i) acc[i] = 0.f;
   const uint8_t* wr[R];
-  bool rok[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    rok[r] = n0 + r < N;
-    wr[r] = w + (rok[r] ? n0 + r : 0) * swn;
-  }
-  for (int k = (wave * kWave + lane) * 16; k < K; k += nw * kChunk8) {
-    u32x4 wv[R];
+  for (int r = 0; r < R; ++r) wr[r] = w + (n0 + r < N ? n0 + r : 0) * swn;  // rows past N: never stored
+  const int step = nw * kChunk8;
+  const int steps = (K + step - 1) / step;
+  const int kbase = (wave * kWave + lane) * 16;
+  auto issue = [&](Step8Regs<T, M, R>& q, int s) {
+    const int k = kbase + s * step;
+    const int kc = k < K ? k : 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) wv[r] = rok[r] ? load16_nt(wr[r] + k) : u32x4{0, 0, 0, 0};
-    V8 xa[M], xb[M];
+    for (int r = 0; r < R; ++r) q.w[r] = load16_nt(wr[r] + kc);
 #pragma unroll
     for (int m = 0; m < M; ++m) {
-      xa[m] = load8<T>(x + m * sxm + k);
-      xb[m] = load8<T>(x + m * sxm + k + 8);
+      q.xa[m] = load8<T>(x + m * sxm + kc);
+      q.xb[m] = load8<T>(x + m * sxm + kc + 8);
     }
+  };
+  auto consume = [&](const Step8Regs<T, M, R>& q, int s) {
+    if (kbase + s * step >= K) return;
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-      for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(wv[r], xa[m], xb[m], acc[r * M + m]);
-  }
+      for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(q.w[r], q.xa[m], q.xb[m], acc[r * M + m]);
+  };
+  Step8Regs<T, M, R> qa, qb;
+  issue(qa, 0);
+  stream_steps(steps, qa, qb, issue, consume);
   butterfly_sum<V>(acc, lane);
   if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
   __syncthreads();
