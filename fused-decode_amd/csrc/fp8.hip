@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
       for (int m = 0; m < M; ++m) acc[r * M + m] = dot_fp8x16<T>(q.w[r], q.xa[m], q.xb[m], acc[r * M + m]);
   };
   Step8Regs<T, M, R> qa, qb;
-  issue(qa, 0);
+  if (steps > 0) issue(qa, 0);  // K = 0 loads nothing (x may be null)
   stream_steps(steps, qa, qb, issue, consume);
   butterfly_sum<V>(acc, lane);
   if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
@@ -675,7 +675,8 @@ extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float
     return set_error(FD_EINVAL, "bias must match x or be float32");
   if (row_add && !check_any_dtype(row_dtype, "row_dtype")) return FD_EINVAL;
   if (M == 0 || N == 0) return FD_OK;
-  if (!y || !w8 || !w_scale || (!x && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
+  // K = 0 reads neither operand (an empty torch tensor's pointer is null)
+  if (!y || !w_scale || ((!x || !w8) && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
   if (K % 16 != 0 || (N > 1 && swn % 16 != 0) || (M > 1 && sxm % 8 != 0))
     return set_error(FD_EUNSUPPORTED, "the fp8 GEMV needs K %% 16 == 0 and 16-byte aligned rows");
   if (!aligned16(x) || !aligned16(w8)) return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");

@@ -95,8 +95,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
         for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.w[r], q.x[m], acc[r * M + m]);
     };
     StepRegs<T, M, R> qa, qb;
-    issue(qa, 0);
-    stream_steps((K + step - 1) / step, qa, qb, issue, consume);
+    const int steps = (K + step - 1) / step;
+    if (steps > 0) issue(qa, 0);  // K = 0 loads nothing (x may be null)
+    stream_steps(steps, qa, qb, issue, consume);
   } else {
     for (int k = kbase; k < K; k += step) {
       V8 wv[R];
@@ -814,7 +815,8 @@ extern "C" int fd_linear_tiled(void* y, const void* x, const void* w, const void
     if (rc != FD_OK) return rc;
   }
   if (M == 0 || N == 0) return FD_OK;
-  if (!y || !w || (!x && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
+  // K = 0 reads neither operand (an empty torch tensor's pointer is null)
+  if (!y || ((!x || !w) && K > 0)) return set_error(FD_EINVAL, "null pointer argument");
   Epi e;
   e.bias = bias;
   e.bias_dtype = bias_dtype;

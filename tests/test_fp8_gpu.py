@@ -155,6 +155,27 @@ def test_post_attn_mlp_fp8_graph_replays_match_eager():
         torch.testing.assert_close(out, eager, rtol=0, atol=0)
 
 
+def test_linear_fp8_k0_is_the_epilogue():
+    """K = 0 through the C entry point: y = round(scale-free bias + row_add), with
+    x null and no code read, for the SIMT (M = 1) and MFMA (M = 6) forms."""
+    from fused_decode import _lib as L
+
+    n = 48
+    codes = torch.zeros(n, 16, device=DEV, dtype=torch.uint8)  # aligned, never read at K = 0
+    scale = torch.ones(n, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    for m in (1, 6):
+        bias = rnd(n, seed=80 + m).to(DEV)
+        ra = rnd(m, n, seed=90 + m).to(DEV)
+        exp = O.linear(np.zeros((m, 0), np.float32), np.zeros((n, 0), np.float32), bias=npf(bias),
+                       row_add=npf(ra), dtype="f16")
+        y = torch.full((m, n), float("nan"), device=DEV, dtype=torch.float16)
+        L.check("fd_linear_fp8", L.lib().fd_linear_fp8(
+            y.data_ptr(), None, codes.data_ptr(), scale.data_ptr(), bias.data_ptr(), L.FD_F16,
+            ra.data_ptr(), L.FD_F16, m, n, 0, 16, 16, 1, n, 1, n, 1, L.FD_F16, st))
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(exp), rtol=0, atol=0)
+
+
 def test_fp8_rejects():
     import fused_decode as fd
 

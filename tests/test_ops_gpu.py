@@ -316,6 +316,31 @@ def test_linear_unaligned_and_empty():
     assert z.shape == (2, 0)
 
 
+def test_linear_k0_is_the_epilogue():
+    """K = 0: y = round(bias + row_add) with x and the weights never read (x is
+    null through the C entry point), for the SIMT (M < 5) and MFMA forms."""
+    from fused_decode import _lib as L
+
+    n = 40
+    w = torch.zeros(n, 8, device=DEV, dtype=torch.float16)  # aligned, never read at K = 0
+    st = torch.cuda.current_stream().cuda_stream
+    for m in (1, 3, 6):
+        bias = randn(n, seed=50 + m).to(DEV)
+        ra = randn(m, n, seed=60 + m).to(DEV)
+        exp = O.linear(np.zeros((m, 0), np.float32), np.zeros((n, 0), np.float32), bias=npf(bias),
+                       row_add=npf(ra), dtype="f16")
+        for kind in (L.FD_KIND_DOT, L.FD_KIND_SIMT):
+            y = torch.full((m, n), float("nan"), device=DEV, dtype=torch.float16)
+            L.check("fd_linear", L.lib().fd_linear(
+                y.data_ptr(), None, w.data_ptr(), bias.data_ptr(), L.FD_F16, ra.data_ptr(), L.FD_F16,
+                m, n, 0, 8, 1, 8, 1, 1, n, 1, n, 1, kind, L.FD_F16, st))
+            torch.testing.assert_close(y.float().cpu(), torch.from_numpy(exp), rtol=0, atol=0)
+    b1 = randn(1, seed=70).to(DEV)
+    y1 = fd().linear_decode(torch.empty(2, 0, device=DEV, dtype=torch.float16),
+                            torch.empty(1, 0, device=DEV, dtype=torch.float16), b1, kind="simt")
+    torch.testing.assert_close(y1, b1.expand(2, 1), rtol=0, atol=0)
+
+
 LINEAR_CONFIGS = [(4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)]
 
 
