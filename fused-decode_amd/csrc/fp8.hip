@@ -280,13 +280,15 @@ struct UnitRegs8 {
   typename Vec8<T>::type b[4];
 };
 
-// Loads of unit u, all unconditional: a lane whose K chunk is past K reads
-// chunk 0 instead (masked when staged), and B fragments past K read x's first
-// fragment (masked in unit_b); rows past N were clamped by the caller.
+// Loads of unit u, all unconditional: a lane whose K chunk is past K reads its
+// row's first 16 codes instead (masked when staged), a B fragment past K its x
+// row's first fragment (masked in unit_b). `wl` are code row bases (rows past N
+// clamped by the caller to row 0), `xr` the lane's x row.
 template <typename T, int S>
 __device__ __forceinline__ void load_unit8(UnitRegs8<T, S>& q, const uint8_t* const (&wl)[S][2],
-                                           const T* xp, int u, int lchunk, int g, int K) {
-  const int kc = u * kUnit + lchunk * 16 < K ? u * kUnit : 0;
+                                           const T* xr, int u, int lchunk, int g, int K) {
+  const int k = u * kUnit + lchunk * 16;
+  const int kc = k < K ? k : 0;
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -294,9 +296,10 @@ __device__ __forceinline__ void load_unit8(UnitRegs8<T, S>& q, const uint8_t* co
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
     const int kb = u * kUnit + (s2 * 4 + g) * 8;
-    q.b[s2] = load8<T>(xp + (kb < K ? u * kUnit + s2 * 32 : 0));
+    q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
   }
 }
+
 // Decode a unit's codes (zeros past K) into the wave's LDS tile and read back
 // the MFMA A fragments.
 template <typename T>
@@ -334,20 +337,20 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const T* xp = x + (r < M ? r : 0) * sxm + g * 8;  // rows past M: output columns never stored
+  const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: output columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;  // load side: row lrow (+8), 16 codes at chunk lchunk
   const uint8_t* wl[1][2];
   const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t n = ROPE ? tr.row(8 * i + lrow) : n0 + 8 * i + lrow;
-    wl[0][i] = w + (n < N ? n : 0) * swn + lchunk * 16;
+    wl[0][i] = w + (n < N ? n : 0) * swn;
   }
   u32x4* tile = tiles[wave];
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
-  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xp, wave + i * nw, lchunk, g, K); };
+  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xr, wave + i * nw, lchunk, g, K); };
   auto consume = [&](const UnitRegs8<T, 1>& q, int i) {
     const int u = wave + i * nw;
     V8 a[4];
@@ -456,21 +459,21 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const T* xp = x + (r < M ? r : 0) * (int64_t)H + g * 8;  // rows past M: columns never stored
+  const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;
-  const uint8_t* wl[2][2];  // [gate, up][row lrow, lrow + 8]
+  const uint8_t* wl[2][2];  // [gate, up][row lrow, lrow + 8] bases
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int64_t j = j0 + 8 * i + lrow;
     const int64_t jc = j < I ? j : 0;
-    wl[0][i] = wgu + jc * H + lchunk * 16;
-    wl[1][i] = wgu + (I + jc) * H + lchunk * 16;
+    wl[0][i] = wgu + jc * H;
+    wl[1][i] = wgu + (I + jc) * H;
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
-  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xp, wave + i * nw, lchunk, g, H); };
+  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xr, wave + i * nw, lchunk, g, H); };
   auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
     const int u = wave + i * nw;
     V8 a[4], c[4];

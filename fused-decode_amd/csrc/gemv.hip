@@ -152,13 +152,15 @@ struct UnitRegs16 {
   typename Vec8<T>::type b[4];
 };
 
-// Loads of unit u, all unconditional: a lane whose K chunk is past K reads
-// chunk 0 instead (zeroed when staged), B fragments past K read x's first
-// fragment (zeroed by unit_b); rows past N were clamped by the caller.
+// Loads of unit u, all unconditional: a lane whose K chunk is past K reads its
+// row's first chunk instead (zeroed when staged), a B fragment past K its x
+// row's first fragment (zeroed by unit_b). `wl` are weight row bases (rows past
+// N clamped by the caller to row 0), `xr` the lane's x row.
 template <typename T, int S, bool NTW>
 __device__ __forceinline__ void load_unit16(UnitRegs16<T, S>& q, const T* const (&wl)[S][4],
-                                            const T* xp, int u, int lchunk, int g, int K) {
-  const int kc = u * kUnit + lchunk * 8 < K ? u * kUnit : 0;
+                                            const T* xr, int u, int lchunk, int g, int K) {
+  const int k = u * kUnit + lchunk * 8;
+  const int kc = k < K ? k : 0;
 #pragma unroll
   for (int s = 0; s < S; ++s)
 #pragma unroll
@@ -169,7 +171,7 @@ __device__ __forceinline__ void load_unit16(UnitRegs16<T, S>& q, const T* const 
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
     const int kb = u * kUnit + (s2 * 4 + g) * 8;
-    q.b[s2] = load8<T>(xp + (kb < K ? u * kUnit + s2 * 32 : 0));
+    q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
   }
 }
 
@@ -208,7 +210,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const T* xp = x + (r < M ? r : 0) * sxm + g * 8;  // rows past M: columns never stored
+  const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: columns never stored
   // load side: lane -> (row 4i + lane/16, chunk lane%16) for instruction i
   const int lrow = lane >> 4, lchunk = lane & 15;
   const T* wl[1][4];
@@ -216,14 +218,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t n = ROPE ? tr.row(4 * i + lrow) : n0 + 4 * i + lrow;
-    wl[0][i] = w + (n < N ? n : 0) * swn + lchunk * 8;  // rows past N: outputs never stored
+    wl[0][i] = w + (n < N ? n : 0) * swn;  // rows past N: outputs never stored
   }
   u32x4* tile = tiles[wave];
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
   auto issue = [&](UnitRegs16<T, 1>& q, int i) {
-    load_unit16<T, 1, NTW>(q, wl, xp, wave + i * nw, lchunk, g, K);
+    load_unit16<T, 1, NTW>(q, wl, xr, wave + i * nw, lchunk, g, K);
   };
   auto consume = [&](const UnitRegs16<T, 1>& q, int i) {
     const int u = wave + i * nw;
@@ -240,14 +242,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
       u32x4 v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(wl[0][i] + u * kUnit);
+        const u32x4* q = reinterpret_cast<const u32x4*>(wl[0][i] + u * kUnit + lchunk * 8);
         v[i] = in ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
       }
       V8 b[4];
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const int kb = u * kUnit + (s2 * 4 + g) * 8;
-        b[s2] = kb < K ? load8<T>(xp + u * kUnit + s2 * 32) : V8{};
+        b[s2] = kb < K ? load8<T>(xr + kb) : V8{};
       }
       V8 a[4];
       stage_unit16<T>(v, tile, lrow, lchunk, u, K, r, g, a);
@@ -492,22 +494,22 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
   const int nw = blockDim.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const T* xp = x + (r < M ? r : 0) * (int64_t)H + g * 8;  // rows past M: columns never stored
+  const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 4, lchunk = lane & 15;
-  const T* wl[2][4];  // [gate, up][row 4i + lrow]
+  const T* wl[2][4];  // [gate, up][row 4i + lrow] bases
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int64_t j = j0 + 4 * i + lrow;
     const int64_t jc = j < I ? j : 0;
-    wl[0][i] = wgu + jc * H + lchunk * 8;
-    wl[1][i] = wgu + (I + jc) * H + lchunk * 8;
+    wl[0][i] = wgu + jc * H;
+    wl[1][i] = wgu + (I + jc) * H;
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   auto issue = [&](UnitRegs16<T, 2>& q, int i) {
-    load_unit16<T, 2, NTW>(q, wl, xp, wave + i * nw, lchunk, g, H);
+    load_unit16<T, 2, NTW>(q, wl, xr, wave + i * nw, lchunk, g, H);
   };
   auto consume = [&](const UnitRegs16<T, 2>& q, int i) {
     const int u = wave + i * nw;

@@ -155,6 +155,20 @@ def test_post_attn_mlp_fp8_graph_replays_match_eager():
         torch.testing.assert_close(out, eager, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("m", [1, 6])
+@pytest.mark.parametrize("k", [16, 48])
+def test_linear_fp8_k_below_one_unit(m, k):
+    """K below one 128-element MFMA unit (and one 1024-code SIMT step)."""
+    import fused_decode as fd
+
+    n = 40
+    x = rnd(m, k, seed=100 + k + m)
+    q, s, qn, sn = quant(rnd(n, k, seed=110 + k, scale=k ** -0.5))
+    y = fd.linear_decode_fp8(x.to(DEV), q, s)
+    ref = O.linear_fp8(npf(x), qn, sn, dtype="f16")
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 def test_linear_fp8_k0_is_the_epilogue():
     """K = 0 through the C entry point: y = round(scale-free bias + row_add), with
     x null and no code read, for the SIMT (M = 1) and MFMA (M = 6) forms."""

@@ -237,8 +237,11 @@ def _linear_case(m, n, k, dtype, seed, bias=False):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("kind", ["dot", "simt"])
-@pytest.mark.parametrize("m,n,k", [(1, 64, 100), (3, 128, 128), (8, 256, 64)])
+@pytest.mark.parametrize("m,n,k", [(1, 64, 100), (3, 128, 128), (8, 256, 64), (6, 48, 8), (5, 40, 24),
+                                   (1, 40, 8)])
 def test_linear_small(dtype, kind, m, n, k):
+    """Small and ragged shapes, including K below one MFMA unit (128) and one B
+    fragment group (32), where most lanes of a unit lie past K."""
     x, w, b = _linear_case(m, n, k, dtype, 6, bias=True)
     y = fd().linear_decode(x.to(DEV), w.to(DEV), b.to(DEV), kind=kind)
     check(y, O.linear(npf(x), npf(w), npf(b), dtype=tag(dtype)), dtype, "linear")
