@@ -154,7 +154,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
 
 // Fused gate/up + SwiGLU with fp8 weights: the RMSNorm prologue of the fp16
 // kernel (normalised rows rounded into LDS), R gate rows and the matching R up
-// rows per tile streamed one K step ahead of the math, and
+// rows per tile streamed through the step pipeline, and
 // mid = round(silu(round(sg*g)) * round(su*u)).
 template <int R>
 struct GateUp8Regs {

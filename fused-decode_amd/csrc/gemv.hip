@@ -15,9 +15,15 @@
 // MFMA kernel (gemv_mfma_relayout_kernel, M padded to 16; kind=dot from 5 rows):
 // a workgroup owns 16 weight rows; waves split K into 128-element units of four
 // v_mfma_f32_16x16x32 steps. A = 16 weight rows x 32 k (lane l: row l%16,
-// k-group l/16), B = x^T with the same lane->k mapping, so padding rows m >= M
-// are zero registers, not loads. The weights are loaded row-contiguously and
-// relaid through LDS into the A layout (see the kernel).
+// k-group l/16), B = x^T with the same lane->k mapping; padding rows m >= M load
+// row 0 again (their output columns are never stored). The weights are loaded
+// row-contiguously and relaid through LDS into the A layout (see the kernel).
+//
+// Every hot loop issues its loads unconditionally (out-of-range lanes read an
+// in-bounds address and are masked where used) and runs its K steps through
+// two register buffers (stream_steps, fd_gemv.h), so a wave always has its next
+// step's loads in flight; a guarded load would make the compiler wait for all
+// outstanding loads at its first use.
 //
 // Fused MLP: launch 1 computes the RMSNorm of hidden in a prologue (each
 // workgroup re-derives the row scale and stages the normalised activations in
