@@ -23,6 +23,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 
+// Threads per workgroup. Every launch in this library uses whole workgroups,
+// so this is the dispatch's workgroup size, read at a fixed offset with a
+// scalar load. blockDim.x also selects the partial-workgroup remainder; the
+// compiler folds that select into a 2-byte vector load at a variable offset,
+// re-issues it at each use, and its vmcnt wait then also waits for every
+// weight load already in flight.
+__device__ __forceinline__ int block_threads() { return __builtin_amdgcn_workgroup_size_x(); }
+
 // 8 activation elements = one 16-byte vector.
 template <typename T> struct Vec8;
 template <> struct Vec8<f16> { typedef f16x8 type; };

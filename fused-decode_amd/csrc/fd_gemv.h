@@ -59,7 +59,7 @@ __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hid
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int nt = blockDim.x, nwv = nt / kWave;
+  const int nt = block_threads(), nwv = nt / kWave;
   float ss[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
@@ -110,7 +110,7 @@ __device__ __forceinline__ void stage_normed(T* xs, float* scratch, const T* hid
 // address and are masked later): a load under a branch leaves the compiler
 // unsure how many loads are outstanding, and it then waits for all of them,
 // the weight loads included, before the norm's first use. Usable when
-// H <= KIT * blockDim.x * 8 (norm_in_regs); the same summation order and
+// H <= KIT * block_threads() * 8 (norm_in_regs); the same summation order and
 // rounding as stage_normed.
 template <typename T, int MMAX, int KIT>
 struct NormRegs {
@@ -125,7 +125,7 @@ __device__ __forceinline__ void norm_load(NormRegs<T, MMAX, KIT>& c, const T* hi
   const int esz = is32 ? 4 : 2;
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
-    const int k = (threadIdx.x + it * blockDim.x) * 8;
+    const int k = (threadIdx.x + it * block_threads()) * 8;
     const int kc = k < H ? k : 0;
 #pragma unroll
     for (int m = 0; m < MMAX; ++m)
@@ -165,13 +165,13 @@ __device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* x
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-  const int nwv = blockDim.x / kWave;
+  const int nwv = block_threads() / kWave;
   float ss[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
-    const bool in = (tid + it * (int)blockDim.x) * 8 < H;
+    const bool in = (tid + it * block_threads()) * 8 < H;
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
 #pragma unroll
@@ -193,7 +193,7 @@ __device__ __forceinline__ void norm_store(const NormRegs<T, MMAX, KIT>& c, T* x
   __syncthreads();
 #pragma unroll
   for (int it = 0; it < KIT; ++it) {
-    const int k = (tid + it * (int)blockDim.x) * 8;
+    const int k = (tid + it * block_threads()) * 8;
     if (k < H) {
       float wf[8];
       norm_w8(c.w0[it], c.w1[it], nw_dtype, wf);
@@ -394,7 +394,7 @@ __device__ __forceinline__ void qkv_tile_out(T* y, const float* part, int V, int
                                              const Scale& sc, int N) {
   constexpr int P = R / 2;
   if (tr.rotated()) {
-    for (int t = threadIdx.x; t < P * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < P * M; t += block_threads()) {
       const int p = t / M, m = t % M;
       float s1 = 0.f, s2 = 0.f;
       for (int i = 0; i < nw; ++i) {
@@ -409,7 +409,7 @@ __device__ __forceinline__ void qkv_tile_out(T* y, const float* part, int V, int
       y[m * (int64_t)N + n2] = from_f32<T>(o2);
     }
   } else {
-    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < R * M; t += block_threads()) {
       const int r = t / M, m = t % M;
       const int64_t n = tr.row(r);
       if (n < N) {

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
   __shared__ float part[kMaxWaves * V];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int64_t n0 = (int64_t)blockIdx.x * R;
   float acc[V];
 #pragma unroll
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
   butterfly_sum<V>(acc, lane);
   if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
   __syncthreads();
-  for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+  for (int t = threadIdx.x; t < R * M; t += block_threads()) {
     const int r = t / M, m = t % M;
     const int64_t n = n0 + r;
     if (n < N) {
@@ -179,8 +179,8 @@ __device__ __forceinline__ void load_gate_up8(GateUp8Regs<R>& b, const uint8_t* 
 
 template <typename T, int M, int R, bool REGS>
 __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
-    T* mid, const T* hidden, const void* nwp, int nw_dtype, const uint8_t* wgu,
-    const float* gu_scale, int H, int I, float eps, int tiles) {
+    T* __restrict__ mid, const T* hidden, const void* nwp, int nw_dtype, const uint8_t* wgu,
+    const float* __restrict__ gu_scale, int H, int I, float eps, int tiles) {
   typedef typename Vec8<T>::type V8;
   constexpr int V = pow2_ceil(2 * R * M);
   extern __shared__ __align__(16) unsigned char smem[];
@@ -189,7 +189,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
   float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const StepPlan p(tiles, H, nw * kChunk8, (wave * kWave + lane) * 16);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
@@ -223,22 +223,35 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
         }
     }
     if (!p.last(s)) return;
+    // The tile's channel scales sit at wave-uniform addresses: scalar loads,
+    // which leave the next step's weight loads in flight (a vector load here
+    // would be waited for behind them).
+    const int j0 = p.tile(s) * R;
+    float sg[R], su[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = __builtin_amdgcn_readfirstlane(j0 + r < I ? j0 + r : I - 1);
+      sg[r] = gu_scale[j];
+      su[r] = gu_scale[I + j];
+    }
     butterfly_sum<V>(acc, lane);
     __syncthreads();  // previous tile's readers of `part` are done
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    const int64_t j0 = (int64_t)p.tile(s) * R;
-    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < R * M; t += block_threads()) {
       const int r = t / M, m = t % M;
-      const int64_t j = j0 + r;
+      const int j = j0 + r;
       if (j < I) {
         float gs = 0.f, us = 0.f;
         for (int i = 0; i < nw; ++i) {
           gs += part[i * V + t];
           us += part[i * V + R * M + t];
         }
-        mid[m * (int64_t)I + j] =
-            swiglu_out<T>(gs * 256.f * gu_scale[j], us * 256.f * gu_scale[I + j]);
+        float gsc = sg[0], usc = su[0];
+#pragma unroll
+        for (int q = 1; q < R; ++q)
+          if (r == q) gsc = sg[q], usc = su[q];
+        mid[m * (int64_t)I + j] = swiglu_out<T>(gs * 256.f * gsc, us * 256.f * usc);
       }
     }
 #pragma unroll
@@ -334,7 +347,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: output columns never stored
@@ -404,7 +417,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
   float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const StepPlan p(tiles, H, nw * kChunk8, (wave * kWave + lane) * 16);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
@@ -456,7 +469,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
   __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
   const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored

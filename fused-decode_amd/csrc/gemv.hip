@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
   __shared__ float part[kMaxWaves * V];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int64_t n0 = (int64_t)blockIdx.x * R;
 
   float acc[V];
@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
   butterfly_sum<V>(acc, lane);
   if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
   __syncthreads();
-  for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+  for (int t = threadIdx.x; t < R * M; t += block_threads()) {
     const int r = t / M, m = t % M;
     const int64_t n = n0 + r;
     if (n < N) {
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
   __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
   const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: columns never stored
@@ -356,7 +356,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
   float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const StepPlan p(tiles, H, nw * kChunk, (wave * kWave + lane) * 8);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
     const int64_t j0 = (int64_t)p.tile(s) * R;
-    for (int t = threadIdx.x; t < R * M; t += blockDim.x) {
+    for (int t = threadIdx.x; t < R * M; t += block_threads()) {
       const int r = t / M, m = t % M;
       const int64_t j = j0 + r;
       if (j < I) {
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   float* part = reinterpret_cast<float*>(smem + (size_t)M * XS * sizeof(T));
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const StepPlan p(tiles, H, nw * kChunk, (wave * kWave + lane) * 8);
 
   NormRegs<T, M, kNormRegRows(M)> nr;
@@ -497,7 +497,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
   __shared__ u32x4 tiles[kMaxWaves][256];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
+  const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
   const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored
