@@ -197,37 +197,96 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// Cross-lane exchanges of the reductions below, none through LDS (a shuffle is
+// a ds_bpermute round trip). The partner of lane l at lane bit b is l ^ 32
+// (v_permlane32_swap), l ^ 16 (v_permlane16_swap), l ^ 15 (DPP row_mirror),
+// l ^ 7 (row_half_mirror), l ^ 2 and l ^ 1 (quad_perm): each flips bit b and at
+// most lower bits, so partners agree on every higher bit, and exchanges taken
+// over the bits from 32 down to 1 still combine all 64 lanes.
+template <int MASK> struct XlaneDpp;
+template <> struct XlaneDpp<8> { static constexpr int ctrl = 0x140; };  // row_mirror
+template <> struct XlaneDpp<4> { static constexpr int ctrl = 0x141; };  // row_half_mirror
+template <> struct XlaneDpp<2> { static constexpr int ctrl = 0x4e; };   // quad_perm 2,3,0,1
+template <> struct XlaneDpp<1> { static constexpr int ctrl = 0xb1; };   // quad_perm 1,0,3,2
+
+template <int MASK>
+__device__ __forceinline__ float xlane_dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), XlaneDpp<MASK>::ctrl, 0xf, 0xf,
+                                      false));
+}
+
+// Lanes with bit MASK clear return lo + the partner's lo, lanes with it set
+// hi + the partner's hi. v_permlane32_swap exchanges lanes 32-63 of its first
+// operand with lanes 0-31 of its second, v_permlane16_swap the odd 16-lane
+// rows of its first with the even rows of its second: afterwards a lane with
+// the bit clear holds its own lo and the partner's lo, a lane with it set the
+// partner's hi and its own hi.
+template <int MASK>
+__device__ __forceinline__ float xlane_keep_sum(float lo, float hi, int lane) {
+  if constexpr (MASK >= 16) {
+    const unsigned a = __builtin_bit_cast(unsigned, lo), b = __builtin_bit_cast(unsigned, hi);
+    const auto r = MASK == 32 ? __builtin_amdgcn_permlane32_swap(a, b, false, false)
+                              : __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    // Copy both results out before any cast: __builtin_bit_cast applied to
+    // r[1] directly reads element 0 (this clang).
+    const unsigned r0 = r[0], r1 = r[1];
+    return __builtin_bit_cast(float, r0) + __builtin_bit_cast(float, r1);
+  } else {
+    const bool upper = (lane & MASK) != 0;
+    return (upper ? hi : lo) + xlane_dpp<MASK>(upper ? lo : hi);
+  }
+}
+
+// v + the partner's v; both partners compute the same sum.
+template <int MASK>
+__device__ __forceinline__ float xlane_sum(float v) {
+  if constexpr (MASK >= 16) {
+    return xlane_keep_sum<MASK>(v, v, 0);
+  } else {
+    return v + xlane_dpp<MASK>(v);
+  }
+}
+
+// The value lane l ^ 32 holds.
+__device__ __forceinline__ float xlane_partner32(float v, int lane) {
+  const unsigned a = __builtin_bit_cast(unsigned, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(a, a, false, false);
+  const unsigned r0 = r[0], r1 = r[1];  // copied out first, as in xlane_keep_sum
+  return __builtin_bit_cast(float, lane < 32 ? r1 : r0);
+}
+
+// Sum over the wave's 64 lanes, identical in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
+  v = xlane_sum<32>(v);
+  v = xlane_sum<16>(v);
+  v = xlane_sum<8>(v);
+  v = xlane_sum<4>(v);
+  v = xlane_sum<2>(v);
+  return xlane_sum<1>(v);
 }
 
 // Transposing butterfly: V (a power of two <= 64) per-lane partial sums become
 // V wave-wide sums using V-1 exchanges instead of 6*V. Afterwards v[0] of lane
 // `l` holds the full sum of value index butterfly_index<V>(l).
-// One exchange step: COUNT live values, partner lane = lane ^ MASK. The lower
-// lane keeps the lower half of the values, the upper lane the upper half; each
-// adds the partner's copy of the half it keeps.
+// One exchange step: COUNT live values, partner = the lane across bit MASK
+// (xlane_keep_sum). The lane with the bit clear keeps the lower half of the
+// values, its partner the upper half; each adds the partner's copy of the half
+// it keeps.
 template <int V, int COUNT, int MASK>
 struct Butterfly {
   static __device__ __forceinline__ void run(float (&v)[V], int lane) {
     constexpr int HALF = COUNT / 2;
-    const bool upper = (lane & MASK) != 0;
 #pragma unroll
-    for (int i = 0; i < HALF; ++i) {
-      const float send = upper ? v[i] : v[i + HALF];
-      const float keep = upper ? v[i + HALF] : v[i];
-      v[i] = keep + __shfl_xor(send, MASK, kWave);
-    }
+    for (int i = 0; i < HALF; ++i) v[i] = xlane_keep_sum<MASK>(v[i], v[i + HALF], lane);
     Butterfly<V, HALF, MASK / 2>::run(v, lane);
   }
 };
-// One value left: plain xor-reduction over the remaining lane bits.
+// One value left: plain reduction over the remaining lane bits.
 template <int V, int MASK>
 struct Butterfly<V, 1, MASK> {
   static __device__ __forceinline__ void run(float (&v)[V], int lane) {
-    v[0] += __shfl_xor(v[0], MASK, kWave);
+    v[0] = xlane_sum<MASK>(v[0]);
     Butterfly<V, 1, MASK / 2>::run(v, lane);
   }
 };

@@ -364,7 +364,7 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
     for (int i = 0; i < 4; ++i) {
       const int64_t n = tr.row(nb + i);
       v[i] = m < M ? round_as<T>(epilogue(e, sc(s[i], n), m, n)) : 0.f;
-      pv[i] = __shfl_xor(v[i], 32, kWave);
+      pv[i] = xlane_partner32(v[i], lane);
     }
     if (m < M) {
       const bool first = nb < 8;
