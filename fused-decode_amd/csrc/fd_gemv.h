@@ -226,6 +226,8 @@ struct StepPlan {
   __device__ __forceinline__ int tile(int s) const { return (int)blockIdx.x + s / steps * (int)gridDim.x; }
   __device__ __forceinline__ int k(int s) const { return kbase + s % steps * step; }
   __device__ __forceinline__ bool last(int s) const { return s % steps == steps - 1; }
+  // Parity of step s's tile among this workgroup's tiles.
+  __device__ __forceinline__ int half(int s) const { return (s / steps) & 1; }
 };
 
 // Streams the plan's steps through two register buffers: the loads of step s+1
@@ -457,9 +459,13 @@ inline int device_cus() {
 }
 
 // Dynamic LDS of a fused kernel: the staged activations and the reduction scratch.
+// LDS of the persistent fused kernels: the staged rows, then two halves of
+// V * kMaxWaves partial sums (consecutive tiles alternate), which the norm
+// prologue uses as scratch before the first tile.
 inline size_t fused_lds(int M, int H, size_t elem, int V) {
+  const int part = 2 * V * kMaxWaves;
   return (size_t)M * xs_stride(H) * elem +
-         sizeof(float) * (size_t)(V * kMaxWaves > kNormScratch ? V * kMaxWaves : kNormScratch);
+         sizeof(float) * (size_t)(part > kNormScratch ? part : kNormScratch);
 }
 
 // Workgroups of the fused kernel: each stages the normalised activations in LDS

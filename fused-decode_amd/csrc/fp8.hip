@@ -235,8 +235,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
       su[r] = gu_scale[I + j];
     }
     butterfly_sum<V>(acc, lane);
-    __syncthreads();  // previous tile's readers of `part` are done
-    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    // Consecutive tiles alternate halves of `part`, so one barrier suffices: the
+    // half written here was last read two tiles ago, before the previous barrier.
+    float* pt = part + p.half(s) * (V * kMaxWaves);
+    if (butterfly_writer<V>(lane)) pt[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
     for (int t = threadIdx.x; t < R * M; t += block_threads()) {
       const int r = t / M, m = t % M;
@@ -244,8 +246,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
       if (j < I) {
         float gs = 0.f, us = 0.f;
         for (int i = 0; i < nw; ++i) {
-          gs += part[i * V + t];
-          us += part[i * V + R * M + t];
+          gs += pt[i * V + t];
+          us += pt[i * V + R * M + t];
         }
         float gsc = sg[0], usc = su[0];
 #pragma unroll
@@ -449,10 +451,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
     }
     if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
-    __syncthreads();  // previous tile's readers of `part` are done
-    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    // Consecutive tiles alternate halves of `part`, so one barrier suffices: the
+    // half written here was last read two tiles ago, before the previous barrier.
+    float* pt = part + p.half(s) * (V * kMaxWaves);
+    if (butterfly_writer<V>(lane)) pt[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    qkv_tile_out<T, M, R>(y, part, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, RowScale{wscale}, N);
+    qkv_tile_out<T, M, R>(y, pt, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, RowScale{wscale}, N);
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
   };

@@ -388,8 +388,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
     }
     if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
-    __syncthreads();  // previous tile's readers of `part` are done
-    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    // Consecutive tiles alternate halves of `part`, so one barrier suffices: the
+    // half written here was last read two tiles ago, before the previous barrier.
+    float* pt = part + p.half(s) * (V * kMaxWaves);
+    if (butterfly_writer<V>(lane)) pt[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
     const int64_t j0 = (int64_t)p.tile(s) * R;
     for (int t = threadIdx.x; t < R * M; t += block_threads()) {
@@ -398,8 +400,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_simt_kernel(
       if (j < I) {
         float gs = 0.f, us = 0.f;
         for (int i = 0; i < nw; ++i) {
-          gs += part[i * V + t];
-          us += part[i * V + R * M + t];
+          gs += pt[i * V + t];
+          us += pt[i * V + R * M + t];
         }
         mid[m * (int64_t)I + j] = swiglu_out<T>(gs, us);
       }
@@ -473,10 +475,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
     }
     if (!p.last(s)) return;
     butterfly_sum<V>(acc, lane);
-    __syncthreads();  // previous tile's readers of `part` are done
-    if (butterfly_writer<V>(lane)) part[wave * V + butterfly_index<V>(lane)] = acc[0];
+    // Consecutive tiles alternate halves of `part`, so one barrier suffices: the
+    // half written here was last read two tiles ago, before the previous barrier.
+    float* pt = part + p.half(s) * (V * kMaxWaves);
+    if (butterfly_writer<V>(lane)) pt[wave * V + butterfly_index<V>(lane)] = acc[0];
     __syncthreads();
-    qkv_tile_out<T, M, R>(y, part, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, NoScale{}, N);
+    qkv_tile_out<T, M, R>(y, pt, V, nw, TileRows<R>(rp, p.tile(s)), e, rp, NoScale{}, N);
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
   };
