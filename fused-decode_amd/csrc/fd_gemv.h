@@ -337,15 +337,13 @@ __device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, floa
 }
 
 // Per-row factor applied to a GEMV sum before the epilogue: none for fp16/bf16
-// weights, 256 * scale[n] for E4M3 codes decoded as value * 2^-8.
+// weights, the channel scale scale[n] for E4M3 codes.
 struct NoScale {
   __device__ __forceinline__ float operator()(float s, int64_t) const { return s; }
 };
 struct RowScale {
   const float* scale;
-  __device__ __forceinline__ float operator()(float s, int64_t n) const {
-    return s * 256.f * scale[n];
-  }
+  __device__ __forceinline__ float operator()(float s, int64_t n) const { return s * scale[n]; }
 };
 
 // Output of one 16-row MFMA tile, from the 64 lanes of one wave holding the

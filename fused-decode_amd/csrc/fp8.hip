@@ -7,19 +7,16 @@
 // activations stay fp16/bf16 and the arithmetic float32: weights are decoded
 // exactly, never the activations quantised.
 //
-// Decode: an E4M3 code s.eeee.mmm placed as s.0eeee.mmm0000000 is an fp16 whose
-// value is exactly 2^-8 times the E4M3 value (the exponent bias differs by 8;
-// E4M3 subnormals land on fp16 subnormals). One v_perm spreads two codes to the
-// high bytes of two 16-bit halves and two masked ops finish the pair, so four
-// codes cost five integer ops; the 2^8 goes into the channel scale. fp16
-// activations then use v_dot2 (two products per op into float32); for bf16 ones
-// the pair is re-packed as bf16 (exactly) for v_dot2 bf16.
+// Decode: gfx950's v_cvt_scalef32_pk_f16_fp8 / _bf16_fp8 (scale 1) turn two
+// codes into a pair of the activation type; every E4M3 value (NaN included) is
+// exact in fp16 and in bf16, so four codes cost two conversions and the
+// products are those of the exact weights. v_dot2 then takes two products per
+// op into float32.
 //
 // Layout per SIMT step (M < 5): a lane streams 16 consecutive codes (16 bytes) of
 // each of its workgroup's R rows, so a wave covers 1024 K elements per step.
 // From 5 rows the products run on MFMA: codes are decoded into the LDS tile of
 // the relayout GEMV (gemv.hip) and multiplied there.
-#include <type_traits>
 
 #include "fd_gemv.h"
 #include "fd_internal.h"
@@ -28,57 +25,42 @@ namespace fd {
 
 constexpr int kChunk8 = 1024;  // K elements one wave covers per fp8 step
 
-// Four E4M3 codes (byte 0 first) -> two fp16 pairs of value * 2^-8.
-__device__ __forceinline__ void fp8x4_to_h2(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  // bytes [0, c0, 0, c1] and [0, c2, 0, c3]: each code in the high byte of a half
-  const uint32_t a = __builtin_amdgcn_perm(0u, w, 0x010c000cu);
-  const uint32_t b = __builtin_amdgcn_perm(0u, w, 0x030c020cu);
-  lo = (a & 0x80008000u) | ((a >> 1) & 0x3f803f80u);
-  hi = (b & 0x80008000u) | ((b >> 1) & 0x3f803f80u);
+// Four E4M3 codes (byte 0 first) -> two pairs of their exact values in T.
+template <typename T>
+__device__ __forceinline__ void fp8x4_to_pairs(uint32_t w, uint32_t& lo, uint32_t& hi);
+template <>
+__device__ __forceinline__ void fp8x4_to_pairs<f16>(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+}
+template <>
+__device__ __forceinline__ void fp8x4_to_pairs<bf16>(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
 }
 
-// acc += sum over 16 elements of (e4m3 weight * 2^-8) * x, x given as two
-// 8-element vectors (elements 0-7, 8-15).
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc, f16) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), acc, false);
+}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float acc, bf16) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b),
+                                         acc, false);
+}
+
+// acc += sum over 16 elements of e4m3(weight) * x, x given as two 8-element
+// vectors (elements 0-7, 8-15).
 template <typename T>
 __device__ __forceinline__ float dot_fp8x16(const u32x4& w, const typename Vec8<T>::type& xa,
-                                            const typename Vec8<T>::type& xb, float acc);
-
-template <>
-__device__ __forceinline__ float dot_fp8x16<f16>(const u32x4& w, const f16x8& xa, const f16x8& xb,
-                                                 float acc) {
+                                            const typename Vec8<T>::type& xb, float acc) {
   const u32x4 xa2 = __builtin_bit_cast(u32x4, xa), xb2 = __builtin_bit_cast(u32x4, xb);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint32_t lo, hi;
-    fp8x4_to_h2(w[i], lo, hi);
+    fp8x4_to_pairs<T>(w[i], lo, hi);
     const uint32_t x0 = i < 2 ? xa2[2 * i] : xb2[2 * i - 4];
     const uint32_t x1 = i < 2 ? xa2[2 * i + 1] : xb2[2 * i - 3];
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, lo), __builtin_bit_cast(f16x2, x0), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, hi), __builtin_bit_cast(f16x2, x1), acc, false);
-  }
-  return acc;
-}
-
-// bf16 activations: each fp16 pair is widened to float32 (exact) and the upper
-// halves packed as a bf16 pair, which is exact too (at most 4 significant bits),
-// so the products run as v_dot2 bf16 with the activations used as loaded.
-template <>
-__device__ __forceinline__ float dot_fp8x16<bf16>(const u32x4& w, const bf16x8& xa,
-                                                  const bf16x8& xb, float acc) {
-  const u32x4 xa2 = __builtin_bit_cast(u32x4, xa), xb2 = __builtin_bit_cast(u32x4, xb);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    uint32_t lo, hi;
-    fp8x4_to_h2(w[i], lo, hi);
-    const f16x2 l = __builtin_bit_cast(f16x2, lo), h = __builtin_bit_cast(f16x2, hi);
-    const uint32_t p0 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)l[1]),
-                                              __builtin_bit_cast(uint32_t, (float)l[0]), 0x07060302u);
-    const uint32_t p1 = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)h[1]),
-                                              __builtin_bit_cast(uint32_t, (float)h[0]), 0x07060302u);
-    const uint32_t x0 = i < 2 ? xa2[2 * i] : xb2[2 * i - 4];
-    const uint32_t x1 = i < 2 ? xa2[2 * i + 1] : xb2[2 * i - 3];
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p0), __builtin_bit_cast(bf16x2, x0), acc, false);
-    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, p1), __builtin_bit_cast(bf16x2, x1), acc, false);
+    acc = dot2(lo, x0, acc, T{});
+    acc = dot2(hi, x1, acc, T{});
   }
   return acc;
 }
@@ -147,7 +129,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
     if (n < N) {
       float s = 0.f;
       for (int i = 0; i < nw; ++i) s += part[i * V + t];
-      y[m * sym + n * syn] = from_f32<T>(epilogue(e, s * 256.f * wscale[n], m, n));
+      y[m * sym + n * syn] = from_f32<T>(epilogue(e, s * wscale[n], m, n));
     }
   }
 }
@@ -253,7 +235,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
 #pragma unroll
         for (int q = 1; q < R; ++q)
           if (r == q) gsc = sg[q], usc = su[q];
-        mid[m * (int64_t)I + j] = swiglu_out<T>(gs * 256.f * gsc, us * 256.f * usc);
+        mid[m * (int64_t)I + j] = swiglu_out<T>(gs * gsc, us * usc);
       }
     }
 #pragma unroll
@@ -265,24 +247,15 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
 // MFMA form of the fp8 GEMV for M >= kFp8MfmaMinM (M padded to 16): the relayout
 // GEMV of gemv.hip with a decode step. A lane loads 16 codes (one 16-byte load)
 // of row lane/8 (+8 for the second load) at K chunk lane%8 of a 128-wide unit,
-// decodes them to two 8-element fp16 chunks (value * 2^-8) and stores those to
-// the wave's XOR-swizzled LDS tile exactly where the fp16 kernel stores a loaded
-// chunk; the A reads, B (x) loads and MFMAs are the fp16 kernel's. The 2^8 and
-// the channel scale are applied to the sums. bf16 activations store the decoded
-// weights as bf16 (exact) and run the bf16 MFMA.
+// decodes them to two 8-element chunks of the activation type (exact values)
+// and stores those to the wave's XOR-swizzled LDS tile exactly where the fp16
+// kernel stores a loaded chunk; the A reads, B (x) loads and MFMAs are the fp16
+// kernel's, and the channel scale is applied to the sums.
 template <typename T>
 __device__ __forceinline__ void fp8x16_to_tile(const u32x4& w, u32x4& c0, u32x4& c1) {
   uint32_t h[8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fp8x4_to_h2(w[i], h[2 * i], h[2 * i + 1]);
-  if constexpr (std::is_same<T, bf16>::value) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const f16x2 p = __builtin_bit_cast(f16x2, h[i]);
-      h[i] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, (float)p[1]),
-                                   __builtin_bit_cast(uint32_t, (float)p[0]), 0x07060302u);
-    }
-  }
+  for (int i = 0; i < 4; ++i) fp8x4_to_pairs<T>(w[i], h[2 * i], h[2 * i + 1]);
   c0 = u32x4{h[0], h[1], h[2], h[3]};
   c1 = u32x4{h[4], h[5], h[6], h[7]};
 }
@@ -525,7 +498,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
         const int64_t jj = j0 + nb + i;
         if (jj < I)
           mid[m * (int64_t)I + jj] =
-              swiglu_out<T>(sg[i] * 256.f * gu_scale[jj], su[i] * 256.f * gu_scale[I + jj]);
+              swiglu_out<T>(sg[i] * gu_scale[jj], su[i] * gu_scale[I + jj]);
       }
     }
   }

@@ -169,6 +169,29 @@ def test_linear_fp8_k_below_one_unit(m, k):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 8])
+def test_linear_fp8_nan_codes_decode_as_nan(dtype, m):
+    """E4M3FN codes 0x7f and 0xff are NaN, as torch's float8_e4m3fn casts and the
+    oracle's decode have them: a row holding one gives NaN outputs and every
+    other row the oracle's values, on the SIMT (M = 1) and MFMA (M = 8) forms."""
+    import fused_decode as fd
+
+    n, k = 64, 512
+    x = rnd(m, k, seed=3, dtype=dtype)
+    _, s, qn, sn = quant(rnd(n, k, seed=4, scale=k ** -0.5))
+    qn = qn.copy()
+    qn[5, 17] = 0x7F
+    qn[40, 300] = 0xFF
+    q = torch.from_numpy(qn).view(torch.float8_e4m3fn).to(DEV)
+    y = fd.linear_decode_fp8(x.to(DEV), q, s).float().cpu()
+    ref = O.linear_fp8(npf(x), qn, sn, dtype=tag(dtype))
+    assert np.isnan(ref[:, [5, 40]]).all()
+    assert torch.isnan(y[:, [5, 40]]).all()
+    keep = [j for j in range(n) if j not in (5, 40)]
+    torch.testing.assert_close(y[:, keep], torch.from_numpy(ref)[:, keep], **tol(dtype))
+
+
 def test_linear_fp8_k0_is_the_epilogue():
     """K = 0 through the C entry point: y = round(scale-free bias + row_add), with
     x null and no code read, for the SIMT (M = 1) and MFMA (M = 6) forms."""
