@@ -507,11 +507,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
 namespace {
 
 template <int M> struct Fp8Rows { static constexpr int R = M <= 8 ? 4 : 2; };
-// Two gate + two up rows per tile with four workgroups per CU (measured at
-// Llama-3-8B widths: M=1 23.3 us against 24.1 for four rows at two per CU, M=3
-// 30.5 against 31.5).
-template <int M> struct Fp8MlpRows { static constexpr int R = 2; };
-template <int M> struct Fp8MlpPerCu { static constexpr int P = M <= 4 ? 4 : 2; };
+// Four gate + four up rows per tile with two workgroups per CU up to 4 rows
+// (Llama-3-8B widths: M=1 20.2 us against 20.8 for two rows at four per CU,
+// M=2 20.9 against 22.0); above, two rows, which keeps 2*R*M sums per lane
+// within the butterfly's 64.
+template <int M> struct Fp8MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
+template <int M> struct Fp8MlpPerCu { static constexpr int P = 2; };
 
 // Fused QKV: R rows per tile (R/2 rotate-half pairs in a rotated tile); eight
 // up to 2 rows (Llama-3-8B widths, M=1: 9.1 against 9.7 us for four).
