@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void gemv_gen_kernel(T* y, const T* x, const T
     }
   }
   __syncthreads();
-  if (threadIdx.x < M) {
+  if ((int)threadIdx.x < M) {
     const int m = threadIdx.x;
     const float s = red[0][m] + red[1][m] + red[2][m] + red[3][m];
     y[m * sym + n * syn] = from_f32<T>(epilogue(e, s, m, n));
