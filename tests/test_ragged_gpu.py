@@ -8,7 +8,6 @@ tests (the reference's, tests/test_ops.py:27-35)."""
 
 from __future__ import annotations
 
-import numpy as np
 import pytest
 import torch
 
