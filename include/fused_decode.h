@@ -207,8 +207,9 @@ int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_
  *   y[m,n] = round(w_scale[n] * sum_k e4m3(w8[n,k]) * x[m,k] + bias[n] + row_add[m,n])
  * M <= 16; x [M,K] activations with unit K stride; K % 16 == 0 and 16-byte
  * aligned rows (else FD_EUNSUPPORTED). bias/row_add as in fd_linear. The
- * weights are decoded exactly and the arithmetic is float32: the activations
- * are never quantised.
+ * weights are decoded exactly (codes 0x7f and 0xff are NaN, as torch's
+ * float8_e4m3fn has them) and the arithmetic is float32: the activations are
+ * never quantised.
  * No reference counterpart (its weights are fp16/bf16 only): a low-precision
  * weight format, halving the bytes the decode GEMV streams.
  */
