@@ -401,6 +401,43 @@ def test_post_attn_mlp_every_m_and_fp32_norm_weight(dtype):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+def test_post_attn_mlp_strided_batched_and_composed_forms(dtype):
+    """The block on inputs the fused launch does not take as they are, each
+    against the oracle: a column-strided hidden (copied into place), a 3-D hidden
+    [2, 3, H] (flattened rows), row-strided weight views (the composed path of
+    the reference's own operators), and M = 20 above the row cutoff (the
+    F.linear fallback inside linear_decode)."""
+    h, i = 256, 384
+    g = torch.Generator().manual_seed(91)
+    w_gu = randn(2 * i, h, dtype=dtype, gen=g, scale=h ** -0.5)
+    w_down = randn(h, i, dtype=dtype, gen=g, scale=i ** -0.5)
+    norm_w = randn(h, dtype=dtype, gen=g, scale=0.1, mean=1.0)
+    wgd, wdd, nwd = w_gu.to(DEV), w_down.to(DEV), norm_w.to(DEV)
+
+    def ref(x):
+        return O.post_attn_mlp(npf(x).reshape(-1, h), npf(norm_w), npf(w_gu), npf(w_down), 1e-5,
+                               tag(dtype)).reshape(tuple(x.shape))
+
+    wide = randn(3, 2 * h, dtype=dtype, gen=g).to(DEV)
+    strided = wide[:, ::2]  # column stride 2
+    assert not strided.is_contiguous()
+    batched = randn(2, 3, h, dtype=dtype, gen=g).to(DEV)
+    many = randn(20, h, dtype=dtype, gen=g).to(DEV)
+    # row-strided views of the same weights: rows 0, 2, 4, ... of a padded copy
+    pad_gu = torch.zeros(4 * i, h, dtype=dtype, device=DEV)
+    pad_gu[::2] = wgd
+    pad_d = torch.zeros(2 * h, i, dtype=dtype, device=DEV)
+    pad_d[::2] = wdd
+    for kind in ("dot", "simt"):
+        for x in (strided, batched, many):
+            y = fd().post_attn_mlp(x, nwd, wgd, wdd, 1e-5, kind=kind)
+            assert y.shape == x.shape
+            check(y, ref(x), dtype, "linear")
+        y = fd().post_attn_mlp(batched, nwd, pad_gu[::2], pad_d[::2], 1e-5, kind=kind)
+        check(y, ref(batched), dtype, "linear")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m", [1, 8])
 def test_post_attn_mlp_llama3_8b(dtype, m):
     """Benchmark configuration: H=4096, I=14336, residual fused, both kinds."""
