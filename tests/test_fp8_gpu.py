@@ -296,6 +296,19 @@ def test_pre_attn_qkv_fp8_matches_oracle(dtype, m):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_pre_attn_qkv_fp8_several_tiles_per_workgroup(m):
+    """128 q + 8 kv heads of 128 (N = 18432): more tiles than the 8 resident
+    workgroups per CU take, so each workgroup streams 2 (M = 1, 8-row tiles) or
+    3 (M = 3, 4-row tiles) tiles and its epilogues alternate the two halves of
+    the partial-sum buffer."""
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 256, 128, 8, 128, torch.float16, seed=60 + m,
+                                                          bias=True)
+    y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_pre_attn_qkv_fp8_shared_angles_and_rope_cols_edges(m):
     """One cos/sin row for every token in each angle dtype; rope_cols 0 (norm +

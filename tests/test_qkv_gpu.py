@@ -135,6 +135,19 @@ def test_pre_attn_qkv_above_row_limit_and_leading_dims():
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 3])
+def test_pre_attn_qkv_several_tiles_per_workgroup(dtype, m):
+    """128 q + 8 kv heads of 128 (N = 18432): more tiles than the 8 resident
+    workgroups per CU take, so each workgroup streams 2 (M = 1, 8-row tiles) or
+    3 (M = 3, 4-row tiles) tiles and its epilogues alternate the two halves of
+    the partial-sum buffer."""
+    hidden, nw, w, b, cos, sin, rc = case(m, 256, 128, 8, 128, dtype, seed=70 + m, bias=True)
+    y = run(hidden, nw, w, b, cos, sin, rc, "simt")
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(oracle(hidden, nw, w, b, cos, sin, rc, dtype)),
+                               **tol(dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m", [1, 8])
 def test_pre_attn_qkv_llama3_8b_matches_composed_ops(dtype, m):
     """Llama-3-8B widths (H=4096, 32 q + 8 kv heads of 128): the fused call against
