@@ -111,6 +111,22 @@ def test_post_attn_mlp_fp8_matches_oracle(dtype, m):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_post_attn_mlp_fp8_several_tiles_per_workgroup(m):
+    """I = 6144 with 4-row tiles: 1536 tiles over two workgroups per CU, so each
+    workgroup streams several tiles of the persistent fp8 gate/up."""
+    import fused_decode as fd
+
+    h, i = 256, 6144
+    hid = rnd(m, h, seed=60 + m)
+    nw = rnd(h, seed=61, scale=0.1, mean=1.0)
+    gq, gs, gqn, gsn = quant(rnd(2 * i, h, seed=62, scale=h ** -0.5))
+    dq, ds, dqn, dsn = quant(rnd(h, i, seed=63, scale=i ** -0.5))
+    y = fd.post_attn_mlp_fp8(hid.to(DEV), nw.to(DEV), gq, gs, dq, ds, 1e-5)
+    ref = O.post_attn_mlp_fp8(npf(hid), npf(nw), gqn, gsn, dqn, dsn, 1e-5, "f16")
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_post_attn_mlp_fp8_llama3_8b(m):
     """Llama-3-8B widths: the fused two-launch path against the composed fp8

@@ -400,6 +400,21 @@ def test_post_attn_mlp_every_m_and_fp32_norm_weight(dtype):
             check(y, ref, dtype, "linear")
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_post_attn_mlp_several_tiles_per_workgroup(m):
+    """I = 6144 with 4-row SIMT tiles: 1536 tiles over at most two 8-wave
+    workgroups per CU, so each workgroup streams several tiles (epilogues on
+    alternating halves of the partial-sum buffer)."""
+    h, i = 256, 6144
+    g = torch.Generator().manual_seed(92 + m)
+    w_gu = randn(2 * i, h, gen=g, scale=h ** -0.5)
+    w_down = randn(h, i, gen=g, scale=i ** -0.5)
+    norm_w = randn(h, gen=g, scale=0.1, mean=1.0)
+    x = randn(m, h, gen=g)
+    y = fd().post_attn_mlp(x.to(DEV), norm_w.to(DEV), w_gu.to(DEV), w_down.to(DEV), 1e-5, kind="simt")
+    check(y, O.post_attn_mlp(npf(x), npf(norm_w), npf(w_gu), npf(w_down), 1e-5, "f16"), torch.float16, "linear")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_post_attn_mlp_strided_batched_and_composed_forms(dtype):
     """The block on inputs the fused launch does not take as they are, each
