@@ -469,7 +469,8 @@ inline size_t fused_lds(int M, int H, size_t elem, int V) {
 // Workgroups of the fused kernel: each stages the normalised activations in LDS
 // once and then loops over weight tiles, so the grid is what can be resident at
 // once, at most `per_cu` per CU and fewer when the LDS stage is large; more would
-// restage x for nothing (measured at H=4096: two 8-wave workgroups per CU).
+// restage x for nothing (measured at H=4096: one 8-wave workgroup per CU for the
+// fp16 gate/up, two 4-wave ones for the fp8 gate/up).
 inline int fused_grid(int tiles, size_t lds, int per_cu) {
   const int fit = (int)(kMaxLds / (lds ? lds : 1));
   const int cap = device_cus() * (fit < 1 ? 1 : fit < per_cu ? fit : per_cu);

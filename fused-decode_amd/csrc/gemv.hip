@@ -643,15 +643,18 @@ int launch_mlp_simt(void* mid, const void* hidden, const void* nw, int nw_dtype,
                     int H, int I, float eps, hipStream_t st) {
   constexpr int R = MlpRows<M>::R;
   constexpr int V = pow2_ceil(2 * R * M);
-  // Eight waves (one 512-element K chunk per row each at H=4096) up to M=2;
-  // four above, where R*M sums per lane cost VGPRs (at M=3..4 the kernel holds
-  // three 4-wave workgroups per CU where two 8-wave ones would not fit).
+  // Up to 4 rows: eight waves (one 512-element K chunk per row each at
+  // H=4096) in one workgroup per CU (Llama-3-8B widths, M=1..4: 34.9 / 35.3 /
+  // 36.9 / 37.4 us against 35.7 / 36.1 for two 8-wave workgroups per CU at
+  // M=1..2 and 38.5 / 39.2 for two 4-wave ones at M=3..4). Above, where 2*R*M
+  // sums per lane cost VGPRs, four waves. Workgroups per CU keep about eight
+  // waves per CU resident.
   const int nwv0 = pick_waves((H + kChunk - 1) / kChunk);
-  const int nwv = M > kNormRegMaxM && nwv0 > 4 ? 4 : nwv0;
+  const int nwv = M > 4 && nwv0 > 4 ? 4 : nwv0;
   const size_t lds = fused_lds(M, H, sizeof(T), V);
   if (lds > kMaxLds) return set_error(FD_EUNSUPPORTED, "M*H too large for the LDS stage");
   const int tiles = (I + R - 1) / R;
-  const int grid = fused_grid(tiles, lds, 2);
+  const int grid = fused_grid(tiles, lds, kMaxWaves / nwv);
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds))
       return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
