@@ -12,6 +12,20 @@ constexpr int kMaxWaves = 8;      // waves per workgroup (512 threads)
 constexpr int kChunk = 512;       // K elements one wave covers per SIMT step
 constexpr int kUnit = 128;        // K elements of one MFMA unit (4 steps of 32)
 
+// Unit i of a wave's share of an MFMA workgroup's K sweep: the wave takes units
+// wave, wave + nw, ... of a sweep that starts at unit `off` and wraps, so every
+// unit is taken once. Workgroups are dealt to the eight XCDs in turn, and
+// blockIdx / 8 numbers a workgroup among those sharing one L2; starting each at
+// its own unit keeps them from reading the same activation lines in step
+// (N = 4096, K = 14336, M = 8: 20.7 against 21.7 us).
+__device__ __forceinline__ int sweep_offset(int units) {
+  return units > 0 ? (int)(blockIdx.x >> 3) % units : 0;
+}
+__device__ __forceinline__ int sweep_unit(int wave, int i, int nw, int off, int units) {
+  const int u = wave + i * nw + off;  // < 2 * units: wave + i * nw < units, off < units
+  return u - (u >= units ? units : 0);
+}
+
 constexpr int pow2_ceil(int v) {
   int p = 1;
   while (p < v) p <<= 1;

@@ -338,9 +338,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int units = (K + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
-  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xr, wave + i * nw, lchunk, g, K); };
+  const int off = sweep_offset(units);
+  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, K); };
   auto consume = [&](const UnitRegs8<T, 1>& q, int i) {
-    const int u = wave + i * nw;
+    const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4];
     stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, K, r, g, a);
 #pragma unroll
@@ -463,9 +464,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
-  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xr, wave + i * nw, lchunk, g, H); };
+  const int off = sweep_offset(units);
+  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, H); };
   auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
-    const int u = wave + i * nw;
+    const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
     stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
     stage_unit8<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
