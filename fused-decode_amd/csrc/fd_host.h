@@ -58,6 +58,24 @@ inline bool same_grid(const fd_rows& x, const fd_rows& o, const char* what) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// True when the byte ranges [a, a + na) and [b, b + nb) share a byte.
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return na > 0 && nb > 0 && pa < pb + (uintptr_t)nb && pb < pa + (uintptr_t)na;
+}
+
+// The MLP entry points write y and mid while hidden is still to be read (the
+// down projection adds hidden as its residual, and from M = 5 y first holds the
+// normalised rows): none of the three may share memory.
+inline int check_mlp_buffers(const void* y, const void* mid, const void* hidden, int64_t M,
+                             int64_t H, int64_t I, int elem_bytes) {
+  const int64_t nh = M * H * elem_bytes, ni = M * I * elem_bytes;
+  if (overlaps(y, nh, hidden, nh)) return set_error(FD_EINVAL, "y must not overlap hidden");
+  if (overlaps(mid, ni, hidden, nh) || overlaps(mid, ni, y, nh))
+    return set_error(FD_EINVAL, "mid must not overlap y or hidden");
+  return FD_OK;
+}
+
 // True when every row of `l` is a run of n contiguous elements whose start is
 // 16-byte aligned and n is a multiple of 8 (so 16-byte vectors tile the row).
 inline bool rows_vectorizable(const void* p, const fd_rows& l, int elem_bytes) {

@@ -708,6 +708,7 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
   if (M == 0) return FD_OK;
   if (!y || !mid || !hidden || !norm_w || !w_gate_up8 || !gate_up_scale || !w_down8 || !down_scale)
     return set_error(FD_EINVAL, "null pointer argument");
+  if (check_mlp_buffers(y, mid, hidden, M, H, I, 2) != FD_OK) return FD_EINVAL;
   if (H % 16 != 0 || I % 16 != 0) return set_error(FD_EUNSUPPORTED, "H and I must be multiples of 16");
   if (H > 0x7fffffffLL || 2 * I > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "too large");
   if (!aligned16(y) || !aligned16(mid) || !aligned16(hidden) || !aligned16(norm_w) ||

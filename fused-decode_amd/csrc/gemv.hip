@@ -928,6 +928,8 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
   if (rc != FD_OK || M == 0) return rc;
   if (!y || !w_down) return set_error(FD_EINVAL, "null pointer argument");
+  rc = check_mlp_buffers(y, mid, hidden, M, H, I, 2);
+  if (rc != FD_OK) return rc;
   if (!aligned16(y) || !aligned16(w_down))
     return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);

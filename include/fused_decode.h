@@ -152,8 +152,10 @@ int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias, int
  *   mid = round(silu(g) * u)                      (written to `mid`, [M,I])
  *   y   = round(mid @ w_down.T + hidden)
  * w_gate_up is [2I,H] (gate rows above up rows), w_down is [H,I], both contiguous.
- * `mid` is caller-owned scratch of M*I activation elements. Two launches (three for
- * kind FD_KIND_DOT at M >= 5, whose RMSNorm runs as its own row kernel into y).
+ * `mid` is caller-owned scratch of M*I activation elements. y, mid and hidden must
+ * not share memory (FD_EINVAL): hidden is read as the residual after y and mid are
+ * written. Two launches (three for kind FD_KIND_DOT at M >= 5, whose RMSNorm runs
+ * as its own row kernel into y).
  * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
  * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
  */
@@ -223,9 +225,12 @@ int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
  * fd_post_attn_mlp with FP8 weights: w_gate_up8 [2I,H] and w_down8 [H,I] E4M3
  * codes (contiguous) with per-row float32 scales gate_up_scale [2I] and
  * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
- * rounding points as fd_post_attn_mlp. Two launches (fused RMSNorm + gate/up +
- * SwiGLU, then down + residual); `mid` is caller scratch of M*I activations.
- * H % 16 == 0 and I % 16 == 0. No reference counterpart (see fd_linear_fp8).
+ * rounding points as fd_post_attn_mlp. Two launches up to M = 4 (fused RMSNorm +
+ * gate/up + SwiGLU, then down + residual), three from M = 5 (the RMSNorm runs
+ * first as a row kernel into y, then the MFMA gate/up and the down projection);
+ * `mid` is caller scratch of M*I activations. y, mid and hidden must not share
+ * memory (FD_EINVAL). H % 16 == 0 and I % 16 == 0. No reference counterpart (see
+ * fd_linear_fp8).
  */
 int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* norm_w,
                          int norm_w_dtype, const void* w_gate_up8, const float* gate_up_scale,

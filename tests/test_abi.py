@@ -160,8 +160,8 @@ def test_fp8_entry_points_reject(L):
     assert lin(x=FAKE + 2) == L.FD_EUNSUPPORTED       # misaligned activations
     assert lib.fd_linear_fp8(FAKE, FAKE, FAKE, None, None, 0, None, 0, 1, 32, 64, 64, 64, 0, 0, 0, 32, 1, 0,
                              None) == L.FD_EINVAL      # scale is required
-    mlp = lambda m, h, i: lib.fd_post_attn_mlp_fp8(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, FAKE, FAKE, m, h, i,  # noqa: E731
-                                                   1e-6, 0, None)
+    mlp = lambda m, h, i: lib.fd_post_attn_mlp_fp8(0x300000, 0x200000, 0x100000, FAKE, 0, FAKE, FAKE, FAKE,  # noqa: E731
+                                                   FAKE, m, h, i, 1e-6, 0, None)
     assert mlp(17, 64, 128) == L.FD_EINVAL
     assert mlp(2, 72, 128) == L.FD_EUNSUPPORTED
     assert mlp(0, 64, 128) == L.FD_OK
@@ -177,3 +177,26 @@ def test_fp8_entry_points_reject(L):
     assert qkv(rope_cols=48) == L.FD_EINVAL                # not a multiple of head_dim
     assert qkv(m=5) == L.FD_EINVAL                         # the MFMA form needs `normed`
     assert qkv(m=0) == L.FD_OK
+
+
+@nogpu
+def test_mlp_rejects_overlapping_buffers(L):
+    """y, mid and hidden of the MLP entry points must not share memory: from 5
+    rows y first holds the normalised rows while hidden is still to be added."""
+    lib = L.lib()
+    m, h, i = 8, 64, 128
+    hid = 0x100000
+    mid = 0x200000
+    y_ok = 0x300000
+
+    def mlp(y, mid_p, kind=0):
+        return lib.fd_post_attn_mlp(y, mid_p, hid, FAKE, 0, FAKE, FAKE, m, h, i, 1e-6, kind, 0, None)
+
+    def mlp8(y, mid_p):
+        return lib.fd_post_attn_mlp_fp8(y, mid_p, hid, FAKE, 0, FAKE, FAKE, FAKE, FAKE, m, h, i, 1e-6, 0, None)
+
+    for call in (mlp, mlp8):
+        assert call(hid, mid) == L.FD_EINVAL and b"hidden" in lib.fd_last_error()
+        assert call(hid + 2 * h, mid) == L.FD_EINVAL          # y starts inside hidden's rows
+        assert call(y_ok, hid + 16) == L.FD_EINVAL and b"mid" in lib.fd_last_error()
+        assert call(y_ok, y_ok) == L.FD_EINVAL

@@ -106,3 +106,100 @@ def test_custom_ops_capture_in_a_hip_graph(fdl):
         g.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(out, ref, rtol=0, atol=0)
+
+
+# ------------------------------------------------ custom ops against the oracle
+#
+# Tolerances follow the reference's tests/test_ops.py:27-38: GEMV-shaped outputs
+# fp16 rtol=atol=2e-2 (bf16 4e-2), pointwise fp16 rtol 1e-2 / atol 5e-3 (bf16 2e-2).
+
+
+def _tol(dtype, kind):
+    if kind == "linear":
+        return {"rtol": 2e-2, "atol": 2e-2} if dtype == torch.float16 else {"rtol": 4e-2, "atol": 4e-2}
+    return {"rtol": 1e-2, "atol": 5e-3} if dtype == torch.float16 else {"rtol": 2e-2, "atol": 2e-2}
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _close(actual, expected, dtype, kind):
+    torch.testing.assert_close(actual.float().cpu(), torch.from_numpy(expected), **_tol(dtype, kind))
+
+
+def _oracle_cases(dtype, m):
+    """(op name, args for torch.ops.fused_decode, oracle output(s), tolerance kind)."""
+    from oracle import decode_oracle as O
+
+    tg = "f16" if dtype == torch.float16 else "bf16"
+    h, i, d, heads, kv = 256, 384, 64, 2, 1
+    n = (heads + 2 * kv) * d
+    g = torch.Generator().manual_seed(70 + m)
+
+    def r(*shape, scale=1.0, mean=0.0, dt=dtype):
+        return (torch.randn(*shape, generator=g) * scale + mean).to(dt).to(DEV)
+
+    x, res, nw = r(m, h), r(m, h), r(h, scale=0.1, mean=1.0)
+    gate, up = r(m, i, scale=2.0), r(m, i, scale=2.0)
+    q = r(1, m, 4, d)
+    cos3, sin3 = r(m, 1, d, dt=torch.float32), r(m, 1, d, dt=torch.float32)
+    w, bias, row = r(n, h, scale=h ** -0.5), r(n, dt=torch.float32), r(m, n)
+    wgu, wd = r(2 * i, h, scale=h ** -0.5), r(h, i, scale=i ** -0.5)
+    ang = torch.arange(d // 2, dtype=torch.float64) * 0.21
+    cos = torch.cat([ang.cos(), ang.cos()]).float().view(1, d).to(DEV)
+    sin = torch.cat([ang.sin(), ang.sin()]).float().view(1, d).to(DEV)
+    rc = (heads + kv) * d
+    import fused_decode as fd
+
+    q8, s8 = fd.quantize_fp8(w)
+    g8, sg = fd.quantize_fp8(wgu)
+    d8, sdn = fd.quantize_fp8(wd)
+    c = lambda t: t.cpu().view(torch.uint8).numpy()  # noqa: E731
+    return [
+        ("rms_norm", (x, nw, 1e-5), O.rms_norm(_np(x), _np(nw), 1e-5, tg), "pointwise"),
+        ("add_rms_norm", (x, res, nw, 1e-5), O.add_rms_norm(_np(x), _np(res), _np(nw), 1e-5, tg), "pointwise"),
+        ("rope", (q, cos3, sin3), O.rope(_np(q), _np(cos3), _np(sin3), tg), "pointwise"),
+        ("swiglu", (gate, up), O.swiglu(_np(gate), _np(up), tg), "pointwise"),
+        ("linear_decode", (x, w, bias, row, "dot"),
+         O.linear(_np(x), _np(w), bias=_np(bias), row_add=_np(row), dtype=tg), "linear"),
+        ("linear_decode", (x, w, bias, row, "simt"),
+         O.linear(_np(x), _np(w), bias=_np(bias), row_add=_np(row), dtype=tg), "linear"),
+        ("post_attn_mlp", (x, nw, wgu, wd, 1e-5, None),
+         O.post_attn_mlp(_np(x), _np(nw), _np(wgu), _np(wd), 1e-5, tg), "linear"),
+        ("pre_attn_qkv", (x, nw, w, cos, sin, 1e-5, rc, bias, None),
+         O.pre_attn_qkv(_np(x), _np(nw), _np(w), _np(cos), _np(sin), 1e-5, rc, bias=_np(bias), dtype=tg),
+         "linear"),
+        ("linear_decode_fp8", (x, q8, s8, bias, row),
+         O.linear_fp8(_np(x), c(q8), _np(s8), bias=_np(bias), row_add=_np(row), dtype=tg), "linear"),
+        ("post_attn_mlp_fp8", (x, nw, g8, sg, d8, sdn, 1e-5),
+         O.post_attn_mlp_fp8(_np(x), _np(nw), c(g8), _np(sg), c(d8), _np(sdn), 1e-5, tg), "linear"),
+        ("pre_attn_qkv_fp8", (x, nw, q8, s8, cos, sin, 1e-5, rc, bias),
+         O.pre_attn_qkv_fp8(_np(x), _np(nw), c(q8), _np(s8), _np(cos), _np(sin), 1e-5, rc,
+                            bias=_np(bias), dtype=tg), "linear"),
+    ]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m", [1, 6])
+def test_custom_ops_match_the_oracle(fdl, dtype, m):
+    """Every torch.ops.fused_decode op, called eagerly and (at 6 rows) through a
+    torch.compile(fullgraph) graph, against the oracle on the same inputs."""
+    seen = set()
+    for name, args, expected, kind in _oracle_cases(dtype, m):
+        op = getattr(fdl, name)
+        outs = [op(*args)]
+        if m == 6:
+            torch.compiler.reset()  # one wrapper code object serves every op: start each afresh
+            compiled = torch.compile(lambda *a, op=op: op(*a), backend="aot_eager", fullgraph=True)
+            outs.append(compiled(*args))
+        for got in outs:
+            if isinstance(expected, tuple):  # add_rms_norm: (out, residual_out)
+                for a, e in zip(got, expected):
+                    _close(a, e, dtype, kind)
+            else:
+                _close(got, expected, dtype, kind)
+        seen.add(name)
+    from fused_decode.library import OPS
+
+    assert seen == set(OPS)

@@ -543,11 +543,14 @@ def _oracle_decode_step(ds, tagd):
     return x, qkv
 
 
-@pytest.mark.parametrize("m", [1, 3])
-def test_decode_step_small_matches_oracle_and_graph(m):
+@pytest.mark.parametrize("fused", [True, False], ids=["fused", "composed"])
+@pytest.mark.parametrize("m", [1, 3, 5, 8, 16])
+def test_decode_step_small_matches_oracle_and_graph(m, fused):
+    """Both forms of the layer, below and above the MFMA switch at 5 rows (where
+    the RMSNorms run as row kernels), against the oracle, then graph replays."""
     from fused_decode.decode_step import DecodeStep
 
-    ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=5)
+    ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=5, fused=fused)
     eager = ds.step().clone()
     ref, ref_qkv = _oracle_decode_step(ds, "f16")
     check(eager, ref, torch.float16, "linear")
@@ -558,18 +561,26 @@ def test_decode_step_small_matches_oracle_and_graph(m):
         out = ds.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, rtol=0, atol=0)
+        _ = (ds.x_in.float() * 2).sum().item()  # unrelated eager work between replays
 
 
-def test_decode_step_llama3_8b_two_layers_finite():
+@pytest.mark.parametrize("m", [1, 8])
+def test_decode_step_llama3_8b_matches_oracle(m):
+    """Two layers at full Llama-3-8B widths (H=4096, 32 q + 8 kv heads of 128,
+    I=14336), the shapes the 32-layer benchmark step runs, against the oracle:
+    the step's output and the last layer's q/k/v, then a graph replay."""
     from fused_decode.decode_step import DecodeStep
 
-    ds = DecodeStep(m=1, layers=2, seed=6)
-    a = ds.step().clone()
-    b = ds.replay().clone()
-    torch.cuda.synchronize()
-    assert torch.isfinite(a.float()).all()
-    torch.testing.assert_close(a, b, rtol=0, atol=0)
+    print(f"[decode step llama3-8b m={m}]", flush=True)
+    ds = DecodeStep(m=m, layers=2, seed=6)
     assert ds.weight_bytes == 2 * 436_207_616 + 2 * 2 * 4096 * 2
+    eager = ds.step().clone()
+    qkv = ds.qkv.clone()
+    ref, ref_qkv = _oracle_decode_step(ds, "f16")
+    check(eager, ref, torch.float16, "linear")
+    check(qkv, ref_qkv, torch.float16, "linear")
+    ds.out.zero_()
+    torch.testing.assert_close(ds.replay(), eager, rtol=0, atol=0)
 
 
 @pytest.mark.parametrize("m,kind", [(1, "simt"), (3, "dot"), (8, "dot"), (16, "dot"), (8, "simt")])

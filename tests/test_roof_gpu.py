@@ -1,0 +1,89 @@
+"""The bandwidth roofs every "% of copy roof" figure divides by: fd_copy must
+copy exactly the bytes it is given (vector path for 16-byte aligned sizes and
+pointers, byte path otherwise) and touch nothing past them; fd_triad must
+compute c = a + b * scale in float32 with one rounding to the element type.
+The launchers of the reference's kernels.py:833-858 (launch_copy,
+launch_triad) are exercised through the same calls."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def L():
+    import fused_decode._lib as lib
+
+    lib.lib()  # raises if the HIP library is missing
+    return lib
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("nbytes", [1, 15, 16, 17, 4096, 4096 + 48, (1 << 20) + 3, 64 << 20])
+@pytest.mark.parametrize("src_off", [0, 1])
+def test_copy_is_exact_and_stays_in_bounds(L, nbytes, src_off):
+    g = torch.Generator(device=DEV).manual_seed(nbytes)
+    src = torch.randint(0, 256, (nbytes + 64,), generator=g, device=DEV, dtype=torch.uint8)
+    dst = torch.full((nbytes + 64,), 0xA5, device=DEV, dtype=torch.uint8)
+    s = src[src_off: src_off + nbytes]
+    L.check("fd_copy", L.lib().fd_copy(dst.data_ptr(), s.data_ptr(), nbytes, _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], s)
+    assert bool((dst[nbytes:] == 0xA5).all())  # nothing written past the copy
+
+
+def test_launch_copy_wrapper(L):
+    from fused_decode.kernels import launch_copy
+
+    src = torch.randn(3, 1000, device=DEV, dtype=torch.float16)
+    dst = torch.empty_like(src)
+    launch_copy(dst, src)
+    torch.cuda.synchronize()
+    assert torch.equal(dst, src)
+    with pytest.raises(ValueError, match="byte"):
+        launch_copy(dst[:2], src)
+
+
+def _triad_expected(a: torch.Tensor, b: torch.Tensor, scale: float) -> torch.Tensor:
+    """a + b*scale from the stored values, in float64, rounded once to the dtype."""
+    return (a.double().cpu() + b.double().cpu() * scale).to(a.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("n", [1, 7, 8, 1000, (1 << 20) + 5])
+@pytest.mark.parametrize("off", [0, 1])
+def test_triad_matches_a_plus_b_scale(L, dtype, n, off):
+    g = torch.Generator(device=DEV).manual_seed(n + off)
+    a = torch.randn(n + off, generator=g, device=DEV, dtype=torch.float32).to(dtype)[off:]
+    b = torch.randn(n + off, generator=g, device=DEV, dtype=torch.float32).to(dtype)[off:]
+    c = torch.full((n + off + 8,), 7.0, device=DEV, dtype=dtype)
+    cv = c[off: off + n]
+    code = L.DTYPE_CODE[dtype]
+    L.check("fd_triad", L.lib().fd_triad(cv.data_ptr(), a.data_ptr(), b.data_ptr(), 1.25, n, code,
+                                         _stream()))
+    torch.cuda.synchronize()
+    # float32 math (the product may be fused into an FMA), then one rounding:
+    # within one unit in the last place of the stored type
+    rtol = {torch.float16: 1e-3, torch.bfloat16: 8e-3, torch.float32: 2.4e-7}[dtype]
+    torch.testing.assert_close(cv.cpu(), _triad_expected(a, b, 1.25), rtol=rtol, atol=1e-6)
+    assert bool((c[off + n:] == 7.0).all())
+    if off:
+        assert float(c[0]) == 7.0
+
+
+def test_launch_triad_wrapper(L):
+    from fused_decode.kernels import launch_triad
+
+    a = torch.randn(4096, device=DEV, dtype=torch.bfloat16)
+    b = torch.randn(4096, device=DEV, dtype=torch.bfloat16)
+    c = torch.empty_like(a)
+    launch_triad(a, b, c, -0.5)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(c.cpu(), _triad_expected(a, b, -0.5), rtol=8e-3, atol=1e-6)
