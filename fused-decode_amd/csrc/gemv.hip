@@ -36,6 +36,8 @@
 // Fused QKV (qkv_simt_kernel, and the MFMA kernel with ROPE): the same prologue
 // and weight stream with tiles placed so that both halves of every rotate-half
 // pair land in one workgroup, which applies RoPE in the epilogue.
+#include <mutex>
+
 #include "fd_gemv.h"
 #include "fd_internal.h"
 
@@ -949,6 +951,74 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   rc = linear_dispatch(y, mid, w_down, e, M, H, I, I, 1, I, 1, H, 1, kind, act_dtype, st);
   if (rc != FD_OK) return rc;
   return check_launch();
+}
+
+// ---------------------------------------------------------------------------
+// fd_post_attn_mlp_noalloc: the same MLP with `mid` in library-owned device
+// memory, for callers that cannot allocate (code under HIP graph capture, tight
+// serving loops, harnesses that forbid hipMalloc).
+
+namespace fd {
+namespace {
+
+// The [M, I] SwiGLU rows of one call: M * I * 2 bytes, 458,752 at Llama-3-8B
+// widths and M = 16. Each GPU holds one copy for the life of the process.
+constexpr int64_t kScratchBytes = int64_t(1) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`. Host code must never pass the
+// array's own name to a kernel or a copy (it names a host-side stand-in), so
+// the address is looked up once per device, with that device current, and
+// kept. Restores the caller's current device.
+int scratch_ptr(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return set_error(FD_EUNSUPPORTED, "device %d: the library scratch covers devices 0..%d", device,
+                     kMaxDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess) return set_error(FD_ELAUNCH, "hipGetDevice failed");
+    if (prev != device && hipSetDevice(device) != hipSuccess)
+      return set_error(FD_ELAUNCH, "hipSetDevice(%d) failed", device);
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (prev != device) (void)hipSetDevice(prev);
+    if (e != hipSuccess || !p)
+      return set_error(FD_ELAUNCH, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[device] = p;
+  }
+  *out = g_scratch_ptr[device];
+  return FD_OK;
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w,
+                                        int norm_w_dtype, const void* w_gate_up,
+                                        const void* w_down, int64_t M, int64_t H, int64_t I,
+                                        float eps, int kind, int act_dtype, void* stream) {
+  using namespace fd;
+  if (!check_act_dtype(act_dtype)) return FD_EINVAL;
+  if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
+  if (H <= 0 || I <= 0) return set_error(FD_EINVAL, "H and I must be positive");
+  if (M * I * 2 > kScratchBytes)
+    return set_error(FD_EINVAL, "M*I*2 = %lld bytes exceeds the %lld-byte library scratch",
+                     (long long)(M * I * 2), (long long)kScratchBytes);
+  if (M == 0) return FD_OK;
+  int device = 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const hipError_t e = st ? hipStreamGetDevice(st, &device) : hipGetDevice(&device);
+  if (e != hipSuccess) return set_error(FD_ELAUNCH, "cannot find the stream's device");
+  void* mid = nullptr;
+  const int rc = scratch_ptr(device, &mid);
+  if (rc != FD_OK) return rc;
+  return fd_post_attn_mlp(y, mid, hidden, norm_w, norm_w_dtype, w_gate_up, w_down, M, H, I, eps,
+                          kind, act_dtype, stream);
 }
 
 extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_w,

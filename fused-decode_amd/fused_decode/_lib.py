@@ -67,6 +67,7 @@ SIGNATURES: dict[str, list] = {
     "fd_linear_tiled": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l,
                         ctypes.POINTER(FdTile), _i, _i, _p],
     "fd_post_attn_mlp": [_p, _p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p],
+    "fd_post_attn_mlp_noalloc": [_p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p],
     "fd_mlp_gate_up": [_p, _p, _p, _p, _i, _p, _l, _l, _l, _f, _i, _i, _p],
     "fd_pre_attn_qkv": [_p, _p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i,
                         _i, _p],

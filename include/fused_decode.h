@@ -165,6 +165,24 @@ int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
                      void* stream);
 
 /*
+ * fd_post_attn_mlp without the `mid` argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). No counterpart in the reference. `mid` lives in a
+ * library-owned device array of 1 MiB per GPU (held until the process ends):
+ * M*I*2 must not exceed 1,048,576 bytes (FD_EINVAL otherwise; Llama-3-8B widths
+ * at M = 16 need 458,752). The call allocates nothing and runs the same kernels,
+ * with the same results, as fd_post_attn_mlp. Every call on one GPU shares that
+ * GPU's array: calls that may overlap on one GPU (different streams, or host
+ * threads) race and must be serialised by the caller. Nothing in the array needs
+ * to start at zero (the gate/up launch writes all M*I values before the down
+ * projection reads them). The array's address is looked up on the first call on
+ * each device (the stream's device).
+ */
+int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
+                             const void* w_gate_up, const void* w_down, int64_t M, int64_t H,
+                             int64_t I, float eps, int kind, int act_dtype, void* stream);
+
+/*
  * The gate/up half of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u))
  * with g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
  * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 5 the RMSNorm is
