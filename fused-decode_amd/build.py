@@ -1,10 +1,12 @@
-"""Build libfused_decode_hip.so for gfx950 from csrc/*.hip with hipcc.
+"""Build libfused_decode_hip.so for gfx950 from csrc/*.hip with hipcc, and the
+CPython binding of its C ABI (csrc/fdcall.c) with the host C compiler.
 
 Usage: python fused-decode_amd/build.py [--jobs N]
 
-The library lands next to the Python package (fused_decode/), where
-fused_decode._lib loads it. Each .hip file is compiled to an object in
-_build/ (git-ignored) and the objects are linked into one shared library.
+Both land next to the Python package (fused_decode/), where fused_decode._lib
+loads them. Each .hip file is compiled to an object in _build/ (git-ignored)
+and the objects are linked into one shared library. The binding needs only
+Python's headers and the C ABI header: it dlopens the library at run time.
 """
 
 from __future__ import annotations
@@ -14,6 +16,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -24,6 +27,7 @@ INCLUDE = ROOT / "include"
 BUILD = HERE / "_build"
 LIB_NAME = "libfused_decode_hip.so"
 OUT = HERE / "fused_decode" / LIB_NAME
+BINDING_OUT = HERE / "fused_decode" / ("_fdcall" + sysconfig.get_config_var("EXT_SUFFIX"))
 ARCH = "gfx950"
 
 
@@ -80,7 +84,23 @@ def build(jobs: int = 4) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, OUT)
+    build_binding()
     return OUT
+
+
+def build_binding() -> Path:
+    """The CPython extension fused_decode._fdcall (plain C, no torch)."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no C compiler found for the Python binding (set CC)")
+    tmp = BINDING_OUT.with_suffix(".so.tmp")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror", f"-I{sysconfig.get_paths()['include']}",
+           f"-I{INCLUDE}", str(CSRC / "fdcall.c"), "-ldl", "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"building the Python binding failed:\n{proc.stderr}")
+    os.replace(tmp, BINDING_OUT)
+    return BINDING_OUT
 
 
 def main() -> None:

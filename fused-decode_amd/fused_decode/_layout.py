@@ -56,6 +56,40 @@ def _rows_from(dims, k: int, col: int, n: int) -> FdRows:
     return FdRows(sizes[0], sizes[1], sizes[2], strides[0], strides[1], strides[2], col, n)
 
 
+def contiguous_strides(shape) -> tuple[int, ...]:
+    """Strides of a dense row-major tensor of ``shape``."""
+    out, step = [], 1
+    for size in reversed(tuple(shape)):
+        out.append(step)
+        step *= max(int(size), 1)
+    return tuple(reversed(out))
+
+
+def plan_rows(shape, strides_list: list[tuple[int, ...]]) -> list[bytes] | None:
+    """Packed ``fd_rows`` (bytes, as the C ABI takes them) for operands that share
+    ``shape``, one per stride tuple, or None when their common row grid needs
+    more than three leading dims (the caller then stages through contiguous
+    copies). Depends on shapes and strides only, so it can be computed once per
+    argument signature."""
+    shape = tuple(shape)
+    n = shape[-1]
+    if n and all(st == strides_list[0] for st in strides_list) and \
+            tuple(strides_list[0]) == contiguous_strides(shape):
+        rows = FdRows(1, 1, _numel(shape) // n, 0, 0, n, 1, n)
+        return [bytes(rows)] * len(strides_list)
+    dims = _plan(shape, [tuple(st) for st in strides_list])
+    if len(dims) > 3:
+        return None
+    return [bytes(_rows_from(dims, k, int(st[-1]) if n != 1 else 1, n)) for k, st in enumerate(strides_list)]
+
+
+def _numel(shape) -> int:
+    total = 1
+    for s in shape:
+        total *= int(s)
+    return total
+
+
 def joint_layout(inputs: list[torch.Tensor], outputs: list[torch.Tensor]) -> tuple[list[Operand], list[Operand]]:
     """Row layouts for operands of one shape (broadcast inputs already expanded)."""
     shape = inputs[0].shape

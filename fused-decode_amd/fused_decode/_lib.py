@@ -1,9 +1,13 @@
-"""ctypes binding of libfused_decode_hip.so (the C ABI in include/fused_decode.h).
+"""Bindings of libfused_decode_hip.so (the C ABI in include/fused_decode.h).
 
-The shared library is loaded after torch, so its dependency on
-``libamdhip64.so.7`` resolves to the HIP runtime torch already loaded: streams
-and graph captures are shared with torch. There is no fallback: if the library
-is missing, every operator raises.
+Two bindings of the same library: ``native()`` is the CPython extension
+``_fdcall`` (csrc/fdcall.c) that the operators launch through, a few tens of
+nanoseconds per argument; ``lib()`` is a ctypes handle with every entry
+point's argument types declared, for tests and tools that call the C ABI the
+way a foreign host would. Both load the one shared library, after torch, so
+its dependency on ``libamdhip64.so.7`` resolves to the HIP runtime torch
+already loaded: streams and graph captures are shared with torch. There is no
+fallback: if the library or the binding is missing, every operator raises.
 """
 
 from __future__ import annotations
@@ -114,6 +118,35 @@ def check(func: str, status: int) -> None:
         raise FusedDecodeError(func, status, msg)
 
 
+_NATIVE = None
+
+
+def native():
+    """The ``_fdcall`` extension, bound to the library (loaded once)."""
+    global _NATIVE
+    if _NATIVE is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built: run `python fused-decode_amd/build.py` "
+                "(or __graft_entry__.build()) first"
+            )
+        try:
+            from . import _fdcall
+        except ImportError as exc:
+            raise RuntimeError(
+                "the Python binding fused_decode._fdcall is not built: run "
+                "`python fused-decode_amd/build.py` (or __graft_entry__.build()) first"
+            ) from exc
+        _fdcall.bind(str(LIB_PATH))
+        _NATIVE = _fdcall
+    return _NATIVE
+
+
+def fail(func: str, status: int) -> None:
+    """Raise the library's error for a non-OK ``status`` of ``func``."""
+    raise FusedDecodeError(func, status, native().last_error())
+
+
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
@@ -122,6 +155,11 @@ def stream_of(t: torch.Tensor) -> int:
     if _raw_stream is not None:
         return _raw_stream(t.device.index if t.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def stream_of_device(index: int) -> int:
+    """Handle of torch's current stream on device ``index``."""
+    return torch.cuda.current_stream(index).cuda_stream
 
 
 def runtime_version() -> int:

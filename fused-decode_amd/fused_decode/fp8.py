@@ -19,26 +19,30 @@ low-precision weight format its roadmap leaves for last.
 
 from __future__ import annotations
 
+import math
+import warnings
+
 import torch
 
 from . import _lib
-from ._lib import DTYPE_CODE, check, lib, stream_of
-from .ops import (
-    _as_mk,
-    _as_row_add,
-    _check_activation,
-    _check_eps,
-    _check_norm_weight,
-    _qkv_args,
-    _rope_qkv_heads,
-    rms_norm,
-    swiglu,
-)
+from ._checks import check
+from ._lib import DTYPE_CODE, fail, native, stream_of
+from .ops import _check_out, _qkv_args, _rope_qkv_heads, _row_add_rows, rms_norm, swiglu
 
 FP8_MAX = 448.0
 FP8_DTYPE = torch.float8_e4m3fn
 _HAND_LIMIT = 16
 _FP8_MFMA_MIN_M = 5  # rows from which the fp8 kernels run on MFMA (fp8.hip)
+_warned: set[str] = set()
+
+
+def _slow_path(why: str) -> None:
+    """The decoded float32 product streams 4x the code bytes: say so, once per reason."""
+    if why not in _warned:
+        _warned.add(why)
+        warnings.warn(f"linear_decode_fp8: {why}; computing a float32 product of the decoded weights "
+                      "(same values, about 4x the weight traffic of the fp8 kernels)", RuntimeWarning,
+                      stacklevel=3)
 
 
 def quantize_fp8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -62,30 +66,10 @@ def dequantize_fp8(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return codes.float() * scale.float()[:, None]
 
 
-def _check_fp8_weight(weight: torch.Tensor, scale: torch.Tensor, like: torch.Tensor, name: str) -> None:
-    if weight.dtype != FP8_DTYPE:
-        raise TypeError(f"{name} must be torch.float8_e4m3fn codes (see quantize_fp8)")
-    if weight.ndim != 2:
-        raise ValueError(f"{name} must have shape [N, K], got {tuple(weight.shape)}")
-    if scale.dtype != torch.float32 or scale.ndim != 1 or scale.shape[0] != weight.shape[0]:
-        raise ValueError(f"{name} scale must be float32 of shape ({weight.shape[0]},)")
-    if weight.device != like.device or scale.device != like.device:
-        raise ValueError(f"{name} and its scale must be on {like.device}")
-
-
-def _fp8_rows_ok(weight: torch.Tensor) -> bool:
+def _kernel_rows_ok(weight: torch.Tensor) -> bool:
+    """Codes the fp8 kernels stream: unit K stride, K % 16 == 0, 16-byte rows."""
     return weight.stride(1) == 1 and (weight.shape[0] == 1 or weight.stride(0) % 16 == 0) \
         and weight.shape[1] % 16 == 0 and weight.data_ptr() % 16 == 0
-
-
-def _decoded_product(x2, weight, scale, bias, ra, dtype):
-    """float32 product of the decoded weights, for shapes the HIP kernel does not take."""
-    y = (x2.float() @ weight.float().t()) * scale
-    if bias is not None:
-        y = y + bias.float()
-    if ra is not None:
-        y = y + ra.float()
-    return y.to(dtype)
 
 
 def linear_decode_fp8(
@@ -100,54 +84,55 @@ def linear_decode_fp8(
     """``y = (x @ dequantize(weight, scale).T) (+ bias) (+ row_add)`` with E4M3
     ``weight [N, K]`` and float32 ``scale [N]``; argument rules as
     ``linear_decode`` (ops.py:212-280 of the reference). Up to 16 rows with
-    ``K % 16 == 0`` this is the HIP fp8 GEMV; otherwise a float32 product of the
-    decoded weights (same values, slower)."""
-    _check_activation(x, "x")
-    _check_fp8_weight(weight, scale, x, "weight")
-    n, k = weight.shape
-    if x.shape[-1] != k:
-        raise ValueError(f"x last dim {x.shape[-1]} != weight K {k}")
-    x2, leading = _as_mk(x)
-    m = x2.shape[0]
-    expected = (n,) if leading is None else (*leading, n)
-    if bias is not None:
-        if bias.ndim != 1 or bias.shape[0] != n:
-            raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
-        if bias.device != x.device:
-            raise ValueError("bias must be on the same device as x")
-        if bias.dtype not in (x.dtype, torch.float32):
-            raise TypeError("bias must match x or be float32")
-    ra = None
-    if row_add is not None:
-        if row_add.device != x.device:
-            raise ValueError("row_add must be on the same device as x")
-        ra = _as_row_add(row_add, m, n, expected)
+    ``K % 16 == 0`` this is the HIP fp8 GEMV; other shapes compute a float32
+    product of the decoded weights (same values, several times the traffic: a
+    RuntimeWarning says so once per reason)."""
+    check("linear_decode_fp8", x=x, weight=weight, scale=scale, bias=bias, row_add=row_add)
+    n, k = (int(d) for d in weight.shape)
+    m = 1 if x.ndim == 1 else math.prod(x.shape[:-1])
+    expected = (n,) if x.ndim == 1 else (*x.shape[:-1], n)
+    ra = None if row_add is None else _row_add_rows(row_add, m, n, expected)
     if out is None:
         out = torch.empty(expected, device=x.device, dtype=x.dtype)
-    elif tuple(out.shape) != expected or out.dtype != x.dtype or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous {expected} tensor of dtype {x.dtype}")
+    else:
+        _check_out(out, expected, x)
     y2 = out.view(m, n)
     if m == 0 or n == 0:
         return out
-    if m > _HAND_LIMIT or not _fp8_rows_ok(weight) or x2.stride(1) != 1 or \
-            (m > 1 and x2.stride(0) % 8 != 0) or x2.data_ptr() % 16 != 0:
-        y2.copy_(_decoded_product(x2, weight, scale, bias, ra, x.dtype))
+    x2 = x.reshape(m, k)
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    why = None
+    if m > _HAND_LIMIT:
+        why = f"{m} rows is above the kernels' {_HAND_LIMIT}"
+    elif not _kernel_rows_ok(weight):
+        why = "the codes are not 16-byte rows with K % 16 == 0"
+    elif x2.stride(1) != 1 or (m > 1 and x2.stride(0) % 8 != 0) or x2.data_ptr() % 16 != 0:
+        why = "x rows are not 16-byte aligned with unit stride"
+    if why is not None:
+        _slow_path(why)
+        y = (x2.float() @ weight.float().t()) * scale
+        if bias is not None:
+            y = y + bias.float()
+        if row_add is not None:
+            y = y + row_add.expand(expected).reshape(m, n).float()
+        y2.copy_(y.to(x.dtype))
         return out
-    bias_ptr, bias_code, sb = None, DTYPE_CODE[x.dtype], 0
-    if bias is not None:
-        bias_ptr, bias_code, sb = bias.data_ptr(), DTYPE_CODE[bias.dtype], int(bias.stride(0))
-    row_ptr, row_code, srm, srn = None, DTYPE_CODE[x.dtype], 0, 0
-    if ra is not None:
-        row_ptr, row_code = ra.data_ptr(), DTYPE_CODE[ra.dtype]
-        srm = 0 if ra.shape[0] == 1 else int(ra.stride(0))
-        srn = 0 if ra.shape[1] == 1 else int(ra.stride(1))
+    act = DTYPE_CODE[x.dtype]
+    r2, srm, srn = None, 0, 0
+    if row_add is not None:  # indexed in place through (srm, srn), or copied when its dims do not merge
+        srm, srn, flat = ra
+        r2 = row_add.expand(expected).reshape(m, n) if flat else row_add
     sc = scale if scale.is_contiguous() else scale.contiguous()
-    status = lib().fd_linear_fp8(
-        y2.data_ptr(), x2.data_ptr(), weight.data_ptr(), sc.data_ptr(), bias_ptr, bias_code,
-        row_ptr, row_code, m, n, k, int(x2.stride(0)), int(weight.stride(0)), sb, srm, srn,
-        int(y2.stride(0)), int(y2.stride(1)), DTYPE_CODE[x.dtype], stream_of(x),
+    status = native().linear_fp8(
+        y2.data_ptr(), x2.data_ptr(), weight.data_ptr(), sc.data_ptr(),
+        None if bias is None else bias.data_ptr(), act if bias is None else DTYPE_CODE[bias.dtype],
+        None if r2 is None else r2.data_ptr(), act if r2 is None else DTYPE_CODE[r2.dtype],
+        m, n, k, int(x2.stride(0)), int(weight.stride(0)), 0 if bias is None else int(bias.stride(0)),
+        srm, srn, int(y2.stride(0)), int(y2.stride(1)), act, stream_of(x),
     )
-    check("fd_linear_fp8", status)
+    if status:
+        fail("fd_linear_fp8", status)
     return out
 
 
@@ -163,19 +148,12 @@ def post_attn_mlp_fp8(
     """``post_attn_mlp`` with E4M3 weights (``w_gate_up [2I, H]``, ``w_down [H, I]``)
     and their float32 per-row scales: the same four rounding points (reference
     reference.py:66-79), each projection as ``linear_decode_fp8``. Two HIP launches
-    up to 16 rows; otherwise composed from the operators."""
-    _check_activation(hidden, "hidden")
-    _check_fp8_weight(w_gate_up, gate_up_scale, hidden, "w_gate_up")
-    _check_fp8_weight(w_down, down_scale, hidden, "w_down")
-    two_i, h = w_gate_up.shape
-    h_down, i = w_down.shape
-    if two_i != 2 * i or h != h_down or hidden.shape[-1] != h:
-        raise ValueError(
-            f"expected w_gate_up [2I, H] and w_down [H, I] with hidden [..., H], "
-            f"got {tuple(w_gate_up.shape)}, {tuple(w_down.shape)}, {tuple(hidden.shape)}"
-        )
-    _check_norm_weight(norm_weight, hidden)
-    eps = _check_eps(eps)
+    up to 4 rows, three up to 16 (the RMSNorm runs first as a row kernel);
+    otherwise composed from the operators."""
+    a = check("post_attn_mlp_fp8", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up,
+              gate_up_scale=gate_up_scale, w_down=w_down, down_scale=down_scale, eps=eps)
+    eps = a["eps"]
+    h, i = int(w_gate_up.shape[1]), int(w_down.shape[1])
     m = hidden.numel() // h if h else 0
     if 0 < m <= _HAND_LIMIT and w_gate_up.is_contiguous() and w_down.is_contiguous() \
             and h % 16 == 0 and i % 16 == 0:
@@ -185,14 +163,15 @@ def post_attn_mlp_fp8(
         nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
         y = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
         mid = torch.empty((m, i), device=hidden.device, dtype=hidden.dtype)
-        status = lib().fd_post_attn_mlp_fp8(
+        status = native().post_attn_mlp_fp8(
             y.data_ptr(), mid.data_ptr(), h2.data_ptr(), nw.data_ptr(), DTYPE_CODE[nw.dtype],
             w_gate_up.data_ptr(), gate_up_scale.contiguous().data_ptr(), w_down.data_ptr(),
-            down_scale.contiguous().data_ptr(), m, h, i, float(eps), DTYPE_CODE[hidden.dtype],
+            down_scale.contiguous().data_ptr(), m, h, i, eps, DTYPE_CODE[hidden.dtype],
             stream_of(hidden),
         )
         if status != _lib.FD_EUNSUPPORTED:
-            check("fd_post_attn_mlp_fp8", status)
+            if status:
+                fail("fd_post_attn_mlp_fp8", status)
             return y.view(hidden.shape)
     normed = rms_norm(hidden, norm_weight, eps=eps)
     gate_up = linear_decode_fp8(normed, w_gate_up, gate_up_scale)
@@ -219,10 +198,10 @@ def pre_attn_qkv_fp8(
     argument rules of ``pre_attn_qkv``. One HIP launch up to 4 rows, two up to 16
     (the norm runs as a row kernel ahead of the MFMA form); otherwise, or for
     shapes the kernels do not take, composed from the operators."""
-    _check_activation(hidden, "hidden")
-    _check_fp8_weight(w_qkv, scale, hidden, "w_qkv")
+    a0 = check("pre_attn_qkv_fp8", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, scale=scale,
+               eps=eps, bias=bias)
     n, h = w_qkv.shape
-    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
     out, m = a.out, a.m
     if m == 0 or n == 0:
         return out
@@ -235,16 +214,17 @@ def pre_attn_qkv_fp8(
         normed = None
         if m >= _FP8_MFMA_MIN_M:
             normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
-        status = lib().fd_pre_attn_qkv_fp8(
+        status = native().pre_attn_qkv_fp8(
             out.data_ptr(), normed.data_ptr() if normed is not None else None, h2.data_ptr(),
             nw.data_ptr(), DTYPE_CODE[nw.dtype], w_qkv.data_ptr(), scale.contiguous().data_ptr(),
             b.data_ptr() if b is not None else None,
             DTYPE_CODE[b.dtype] if b is not None else DTYPE_CODE[hidden.dtype],
             a.cos.data_ptr(), a.sin.data_ptr(), DTYPE_CODE[a.cos.dtype], a.cs_row_stride, m, h, n,
-            a.rope_cols, a.d, float(a.eps), DTYPE_CODE[hidden.dtype], stream_of(hidden),
+            a.rope_cols, a.d, a.eps, DTYPE_CODE[hidden.dtype], stream_of(hidden),
         )
         if status != _lib.FD_EUNSUPPORTED:
-            check("fd_pre_attn_qkv_fp8", status)
+            if status:
+                fail("fd_pre_attn_qkv_fp8", status)
             return out
     normed = rms_norm(hidden, norm_weight, eps=a.eps)
     linear_decode_fp8(normed, w_qkv, scale, bias, out=out)

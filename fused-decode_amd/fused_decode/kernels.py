@@ -3,14 +3,15 @@
 Same launcher boundary as the reference's src/fused_decode/kernels.py
 (``rms_out``, ``swiglu_out``, ``rope_out``, ``linear_out``, ``resolve_kind``,
 ``linear_config``, ``launch_copy``, ``launch_triad``), but every launch goes
-through the C ABI of libfused_decode_hip.so on torch's current stream. The
-launchers write into caller-provided tensors and never synchronise, so they can
-be captured into a HIP graph.
+through the C ABI of libfused_decode_hip.so (its ``_fdcall`` binding) on
+torch's current stream. The launchers write into caller-provided tensors and
+never synchronise, so they can be captured into a HIP graph. They plan row
+layouts on every call; the public operators (``ops``) cache that planning per
+argument signature and call the binding directly.
 """
 
 from __future__ import annotations
 
-import ctypes
 import json
 import os
 import warnings
@@ -19,7 +20,7 @@ import torch
 
 from . import _lib
 from ._layout import finish, joint_layout
-from ._lib import DTYPE_CODE, KIND_CODE, FdTile, check, lib, stream_of
+from ._lib import DTYPE_CODE, KIND_CODE, FdTile, fail, native, stream_of
 
 _warned: set[str] = set()
 
@@ -68,19 +69,22 @@ def rms_out(
     act = DTYPE_CODE[x.dtype]
     w_code = DTYPE_CODE[weight.dtype]
     st = stream_of(x)
+    rows = [bytes(op.rows) for op in li + lo]
     if add:
-        status = lib().fd_add_rms_norm(
+        status = native().add_rms_norm(
             lo[0].tensor.data_ptr(), lo[1].tensor.data_ptr(), li[0].tensor.data_ptr(),
             li[1].tensor.data_ptr(), weight.data_ptr(), w_code, int(weight.stride(0)),
-            li[0].rows, li[1].rows, lo[0].rows, lo[1].rows, float(eps), act, st,
+            rows[0], rows[1], rows[2], rows[3], float(eps), act, st,
         )
-        check("fd_add_rms_norm", status)
+        if status:
+            fail("fd_add_rms_norm", status)
     else:
-        status = lib().fd_rms_norm(
+        status = native().rms_norm(
             lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), weight.data_ptr(), w_code,
-            int(weight.stride(0)), li[0].rows, lo[0].rows, float(eps), act, st,
+            int(weight.stride(0)), rows[0], rows[1], float(eps), act, st,
         )
-        check("fd_rms_norm", status)
+        if status:
+            fail("fd_rms_norm", status)
     finish(lo)
 
 
@@ -89,11 +93,12 @@ def swiglu_out(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:
     if gate.numel() == 0:
         return
     li, lo = joint_layout([gate, up], [out])
-    status = lib().fd_swiglu(
+    status = native().swiglu(
         lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), li[1].tensor.data_ptr(),
-        li[0].rows, li[1].rows, lo[0].rows, DTYPE_CODE[gate.dtype], stream_of(gate),
+        bytes(li[0].rows), bytes(li[1].rows), bytes(lo[0].rows), DTYPE_CODE[gate.dtype], stream_of(gate),
     )
-    check("fd_swiglu", status)
+    if status:
+        fail("fd_swiglu", status)
     finish(lo)
 
 
@@ -106,12 +111,13 @@ def rope_out(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, out: torch.T
         # one dtype code per launch: widen both (exact for fp16/bf16 -> fp32)
         cos, sin = cos.float(), sin.float()
     li, lo = joint_layout([x, cos, sin], [out])
-    status = lib().fd_rope(
+    status = native().rope(
         lo[0].tensor.data_ptr(), li[0].tensor.data_ptr(), li[1].tensor.data_ptr(),
-        li[2].tensor.data_ptr(), DTYPE_CODE[cos.dtype], li[0].rows, li[1].rows, li[2].rows,
-        lo[0].rows, DTYPE_CODE[x.dtype], stream_of(x),
+        li[2].tensor.data_ptr(), DTYPE_CODE[cos.dtype], bytes(li[0].rows), bytes(li[1].rows),
+        bytes(li[2].rows), bytes(lo[0].rows), DTYPE_CODE[x.dtype], stream_of(x),
     )
-    check("fd_rope", status)
+    if status:
+        fail("fd_rope", status)
     finish(lo)
 
 
@@ -229,12 +235,12 @@ def linear_out(
         x = x.contiguous()
     if any(s < 0 for s in weight.stride()):
         weight = weight.contiguous()
-    bias_ptr, bias_code, sb = 0, DTYPE_CODE[x.dtype], 0
+    bias_ptr, bias_code, sb = None, DTYPE_CODE[x.dtype], 0
     if bias is not None:
         if bias.stride(0) < 0:
             bias = bias.contiguous()
         bias_ptr, bias_code, sb = bias.data_ptr(), DTYPE_CODE[bias.dtype], int(bias.stride(0))
-    row_ptr, row_code, srm, srn = 0, DTYPE_CODE[x.dtype], 0, 0
+    row_ptr, row_code, srm, srn = None, DTYPE_CODE[x.dtype], 0, 0
     if row_add is not None:
         if any(s < 0 for s in row_add.stride()):
             row_add = row_add.contiguous()
@@ -244,13 +250,14 @@ def linear_out(
     if tile is None:
         rows, _, waves, stages = linear_config(kind, n, k, m)
         tile = (rows, waves, stages)
-    status = lib().fd_linear_tiled(
+    status = native().linear_tiled(
         y.data_ptr(), x.data_ptr(), weight.data_ptr(), bias_ptr, bias_code, row_ptr, row_code,
         m, n, k, int(x.stride(0)), int(x.stride(1)), int(weight.stride(0)), int(weight.stride(1)),
-        sb, srm, srn, int(y.stride(0)), int(y.stride(1)), ctypes.byref(FdTile(*tile)),
+        sb, srm, srn, int(y.stride(0)), int(y.stride(1)), bytes(FdTile(*tile)),
         KIND_CODE[kind], DTYPE_CODE[x.dtype], stream_of(x),
     )
-    check("fd_linear_tiled", status)
+    if status:
+        fail("fd_linear_tiled", status)
 
 
 def post_attn_mlp_out(
@@ -268,14 +275,13 @@ def post_attn_mlp_out(
     caller fall back to the composed operators)."""
     m, h = hidden.shape
     i = w_down.shape[1]
-    status = lib().fd_post_attn_mlp(
+    status = native().post_attn_mlp(
         out.data_ptr(), mid.data_ptr(), hidden.data_ptr(), norm_weight.data_ptr(),
         DTYPE_CODE[norm_weight.dtype], w_gate_up.data_ptr(), w_down.data_ptr(), m, h, i,
         float(eps), KIND_CODE[kind], DTYPE_CODE[hidden.dtype], stream_of(hidden),
     )
-    if status == _lib.FD_EUNSUPPORTED:
-        return status
-    check("fd_post_attn_mlp", status)
+    if status not in (_lib.FD_OK, _lib.FD_EUNSUPPORTED):
+        fail("fd_post_attn_mlp", status)
     return status
 
 
@@ -301,7 +307,7 @@ def pre_attn_qkv_out(
     lets the caller compose the operators instead)."""
     m, h = hidden.shape
     n = w_qkv.shape[0]
-    status = lib().fd_pre_attn_qkv(
+    status = native().pre_attn_qkv(
         out.data_ptr(), normed.data_ptr() if normed is not None else None, hidden.data_ptr(),
         norm_weight.data_ptr(), DTYPE_CODE[norm_weight.dtype], w_qkv.data_ptr(),
         bias.data_ptr() if bias is not None else None,
@@ -311,9 +317,8 @@ def pre_attn_qkv_out(
         cs_row_stride, m, h, n, rope_cols, head_dim, float(eps), KIND_CODE[kind],
         DTYPE_CODE[hidden.dtype], stream_of(hidden),
     )
-    if status == _lib.FD_EUNSUPPORTED:
-        return status
-    check("fd_pre_attn_qkv", status)
+    if status not in (_lib.FD_OK, _lib.FD_EUNSUPPORTED):
+        fail("fd_pre_attn_qkv", status)
     return status
 
 
@@ -322,13 +327,16 @@ def launch_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
     nbytes = src.numel() * src.element_size()
     if dst.numel() * dst.element_size() != nbytes:
         raise ValueError("copy needs equal byte sizes")
-    check("fd_copy", lib().fd_copy(dst.data_ptr(), src.data_ptr(), nbytes, stream_of(src)))
+    status = native().copy(dst.data_ptr(), src.data_ptr(), nbytes, stream_of(src))
+    if status:
+        fail("fd_copy", status)
 
 
 def launch_triad(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: float = 1.0) -> None:
     """``c = a + b * scale`` over contiguous tensors of one dtype."""
-    status = lib().fd_triad(
+    status = native().triad(
         c.data_ptr(), a.data_ptr(), b.data_ptr(), float(scale), a.numel(), DTYPE_CODE[a.dtype],
         stream_of(a),
     )
-    check("fd_triad", status)
+    if status:
+        fail("fd_triad", status)

@@ -1,25 +1,46 @@
 """Public operators (drop-in for the reference's src/fused_decode/ops.py).
 
-Inference only: these launches record no backward. Signatures, argument
-checks, exception types and message keywords follow the reference
-(ops.py:34-69 validation, :72-315 operators); the device work is the gfx950 HIP
-library behind ``kernels``. ``linear_decode`` uses the hand-written GEMV up to
-``DECODE_LINEAR_MAX_M`` rows by default and ``F.linear`` (hipBLASLt) above it;
-passing ``kind`` forces the GEMV up to 16 rows, as in the reference.
+Inference only: these launches record no backward. The signatures, defaults,
+exception types and message keywords are the reference's (ops.py:72-315); the
+argument rules live in ``_checks.CONTRACT`` and the device work in the gfx950
+HIP library, reached through its CPython binding (``_lib.native()``).
+
+Launch plans. At one token a kernel runs for 2-7 us, and a HIP launch alone
+costs about 2.4 us of host time, so the rest of a call's host work has to stay
+near a microsecond or the host, not the GPU, sets the pace of an eager decode
+loop. Each call is therefore keyed by its argument signature: every tensor's
+shape, strides, dtype and device, the scalars, and the environment variables
+that steer dispatch (the reference reads them on every call, kernels.py:92,
+:103, :583, :595, and so does the key). The first call with a signature checks
+the arguments against the contract, resolves the kernel, tile, row layouts and
+dtype codes, and stores a plan: a closure that allocates the outputs, reads the
+data pointers and torch's current stream, and calls the library. Later calls
+with that signature run the plan directly. Nothing in a plan depends on data
+pointers (the library checks alignment and picks its vector or generic kernels
+itself on every call).
+
+``linear_decode`` uses the hand-written GEMV up to ``DECODE_LINEAR_MAX_M`` rows
+by default and ``F.linear`` (hipBLASLt) above it; passing ``kind`` forces the
+GEMV up to 16 rows, as in the reference.
 """
 
 from __future__ import annotations
 
 import math
-from typing import NamedTuple
+import os
+from typing import Callable, NamedTuple
 
 import torch
 import torch.nn.functional as F
 
 from . import _lib
+from ._checks import check
+from ._layout import contiguous_strides, plan_rows
+from ._lib import DTYPE_CODE, FD_EUNSUPPORTED, KIND_CODE, FdTile, fail, native
 from .kernels import (
     _MFMA_MIN_M,
-    linear_out,
+    _rms_env,
+    linear_config,
     post_attn_mlp_out,
     pre_attn_qkv_out,
     resolve_kind,
@@ -36,9 +57,7 @@ from .kernels import (
 # hipBLASLt's F.linear, none of them more than 5% slower (each strictly faster
 # up to 14 rows), so the HIP GEMV is the default over the whole hand range.
 DECODE_LINEAR_MAX_M = 16
-_HAND_LIMIT = 16
-_ACTIVATION = (torch.float16, torch.bfloat16)
-_NORM_WEIGHT = (torch.float16, torch.bfloat16, torch.float32)
+_FORCED_LIMIT = 16  # rows the GEMV takes when the caller names a kind
 
 __all__ = [
     "DECODE_LINEAR_MAX_M",
@@ -51,43 +70,62 @@ __all__ = [
     "swiglu",
 ]
 
+# ------------------------------------------------------------------ plans
 
-def _check_activation(t: torch.Tensor, name: str) -> None:
-    if not isinstance(t, torch.Tensor):
-        raise TypeError(f"{name} must be a tensor")
-    if not t.is_cuda:
-        raise ValueError(f"{name} must be a CUDA tensor")
-    if t.dtype not in _ACTIVATION:
-        raise TypeError(f"{name} must be float16 or bfloat16, got {t.dtype}")
+Plan = Callable[..., object]
+_PLANS: dict[tuple, Plan] = {}
+_PLAN_LIMIT = 4096
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or _lib.stream_of_device
 
 
-def _check_same(t: torch.Tensor, like: torch.Tensor, name: str) -> None:
-    if t.shape != like.shape:
-        raise ValueError(f"{name} shape {tuple(t.shape)} != {tuple(like.shape)}")
-    if t.dtype != like.dtype:
-        raise TypeError(f"{name} dtype {t.dtype} != {like.dtype}")
-    if t.device != like.device:
-        raise ValueError(f"{name} is on {t.device}, expected {like.device}")
+def _remember(key, plan: Plan) -> Plan:
+    if key is not None:
+        if len(_PLANS) >= _PLAN_LIMIT:
+            _PLANS.clear()
+        _PLANS[key] = plan
+    return plan
 
 
-def _check_norm_weight(weight: torch.Tensor, x: torch.Tensor) -> None:
-    if weight.device != x.device:
-        raise ValueError(f"weight is on {weight.device}, expected {x.device}")
-    if weight.dtype not in _NORM_WEIGHT:
-        raise TypeError("weight must be float16, bfloat16, or float32")
-    if weight.ndim != 1 or weight.shape[0] != x.shape[-1]:
-        raise ValueError(f"weight must have shape ({x.shape[-1]},), got {tuple(weight.shape)}")
+def clear_plans() -> None:
+    """Forget every cached launch plan (the next call per signature re-checks)."""
+    _PLANS.clear()
 
 
-def _check_eps(eps: float) -> float:
-    eps = float(eps)
-    if not math.isfinite(eps) or eps < 0:
-        raise ValueError("eps must be a finite value >= 0")
-    return eps
+def _sig(t):
+    """Signature of an optional tensor argument."""
+    return None if t is None else (t.shape, t.stride(), t.dtype, t.device)
 
 
-def _check_out(out: torch.Tensor, like: torch.Tensor) -> None:
-    _check_same(out, like, "out")
+# os.environ keeps its values in a bytes-keyed dict on POSIX; reading that dict
+# costs a dict lookup where os.environ.get costs an encode and, for an unset
+# variable, a raised KeyError.
+_ENV_DATA = getattr(os.environ, "_data", None)
+
+
+def _env(name: str, _keys: dict = {}):  # noqa: B006 (a per-process key cache)
+    if _ENV_DATA is None:
+        return os.environ.get(name)
+    key = _keys.get(name)
+    if key is None:
+        key = _keys[name] = os.environ.encodekey(name)
+    return _ENV_DATA.get(key)
+
+
+def _dense(t: torch.Tensor) -> bool:
+    return t.is_contiguous()
+
+
+def _empty(shape, like: torch.Tensor) -> Callable[[torch.Tensor], torch.Tensor]:
+    """Allocator of a contiguous output of ``shape`` in ``like``'s dtype/device:
+    ``empty_like`` when that is the same thing (the cheapest torch allocation)."""
+    shape = tuple(shape)
+    if _dense(like) and tuple(like.shape) == shape:
+        return torch.empty_like
+    dtype, device = like.dtype, like.device
+    return lambda _ref: torch.empty(shape, dtype=dtype, device=device)
+
+
+# ------------------------------------------------------------------ norms
 
 
 def rms_norm(
@@ -99,15 +137,15 @@ def rms_norm(
 ) -> torch.Tensor:
     """RMSNorm over the last dimension with a float32 reduction. ``weight`` is ``(N,)``
     (float16, bfloat16 or float32). Reference: ops.py:72-88."""
-    _check_activation(x, "x")
-    _check_norm_weight(weight, x)
-    eps = _check_eps(eps)
-    if out is None:
-        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
-    else:
-        _check_out(out, x)
-    rms_out(x, weight, eps, out)
-    return out
+    try:
+        key = ("rms", x.shape, x.stride(), x.dtype, x.device, weight.shape, weight.stride(), weight.dtype,
+               weight.device, eps, _sig(out), _env("FUSED_DECODE_RMS_BLOCK"), _env("FUSED_DECODE_RMS_WARPS"))
+        plan = _PLANS.get(key)
+    except AttributeError:  # not a tensor: let the contract say so
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_norm(False, x, weight, eps, out, None, None))
+    return plan(x, weight, out, None, None)
 
 
 def add_rms_norm(
@@ -122,37 +160,82 @@ def add_rms_norm(
     """``residual_out = x + residual``, then RMSNorm of the float32 sum (not of the
     rounded stored residual). ``residual_out=residual`` updates the residual
     stream in place. Reference: ops.py:91-119."""
-    _check_activation(x, "x")
-    _check_activation(residual, "residual")
-    _check_same(residual, x, "residual")
-    _check_norm_weight(weight, x)
-    eps = _check_eps(eps)
-    if out is None:
-        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
-    else:
-        _check_out(out, x)
-    if residual_out is None:
-        residual_out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
-    else:
-        _check_same(residual_out, x, "residual_out")
-    rms_out(x, weight, eps, out, residual=residual, residual_out=residual_out)
-    return out, residual_out
-
-
-def _broadcast_angles(src: torch.Tensor, like: torch.Tensor, name: str) -> torch.Tensor:
-    """Broadcast like PyTorch (shapes align on the right). Reference: ops.py:122-135."""
-    if src.device != like.device:
-        raise ValueError(f"{name} is on {src.device}, expected {like.device}")
-    if src.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise TypeError(f"{name} must be float16, bfloat16, or float32")
-    if src.shape[-1] != like.shape[-1]:
-        raise ValueError(f"{name} last dim {src.shape[-1]} != x last dim {like.shape[-1]}")
     try:
-        return src.expand(like.shape)
-    except RuntimeError as exc:
-        raise ValueError(
-            f"cannot broadcast {name} shape {tuple(src.shape)} to {tuple(like.shape)}"
-        ) from exc
+        key = ("add_rms", x.shape, x.stride(), x.dtype, x.device, residual.shape, residual.stride(),
+               residual.dtype, residual.device, weight.shape, weight.stride(), weight.dtype, weight.device,
+               eps, _sig(out), _sig(residual_out), _env("FUSED_DECODE_RMS_BLOCK"),
+               _env("FUSED_DECODE_RMS_WARPS"))
+        plan = _PLANS.get(key)
+    except AttributeError:
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_norm(True, x, weight, eps, out, residual, residual_out))
+    return plan(x, weight, out, residual, residual_out)
+
+
+def _plan_norm(add: bool, x, weight, eps, out, residual, residual_out) -> Plan:
+    if add:
+        a = check("add_rms_norm", x=x, residual=residual, weight=weight, eps=eps, out=out,
+                  residual_out=residual_out)
+    else:
+        a = check("rms_norm", x=x, weight=weight, eps=eps, out=out)
+    eps = a["eps"]
+    _rms_env()
+    shape = tuple(x.shape)
+    alloc = _empty(shape, x)
+    if x.numel() == 0:
+        def empty(x, w, out, r, ro):
+            y = alloc(x) if out is None else out
+            if add:
+                return y, alloc(x) if ro is None else ro
+            return y
+        return empty
+
+    dense = contiguous_strides(shape)
+    strides = [tuple(x.stride())] + ([tuple(residual.stride())] if add else [])
+    strides += [dense if out is None else tuple(out.stride())]
+    if add:
+        strides.append(dense if residual_out is None else tuple(residual_out.stride()))
+    rows = plan_rows(shape, strides)
+    if rows is None:  # more than three unmergeable leading dims: the staging launcher
+        def staged(x, w, out, r, ro):
+            y = alloc(x) if out is None else out
+            if add:
+                ro = alloc(x) if ro is None else ro
+                rms_out(x, w, eps, y, residual=r, residual_out=ro)
+                return y, ro
+            rms_out(x, w, eps, y)
+            return y
+        return staged
+
+    call = native().add_rms_norm if add else native().rms_norm
+    act, wcode, wstride, dev = DTYPE_CODE[x.dtype], DTYPE_CODE[weight.dtype], int(weight.stride(0)), x.device.index
+    if add:
+        rx, rr, ry, rro = rows
+
+        def run_add(x, w, out, r, ro):
+            y = alloc(x) if out is None else out
+            ro = alloc(x) if ro is None else ro
+            status = call(y.data_ptr(), ro.data_ptr(), x.data_ptr(), r.data_ptr(), w.data_ptr(), wcode, wstride,
+                          rx, rr, ry, rro, eps, act, _raw_stream(dev))
+            if status:
+                fail("fd_add_rms_norm", status)
+            return y, ro
+        return run_add
+
+    rx, ry = rows
+
+    def run(x, w, out, r, ro):
+        y = alloc(x) if out is None else out
+        status = call(y.data_ptr(), x.data_ptr(), w.data_ptr(), wcode, wstride, rx, ry, eps, act,
+                      _raw_stream(dev))
+        if status:
+            fail("fd_rms_norm", status)
+        return y
+    return run
+
+
+# ------------------------------------------------------------------ pointwise
 
 
 def rope(
@@ -165,17 +248,50 @@ def rope(
     """Llama rotate-half RoPE on the last dimension (GPT-NeoX pairing, not GPT-J
     interleaved pairs). ``cos``/``sin`` broadcast over leading dims.
     Reference: ops.py:138-160."""
-    _check_activation(x, "x")
-    if x.shape[-1] % 2 != 0:
-        raise ValueError("rope last dimension must be even")
-    cos_b = _broadcast_angles(cos, x, "cos")
-    sin_b = _broadcast_angles(sin, x, "sin")
-    if out is None:
-        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
-    else:
-        _check_out(out, x)
-    rope_out(x, cos_b, sin_b, out)
-    return out
+    try:
+        key = ("rope", x.shape, x.stride(), x.dtype, x.device, cos.shape, cos.stride(), cos.dtype, cos.device,
+               sin.shape, sin.stride(), sin.dtype, sin.device, _sig(out))
+        plan = _PLANS.get(key)
+    except AttributeError:
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_rope(x, cos, sin, out))
+    return plan(x, cos, sin, out)
+
+
+def _plan_rope(x, cos, sin, out) -> Plan:
+    check("rope", x=x, cos=cos, sin=sin, out=out)
+    shape = tuple(x.shape)
+    alloc = _empty(shape, x)
+    mixed = cos.dtype != sin.dtype  # one dtype code per launch: widen both (exact)
+    if x.numel() == 0 or mixed:
+        def general(x, c, s, out):
+            y = alloc(x) if out is None else out
+            if x.numel():
+                rope_out(x, c.expand(x.shape), s.expand(x.shape), y)
+            return y
+        return general
+    cb, sb = cos.expand(shape), sin.expand(shape)  # stride-0 broadcast dims, never copied
+    strides = [tuple(x.stride()), tuple(cb.stride()), tuple(sb.stride()),
+               contiguous_strides(shape) if out is None else tuple(out.stride())]
+    rows = plan_rows(shape, strides)
+    if rows is None:
+        def staged(x, c, s, out):
+            y = alloc(x) if out is None else out
+            rope_out(x, c.expand(x.shape), s.expand(x.shape), y)
+            return y
+        return staged
+    rx, rc, rs, ry = rows
+    call, cs, act, dev = native().rope, DTYPE_CODE[cos.dtype], DTYPE_CODE[x.dtype], x.device.index
+
+    def run(x, c, s, out):
+        y = alloc(x) if out is None else out
+        status = call(y.data_ptr(), x.data_ptr(), c.data_ptr(), s.data_ptr(), cs, rx, rc, rs, ry, act,
+                      _raw_stream(dev))
+        if status:
+            fail("fd_rope", status)
+        return y
+    return run
 
 
 def swiglu(
@@ -185,48 +301,94 @@ def swiglu(
     out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """``silu(gate) * up`` in float32, stored in ``gate.dtype``. Reference: ops.py:163-178."""
-    _check_activation(gate, "gate")
-    _check_activation(up, "up")
-    _check_same(up, gate, "up")
-    if out is None:
-        out = torch.empty(gate.shape, device=gate.device, dtype=gate.dtype)
-    else:
-        _check_out(out, gate)
-    swiglu_out(gate, up, out)
-    return out
-
-
-def _as_mk(x: torch.Tensor) -> tuple[torch.Tensor, tuple[int, ...] | None]:
-    """Flatten x to ``[M, K]``; 2-D strided x passes through. Reference: ops.py:181-192."""
-    k = x.shape[-1]
-    if x.ndim == 1:
-        if not x.is_contiguous():
-            x = x.contiguous()
-        return x.view(1, k), None
-    leading = tuple(x.shape[:-1])
-    if x.ndim == 2 and x.stride(0) >= 0 and x.stride(1) >= 0:
-        return x, leading
-    if not x.is_contiguous():
-        x = x.contiguous()
-    return x.view(-1, k), leading
-
-
-def _as_row_add(row_add: torch.Tensor, m: int, n: int, expected: tuple[int, ...]) -> torch.Tensor:
-    """row_add as ``[M, N]``-indexable (size-1 dims broadcast). Reference: ops.py:195-209."""
-    if row_add.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise TypeError("row_add must be float16, bfloat16, or float32")
-    if row_add.ndim == 1 and row_add.numel() == n:
-        return row_add.view(1, n)
-    if row_add.shape == torch.Size(expected) and row_add.is_contiguous():
-        return row_add.view(m, n)
-    if row_add.ndim == 2 and row_add.shape[0] in (1, m) and row_add.shape[1] in (1, n):
-        return row_add
     try:
-        return row_add.expand(expected).contiguous().view(m, n)
+        key = ("swiglu", gate.shape, gate.stride(), gate.dtype, gate.device, up.shape, up.stride(), up.dtype,
+               up.device, _sig(out))
+        plan = _PLANS.get(key)
+    except AttributeError:
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_swiglu(gate, up, out))
+    return plan(gate, up, out)
+
+
+def _plan_swiglu(gate, up, out) -> Plan:
+    check("swiglu", gate=gate, up=up, out=out)
+    shape = tuple(gate.shape)
+    alloc = _empty(shape, gate)
+    strides = [tuple(gate.stride()), tuple(up.stride()),
+               contiguous_strides(shape) if out is None else tuple(out.stride())]
+    rows = plan_rows(shape, strides) if gate.numel() else None
+    if rows is None:
+        def general(g, u, out):
+            y = alloc(g) if out is None else out
+            swiglu_out(g, u, y)
+            return y
+        return general
+    rg, ru, ry = rows
+    call, act, dev = native().swiglu, DTYPE_CODE[gate.dtype], gate.device.index
+
+    def run(g, u, out):
+        y = alloc(g) if out is None else out
+        status = call(y.data_ptr(), g.data_ptr(), u.data_ptr(), rg, ru, ry, act, _raw_stream(dev))
+        if status:
+            fail("fd_swiglu", status)
+        return y
+    return run
+
+
+# ------------------------------------------------------------------ GEMV
+
+
+class _Rows(NamedTuple):
+    """How an operand is addressed as ``[M, X]`` rows: element (m, j) at
+    ``m * row + j * col``; ``flat`` re-derives the view per call when the
+    leading dims do not merge into one stride (a copy)."""
+
+    row: int
+    col: int
+    flat: bool
+
+
+def _as_rows(t: torch.Tensor, m: int) -> _Rows:
+    """``t [..., X]`` as ``m`` rows of X (1-D: one row), without a copy when the
+    leading dims merge into one stride."""
+    if t.ndim == 1:
+        return _Rows(0, int(t.stride(0)), False)
+    lead = [(s, st) for s, st in zip(t.shape[:-1], t.stride()[:-1]) if s != 1]
+    row = lead[-1][1] if lead else 0
+    for (s0, st0), (s1, st1) in zip(lead, lead[1:]):
+        if st0 != st1 * s1:
+            return _Rows(int(t.shape[-1]), 1, True)  # per-call contiguous copy
+    return _Rows(int(row), int(t.stride(-1)), False)
+
+
+def _row_add_rows(row_add: torch.Tensor, m: int, n: int, expected: tuple) -> tuple[int, int, bool]:
+    """Strides (srm, srn) that index ``row_add`` as the ``[M, N]`` output (0 for a
+    broadcast dim), or flat=True for a per-call contiguous copy. Legal shapes:
+    ``[N]``; 2-D with dims 1 or M and 1 or N; anything that broadcasts to the
+    output's shape (the set the reference accepts, ops.py:195-209)."""
+    shp = tuple(row_add.shape)
+    if row_add.ndim == 1 and shp[0] == n:
+        return 0, int(row_add.stride(0)), False
+    if row_add.ndim == 2 and shp[0] in (1, m) and shp[1] in (1, n):
+        return (0 if shp[0] == 1 else int(row_add.stride(0)),
+                0 if shp[1] == 1 else int(row_add.stride(1)), False)
+    try:
+        view = row_add.expand(expected)
     except RuntimeError as exc:
-        raise ValueError(
-            f"row_add shape {tuple(row_add.shape)} is not broadcastable to {expected}"
-        ) from exc
+        raise ValueError(f"row_add shape {shp} is not broadcastable to {expected}") from exc
+    r = _as_rows(view, m)
+    if r.flat:
+        return n, 1, True
+    return r.row, r.col, False
+
+
+def _check_out(out, expected: tuple, like: torch.Tensor) -> None:
+    if tuple(out.shape) != expected or out.dtype != like.dtype or out.device != like.device:
+        raise ValueError(f"out must be a contiguous {expected} tensor of dtype {like.dtype} on {like.device}")
+    if not out.is_contiguous():
+        raise ValueError("out must be contiguous")
 
 
 def linear_decode(
@@ -245,57 +407,79 @@ def linear_decode(
     ``F.linear`` (bit-identical to it), with row_add added in float32.
     Reference: ops.py:212-280.
     """
-    _check_activation(x, "x")
-    if weight.ndim != 2:
-        raise ValueError(f"weight must have shape [N, K], got {tuple(weight.shape)}")
-    if weight.device != x.device or weight.dtype != x.dtype:
-        raise ValueError("weight device and dtype must match x")
-    n, k = weight.shape
-    if x.shape[-1] != k:
-        raise ValueError(f"x last dim {x.shape[-1]} != weight K {k}")
-    hand_limit = _HAND_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
-    kind = resolve_kind(kind)
-    x2, leading = _as_mk(x)
-    m = x2.shape[0]
-    expected = (n,) if leading is None else (*leading, n)
-    if bias is not None:
-        if bias.ndim != 1 or bias.shape[0] != n:
-            raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
-        if bias.device != x.device:
-            raise ValueError("bias must be on the same device as x")
-        if bias.dtype not in (x.dtype, torch.float32):
-            raise TypeError("bias must match x or be float32")
-    ra = None
-    if row_add is not None:
-        if row_add.device != x.device:
-            raise ValueError("row_add must be on the same device as x")
-        ra = _as_row_add(row_add, m, n, expected)
-    if m > hand_limit and out is None:
-        produced = F.linear(x2, weight, bias)
-        if ra is not None:
-            produced = (produced.float() + ra.float()).to(dtype=x.dtype)
-        if x.ndim == 1:
-            return produced.view(n)
-        return produced.view(expected)
-    if out is None:
-        y_full = torch.empty(expected, device=x.device, dtype=x.dtype)
-    else:
-        if tuple(out.shape) != expected or out.dtype != x.dtype or out.device != x.device:
-            raise ValueError(f"out must be a contiguous {expected} tensor of dtype {x.dtype}")
-        if not out.is_contiguous():
-            raise ValueError("out must be contiguous")
-        y_full = out
-    y2 = y_full.view(m, n)
+    try:
+        key = ("linear", x.shape, x.stride(), x.dtype, x.device, weight.shape, weight.stride(), weight.dtype,
+               weight.device, _sig(bias), _sig(row_add), _sig(out), kind,
+               _env("FUSED_DECODE_LINEAR_KIND"), _env("FUSED_DECODE_LINEAR"))
+        plan = _PLANS.get(key)
+    except AttributeError:
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_linear(x, weight, bias, row_add, out, kind))
+    return plan(x, weight, bias, row_add, out)
+
+
+def _plan_linear(x, weight, bias, row_add, out, kind) -> Plan:
+    check("linear_decode", x=x, weight=weight, bias=bias, row_add=row_add, kind=kind)
+    limit = _FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
+    kind_r = resolve_kind(kind)
+    n, k = (int(d) for d in weight.shape)
+    m = 1 if x.ndim == 1 else math.prod(x.shape[:-1])
+    expected = (n,) if x.ndim == 1 else (*x.shape[:-1], n)
+    ra = None if row_add is None else _row_add_rows(row_add, m, n, expected)
+    if out is not None:
+        _check_out(out, expected, x)
+    alloc = _empty(expected, x)
     if m == 0 or n == 0:
-        return y_full
-    if m > hand_limit:
-        produced = F.linear(x2, weight, bias)
-        if ra is not None:
-            produced = (produced.float() + ra.float()).to(dtype=x.dtype)
-        y2.copy_(produced)
-        return y_full
-    linear_out(x2, weight, y2, bias=bias, row_add=ra, kind=kind)
-    return y_full
+        return lambda x, w, b, r, out: alloc(x) if out is None else out
+    xr = _as_rows(x, m)
+
+    def operands(x, r):
+        """x as [M, K] and row_add as [M, N]-indexable tensors for F.linear."""
+        x2 = x.reshape(m, k)
+        if r is None:
+            return x2, None
+        if r.ndim == 1 or (r.ndim == 2 and r.shape[0] in (1, m) and r.shape[1] in (1, n)):
+            return x2, r
+        return x2, r.expand(expected).reshape(m, n)
+
+    if m > limit:  # hipBLASLt, bit-identical to F.linear; row_add in float32, one rounding
+        def fallback(x, w, b, r, out):
+            x2, r2 = operands(x, r)
+            y = F.linear(x2, w, b)
+            if r2 is not None:
+                y = (y.float() + r2.float()).to(x.dtype)
+            if out is None:
+                return y.view(expected)
+            out.view(m, n).copy_(y)
+            return out
+        return fallback
+
+    rows, _, waves, stages = linear_config(kind_r, n, k, m)
+    tile = bytes(FdTile(rows, waves, stages))
+    call, act, kcode, dev = native().linear_tiled, DTYPE_CODE[x.dtype], KIND_CODE[kind_r], x.device.index
+    swn, swk = int(weight.stride(0)), int(weight.stride(1))
+    bcode = DTYPE_CODE[bias.dtype] if bias is not None else act
+    sb = int(bias.stride(0)) if bias is not None else 0
+    rcode = DTYPE_CODE[row_add.dtype] if row_add is not None else act
+    srm, srn, r_flat = ra if ra is not None else (0, 0, False)
+
+    def run(x, w, b, r, out):
+        y = alloc(x) if out is None else out
+        if xr.flat:
+            x = x.reshape(m, k)
+        if r_flat:
+            r = r.expand(expected).reshape(m, n)
+        status = call(y.data_ptr(), x.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(), bcode,
+                      None if r is None else r.data_ptr(), rcode, m, n, k, xr.row, xr.col, swn, swk, sb, srm,
+                      srn, n, 1, tile, kcode, act, _raw_stream(dev))
+        if status:
+            fail("fd_linear_tiled", status)
+        return y
+    return run
+
+
+# ------------------------------------------------------------------ fused blocks
 
 
 def post_attn_mlp(
@@ -315,39 +499,51 @@ def post_attn_mlp(
     row limit this is two HIP launches: norm + gate/up GEMV + SwiGLU fused, then
     the down GEMV with the residual fused. Reference: ops.py:283-315.
     """
-    _check_activation(hidden, "hidden")
-    if w_gate_up.ndim != 2 or w_down.ndim != 2:
-        raise ValueError("w_gate_up and w_down must be rank-2")
-    two_i, h = w_gate_up.shape
-    h_down, i = w_down.shape
-    if two_i != 2 * i or h != h_down or hidden.shape[-1] != h:
-        raise ValueError(
-            f"expected w_gate_up [2I, H] and w_down [H, I] with hidden [..., H], "
-            f"got {tuple(w_gate_up.shape)}, {tuple(w_down.shape)}, {tuple(hidden.shape)}"
-        )
-    if w_gate_up.dtype != hidden.dtype or w_down.dtype != hidden.dtype:
-        raise TypeError("MLP weights must match hidden dtype")
-    if w_gate_up.device != hidden.device or w_down.device != hidden.device:
-        raise ValueError("MLP weights must be on the same device as hidden")
-    _check_norm_weight(norm_weight, hidden)
-    eps = _check_eps(eps)
-    hand_limit = _HAND_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
+    try:
+        key = ("mlp", _sig(hidden), _sig(norm_weight), _sig(w_gate_up), _sig(w_down), eps, kind,
+               _env("FUSED_DECODE_LINEAR_KIND"))
+        plan = _PLANS.get(key)
+    except AttributeError:
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_mlp(hidden, norm_weight, w_gate_up, w_down, eps, kind))
+    return plan(hidden, norm_weight, w_gate_up, w_down)
+
+
+def _plan_mlp(hidden, norm_weight, w_gate_up, w_down, eps, kind) -> Plan:
+    a = check("post_attn_mlp", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up, w_down=w_down,
+              eps=eps, kind=kind)
+    eps = a["eps"]
+    limit = _FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
     kind_r = resolve_kind(kind)
+    h, i = int(w_gate_up.shape[1]), int(w_down.shape[1])
     m = hidden.numel() // h if h else 0
-    if 0 < m <= hand_limit and w_gate_up.is_contiguous() and w_down.is_contiguous():
-        h2 = hidden.reshape(m, h)
-        if not h2.is_contiguous():
-            h2 = h2.contiguous()
-        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
-        y = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
-        mid = torch.empty((m, i), device=hidden.device, dtype=hidden.dtype)
-        status = post_attn_mlp_out(h2, nw, w_gate_up, w_down, eps, y, mid, kind_r)
-        if status == _lib.FD_OK:
-            return y.view(hidden.shape)
-    normed = rms_norm(hidden, norm_weight, eps=eps)
-    gate_up = linear_decode(normed, w_gate_up, kind=kind)
-    gate, up = gate_up.split(i, dim=-1)
-    return linear_decode(swiglu(gate, up), w_down, row_add=hidden, kind=kind)
+
+    def composed(x, nw, wgu, wd):
+        normed = rms_norm(x, nw, eps=eps)
+        gate, up = linear_decode(normed, wgu, kind=kind).split(i, dim=-1)
+        return linear_decode(swiglu(gate, up), wd, row_add=x, kind=kind)
+
+    if not (0 < m <= limit and w_gate_up.is_contiguous() and w_down.is_contiguous()):
+        return composed
+    shape = tuple(hidden.shape)
+    dense_h, dense_nw = _dense(hidden), _dense(norm_weight)
+    call, act, nwc, kcode, dev = (native().post_attn_mlp, DTYPE_CODE[hidden.dtype], DTYPE_CODE[norm_weight.dtype],
+                                  KIND_CODE[kind_r], hidden.device.index)
+
+    def fused(x, nw, wgu, wd):
+        x2 = x if dense_h else x.contiguous()
+        nw = nw if dense_nw else nw.contiguous()
+        y = x2.new_empty((m, h))
+        mid = x2.new_empty((m, i))
+        status = call(y.data_ptr(), mid.data_ptr(), x2.data_ptr(), nw.data_ptr(), nwc, wgu.data_ptr(),
+                      wd.data_ptr(), m, h, i, eps, kcode, act, _raw_stream(dev))
+        if status == FD_EUNSUPPORTED:  # e.g. H % 8 or an unaligned operand: the composed operators
+            return composed(x, nw, wgu, wd)
+        if status:
+            fail("fd_post_attn_mlp", status)
+        return y.view(shape)
+    return fused
 
 
 def _token_angles(src: torch.Tensor, lead: tuple, name: str) -> torch.Tensor:
@@ -385,12 +581,8 @@ class _QkvArgs(NamedTuple):
 
 
 def _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out) -> _QkvArgs:
-    """Checks and operands shared by ``pre_attn_qkv`` and its fp8 form, for a
-    projection of ``n`` rows over ``h`` (``hidden [..., h]``)."""
-    if hidden.shape[-1] != h:
-        raise ValueError(f"hidden last dim {hidden.shape[-1]} != w_qkv H {h}")
-    _check_norm_weight(norm_weight, hidden)
-    eps = _check_eps(eps)
+    """Operands shared by ``pre_attn_qkv`` and its fp8 form, for a projection of
+    ``n`` rows over ``h`` (``hidden [..., h]``), after the contract's checks."""
     for name, t in (("cos", cos), ("sin", sin)):
         if isinstance(t, torch.Tensor) and t.device != hidden.device:
             raise ValueError(f"{name} is on {t.device}, expected {hidden.device}")
@@ -402,13 +594,6 @@ def _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out) ->
         raise ValueError("rope head dimension must be even")
     if rope_cols < 0 or rope_cols > n or rope_cols % d != 0:
         raise ValueError(f"rope_cols must be a multiple of {d} in [0, {n}], got {rope_cols}")
-    if bias is not None:
-        if bias.ndim != 1 or bias.shape[0] != n:
-            raise ValueError(f"bias must have shape ({n},), got {tuple(bias.shape)}")
-        if bias.device != hidden.device:
-            raise ValueError("bias must be on the same device as hidden")
-        if bias.dtype not in (hidden.dtype, torch.float32):
-            raise TypeError("bias must match hidden or be float32")
     lead = tuple(hidden.shape[:-1])
     cos_r = _token_angles(cos, lead, "cos")
     sin_r = _token_angles(sin, lead, "sin")
@@ -418,15 +603,12 @@ def _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out) ->
     if out is None:
         out = torch.empty(expected, device=hidden.device, dtype=hidden.dtype)
     else:
-        if tuple(out.shape) != expected or out.dtype != hidden.dtype or out.device != hidden.device:
-            raise ValueError(f"out must be a contiguous {expected} tensor of dtype {hidden.dtype}")
-        if not out.is_contiguous():
-            raise ValueError("out must be contiguous")
+        _check_out(out, expected, hidden)
     m = hidden.numel() // h if h else 0
     if m and n and cos_r.shape[0] not in (1, m):
         raise ValueError(f"cos/sin need 1 or {m} rows, got {cos_r.shape[0]}")
     rs = 0 if cos_r.shape[0] == 1 else d
-    return _QkvArgs(m, n, h, d, rope_cols, eps, cos_r, sin_r, rs, out)
+    return _QkvArgs(m, n, h, d, rope_cols, float(eps), cos_r, sin_r, rs, out)
 
 
 def _rope_qkv_heads(a: _QkvArgs) -> None:
@@ -464,21 +646,16 @@ def pre_attn_qkv(
     No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
     :138-160.
     """
-    _check_activation(hidden, "hidden")
-    if w_qkv.ndim != 2:
-        raise ValueError(f"w_qkv must have shape [N, H], got {tuple(w_qkv.shape)}")
+    a0 = check("pre_attn_qkv", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, eps=eps, kind=kind,
+               bias=bias)
     n, h = w_qkv.shape
-    if w_qkv.dtype != hidden.dtype:
-        raise TypeError("w_qkv must match hidden dtype")
-    if w_qkv.device != hidden.device:
-        raise ValueError("w_qkv must be on the same device as hidden")
-    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
     out, m, eps = a.out, a.m, a.eps
     if m == 0 or n == 0:
         return out
-    hand_limit = _HAND_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
+    limit = _FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
     kind_r = resolve_kind(kind)
-    if m <= hand_limit and w_qkv.is_contiguous():
+    if m <= limit and w_qkv.is_contiguous():
         h2 = hidden.reshape(m, h)
         if not h2.is_contiguous():
             h2 = h2.contiguous()

@@ -200,3 +200,37 @@ def test_mlp_rejects_overlapping_buffers(L):
         assert call(hid + 2 * h, mid) == L.FD_EINVAL          # y starts inside hidden's rows
         assert call(y_ok, hid + 16) == L.FD_EINVAL and b"mid" in lib.fd_last_error()
         assert call(y_ok, y_ok) == L.FD_EINVAL
+
+
+def _header_signatures() -> dict[str, str]:
+    """Argument codes of every entry point the header declares (p pointer, s stream,
+    i int, l int64_t, f float, r fd_rows*, t fd_tile*)."""
+    sigs = {}
+    for m in re.finditer(r"^(?:int|const char\*)\s+(fd_\w+)\(([^;]*?)\);", HEADER.read_text(), re.M | re.S):
+        codes = []
+        for p in (q.strip() for q in m.group(2).replace("\n", " ").split(",")):
+            if not p or p == "void":
+                continue
+            if "fd_rows*" in p:
+                codes.append("r")
+            elif "fd_tile*" in p:
+                codes.append("t")
+            elif p.startswith("void* stream"):
+                codes.append("s")
+            elif "*" in p:
+                codes.append("p")
+            else:
+                codes.append({"int64_t": "l", "int": "i", "float": "f"}[p.split()[0]])
+        sigs[m.group(1)] = "".join(codes)
+    return sigs
+
+
+def test_python_binding_matches_the_header():
+    """fdcall.c converts each entry point's arguments by a code string: it must
+    match the declaration in include/fused_decode.h argument for argument."""
+    src = (ROOT / "fused-decode_amd" / "csrc" / "fdcall.c").read_text()
+    sigs = _header_signatures()
+    wrapped = dict(re.findall(r'WRAP\((\w+), "(\w+)"', src))
+    assert wrapped, "no wrappers found"
+    for name, fmt in wrapped.items():
+        assert sigs["fd_" + name] == fmt, name
