@@ -12,7 +12,8 @@ A step is one post_attn_mlp call launched eagerly (the reference's method,
 bench.py:42-56: back-to-back calls between events); W untimed warmup steps,
 then exactly K timed steps between HIP events, bracketed by synchronisation.
 `value` is microseconds per step at M=1 (lower is better). The same steps
-replayed one HIP graph per call (`graph_us`) and the 32-layer decode step
+replayed from a HIP graph holding 100 steps (`graph_us`), from one graph
+per call (`graph_per_call_us`, the reference's _graph_time), and the 32-layer decode step
 minus attention, graph-captured (`decode_step`: the fused form with
 pre_attn_qkv, and the reference's operators composed), are reported beside it.
 
@@ -20,8 +21,14 @@ roofline: the dominant kernel, the fused RMSNorm + gate/up GEMV + SwiGLU
 launch, timed alone with HIP events on the stream it is launched on;
 achieved = its algorithmic bytes / its average duration.
 
-cpu_baseline: the NumPy oracle of the same block at M=1 on the host cores
-(a bounded sample of calls), in the same unit.
+ops: one compact row per norm, SwiGLU, RoPE and decode-GEMV benchmark
+configuration (device and eager microseconds, GB/s, % of the copy roof and of
+8 TB/s, and the largest deviation from the reference's float32 formulas).
+
+cpu_baseline: the reference's eager formula of the same block
+(src/fused_decode/bench.py:395-398: F.rms_norm, F.linear, F.silu, F.linear + residual)
+run by PyTorch on the host CPU in fp16 at M=1, over a bounded sample of calls,
+with the thread count and CPU model.
 """
 
 from __future__ import annotations
@@ -41,6 +48,7 @@ for _p in (ROOT, ROOT / "fused-decode_amd"):
 H, I = 4096, 14336
 EPS = 1e-5
 N_SETS = 4
+GRAPH_ROTATIONS = 25  # the graph_us graph holds 25 rotations of the 4 weight sets: 100 steps per launch
 HBM_PEAK_GBS = 8000.0
 
 
@@ -50,8 +58,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=8.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-decode-step", action="store_true", help="skip the 32-layer decode step")
+    ap.add_argument("--no-ops", action="store_true", help="skip the per-op block")
     return ap.parse_args()
 
 
@@ -67,9 +76,14 @@ def make_sets(torch, m: int, dtype, dev):
     return sets
 
 
-def time_graph_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None) -> float:
-    """Microseconds per step: step s replays the captured MLP of weight set s % N_SETS."""
-    graphs, outs = [], []
+def time_graph_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None) -> tuple[float, float]:
+    """Microseconds per step of the same rotation replayed from HIP graphs, two ways:
+    one graph holding GRAPH_ROTATIONS rotations of the N_SETS steps (what a decode
+    loop that captures its whole step does), and one graph per call (the
+    reference's _graph_time, bench.py:451-472). Every hipGraphLaunch leaves the
+    GPU idle for about 4 us before its first kernel (measured: one step per graph
+    +4.2 us/step, four steps +0.4, twenty steps none), so the second pays that
+    once per step."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -77,21 +91,34 @@ def time_graph_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None)
             fd.post_attn_mlp(*st, EPS, kind=kind)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
+    whole = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(whole):
+        for st in sets * GRAPH_ROTATIONS:
+            fd.post_attn_mlp(*st, EPS, kind=kind)
+    per_call = []
     for st in sets:
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
-            outs.append(fd.post_attn_mlp(*st, EPS, kind=kind))
-        graphs.append(gr)
-    for s in range(warmup):
-        graphs[s % N_SETS].replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for s in range(steps):
-        graphs[s % N_SETS].replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1000.0 / steps
+            fd.post_attn_mlp(*st, EPS, kind=kind)
+        per_call.append(gr)
+
+    def timed(run, n):
+        for s in range(max(2, warmup // per_replay)):
+            run(s)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for s in range(n):
+            run(s)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1000.0
+
+    per_replay = N_SETS * GRAPH_ROTATIONS
+    reps = max(1, steps // per_replay)
+    rotation_us = timed(lambda s: whole.replay(), reps) / (reps * per_replay)
+    per_call_us = timed(lambda s: per_call[s % N_SETS].replay(), steps) / steps
+    return rotation_us, per_call_us
 
 
 def time_eager_steps(torch, fd, sets, steps: int, warmup: int, kind: str | None) -> float:
@@ -166,38 +193,57 @@ def pmc_traffic() -> int | None:
         return None
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """NumPy oracle of the same block at M=1, fp16 semantics, bounded sample."""
-    import numpy as np
-
-    from oracle import decode_oracle as O
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        threads = max((d.get("num_threads", 1) for d in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
-    rng = np.random.default_rng(7)
-    hid = O.round_to(rng.standard_normal((1, H), dtype=np.float32), "f16")
-    nw = O.round_to(1 + 0.1 * rng.standard_normal(H, dtype=np.float32), "f16")
-    wgu = O.round_to(rng.standard_normal((2 * I, H), dtype=np.float32) * np.float32(H ** -0.5), "f16")
-    wd = O.round_to(rng.standard_normal((H, I), dtype=np.float32) * np.float32(I ** -0.5), "f16")
-    O.post_attn_mlp(hid, nw, wgu, wd, EPS, "f16")  # warm
+
+def cpu_baseline(torch, seconds: float) -> dict:
+    """The reference's eager MLP block (bench.py:395-398) on the host CPU, fp16,
+    M=1, Llama-3-8B widths, random weights of the benchmark's distributions:
+    microseconds per call over a bounded sample. Threads: the job's share of the
+    host (OMP_NUM_THREADS when set, else the CPUs this process may run on)."""
+    import torch.nn.functional as F
+
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    threads = min(allowed, int(os.environ.get("OMP_NUM_THREADS") or allowed))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(7)
+    dt = torch.float16
+    hid = torch.randn(1, H, generator=g).to(dt)
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(dt)
+    wgu = (torch.randn(2 * I, H, generator=g) * H ** -0.5).to(dt)
+    wd = (torch.randn(H, I, generator=g) * I ** -0.5).to(dt)
+
+    def block():
+        h = F.rms_norm(hid, (H,), nw, EPS)
+        gate, up = F.linear(h, wgu).split(I, dim=-1)
+        return F.linear(F.silu(gate) * up, wd) + hid
+
+    block()  # warm
     calls, t0 = 0, time.perf_counter()
     while True:
-        O.post_attn_mlp(hid, nw, wgu, wd, EPS, "f16")
+        block()
         calls += 1
         el = time.perf_counter() - t0
-        if el >= seconds or calls >= 5000:
+        if el >= seconds or calls >= 20000:
             break
     return {
-        "value": el / calls * 1e6,
+        "value": round(el / calls * 1e6, 1),
         "unit": "us",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{calls} calls of the NumPy oracle post_attn_mlp at M=1, H=4096, I=14336 "
-                  f"(fp32 math, fp16 rounding points), {el:.1f} s",
+        "sample": f"{calls} calls of the reference's eager post_attn_mlp block (bench.py:395-398) on torch "
+                  f"{torch.__version__} CPU, fp16, M=1, H=4096, I=14336, {el:.1f} s",
+        "cpu_model": _cpu_model(),
+        "cpus_visible": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
     }
 
 
@@ -227,13 +273,16 @@ def main() -> None:
     results = {}
     for m in (1, 8):
         sets = make_sets(torch, m, dtype, dev)
+        graph_us, graph_per_call_us = time_graph_steps(torch, fd, sets, args.steps, args.warmup, None)
         results[m] = {
-            "graph_us": time_graph_steps(torch, fd, sets, args.steps, args.warmup, None),
+            "graph_us": graph_us,
+            "graph_per_call_us": graph_per_call_us,
             "eager_us": time_eager_steps(torch, fd, sets, args.steps, args.warmup, None),
         }
         if m == 1:
             gate_us = time_gate_up_kernel(torch, lib(), sets, m, max(args.steps, 50), KIND_CODE[kind])
-        progress(f"post_attn_mlp M={m}: eager {results[m]['eager_us']:.2f} us, graph {results[m]['graph_us']:.2f} us")
+        progress(f"post_attn_mlp M={m}: eager {results[m]['eager_us']:.2f} us, graph {results[m]['graph_us']:.2f} us, "
+                 f"one graph per call {results[m]['graph_per_call_us']:.2f} us")
         del sets
         torch.cuda.empty_cache()
 
@@ -261,7 +310,12 @@ def main() -> None:
             "m": 1,
         },
         "m8_us": round(results[8]["eager_us"], 3),
-        "graph_us": {"m1": round(results[1]["graph_us"], 3), "m8": round(results[8]["graph_us"], 3)},
+        "graph_us": {"m1": round(results[1]["graph_us"], 3), "m8": round(results[8]["graph_us"], 3),
+                     "method": "one HIP graph holding 100 steps (25 rotations of the 4 weight sets), per step"},
+        "graph_per_call_us": {"m1": round(results[1]["graph_per_call_us"], 3),
+                              "m8": round(results[8]["graph_per_call_us"], 3),
+                              "method": "one HIP graph per call (the reference's _graph_time): each "
+                                        "hipGraphLaunch adds an idle gap before its first kernel"},
         "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
         "copy_roof_gbs": round(roof, 1),
         "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
@@ -299,8 +353,18 @@ def main() -> None:
             "32-layer Llama-3-8B decode step minus attention, hipGraph; fused = pre_attn_qkv + "
             "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed, "
             "fp8 = the fused layer with E4M3 projection weights (gbs over its own weight bytes)")
+    if not args.no_ops:
+        from fused_decode.bench import ops_block
+
+        line["ops"] = ops_block(roof, log=lambda row: progress(
+            f"{row['op']} {row['shape']} {row['dtype']} {row.get('kind', '')}: dev {row['dev_us']} us, "
+            f"eager {row['eager_us']} us, {row['pct_copy_roof']}% of copy roof, max_abs {row['max_abs_vs_fp32']:.3g}"))
+        line["ops_note"] = ("dev_us: one HIP graph over rotated buffer sets (HBM reads); eager_us: allocating calls "
+                            "back to back; gbs and pct_* from dev_us and the reference's useful bytes; "
+                            "max_abs_vs_fp32 against the reference's formulas in float32, rounded once")
+        torch.cuda.empty_cache()
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
         progress("cpu baseline done")
     print(json.dumps(line), flush=True)
 

@@ -442,6 +442,214 @@ def bench_fp8(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
+# ------------------------------------------------------------------ ops block
+#
+# One compact row per benchmark configuration of the norms, SwiGLU, RoPE and the
+# decode GEMV, for the headline bench line. `max_abs_vs_fp32` compares each op
+# with the reference's PyTorch formulas (reference.py:14-63) evaluated in float32
+# on the GPU and rounded once, as the reference's bench does (bench.py:224-227,
+# :373-374).
+
+
+def fp32_rms(x, w, eps, residual=None):
+    """(y, residual_out) of the reference's rms_norm / add_rms_norm formula."""
+    s = x.float() if residual is None else x.float() + residual.float()
+    y = s * torch.rsqrt(s.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    return y.to(x.dtype), s.to(x.dtype)
+
+
+def fp32_swiglu(gate, up):
+    return (F.silu(gate.float()) * up.float()).to(gate.dtype)
+
+
+def fp32_rope(x, cos, sin):
+    h = x.shape[-1] // 2
+    xf, c, s = x.float(), cos.float().expand(x.shape), sin.float().expand(x.shape)
+    return torch.cat((xf[..., :h] * c[..., :h] - xf[..., h:] * s[..., :h],
+                      xf[..., h:] * c[..., h:] + xf[..., :h] * s[..., h:]), -1).to(x.dtype)
+
+
+def fp32_linear(x, w, bias=None, row_add=None):
+    y = x.float() @ w.float().t()
+    if bias is not None:
+        y = y + bias.float()
+    if row_add is not None:
+        y = y + row_add.float()
+    return y.to(x.dtype)
+
+
+def _max_abs(a, b) -> float:
+    return float((a.float() - b.float()).abs().max().item())
+
+
+def _compact(op, shape, dtype, nbytes, dev_us, eager_us, roof, max_abs, **extra) -> dict:
+    gbs = nbytes / (dev_us * 1e-6) / 1e9
+    row = {"op": op, "shape": list(shape), "dtype": str(dtype).replace("torch.", ""), "bytes": nbytes,
+           "dev_us": round(dev_us, 2), "eager_us": round(eager_us, 2), "gbs": round(gbs, 1),
+           "eager_gbs": round(nbytes / (eager_us * 1e-6) / 1e9, 1),
+           "pct_copy_roof": round(100.0 * gbs / roof, 1), "pct_8tbs": round(100.0 * gbs / DATASHEET_GBS, 1),
+           "max_abs_vs_fp32": max_abs}
+    row.update({k: (round(v, 2) if isinstance(v, float) else v) for k, v in extra.items()})
+    return row
+
+
+def ops_block(roof: float, log=print) -> list[dict]:
+    """Every norm, SwiGLU, RoPE and GEMV benchmark configuration: device time (one
+    HIP graph over rotated buffer sets, so each call reads HBM), eager time (back
+    to back allocating calls over the same rotation, the reference's method),
+    GB/s of the device time, % of the copy roof and of 8 TB/s, and the largest
+    deviation from the float32 formula."""
+    rows = []
+    g = torch.Generator(device="cuda").manual_seed(11)
+    eps = 1e-5
+
+    def timed(call, k, iters=None):
+        dev = graph_us(call, k)
+        eager = time_us(call, iters=iters or max(30, 2 * k), warmup=5, rounds=3)
+        return dev, eager
+
+    # norms: x, residual ~N(0,1), weight ~N(1, 0.1), eps 1e-5, residual_out in place
+    for r in (8192, 1):
+        dt, h = torch.float16, LLAMA_H
+        e = 2
+        k = copies_for(4 * r * h * e)
+        xs = [_gen((r, h), dt, g) for _ in range(k)]
+        rs = [_gen((r, h), dt, g) for _ in range(k)]
+        w = _gen((h,), dt, g, 0.1, 1.0)
+        err = _max_abs(rms_norm(xs[0], w, eps), fp32_rms(xs[0], w, eps)[0])
+        dev, eager = timed(lambda i: rms_norm(xs[i % k], w, eps), k)
+        rows.append(_compact("rms_norm", (r, h), dt, (2 * r * h + h) * e, dev, eager, roof, err))
+        y_ref, ro_ref = fp32_rms(xs[0], w, eps, rs[0])
+        r0 = rs[0].clone()
+        y, ro = add_rms_norm(xs[0], r0, w, eps, residual_out=r0)
+        err = max(_max_abs(y, y_ref), _max_abs(ro, ro_ref))
+        dev, eager = timed(lambda i: add_rms_norm(xs[i % k], rs[i % k], w, eps, residual_out=rs[i % k]), k)
+        rows.append(_compact("add_rms_norm", (r, h), dt, (4 * r * h + h) * e, dev, eager, roof, err))
+        log(rows[-2]), log(rows[-1])
+        del xs, rs
+    # SwiGLU: gate, up ~N(0, 2)
+    for dt in (torch.float16, torch.bfloat16):
+        for r in (2048, 1):
+            n = LLAMA_I
+            k = copies_for(3 * r * n * 2)
+            gs = [_gen((r, n), dt, g, 2.0) for _ in range(k)]
+            us_ = [_gen((r, n), dt, g, 2.0) for _ in range(k)]
+            err = _max_abs(swiglu(gs[0], us_[0]), fp32_swiglu(gs[0], us_[0]))
+            dev, eager = timed(lambda i: swiglu(gs[i % k], us_[i % k]), k)
+            rows.append(_compact("swiglu", (r, n), dt, 3 * r * n * 2, dev, eager, roof, err))
+            log(rows[-1])
+            del gs, us_
+    # RoPE with Llama-3 tables (theta 500000), cos/sin [2048, 128] viewed [2048, 1, 128]
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float64, device="cuda") / 128))
+    emb = torch.cat([torch.outer(torch.arange(2048, dtype=torch.float64, device="cuda"), inv)] * 2, -1)
+    for dt in (torch.float16, torch.bfloat16):
+        cos_t, sin_t = emb.cos().to(dt), emb.sin().to(dt)
+        for xshape, c, s_ in (((1, 2048, 32, 128), cos_t.view(2048, 1, 128), sin_t.view(2048, 1, 128)),
+                              ((1, 1, 32, 128), cos_t[1024].view(1, 1, 128), sin_t[1024].view(1, 1, 128))):
+            nbytes = 2 * math.prod(xshape) * 2 + 2 * c.numel() * 2
+            k = copies_for(nbytes)
+            xs = [_gen(xshape, dt, g) for _ in range(k)]
+            err = _max_abs(rope(xs[0], c, s_), fp32_rope(xs[0], c, s_))
+            dev, eager = timed(lambda i: rope(xs[i % k], c, s_), k)
+            rows.append(_compact("rope", xshape, dt, nbytes, dev, eager, roof, err))
+            log(rows[-1])
+            del xs
+    # decode GEMV: x ~N(0,1), W ~N(0, 1/sqrt(K)), bias and row_add in the error check
+    for dt, kinds in ((torch.float16, ("dot", "simt")), (torch.bfloat16, ("dot",))):
+        for n, kk in ((4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)):
+            k = copies_for(n * kk * 2)
+            ws = [_gen((n, kk), dt, g, kk ** -0.5) for _ in range(k)]
+            bias, wf = _gen((n,), dt, g), ws[0]
+            for m in (1, 2, 4, 8, 16):
+                x = _gen((m, kk), dt, g)
+                ra = _gen((m, n), dt, g)
+                ref = fp32_linear(x, wf, bias, ra)
+                hip = graph_us(lambda i: F.linear(x, ws[i % k]), k) if dt == torch.float16 else None
+                for kind in kinds:
+                    err = _max_abs(linear_decode(x, wf, bias, row_add=ra, kind=kind), ref)
+                    dev, eager = timed(lambda i: linear_decode(x, ws[i % k], kind=kind), k)
+                    extra = {"kind": kind}
+                    if hip is not None:
+                        extra["hipblaslt_dev_us"] = hip
+                    rows.append(_compact("linear_decode", (m, n, kk), dt, (m * kk + n * kk + m * n) * 2, dev, eager,
+                                         roof, err, **extra))
+                    log(rows[-1])
+            del ws
+            torch.cuda.empty_cache()
+    torch.cuda.empty_cache()
+    return rows
+
+
+def bench_graph_modes(dtype) -> list[dict]:
+    """post_attn_mlp at Llama-3-8B widths, M = 1 and 8, over a rotation of 4 weight
+    sets: per-step time launched eagerly, and replayed from HIP graphs holding 1,
+    4 or 20 steps. Each hipGraphLaunch leaves the GPU idle before its first
+    kernel (a kernel trace of this function shows the gaps), so the per-step cost
+    of graph replay depends on how many steps one graph holds."""
+    g = torch.Generator(device="cuda").manual_seed(6)
+    h, i_, ns = LLAMA_H, LLAMA_I, 4
+    rows = []
+    for m in (1, 8):
+        sets = [(_gen((m, h), dtype, g), _gen((h,), dtype, g, 0.1, 1.0), _gen((2 * i_, h), dtype, g, h ** -0.5),
+                 _gen((h, i_), dtype, g, i_ ** -0.5)) for _ in range(ns)]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for st in sets:
+                post_attn_mlp(*st, 1e-5)
+        torch.cuda.current_stream().wait_stream(side)
+        _sync()
+        row = {"name": f"post_attn_mlp M={m} {dtype} graph modes"}
+        marker_a = torch.zeros(16, dtype=torch.uint8, device="cuda")
+        marker_b = torch.empty_like(marker_a)
+        launch_copy(marker_b, marker_a)  # phase marker in a kernel trace (copy_vec_kernel)
+        row["eager_us"] = time_us(lambda j: post_attn_mlp(*sets[j % ns], 1e-5), iters=120, warmup=8, rounds=3)
+        for per in (1, 4, 20):
+            launch_copy(marker_b, marker_a)
+            graphs = []
+            for first in range(0, ns if per == 1 else 1):
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for j in range(per):
+                        post_attn_mlp(*sets[(first + j) % ns], 1e-5)
+                graphs.append(gr)
+            us = time_us(lambda j: graphs[j % len(graphs)].replay(), iters=max(6, 120 // per), warmup=2, rounds=3)
+            row[f"graph_{per}_steps_us"] = us / per
+            del graphs
+        rows.append(row)
+        print(json.dumps({k: (round(v, 2) if isinstance(v, float) else v) for k, v in row.items()}), flush=True)
+        del sets
+        torch.cuda.empty_cache()
+    return rows
+
+
+def trace_gaps(csv_path: str) -> None:
+    """Summarise a rocprofv3 kernel-trace CSV of ``--only graph``: per phase
+    (between copy_vec_kernel markers), the kernels' mean durations and the idle
+    gaps between one kernel's end and the next one's start."""
+    import csv
+
+    with open(csv_path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    phases, cur = [], []
+    for r in rows:
+        if "copy_vec_kernel" in r["Kernel_Name"]:
+            phases.append(cur)
+            cur = []
+        else:
+            cur.append(r)
+    phases.append(cur)
+    names = [f"M={m} {mode}" for m in (1, 8) for mode in ("eager", "graph of 1 step", "graph of 4 steps",
+                                                            "graph of 20 steps")]
+    for name, ph in zip(names, [p for p in phases if p][-8:]):
+        gaps = [(int(b["Start_Timestamp"]) - int(a["End_Timestamp"])) / 1e3 for a, b in zip(ph, ph[1:])]
+        busy = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in ph) / 1e3
+        big = [g for g in gaps if g > 1.0]
+        print(f"{name:22s} {len(ph):4d} kernels  busy {busy / max(1, len(ph)):7.2f} us/kernel  "
+              f"idle gaps > 1 us: {len(big):3d} (mean {statistics.mean(big) if big else 0.0:5.2f} us)  "
+              f"all gaps mean {statistics.mean(gaps) if gaps else 0.0:5.2f} us")
+
+
 TIE_BAND = 1.05  # per-shape slack of the cutoff rule
 
 
@@ -516,10 +724,15 @@ def main() -> None:
     ap.add_argument("--quick", action="store_true")
     ap.add_argument("--dtype", choices=["fp16", "bf16", "both"], default="fp16")
     ap.add_argument("--no-cpu", action="store_true", help="skip PyTorch-eager-on-CPU timings")
-    ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv", "fp8"], default=None)
+    ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv", "fp8", "graph"], default=None)
     ap.add_argument("--tune", action="store_true", help="GEMV tile search (writes --tune-out if given)")
     ap.add_argument("--tune-out", default=None)
+    ap.add_argument("--trace-gaps", default=None, metavar="CSV",
+                    help="summarise a rocprofv3 kernel trace of --only graph and exit")
     args = ap.parse_args()
+    if args.trace_gaps:
+        trace_gaps(args.trace_gaps)
+        return
     _lib.lib()
     torch.cuda.set_device(0)
     if args.tune:
@@ -534,6 +747,9 @@ def main() -> None:
         "os_cpu_count": os.cpu_count(),
         "cache_note": f"cold = rotation over >= {ROTATE_TARGET >> 20} MiB of distinct buffers; warm = same buffers",
     }
+    if args.only == "graph":
+        bench_graph_modes(torch.float16)
+        return
     roof = bench_roofline()
     payload["roofline"] = roof
     print(f"copy roof {roof['copy_gbs']:.1f} GB/s  triad {roof['triad_gbs']:.1f} GB/s  (datasheet {DATASHEET_GBS:.0f})", flush=True)

@@ -92,8 +92,8 @@ def clear_plans() -> None:
 
 
 def _sig(t):
-    """Signature of an optional tensor argument."""
-    return None if t is None else (t.shape, t.stride(), t.dtype, t.device)
+    """Signature of an optional tensor argument (the device as its index: -1 is the CPU)."""
+    return None if t is None else (t.shape, t.stride(), t.dtype, t.get_device())
 
 
 # os.environ keeps its values in a bytes-keyed dict on POSIX; reading that dict
@@ -138,8 +138,9 @@ def rms_norm(
     """RMSNorm over the last dimension with a float32 reduction. ``weight`` is ``(N,)``
     (float16, bfloat16 or float32). Reference: ops.py:72-88."""
     try:
-        key = ("rms", x.shape, x.stride(), x.dtype, x.device, weight.shape, weight.stride(), weight.dtype,
-               weight.device, eps, _sig(out), _env("FUSED_DECODE_RMS_BLOCK"), _env("FUSED_DECODE_RMS_WARPS"))
+        key = ("rms", x.shape, x.stride(), x.dtype, x.get_device(), weight.shape, weight.stride(), weight.dtype,
+               weight.get_device(), eps, None if out is None else _sig(out), _env("FUSED_DECODE_RMS_BLOCK"),
+               _env("FUSED_DECODE_RMS_WARPS"))
         plan = _PLANS.get(key)
     except AttributeError:  # not a tensor: let the contract say so
         key, plan = None, None
@@ -161,10 +162,10 @@ def add_rms_norm(
     rounded stored residual). ``residual_out=residual`` updates the residual
     stream in place. Reference: ops.py:91-119."""
     try:
-        key = ("add_rms", x.shape, x.stride(), x.dtype, x.device, residual.shape, residual.stride(),
-               residual.dtype, residual.device, weight.shape, weight.stride(), weight.dtype, weight.device,
-               eps, _sig(out), _sig(residual_out), _env("FUSED_DECODE_RMS_BLOCK"),
-               _env("FUSED_DECODE_RMS_WARPS"))
+        key = ("add_rms", x.shape, x.stride(), x.dtype, x.get_device(), residual.shape, residual.stride(),
+               residual.dtype, residual.get_device(), weight.shape, weight.stride(), weight.dtype, weight.get_device(),
+               eps, None if out is None else _sig(out), None if residual_out is None else _sig(residual_out),
+               _env("FUSED_DECODE_RMS_BLOCK"), _env("FUSED_DECODE_RMS_WARPS"))
         plan = _PLANS.get(key)
     except AttributeError:
         key, plan = None, None
@@ -249,8 +250,8 @@ def rope(
     interleaved pairs). ``cos``/``sin`` broadcast over leading dims.
     Reference: ops.py:138-160."""
     try:
-        key = ("rope", x.shape, x.stride(), x.dtype, x.device, cos.shape, cos.stride(), cos.dtype, cos.device,
-               sin.shape, sin.stride(), sin.dtype, sin.device, _sig(out))
+        key = ("rope", x.shape, x.stride(), x.dtype, x.get_device(), cos.shape, cos.stride(), cos.dtype, cos.get_device(),
+               sin.shape, sin.stride(), sin.dtype, sin.get_device(), None if out is None else _sig(out))
         plan = _PLANS.get(key)
     except AttributeError:
         key, plan = None, None
@@ -302,8 +303,8 @@ def swiglu(
 ) -> torch.Tensor:
     """``silu(gate) * up`` in float32, stored in ``gate.dtype``. Reference: ops.py:163-178."""
     try:
-        key = ("swiglu", gate.shape, gate.stride(), gate.dtype, gate.device, up.shape, up.stride(), up.dtype,
-               up.device, _sig(out))
+        key = ("swiglu", gate.shape, gate.stride(), gate.dtype, gate.get_device(), up.shape, up.stride(), up.dtype,
+               up.get_device(), None if out is None else _sig(out))
         plan = _PLANS.get(key)
     except AttributeError:
         key, plan = None, None
@@ -408,8 +409,8 @@ def linear_decode(
     Reference: ops.py:212-280.
     """
     try:
-        key = ("linear", x.shape, x.stride(), x.dtype, x.device, weight.shape, weight.stride(), weight.dtype,
-               weight.device, _sig(bias), _sig(row_add), _sig(out), kind,
+        key = ("linear", x.shape, x.stride(), x.dtype, x.get_device(), weight.shape, weight.stride(), weight.dtype,
+               weight.get_device(), _sig(bias), _sig(row_add), _sig(out), kind,
                _env("FUSED_DECODE_LINEAR_KIND"), _env("FUSED_DECODE_LINEAR"))
         plan = _PLANS.get(key)
     except AttributeError:
