@@ -26,6 +26,51 @@ __device__ __forceinline__ int sweep_unit(int wave, int i, int nw, int off, int 
   return u - (u >= units ? units : 0);
 }
 
+// ---------------------------------------------------------------------------
+// Global -> LDS streaming for the MFMA forms (gfx950 global_load_lds_dwordx4).
+// One instruction moves 16 bytes per lane straight into LDS, lane L landing at
+// byte 16*L of the (wave-uniform) destination, without passing through VGPRs,
+// so a wave can keep several weight tiles in flight at the register cost of
+// none. The compiler orders a DMA against later LDS reads only by waiting for
+// every outstanding load (vmcnt(0)), which would drain the ring; so the ring is
+// read with ds_read_b128 in inline assembly, out of its view, and each read is
+// guarded by an explicit s_waitcnt vmcnt(n) that lets exactly the younger
+// DMAs stay in flight (vector-memory loads complete in issue order).
+
+__device__ __forceinline__ void dma16(const void* src, u32x4* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_dst, 16, 0, 0);
+}
+
+// Byte address of an LDS location, as ds_read takes it.
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ void ds_zero16(unsigned addr) {
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(z) : "memory");
+}
+
+__device__ __forceinline__ u32x4 ds_read16(unsigned addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Make eight ds_read16 results usable: wait for the wave's LDS reads, tying the
+// wait to the registers so no use is scheduled ahead of it.
+__device__ __forceinline__ void wait_lds(u32x4 (&a)[4], u32x4 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]),
+                 "+v"(b[3])::"memory");
+}
+
 constexpr int pow2_ceil(int v) {
   int p = 1;
   while (p < v) p <<= 1;

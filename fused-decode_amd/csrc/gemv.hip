@@ -206,75 +206,127 @@ __device__ __forceinline__ void stage_unit16(const u32x4 (&v)[4], u32x4* tile, i
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <typename T, int U, bool NTW, bool ROPE>
-__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_mfma_relayout_kernel(
-    T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
-    int64_t syn, Epi e, Rope rp) {
+// MFMA GEMV with its tiles streamed into LDS by DMA (kind=dot from kMfmaMinM rows).
+// A workgroup of NW waves owns 16 weight rows; wave w takes K units w, w + NW,
+// ... of a sweep that starts at the workgroup's XCD offset (sweep_unit). A unit
+// is the 16 x 128 weight tile (4 KiB) and the BR x 128 activation tile (BR = M
+// rounded up to 4, 8 or 16), moved by 4 + BR/4 DMA instructions into one of the
+// wave's D ring slots, D units in flight. Each instruction covers 4 whole rows
+// (2 full 128-byte lines each): lane L fetches row 4i + L/16 at chunk
+// (L%16) ^ row, so the slot holds every row XOR-swizzled and the A fragment
+// reads (lane: row r, chunk 4*s2 + g) hit 16 distinct bank groups. Activation
+// rows past M re-read row 0 and weight rows past N row 0 (their outputs are
+// never stored). In a unit that crosses K, lanes fetch their row's first chunk
+// for chunks past K and then overwrite those ring entries with zeros, so every
+// unit runs the same four MFMAs. Partial sums meet in LDS, and wave 0 writes the
+// tile through mfma_tile_out (with ROPE the tile rows follow TileRows<16> and
+// the epilogue rotates them).
+template <typename T, int NW, int D, int BR, bool ROPE>
+__global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(T* y, const T* x, const T* w,
+                                                                 int M, int N, int K, int64_t sxm,
+                                                                 int64_t swn, int64_t sym,
+                                                                 int64_t syn, Epi e, Rope rp) {
   typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * kWave];
-  __shared__ u32x4 tiles[kMaxWaves][256];
+  constexpr int SLOT = 256 + BR * 16;  // 16-byte entries: the A tile, then the B rows
+  constexpr int OPS = 4 + BR / 4;      // DMA instructions per unit
+  __shared__ u32x4 ring[NW][D][SLOT];
+  __shared__ f32x4 part[NW * kWave];
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int nw = block_threads() / kWave;
+  // wave-uniform, so the unit indices, the K-tail tests and the ring addresses
+  // are scalar (a per-lane value here turns the tail test into exec-masked
+  // branches that shuttle the accumulator out of the MFMA registers every unit)
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane & 15, g = lane >> 4;
   const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: columns never stored
-  // load side: lane -> (row 4i + lane/16, chunk lane%16) for instruction i
-  const int lrow = lane >> 4, lchunk = lane & 15;
-  const T* wl[1][4];
   const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
+  const T* wrow[4];
+  int wch[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t n = ROPE ? tr.row(4 * i + lrow) : n0 + 4 * i + lrow;
-    wl[0][i] = w + (n < N ? n : 0) * swn;  // rows past N: outputs never stored
+    const int row = 4 * i + (lane >> 4);
+    const int64_t n = ROPE ? tr.row(row) : n0 + row;
+    wrow[i] = w + (n < N ? n : 0) * swn;
+    wch[i] = ((lane & 15) ^ row) * 8;
   }
-  u32x4* tile = tiles[wave];
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int units = (K + kUnit - 1) / kUnit;
-  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
-  const int off = sweep_offset(units);
-  auto issue = [&](UnitRegs16<T, 1>& q, int i) {
-    load_unit16<T, 1, NTW>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, K);
-  };
-  auto consume = [&](const UnitRegs16<T, 1>& q, int i) {
-    const int u = sweep_unit(wave, i, nw, off, units);
-    V8 a[4];
-    stage_unit16<T>(q.v[0], tile, lrow, lchunk, u, K, r, g, a);
+  const T* xrow[BR / 4];
+  int xch[BR / 4];
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], unit_b(q.b[s2], u, s2, g, K), acc);
-  };
-  if constexpr (U == 1) {
-    // one unit at a time; loads under a condition, which suits this form (the
-    // same loop with the pipeline's unconditional loads measured 30% slower)
-    for (int u = wave; u < units; u += nw) {
-      const bool in = u * kUnit + lchunk * 8 < K;
-      u32x4 v[4];
+  for (int i = 0; i < BR / 4; ++i) {
+    const int row = 4 * i + (lane >> 4);
+    xrow[i] = x + (row < M ? row : 0) * sxm;
+    xch[i] = ((lane & 15) ^ row) * 8;
+  }
+  const int units = (K + kUnit - 1) / kUnit;
+  const int mine = wave < units ? (units - wave + NW - 1) / NW : 0;
+  const int off = sweep_offset(units);
+  auto issue = [&](int j) {
+    const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
+    u32x4* slot = ring[wave][j % D];
+    if (k0 + kUnit <= K) {  // a whole unit (every unit but a K tail): no clamps
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dma16(wrow[i] + k0 + wch[i], slot + i * kWave);
+#pragma unroll
+      for (int i = 0; i < BR / 4; ++i) dma16(xrow[i] + k0 + xch[i], slot + 256 + i * kWave);
+    } else {  // the same instruction count, chunks past K clamped to the row's first
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const u32x4* q = reinterpret_cast<const u32x4*>(wl[0][i] + u * kUnit + lchunk * 8);
-        v[i] = in ? (NTW ? __builtin_nontemporal_load(q) : *q) : u32x4{0, 0, 0, 0};
+        const int k = k0 + wch[i];
+        dma16(wrow[i] + (k < K ? k : 0), slot + i * kWave);
       }
-      V8 b[4];
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const int kb = u * kUnit + (s2 * 4 + g) * 8;
-        b[s2] = kb < K ? load8<T>(xr + kb) : V8{};
+      for (int i = 0; i < BR / 4; ++i) {
+        const int k = k0 + xch[i];
+        dma16(xrow[i] + (k < K ? k : 0), slot + 256 + i * kWave);
       }
-      V8 a[4];
-      stage_unit16<T>(v, tile, lrow, lchunk, u, K, r, g, a);
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], b[s2], acc);
     }
-  } else {
-    UnitRegs16<T, 1> qa, qb;
-    if (mine > 0) issue(qa, 0);
-    stream_steps(mine, qa, qb, issue, consume);
+  };
+  // this lane's fragment entries within a slot, and the entries its DMAs fill (bytes)
+  const unsigned ring0 = lds_addr(&ring[wave][0][0]);
+  const int rb = r % BR;
+  unsigned fa[4], fb[4];
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+    fa[s2] = ring0 + (unsigned)(r * 16 + ((s2 * 4 + g) ^ r)) * 16u;
+    fb[s2] = ring0 + (unsigned)(256 + rb * 16 + ((s2 * 4 + g) ^ rb)) * 16u;
   }
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int j) {
+    const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
+    const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
+    if (k0 + kUnit > K) {  // K tail: zero the entries fetched past K
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (k0 + wch[i] >= K) ds_zero16(ring0 + so + (unsigned)(i * kWave + lane) * 16u);
+#pragma unroll
+      for (int i = 0; i < BR / 4; ++i)
+        if (k0 + xch[i] >= K) ds_zero16(ring0 + so + (unsigned)(256 + i * kWave + lane) * 16u);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    u32x4 a[4], b[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) {
+      a[s2] = ds_read16(fa[s2] + so);
+      b[s2] = ds_read16(fb[s2] + so);
+    }
+    wait_lds(a, b);
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(__builtin_bit_cast(V8, a[s2]), __builtin_bit_cast(V8, b[s2]), acc);
+  };
+  const int pre = mine < D ? mine : D;
+  for (int j = 0; j < pre; ++j) issue(j);
+  int j = 0;
+  for (; j + D <= mine; ++j) {  // D units in flight: the D-1 after unit j may stay outstanding
+    wait_vm<OPS * (D - 1)>();
+    consume(j);
+    if (j + D < mine) issue(j + D);
+  }
+  wait_vm<0>();
+  for (; j < mine; ++j) consume(j);
   part[wave * kWave + lane] = acc;
   __syncthreads();
   if (threadIdx.x < kWave) {
     f32x4 s = part[threadIdx.x];
-    for (int i = 1; i < nw; ++i) s += part[i * kWave + threadIdx.x];
+    for (int i = 1; i < NW; ++i) s += part[i * kWave + threadIdx.x];
     mfma_tile_out<T, ROPE>(y, s, threadIdx.x, n0, tr, e, rp, NoScale{}, M, N, sym, syn);
   }
 }
@@ -617,29 +669,76 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
   }
 }
 
+// LDS of one DMA MFMA workgroup: its ring and the cross-wave partial sums.
+constexpr size_t dma_lds(int nw, int d, int br) {
+  return (size_t)nw * d * (256 + br * 16) * 16 + (size_t)nw * kWave * 16;
+}
+
+// Activation rows a DMA MFMA launch stages: M rounded up to 4, 8 or 16.
+inline int dma_rows(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
+
+// Shapes of the DMA MFMA GEMV a tile may name: waves 2, 4 or 8, units in flight
+// 1-3, within the LDS of one CU.
+inline bool dma_shape_ok(int nw, int d, int M) {
+  return (nw == 2 || nw == 4 || nw == 8) && d >= 1 && d <= 3 && dma_lds(nw, d, dma_rows(M)) <= kMaxLds;
+}
+
+template <typename T, int NW, int D, int BR, bool ROPE>
+void launch_dma(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
+                int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Rope& r,
+                hipStream_t st) {
+  if constexpr (dma_lds(NW, D, BR) <= kMaxLds) {
+    hipLaunchKernelGGL((gemv_mfma_dma_kernel<T, NW, D, BR, ROPE>), dim3(blocks), dim3(NW * kWave), 0,
+                       st, static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), M,
+                       N, K, sxm, swn, sym, syn, e, r);
+  }
+}
+
+template <typename T, int NW, int D, bool ROPE>
+void launch_dma_rows(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
+                     int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                     const Rope& r, hipStream_t st) {
+  const int br = dma_rows(M);
+  if (br == 4)
+    launch_dma<T, NW, D, 4, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+  else if (br == 8)
+    launch_dma<T, NW, D, 8, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+  else
+    launch_dma<T, NW, D, 16, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+}
+
+// Default shape: four waves (fewer when K has fewer units) with two units in
+// flight each; measured best or within 3% of the best of 2-8 waves and 1-3
+// units on the four decode shapes at M = 5, 8 and 16 (e.g. N = K = 4096, M = 8:
+// 7.2 us, against 8.6 for the relayout kernel this replaced, whose two units per
+// wave sat in 114 VGPRs). The fused QKV (rp) always runs the default shape.
 template <typename T>
 void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
                  const Rope* rp = nullptr, const Tile* t = nullptr) {
-  const int nw = t && t->waves ? t->waves : pick_waves((K + kUnit - 1) / kUnit);
-  // Two units in flight per wave by default: the pipelined form measured faster
-  // than one unit at a time on all four decode shapes at M = 5, 8 and 16
-  // (N = 4096, K = 14336, M = 8: 21.2 against 22.4 us).
-  const int stages = t && t->stages ? t->stages : 2;
+  const int units = (K + kUnit - 1) / kUnit;
+  const int nw = t && t->waves ? t->waves : units >= 4 ? 4 : units >= 2 ? 2 : 1;
+  const int d = t && t->stages ? t->stages : 2;
   Rope none{};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
   const Rope& r = rp ? *rp : none;
-#define FD_MFMA(UU, RR)                                                                    \
-  hipLaunchKernelGGL((gemv_mfma_relayout_kernel<T, UU, true, RR>), dim3(blocks),          \
-                     dim3(nw * kWave), 0, st, static_cast<T*>(y), static_cast<const T*>(x), \
-                     static_cast<const T*>(w), M, N, K, sxm, swn, sym, syn, e, r)
   if (rp) {
-    if (stages == 1) FD_MFMA(1, true); else FD_MFMA(2, true);
-  } else {
-    if (stages == 1) FD_MFMA(1, false); else FD_MFMA(2, false);
+    if (nw >= 4)
+      launch_dma_rows<T, 4, 2, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+    else
+      launch_dma_rows<T, 2, 2, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+    return;
   }
-#undef FD_MFMA
+#define FD_DMA(NW, D) launch_dma_rows<T, NW, D, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st)
+  if (nw <= 2) {
+    if (d == 1) FD_DMA(2, 1); else if (d == 2) FD_DMA(2, 2); else FD_DMA(2, 3);
+  } else if (nw <= 4) {
+    if (d == 1) FD_DMA(4, 1); else if (d == 2) FD_DMA(4, 2); else FD_DMA(4, 3);
+  } else {
+    if (d == 1) FD_DMA(8, 1); else if (d == 2) FD_DMA(8, 2); else FD_DMA(8, 3);
+  }
+#undef FD_DMA
 }
 
 template <typename T, int M>
@@ -759,7 +858,9 @@ int check_tile(const Tile& t, int64_t M, int kind) {
   if (t.rows == 16 && kind != FD_KIND_DOT)
     return set_error(FD_EINVAL, "16 rows per workgroup is the MFMA GEMV (kind=dot only)");
   if (linear_uses_mfma(M, kind, t)) {
-    if (t.stages < 0 || t.stages > 2) return set_error(FD_EINVAL, "MFMA stages must be 0, 1 or 2");
+    if (t.stages < 0 || t.stages > 3) return set_error(FD_EINVAL, "MFMA stages must be 0 to 3");
+    if (t.waves != 0 && !dma_shape_ok(t.waves, t.stages ? t.stages : 2, (int)M))
+      return set_error(FD_EINVAL, "MFMA waves must be 2, 4 or 8, within the LDS of a CU");
   } else {
     if (t.rows != 0 && t.rows != 2 && t.rows != 4 && t.rows != 8)
       return set_error(FD_EINVAL, "rows per workgroup must be 2, 4 or 8 (SIMT) or 16 (MFMA)");

@@ -168,8 +168,8 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
 
     ``FUSED_DECODE_LINEAR=block_n,block_k,warps,stages`` overrides it as in the
     reference (kernels.py:589-603): block_n = rows per workgroup, block_k the
-    kernel's step (SIMT 512, MFMA 128), warps = waves (1-8), stages = MFMA K
-    units (1 or 2; SIMT 1). Otherwise the measured table
+    kernel's step (SIMT 512, MFMA 128), warps = waves (SIMT 1-8, MFMA 2, 4 or
+    8), stages = MFMA K units in flight per wave (1-3; SIMT 1). Otherwise the measured table
     (``tiles_gfx950.json``, per kind, N, K and M) decides for its shapes, and
     the library's defaults (MFMA for "dot" from 5 rows) for the rest."""
     forced = os.environ.get("FUSED_DECODE_LINEAR")
@@ -195,9 +195,11 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
 
 
 def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
-    """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot")."""
+    """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot"):
+    the MFMA GEMV runs four waves (two below four K units) with two units in
+    flight each; the SIMT GEMV one wave per 512-element K chunk, up to eight."""
     if kern == "dot":
-        return 16, _waves(-(-k // 128)), 2
+        return 16, (4 if -(-k // 128) >= 4 else 2), 2
     return 4, _waves(-(-k // 512)), 1
 
 

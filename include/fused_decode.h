@@ -120,10 +120,10 @@ int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_
 /*
  * GEMV tiling: weight rows per workgroup, which also names the kernel (2, 4 or 8:
  * the SIMT kernel, 8 only up to M = 8; 16: the MFMA kernel, kind FD_KIND_DOT
- * only), waves per workgroup (1..8) and, for the MFMA kernel, K units of 128 in
- * flight per wave (1, or 2: the next unit's loads issued before the current one
- * is multiplied, the default). 0 = the library's default for that
- * field; with rows 0 the kernel is chosen as in fd_linear (MFMA for kind
+ * only), waves per workgroup (SIMT 1..8; MFMA 2, 4 or 8) and, for the MFMA
+ * kernel, K units of 128 each wave keeps in flight in its LDS ring (1..3; 2 by
+ * default; waves x units must fit one CU's LDS). 0 = the library's default for
+ * that field; with rows 0 the kernel is chosen as in fd_linear (MFMA for kind
  * FD_KIND_DOT from M = 5).
  */
 typedef struct fd_tile {

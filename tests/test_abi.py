@@ -142,7 +142,9 @@ def test_tiled_linear_rejects_tiles_the_kernel_cannot_run(L):
     assert call(1, 1, stages=2) == L.FD_EINVAL        # SIMT has one stage
     assert call(1, 1, rows=16) == L.FD_EINVAL         # 16 rows = the MFMA kernel, kind dot only
     assert call(8, 0, rows=5) == L.FD_EINVAL
-    assert call(8, 0, stages=3) == L.FD_EINVAL
+    assert call(8, 0, stages=4) == L.FD_EINVAL        # MFMA: 1-3 units in flight
+    assert call(8, 0, waves=3) == L.FD_EINVAL         # MFMA: 2, 4 or 8 waves
+    assert call(16, 0, rows=16, waves=8, stages=3) == L.FD_EINVAL  # ring beyond a CU's LDS
     assert call(1, 0, waves=9) == L.FD_EINVAL
     assert lib.fd_linear_tiled(FAKE, FAKE, FAKE, None, 0, None, 0, 0, 64, 64, 64, 1, 64, 1, 0, 0, 0,
                                64, 1, None, 1, 0, None) == L.FD_OK   # M = 0, default tile

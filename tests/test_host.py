@@ -85,8 +85,9 @@ def test_rms_block_env_validation(monkeypatch):
 def test_linear_config_tiling(monkeypatch):
     monkeypatch.delenv("FUSED_DECODE_LINEAR", raising=False)
     monkeypatch.setattr(kernels, "_TILE_TABLE", {})
-    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 8, 2)        # MFMA kernel, 2 units in flight
-    assert kernels.linear_config("dot", 28672, 4096, 8) == (16, 128, 8, 2)
+    assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 4, 2)        # MFMA kernel, 2 units in flight
+    assert kernels.linear_config("dot", 28672, 4096, 8) == (16, 128, 4, 2)
+    assert kernels.linear_config("dot", 64, 256, 8) == (16, 128, 2, 2)        # two K units: two waves
     assert kernels.linear_config("dot", 4096, 4096, 1) == (4, 512, 8, 1)      # dot below 8 rows: SIMT
     monkeypatch.setattr(kernels, "_TILE_TABLE", {"dot:4096x4096:m4": [16, 8, 1]})
     assert kernels.linear_config("dot", 4096, 4096, 4) == (16, 128, 8, 1)     # the table picks MFMA
