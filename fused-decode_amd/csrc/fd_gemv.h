@@ -63,6 +63,14 @@ __device__ __forceinline__ u32x4 ds_read16(unsigned addr) {
   return v;
 }
 
+// Make twelve ds_read16 results usable (the norm-weight fragments as well).
+__device__ __forceinline__ void wait_lds(u32x4 (&a)[4], u32x4 (&b)[4], u32x4 (&c)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]),
+                 "+v"(b[3]), "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
+                 "+v"(c[6]), "+v"(c[7])::"memory");
+}
+
 // Make eight ds_read16 results usable: wait for the wave's LDS reads, tying the
 // wait to the registers so no use is scheduled ahead of it.
 __device__ __forceinline__ void wait_lds(u32x4 (&a)[4], u32x4 (&b)[4]) {
@@ -102,6 +110,107 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
     load8_f32<bf16>(static_cast<const bf16*>(p) + k, f);
   else
     load8_f32<f16>(static_cast<const f16*>(p) + k, f);
+}
+
+// RMSNorm folded into a DMA MFMA kernel. The workgroup stages the norm weight
+// in LDS as float32 (zeros from H to `hp`, a whole number of K units) and the
+// inverse RMS of every activation row (inv[m], zero for rows past M); each B
+// fragment of raw activations is then normalised as the row kernels do it,
+// round(x * inv[m] * w[k]) (norm.hip). The caller issues its first DMAs
+// between the two steps, so the weight stream is in flight while the rows are
+// reduced.
+__device__ __forceinline__ void stage_norm_w(float* wl, const void* nwp, int nw_dtype, int H, int hp) {
+  for (int k = threadIdx.x * 8; k < hp; k += block_threads() * 8) {
+    float f[8];
+    if (k < H) {
+      load8_norm_w(nwp, nw_dtype, k, f);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) f[i] = 0.f;
+    }
+    reinterpret_cast<f32x4*>(wl + k)[0] = f32x4{f[0], f[1], f[2], f[3]};
+    reinterpret_cast<f32x4*>(wl + k)[1] = f32x4{f[4], f[5], f[6], f[7]};
+  }
+}
+
+// inv[m] = rsqrt(mean(x[m]^2) + eps) for m < M (0 up to MMAX), every thread of
+// the workgroup; `scratch` holds kMaxWaves * pow2_ceil(MMAX) floats. Ends with
+// a barrier (inv and the caller's staged norm weight are then visible).
+template <typename T, int MMAX>
+__device__ __forceinline__ void row_inv_rms(float* inv, float* scratch, const T* x, int64_t sxm,
+                                            int M, int H, float eps) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int MP = pow2_ceil(MMAX);
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int nt = block_threads(), nwv = nt / kWave;
+  float ss[MP];
+#pragma unroll
+  for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+  for (int k = tid * 8; k < H; k += nt * 8) {
+    // every load unconditional (rows past M re-read the last row, masked below):
+    // a load under a branch would make the compiler wait for all outstanding
+    // loads, the caller's in-flight DMAs included, before each use
+    V8 h[MMAX];
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      const float keep = m < M ? 1.f : 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss[m] += keep * (to_f32(h[m][i]) * to_f32(h[m][i]));
+    }
+  }
+  butterfly_sum<MP>(ss, lane);
+  if (butterfly_writer<MP>(lane)) scratch[wave * MP + butterfly_index<MP>(lane)] = ss[0];
+  __syncthreads();
+  if (tid < MMAX) {
+    float s = 0.f;
+    for (int i = 0; i < nwv; ++i) s += scratch[i * MP + tid];
+    inv[tid] = tid < M ? rsqrtf(s / (float)H + eps) : 0.f;
+  }
+  __syncthreads();
+}
+
+// x * inv in float32 for the low / high f16 of a packed pair: one v_fma_mix_f32
+// (f16 operand converted exactly, addend -0.0, so the result is the rounded
+// product, sign of zero included) in place of a conversion and a multiply.
+// The compiler folds fma(x, inv, -0) back into a multiply, hence the asm.
+__device__ __forceinline__ float mul_lo_f16(unsigned pair, float inv) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(inv));
+  return r;
+}
+__device__ __forceinline__ float mul_hi_f16(unsigned pair, float inv) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(inv));
+  return r;
+}
+
+// B fragment of raw activations -> round(x * inv * w) for its 8 k (w as 8 floats).
+template <typename T>
+__device__ __forceinline__ u32x4 norm_frag(const u32x4& raw, float inv, const u32x4& w0, const u32x4& w1) {
+  if constexpr (std::is_same<T, f16>::value) {
+    const f32x4 wa = __builtin_bit_cast(f32x4, w0), wb = __builtin_bit_cast(f32x4, w1);
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      o[2 * j] = (f16)(mul_lo_f16(raw[j], inv) * wa[2 * j]);
+      o[2 * j + 1] = (f16)(mul_hi_f16(raw[j], inv) * wa[2 * j + 1]);
+      o[2 * j + 4] = (f16)(mul_lo_f16(raw[j + 2], inv) * wb[2 * j]);
+      o[2 * j + 5] = (f16)(mul_hi_f16(raw[j + 2], inv) * wb[2 * j + 1]);
+    }
+    return __builtin_bit_cast(u32x4, o);
+  }
+  typedef typename Vec8<T>::type V8;
+  const V8 h = __builtin_bit_cast(V8, raw);
+  const f32x4 wa = __builtin_bit_cast(f32x4, w0), wb = __builtin_bit_cast(f32x4, w1);
+  V8 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[i] = from_f32<T>(to_f32(h[i]) * inv * wa[i]);
+    o[i + 4] = from_f32<T>(to_f32(h[i + 4]) * inv * wb[i]);
+  }
+  return __builtin_bit_cast(u32x4, o);
 }
 
 // LDS row stride of the staged activations: H plus 16 bytes, so the 16 rows an
@@ -395,6 +504,28 @@ __device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, floa
   o2 = x2 * load_any(rp.cos, rp.dtype, c + h) + x1 * load_any(rp.sin, rp.dtype, c + h);
 }
 
+// cos/sin of the four outputs one MFMA-epilogue lane rotates in a rotated tile
+// (lane l: column m = l%16, slots nb..nb+3 with nb = 4*(l/16); slots below 8
+// are first-half columns, the rest their partners dim/2 further on), so the
+// loads can be issued before a kernel's main loop and wait under it.
+struct TileAngles {
+  float c[4], s[4];
+};
+__device__ __forceinline__ TileAngles tile_angles(const Rope& rp, const TileRows<16>& tr, int lane,
+                                                  int M) {
+  TileAngles a;
+  const int m = lane & 15, nb = (lane >> 4) * 4;
+  const bool first = nb < 8;
+  const int64_t row = (int64_t)(m < M ? m : M - 1) * rp.rs;  // rows past M: never stored
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t c = row + tr.col(first ? nb + i : nb + i - 8) + (first ? 0 : rp.dim >> 1);
+    a.c[i] = load_any(rp.cos, rp.dtype, c);
+    a.s[i] = load_any(rp.sin, rp.dtype, c);
+  }
+  return a;
+}
+
 // Per-row factor applied to a GEMV sum before the epilogue: none for fp16/bf16
 // weights, the channel scale scale[n] for E4M3 codes.
 struct NoScale {
@@ -409,12 +540,13 @@ struct RowScale {
 // cross-wave sums: lane l has rows nb..nb+3 (nb = 4*(l/16)) of column m = l%16.
 // With ROPE the rows follow TileRows<16>, and a rotated tile rotates its rounded
 // outputs: lanes 0-31 hold slots 0-7 and lanes 32-63 their partners 8-15 (same
-// m), one lane-xor-32 exchange apart, so every lane of the wave must call this.
+// m), one lane-xor-32 exchange apart, so every lane of the wave must call this;
+// `ang` is tile_angles() of the lane (read in rotated tiles only).
 template <typename T, bool ROPE, typename Scale>
 __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, int64_t n0,
                                               const TileRows<16>& tr, const Epi& e,
-                                              const Rope& rp, const Scale& sc, int M, int N,
-                                              int64_t sym, int64_t syn) {
+                                              const TileAngles& ang, const Scale& sc, int M,
+                                              int N, int64_t sym, int64_t syn) {
   const int m = lane & 15;
   const int nb = (lane >> 4) * 4;
   if (ROPE && tr.rotated()) {
@@ -429,10 +561,10 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
       const bool first = nb < 8;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float o1, o2;
-        rope_pair(rp, m, tr.col(first ? nb + i : nb + i - 8), first ? v[i] : pv[i],
-                  first ? pv[i] : v[i], o1, o2);
-        y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(first ? o1 : o2);
+        // the rope op's pair rotation: x1 cos - x2 sin (first half), x2 cos + x1 sin
+        const float x1 = first ? v[i] : pv[i], x2 = first ? pv[i] : v[i];
+        const float o = first ? x1 * ang.c[i] - x2 * ang.s[i] : x2 * ang.c[i] + x1 * ang.s[i];
+        y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(o);
       }
     }
   } else if (m < M) {

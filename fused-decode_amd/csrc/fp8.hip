@@ -355,7 +355,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
   if (threadIdx.x < kWave) {
     f32x4 sm = part[threadIdx.x];
     for (int i = 1; i < nw; ++i) sm += part[i * kWave + threadIdx.x];
-    mfma_tile_out<T, ROPE>(y, sm, threadIdx.x, n0, tr, e, rp, RowScale{wscale}, M, N, sym, syn);
+    const TileAngles ang = ROPE && tr.rotated() ? tile_angles(rp, tr, threadIdx.x, M) : TileAngles{};
+    mfma_tile_out<T, ROPE>(y, sm, threadIdx.x, n0, tr, e, ang, RowScale{wscale}, M, N, sym, syn);
   }
 }
 

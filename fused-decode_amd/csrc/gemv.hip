@@ -221,16 +221,21 @@ __device__ __forceinline__ void stage_unit16(const u32x4 (&v)[4], u32x4* tile, i
 // unit runs the same four MFMAs. Partial sums meet in LDS, and wave 0 writes the
 // tile through mfma_tile_out (with ROPE the tile rows follow TileRows<16> and
 // the epilogue rotates them).
-template <typename T, int NW, int D, int BR, bool ROPE>
-__global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(T* y, const T* x, const T* w,
-                                                                 int M, int N, int K, int64_t sxm,
-                                                                 int64_t swn, int64_t sym,
-                                                                 int64_t syn, Epi e, Rope rp) {
+//
+// With NORM, x is the raw activation and the kernel applies the RMSNorm itself:
+// the norm weight (float32) and the rows' inverse RMS are staged in dynamic LDS
+// (norm_dma_lds bytes) by a prologue that runs while the first units' DMAs are
+// in flight, and every B fragment is normalised after its LDS read.
+template <typename T, int NW, int D, int BR, bool ROPE, bool NORM>
+__global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
+    T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
+    int64_t syn, Epi e, Rope rp, const void* nwp, int nw_dtype, float eps) {
   typedef typename Vec8<T>::type V8;
   constexpr int SLOT = 256 + BR * 16;  // 16-byte entries: the A tile, then the B rows
   constexpr int OPS = 4 + BR / 4;      // DMA instructions per unit
   __shared__ u32x4 ring[NW][D][SLOT];
   __shared__ f32x4 part[NW * kWave];
+  extern __shared__ float norm_lds[];  // NORM: w [units * 128], inv [16], scratch
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform, so the unit indices, the K-tail tests and the ring addresses
   // are scalar (a per-lane value here turns the tail test into exec-masked
@@ -290,6 +295,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(T* y, const T
     fb[s2] = ring0 + (unsigned)(256 + rb * 16 + ((s2 * 4 + g) ^ rb)) * 16u;
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float rinv = 0.f;  // NORM: inverse RMS of this lane's B row
+  unsigned fw = 0;   // NORM: this lane's norm-weight fragment base (bytes)
   auto consume = [&](int j) {
     const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
     const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
@@ -308,12 +315,40 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(T* y, const T
       a[s2] = ds_read16(fa[s2] + so);
       b[s2] = ds_read16(fb[s2] + so);
     }
-    wait_lds(a, b);
+    if constexpr (NORM) {
+      u32x4 c[8];  // norm weight of fragment s2: floats k0 + (4 s2 + g) * 8 .. + 8
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const unsigned wa = fw + (unsigned)(k0 + s2 * 32) * 4u;
+        c[2 * s2] = ds_read16(wa);
+        c[2 * s2 + 1] = ds_read16(wa + 16u);
+      }
+      wait_lds(a, b, c);
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) b[s2] = norm_frag<T>(b[s2], rinv, c[2 * s2], c[2 * s2 + 1]);
+    } else {
+      wait_lds(a, b);
+    }
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(__builtin_bit_cast(V8, a[s2]), __builtin_bit_cast(V8, b[s2]), acc);
   };
   const int pre = mine < D ? mine : D;
-  for (int j = 0; j < pre; ++j) issue(j);
+  // wave 0 writes the tile: its cos/sin loads go out first, so they complete
+  // under the main loop's first wait instead of after the loop
+  TileAngles ang{};
+  if constexpr (ROPE)
+    if (wave == 0 && tr.rotated()) ang = tile_angles(rp, tr, lane, M);
+  if constexpr (NORM) {
+    float* wl = norm_lds;
+    float* inv = norm_lds + units * kUnit;
+    stage_norm_w(wl, nwp, nw_dtype, K, units * kUnit);
+    for (int j = 0; j < pre; ++j) issue(j);
+    row_inv_rms<T, BR>(inv, inv + 16, x, sxm, M, K, eps);
+    rinv = inv[rb];
+    fw = lds_addr(wl) + (unsigned)(g * 8) * 4u;
+  } else {
+    for (int j = 0; j < pre; ++j) issue(j);
+  }
   int j = 0;
   for (; j + D <= mine; ++j) {  // D units in flight: the D-1 after unit j may stay outstanding
     wait_vm<OPS * (D - 1)>();
@@ -327,7 +362,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(T* y, const T
   if (threadIdx.x < kWave) {
     f32x4 s = part[threadIdx.x];
     for (int i = 1; i < NW; ++i) s += part[i * kWave + threadIdx.x];
-    mfma_tile_out<T, ROPE>(y, s, threadIdx.x, n0, tr, e, rp, NoScale{}, M, N, sym, syn);
+    mfma_tile_out<T, ROPE>(y, s, threadIdx.x, n0, tr, e, ang, NoScale{}, M, N, sym, syn);
   }
 }
 
@@ -683,28 +718,49 @@ inline bool dma_shape_ok(int nw, int d, int M) {
   return (nw == 2 || nw == 4 || nw == 8) && d >= 1 && d <= 3 && dma_lds(nw, d, dma_rows(M)) <= kMaxLds;
 }
 
-template <typename T, int NW, int D, int BR, bool ROPE>
-void launch_dma(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
-                int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Rope& r,
-                hipStream_t st) {
-  if constexpr (dma_lds(NW, D, BR) <= kMaxLds) {
-    hipLaunchKernelGGL((gemv_mfma_dma_kernel<T, NW, D, BR, ROPE>), dim3(blocks), dim3(NW * kWave), 0,
-                       st, static_cast<T*>(y), static_cast<const T*>(x), static_cast<const T*>(w), M,
-                       N, K, sxm, swn, sym, syn, e, r);
-  }
+// The RMSNorm folded into a DMA MFMA launch (x = raw activations, normalised in
+// the kernel with norm_w / eps).
+struct FoldNorm {
+  const void* w;
+  int dtype;
+  float eps;
+};
+
+// Dynamic LDS of a NORM launch: the float32 norm weight over whole K units, the
+// 16 inverse RMS values and the reduction scratch.
+inline size_t norm_dma_lds(int K) {
+  return sizeof(float) * ((size_t)((K + kUnit - 1) / kUnit) * kUnit + 16 + kMaxWaves * 16);
 }
 
-template <typename T, int NW, int D, bool ROPE>
-void launch_dma_rows(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
-                     int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-                     const Rope& r, hipStream_t st) {
+template <typename T, int NW, int D, int BR, bool ROPE, bool NORM>
+int launch_dma(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
+               int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Rope& r,
+               const FoldNorm& fn, hipStream_t st) {
+  if constexpr (dma_lds(NW, D, BR) <= kMaxLds) {
+    const size_t dyn = NORM ? norm_dma_lds(K) : 0;
+    auto kernel = gemv_mfma_dma_kernel<T, NW, D, BR, ROPE, NORM>;
+    if (dma_lds(NW, D, BR) + dyn > kMaxLds)
+      return set_error(FD_EUNSUPPORTED, "K too large for the folded RMSNorm's LDS stage");
+    if (!allow_lds(kernel, dyn))
+      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", dyn);
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(NW * kWave), dyn, st, static_cast<T*>(y),
+                       static_cast<const T*>(x), static_cast<const T*>(w), M, N, K, sxm, swn, sym,
+                       syn, e, r, fn.w, fn.dtype, fn.eps);
+    return FD_OK;
+  }
+  return set_error(FD_EINVAL, "MFMA tile beyond the LDS of a CU");
+}
+
+template <typename T, int NW, int D, bool ROPE, bool NORM>
+int launch_dma_rows(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
+                    int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                    const Rope& r, const FoldNorm& fn, hipStream_t st) {
   const int br = dma_rows(M);
   if (br == 4)
-    launch_dma<T, NW, D, 4, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
-  else if (br == 8)
-    launch_dma<T, NW, D, 8, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
-  else
-    launch_dma<T, NW, D, 16, ROPE>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
+    return launch_dma<T, NW, D, 4, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
+  if (br == 8)
+    return launch_dma<T, NW, D, 8, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
+  return launch_dma<T, NW, D, 16, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
 }
 
 // Default shape: four waves (fewer when K has fewer units) with two units in
@@ -713,24 +769,31 @@ void launch_dma_rows(unsigned blocks, void* y, const void* x, const void* w, int
 // 7.2 us, against 8.6 for the relayout kernel this replaced, whose two units per
 // wave sat in 114 VGPRs). The fused QKV (rp) always runs the default shape.
 template <typename T>
-void launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
-                 int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
-                 const Rope* rp = nullptr, const Tile* t = nullptr) {
+int launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
+                int64_t swn, int64_t sym, int64_t syn, const Epi& e, hipStream_t st,
+                const Rope* rp = nullptr, const Tile* t = nullptr, const FoldNorm* fold = nullptr) {
   const int units = (K + kUnit - 1) / kUnit;
   const int nw = t && t->waves ? t->waves : units >= 4 ? 4 : units >= 2 ? 2 : 1;
   const int d = t && t->stages ? t->stages : 2;
   Rope none{};
+  const FoldNorm nofold{nullptr, FD_F32, 0.f};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
   const Rope& r = rp ? *rp : none;
-  if (rp) {
-    if (nw >= 4)
-      launch_dma_rows<T, 4, 2, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
-    else
-      launch_dma_rows<T, 2, 2, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st);
-    return;
+  if (fold) {  // the fused QKV from kMfmaMinM rows: RoPE epilogue, RMSNorm folded in
+    return nw >= 4 ? launch_dma_rows<T, 4, 2, true, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
+                                                          *fold, st)
+                   : launch_dma_rows<T, 2, 2, true, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
+                                                          *fold, st);
   }
-#define FD_DMA(NW, D) launch_dma_rows<T, NW, D, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, st)
+  if (rp) {
+    return nw >= 4 ? launch_dma_rows<T, 4, 2, true, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
+                                                           nofold, st)
+                   : launch_dma_rows<T, 2, 2, true, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
+                                                           nofold, st);
+  }
+#define FD_DMA(NW, D) \
+  return launch_dma_rows<T, NW, D, false, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, nofold, st)
   if (nw <= 2) {
     if (d == 1) FD_DMA(2, 1); else if (d == 2) FD_DMA(2, 2); else FD_DMA(2, 3);
   } else if (nw <= 4) {
@@ -892,14 +955,12 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
   const bool mfma = linear_uses_mfma(M, kind, t);
   if (act_dtype == FD_F16) {
     if (mfma)
-      launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
-    else
-      launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
+      return launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
+    launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   } else {
     if (mfma)
-      launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
-    else
-      launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
+      return launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
+    launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   }
   return FD_OK;
 }
@@ -1135,21 +1196,21 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
   Epi e;
   Rope rp;
   bool empty = false;
+  // the MFMA form folds the RMSNorm in: `normed` is not used at any M
   const int checked = qkv_prepare(y, normed, hidden, norm_w, norm_w_dtype, w_qkv, bias, bias_dtype,
                                   cos, sin, cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim,
-                                  eps, act_dtype, mfma, e, rp, empty);
+                                  eps, act_dtype, false, e, rp, empty);
   if (checked != FD_OK || empty) return checked;
   if (H % 8 != 0) return set_error(FD_EUNSUPPORTED, "H must be a multiple of 8");
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc;
-  if (mfma) {
+  if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
-    rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    const FoldNorm fn{norm_w, norm_w_dtype, eps};
+    rc = act_dtype == FD_F16
+             ? launch_mfma<f16>((int)M, y, hidden, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp, nullptr, &fn)
+             : launch_mfma<bf16>((int)M, y, hidden, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp, nullptr, &fn);
     if (rc != FD_OK) return rc;
-    if (act_dtype == FD_F16)
-      launch_mfma<f16>((int)M, y, normed, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp);
-    else
-      launch_mfma<bf16>((int)M, y, normed, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp);
   } else {
     rc = act_dtype == FD_F16
              ? launch_qkv_simt_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H,

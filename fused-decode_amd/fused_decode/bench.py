@@ -657,7 +657,7 @@ def tune(dtype, out_path: str | None = None) -> dict:
     """Tile search for the HIP GEMV on this GPU (replaces the reference's Triton
     tile sweep, bench.py:475-517): for every decode weight shape and M = 1..16,
     each kind is timed over the tiles of the kernels it may run (kind "simt":
-    SIMT; kind "dot": SIMT, and MFMA from 2 rows; graph-replayed device time,
+    SIMT; kind "dot": SIMT and MFMA; graph-replayed device time,
     cold weights) next to F.linear. Returns and optionally writes the table
     ``linear_config`` reads: the best tile per (kind, N, K, M) where it beats
     the default by 3% or more (its row count names the kernel), and
@@ -679,9 +679,10 @@ def tune(dtype, out_path: str | None = None) -> dict:
             for kind in ("simt", "dot"):
                 dflt = kernels.default_tile(kernels._kernel_of(kind, m), n, kk)
                 cands = {(r, w, 1) for r in (2, 4, 8) if r * m <= 64 for w in (4, 8, dflt[1])}
-                if kind == "dot" and m >= 2:
-                    dw = kernels.default_tile("dot", n, kk)[1]
-                    cands |= {(16, w, st) for w in (4, 8, dw) for st in (1, 2)}
+                if kind == "dot":  # the DMA MFMA GEMV: waves x units in flight within a CU's LDS
+                    br = 4 if m <= 4 else 8 if m <= 8 else 16
+                    cands |= {(16, w, st) for w in (2, 4, 8) for st in (1, 2, 3)
+                              if w * st * (256 + 16 * br) * 16 + w * 1024 <= 160 * 1024}
                 cands.add(dflt)
                 times = {}
                 for t in sorted(cands):

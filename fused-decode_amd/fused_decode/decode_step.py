@@ -10,8 +10,8 @@ fused form (the default):
     h    = linear_decode(attn, w_o, row_add=x)           # O-proj with the residual fused
     x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
 
-That is four launches per layer at M < 5 (six from 5 rows with kind "dot",
-where both RMSNorms run as row kernels ahead of MFMA GEMVs). The unfused form
+That is four launches per layer at M < 5 (five from 5 rows with kind "dot",
+where the MLP's RMSNorm runs as a row kernel ahead of its MFMA gate/up). The unfused form
 composes the reference's operators instead, six launches per layer (seven):
 
     normed, stream = add_rms_norm(x, zero, attn_norm_w)   # stream <- x, normed <- rms(x)
@@ -155,14 +155,14 @@ class DecodeStep:
 
     @property
     def launches_per_layer(self) -> int:
-        """HIP launches one layer issues (the MFMA forms at kind "dot" from 5 rows
-        add a row kernel for the RMSNorm)."""
+        """HIP launches one layer issues (the MFMA MLP at kind "dot" from 5 rows adds
+        a row kernel for its RMSNorm; the fused QKV folds its norm in at every M)."""
         mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
         mlp = 3 if mfma else 2
         if self.fp8:  # the fp8 kernels take the MFMA forms from 5 rows whatever the kind
             return (2 if self.m >= _MFMA_MIN_M else 1) + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
         if self.fused:
-            return (2 if mfma else 1) + 1 + mlp
+            return 1 + 1 + mlp
         return 4 + mlp
 
     def capture(self) -> None:

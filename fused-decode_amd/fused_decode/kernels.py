@@ -304,8 +304,8 @@ def pre_attn_qkv_out(
 ) -> int:
     """Fused RMSNorm + QKV GEMV + RoPE for contiguous ``hidden [M, H]`` (M <= 16)
     into contiguous ``out [M, N]``; ``cos``/``sin`` are contiguous rows of
-    ``head_dim`` (row stride ``cs_row_stride``, 0 = shared). ``normed`` is ``[M, H]``
-    scratch for kind=dot at M >= 5. Returns the library status (FD_EUNSUPPORTED
+    ``head_dim`` (row stride ``cs_row_stride``, 0 = shared). ``normed`` is unused
+    (the MFMA form folds the norm in) and may be None. Returns the library status (FD_EUNSUPPORTED
     lets the caller compose the operators instead)."""
     m, h = hidden.shape
     n = w_qkv.shape[0]

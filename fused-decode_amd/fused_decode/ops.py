@@ -38,7 +38,6 @@ from ._checks import check
 from ._layout import contiguous_strides, plan_rows
 from ._lib import DTYPE_CODE, FD_EUNSUPPORTED, KIND_CODE, FdTile, fail, native
 from .kernels import (
-    _MFMA_MIN_M,
     _rms_env,
     linear_config,
     post_attn_mlp_out,
@@ -643,7 +642,7 @@ def pre_attn_qkv(
     or ``[..., 1, D]`` per token). Returns ``[..., N]`` equal to
     ``rope(linear_decode(rms_norm(hidden), w_qkv, bias)[..., :rope_cols])`` with
     the reference's rounding after each step. Up to the GEMV row limit this is one
-    HIP launch (two for kind "dot" from 5 rows: the norm runs as a row kernel).
+    HIP launch (from 5 rows with kind "dot" an MFMA kernel with the norm folded in).
     No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
     :138-160.
     """
@@ -662,11 +661,8 @@ def pre_attn_qkv(
             h2 = h2.contiguous()
         nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
         b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
-        normed = None
-        if kind_r == "dot" and m >= _MFMA_MIN_M:
-            normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
         status = pre_attn_qkv_out(h2, nw, w_qkv, b, a.cos, a.sin, a.cs_row_stride, a.rope_cols,
-                                  a.d, eps, out.view(m, n), normed, kind_r)
+                                  a.d, eps, out.view(m, n), None, kind_r)
         if status == _lib.FD_OK:
             return out
     normed = rms_norm(hidden, norm_weight, eps=eps)

@@ -197,8 +197,7 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
                    float eps, int kind, int act_dtype, void* stream);
 
 /*
- * Pre-attention QKV projection of a decode step in one launch (two for kind
- * FD_KIND_DOT at M >= 5):
+ * Pre-attention QKV projection of a decode step in one launch:
  *   h   = round(rms_norm(hidden, norm_w, eps))                       [M,H]
  *   qkv = round(h @ w_qkv.T + bias)                                  [M,N]
  *   y   = qkv with rope(qkv[:, :rope_cols] viewed as heads of head_dim, cos, sin)
@@ -208,8 +207,11 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
  * [M,N] are contiguous; bias ([N], bias_dtype) may be NULL. rope_cols is a
  * multiple of head_dim (0: no rotation); this build needs head_dim % 16 == 0 and
  * H % 8 == 0 (FD_EUNSUPPORTED otherwise: compose fd_rms_norm, fd_linear, fd_rope).
- * With kind FD_KIND_DOT and M >= 5 the RMSNorm goes to `normed` ([M,H], 16-byte
- * aligned) first; otherwise `normed` is unused and may be NULL.
+ * With kind FD_KIND_DOT from M = 5 the projection runs on MFMA with the RMSNorm
+ * folded into the kernel (H up to about 30,000); below that, or with
+ * FD_KIND_SIMT, a SIMT kernel normalises in its prologue. `normed` is unused at
+ * every M and may be NULL (it stays in the signature for callers written against
+ * earlier builds).
  * No reference counterpart as one call: it fuses the composition a caller of the
  * reference writes from rms_norm (ops.py:72-88), linear_decode (ops.py:212-280)
  * and rope (ops.py:138-160) on the q and k heads, the first cross-op fusion the

@@ -124,7 +124,6 @@ def test_qkv_rejects(L):
     assert call(eps=float("nan")) == L.FD_EINVAL
     assert call(kind=5) == L.FD_EINVAL
     assert call(cs_rs=-1) == L.FD_EINVAL
-    assert call(m=8, kind=0) == L.FD_EINVAL              # kind=dot at 8 rows needs `normed`
     assert call(m=0) == L.FD_OK
 
 

@@ -147,7 +147,7 @@ def test_tile_table_matches_the_dispatch_constants():
         m = int(m[1:])
         assert kind in ("dot", "simt") and 1 <= waves <= 8
         if rows == 16:
-            assert kind == "dot" and stages in (1, 2)
+            assert kind == "dot" and stages in (1, 2, 3) and waves in (2, 4, 8)
         else:
             assert rows in (2, 4, 8) and rows * m <= 64 and stages == 1
 
