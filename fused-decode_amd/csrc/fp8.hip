@@ -15,9 +15,11 @@
 //
 // Layout per SIMT step (M < 5): a lane streams 16 consecutive codes (16 bytes) of
 // each of its workgroup's R rows, so a wave covers 1024 K elements per step.
-// From 5 rows the products run on MFMA: codes are decoded into the LDS tile of
-// the relayout GEMV (gemv.hip) and multiplied there.
+// From 5 rows the products run on MFMA: the GEMV and the fused QKV in the DMA
+// GEMV of fd_dma.h (codes decoded after their LDS read), the MLP's gate/up in a
+// relayout kernel that decodes the codes into an LDS tile.
 
+#include "fd_dma.h"
 #include "fd_gemv.h"
 #include "fd_internal.h"
 
@@ -244,13 +246,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_kernel(
   stream_steps(p.total, a, b, issue, consume);
 }
 
-// MFMA form of the fp8 GEMV for M >= kFp8MfmaMinM (M padded to 16): the relayout
-// GEMV of gemv.hip with a decode step. A lane loads 16 codes (one 16-byte load)
-// of row lane/8 (+8 for the second load) at K chunk lane%8 of a 128-wide unit,
-// decodes them to two 8-element chunks of the activation type (exact values)
-// and stores those to the wave's XOR-swizzled LDS tile exactly where the fp16
-// kernel stores a loaded chunk; the A reads, B (x) loads and MFMAs are the fp16
-// kernel's, and the channel scale is applied to the sums.
+// Relayout form of the MFMA gate/up for M >= kFp8MfmaMinM (M padded to 16). A
+// lane loads 16 codes (one 16-byte load) of row lane/8 (+8 for the second load)
+// at K chunk lane%8 of a 128-wide unit, decodes them to two 8-element chunks of
+// the activation type (exact values) and stores those to the wave's
+// XOR-swizzled LDS tile exactly where the fp16 relayout kernel (gemv.hip) stores
+// a loaded chunk; the A reads, B (x) loads and MFMAs are that kernel's, and the
+// channel scale is applied to the sums.
 template <typename T>
 __device__ __forceinline__ void fp8x16_to_tile(const u32x4& w, u32x4& c0, u32x4& c1) {
   uint32_t h[8];
@@ -311,53 +313,6 @@ __device__ __forceinline__ void stage_unit8(const u32x4 (&v)[2], u32x4* tile, in
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <typename T, bool ROPE>
-__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_relayout_kernel(
-    T* y, const T* x, const uint8_t* w, const float* wscale, int M, int N, int K, int64_t sxm,
-    int64_t swn, int64_t sym, int64_t syn, Epi e, Rope rp) {
-  typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * kWave];
-  __shared__ u32x4 tiles[kMaxWaves][256];
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int nw = block_threads() / kWave;
-  const int r = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const T* xr = x + (r < M ? r : 0) * sxm;  // rows past M: output columns never stored
-  const int lrow = lane >> 3, lchunk = lane & 7;  // load side: row lrow (+8), 16 codes at chunk lchunk
-  const uint8_t* wl[1][2];
-  const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int64_t n = ROPE ? tr.row(8 * i + lrow) : n0 + 8 * i + lrow;
-    wl[0][i] = w + (n < N ? n : 0) * swn;
-  }
-  u32x4* tile = tiles[wave];
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int units = (K + kUnit - 1) / kUnit;
-  const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;  // this wave's units
-  const int off = sweep_offset(units);
-  auto issue = [&](UnitRegs8<T, 1>& q, int i) { load_unit8<T, 1>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, K); };
-  auto consume = [&](const UnitRegs8<T, 1>& q, int i) {
-    const int u = sweep_unit(wave, i, nw, off, units);
-    V8 a[4];
-    stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, K, r, g, a);
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(a[s2], unit_b(q.b[s2], u, s2, g, K), acc);
-  };
-  UnitRegs8<T, 1> qa, qb;
-  if (mine > 0) issue(qa, 0);
-  stream_steps(mine, qa, qb, issue, consume);
-  part[wave * kWave + lane] = acc;
-  __syncthreads();
-  if (threadIdx.x < kWave) {
-    f32x4 sm = part[threadIdx.x];
-    for (int i = 1; i < nw; ++i) sm += part[i * kWave + threadIdx.x];
-    const TileAngles ang = ROPE && tr.rotated() ? tile_angles(rp, tr, threadIdx.x, M) : TileAngles{};
-    mfma_tile_out<T, ROPE>(y, sm, threadIdx.x, n0, tr, e, ang, RowScale{wscale}, M, N, sym, syn);
-  }
 }
 
 // Pre-attention QKV with fp8 weights for M < 5: the fp16 fused QKV kernel's
@@ -524,24 +479,36 @@ template <int M> struct Fp8QkvRows { static constexpr int R = M <= 2 ? 8 : 4; };
 // From this many rows the fp8 GEMV and MLP take the MFMA (relayout) forms.
 constexpr int kFp8MfmaMinM = 5;
 
-// `rp` (fused QKV): tiles placed by TileRows<16> with RoPE in the epilogue.
+
+// The MFMA form (kFp8MfmaMinM rows and up): the DMA GEMV of fd_dma.h. `rp`
+// (fused QKV): tiles placed by TileRows<16> with RoPE in the epilogue; `fold`:
+// the RMSNorm of x folded in (x = raw activations).
 template <typename T>
-void launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
-                          int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-                          hipStream_t st, const Rope* rp = nullptr) {
-  // Each wave keeps two units in flight; with four or more 16-row tiles per CU
-  // (N = 28672: 1792 tiles), 4-wave workgroups measured faster than 8 (29.7
-  // against 35.5 us at M=8), with fewer, 8-wave ones (N = 4096: 7.6 against 9.1).
-  const int tiles = (N + 15) / 16;
-  int nw = pick_waves((K + kUnit - 1) / kUnit);
-  if (tiles >= 4 * device_cus() && nw > 4) nw = 4;
-  const dim3 grid((unsigned)tiles), block(nw * kWave);
+int launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
+                         int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                         hipStream_t st, const Rope* rp = nullptr, const FoldNorm* fold = nullptr) {
+  const FoldNorm nofold{nullptr, FD_F32, 0.f};
+  const Rope none{};
+  const unsigned blocks =
+      rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
+  if (rp && fold)
+    return launch_dma_default<T, uint8_t, EPI_ROPE, true>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn, e,
+                                                          *rp, *fold, st);
   if (rp)
-    hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T, true>), grid, block, 0, st, static_cast<T*>(y),
-                       static_cast<const T*>(x), w, s, M, N, K, sxm, swn, sym, syn, e, *rp);
-  else
-    hipLaunchKernelGGL((gemv_fp8_relayout_kernel<T, false>), grid, block, 0, st, static_cast<T*>(y),
-                       static_cast<const T*>(x), w, s, M, N, K, sxm, swn, sym, syn, e, Rope{});
+    return launch_dma_default<T, uint8_t, EPI_ROPE, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn, e,
+                                                           *rp, nofold, st);
+  if ((K + kUnit - 1) / kUnit < 4)
+    return launch_dma_rows<T, uint8_t, 2, 2, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
+                                                               e, none, nofold, st);
+  // Three units in flight where the tiles fit on the chip in two rounds or
+  // fewer, two on wide layers (Llama-3-8B widths, M=8: N=4096 K=14336 14.5 us
+  // against 17.0 for two; N=28672 K=4096 26.4 against 27.6 for three; the
+  // relayout kernel this replaced: 15.6 and 29.8).
+  if (blocks <= 2u * (unsigned)device_cus())
+    return launch_dma_rows<T, uint8_t, 4, 3, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
+                                                               e, none, nofold, st);
+  return launch_dma_rows<T, uint8_t, 4, 2, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn, e,
+                                                             none, nofold, st);
 }
 
 template <typename T, int M>
@@ -556,13 +523,10 @@ void launch_gemv_fp8(void* y, const void* x, const uint8_t* w, const float* s, i
 }
 
 template <typename T>
-void launch_gemv_fp8_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
-                       int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-                       hipStream_t st) {
-  if (M >= kFp8MfmaMinM) {
-    launch_gemv_fp8_mfma<T>(M, y, x, w, s, N, K, sxm, swn, sym, syn, e, st);
-    return;
-  }
+int launch_gemv_fp8_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N,
+                      int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                      hipStream_t st) {
+  if (M >= kFp8MfmaMinM) return launch_gemv_fp8_mfma<T>(M, y, x, w, s, N, K, sxm, swn, sym, syn, e, st);
   switch (M) {
 #define FD_CASE(MM) \
   case MM: launch_gemv_fp8<T, MM>(y, x, w, s, N, K, sxm, swn, sym, syn, e, st); break;
@@ -572,6 +536,7 @@ void launch_gemv_fp8_m(int M, void* y, const void* x, const uint8_t* w, const fl
 #undef FD_CASE
     default: break;
   }
+  return FD_OK;
 }
 
 template <typename T, int M>
@@ -688,10 +653,10 @@ extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float
   e.srn = srn;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w8);
-  if (act_dtype == FD_F16)
-    launch_gemv_fp8_m<f16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
-  else
-    launch_gemv_fp8_m<bf16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  const int rc = act_dtype == FD_F16
+                     ? launch_gemv_fp8_m<f16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st)
+                     : launch_gemv_fp8_m<bf16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  if (rc != FD_OK) return rc;
   return check_launch();
 }
 
@@ -751,10 +716,10 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
   e.srm = H;
   e.srn = 1;
   const uint8_t* wd = static_cast<const uint8_t*>(w_down8);
-  if (act_dtype == FD_F16)
-    launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
-  else
-    launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  rc = act_dtype == FD_F16
+           ? launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st)
+           : launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  if (rc != FD_OK) return rc;
   return check_launch();
 }
 
@@ -771,20 +736,21 @@ extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, co
   bool empty = false;
   const int checked = qkv_prepare(y, normed, hidden, norm_w, norm_w_dtype, w_qkv8, bias,
                                   bias_dtype, cos, sin, cs_dtype, cs_row_stride, M, H, N,
-                                  rope_cols, head_dim, eps, act_dtype, mfma, e, rp, empty);
+                                  rope_cols, head_dim, eps, act_dtype, false, e, rp, empty);
   if (checked != FD_OK || empty) return checked;
   if (!w_scale) return set_error(FD_EINVAL, "null pointer argument");
   if (H % 16 != 0) return set_error(FD_EUNSUPPORTED, "the fp8 QKV needs H %% 16 == 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w_qkv8);
-  if (mfma) {
+  if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
-    const int rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
+    const FoldNorm fn{norm_w, norm_w_dtype, eps};
+    const int rc = act_dtype == FD_F16
+                       ? launch_gemv_fp8_mfma<f16>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1,
+                                                   e, st, &rp, &fn)
+                       : launch_gemv_fp8_mfma<bf16>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N,
+                                                    1, e, st, &rp, &fn);
     if (rc != FD_OK) return rc;
-    if (act_dtype == FD_F16)
-      launch_gemv_fp8_mfma<f16>((int)M, y, normed, w, w_scale, (int)N, (int)H, H, H, N, 1, e, st, &rp);
-    else
-      launch_gemv_fp8_mfma<bf16>((int)M, y, normed, w, w_scale, (int)N, (int)H, H, H, N, 1, e, st, &rp);
   } else {
     const int rc = act_dtype == FD_F16
                        ? launch_qkv_fp8_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w, w_scale,

@@ -38,6 +38,7 @@
 // pair land in one workgroup, which applies RoPE in the epilogue.
 #include <mutex>
 
+#include "fd_dma.h"
 #include "fd_gemv.h"
 #include "fd_internal.h"
 
@@ -204,166 +205,6 @@ __device__ __forceinline__ void stage_unit16(const u32x4 (&v)[4], u32x4* tile, i
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// MFMA GEMV with its tiles streamed into LDS by DMA (kind=dot from kMfmaMinM rows).
-// A workgroup of NW waves owns 16 weight rows; wave w takes K units w, w + NW,
-// ... of a sweep that starts at the workgroup's XCD offset (sweep_unit). A unit
-// is the 16 x 128 weight tile (4 KiB) and the BR x 128 activation tile (BR = M
-// rounded up to 4, 8 or 16), moved by 4 + BR/4 DMA instructions into one of the
-// wave's D ring slots, D units in flight. Each instruction covers 4 whole rows
-// (2 full 128-byte lines each): lane L fetches row 4i + L/16 at chunk
-// (L%16) ^ row, so the slot holds every row XOR-swizzled and the A fragment
-// reads (lane: row r, chunk 4*s2 + g) hit 16 distinct bank groups. Activation
-// rows past M re-read row 0 and weight rows past N row 0 (their outputs are
-// never stored). In a unit that crosses K, lanes fetch their row's first chunk
-// for chunks past K and then overwrite those ring entries with zeros, so every
-// unit runs the same four MFMAs. Partial sums meet in LDS, and wave 0 writes the
-// tile through mfma_tile_out (with ROPE the tile rows follow TileRows<16> and
-// the epilogue rotates them).
-//
-// With NORM, x is the raw activation and the kernel applies the RMSNorm itself:
-// the norm weight (float32) and the rows' inverse RMS are staged in dynamic LDS
-// (norm_dma_lds bytes) by a prologue that runs while the first units' DMAs are
-// in flight, and every B fragment is normalised after its LDS read.
-template <typename T, int NW, int D, int BR, bool ROPE, bool NORM>
-__global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
-    T* y, const T* x, const T* w, int M, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
-    int64_t syn, Epi e, Rope rp, const void* nwp, int nw_dtype, float eps) {
-  typedef typename Vec8<T>::type V8;
-  constexpr int SLOT = 256 + BR * 16;  // 16-byte entries: the A tile, then the B rows
-  constexpr int OPS = 4 + BR / 4;      // DMA instructions per unit
-  __shared__ u32x4 ring[NW][D][SLOT];
-  __shared__ f32x4 part[NW * kWave];
-  extern __shared__ float norm_lds[];  // NORM: w [units * 128], inv [16], scratch
-  const int lane = threadIdx.x & (kWave - 1);
-  // wave-uniform, so the unit indices, the K-tail tests and the ring addresses
-  // are scalar (a per-lane value here turns the tail test into exec-masked
-  // branches that shuttle the accumulator out of the MFMA registers every unit)
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int r = lane & 15, g = lane >> 4;
-  const int64_t n0 = (int64_t)blockIdx.x * 16;
-  const TileRows<16> tr(rp, ROPE ? (int)blockIdx.x : 0);
-  const T* wrow[4];
-  int wch[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * i + (lane >> 4);
-    const int64_t n = ROPE ? tr.row(row) : n0 + row;
-    wrow[i] = w + (n < N ? n : 0) * swn;
-    wch[i] = ((lane & 15) ^ row) * 8;
-  }
-  const T* xrow[BR / 4];
-  int xch[BR / 4];
-#pragma unroll
-  for (int i = 0; i < BR / 4; ++i) {
-    const int row = 4 * i + (lane >> 4);
-    xrow[i] = x + (row < M ? row : 0) * sxm;
-    xch[i] = ((lane & 15) ^ row) * 8;
-  }
-  const int units = (K + kUnit - 1) / kUnit;
-  const int mine = wave < units ? (units - wave + NW - 1) / NW : 0;
-  const int off = sweep_offset(units);
-  auto issue = [&](int j) {
-    const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
-    u32x4* slot = ring[wave][j % D];
-    if (k0 + kUnit <= K) {  // a whole unit (every unit but a K tail): no clamps
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(wrow[i] + k0 + wch[i], slot + i * kWave);
-#pragma unroll
-      for (int i = 0; i < BR / 4; ++i) dma16(xrow[i] + k0 + xch[i], slot + 256 + i * kWave);
-    } else {  // the same instruction count, chunks past K clamped to the row's first
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int k = k0 + wch[i];
-        dma16(wrow[i] + (k < K ? k : 0), slot + i * kWave);
-      }
-#pragma unroll
-      for (int i = 0; i < BR / 4; ++i) {
-        const int k = k0 + xch[i];
-        dma16(xrow[i] + (k < K ? k : 0), slot + 256 + i * kWave);
-      }
-    }
-  };
-  // this lane's fragment entries within a slot, and the entries its DMAs fill (bytes)
-  const unsigned ring0 = lds_addr(&ring[wave][0][0]);
-  const int rb = r % BR;
-  unsigned fa[4], fb[4];
-#pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2) {
-    fa[s2] = ring0 + (unsigned)(r * 16 + ((s2 * 4 + g) ^ r)) * 16u;
-    fb[s2] = ring0 + (unsigned)(256 + rb * 16 + ((s2 * 4 + g) ^ rb)) * 16u;
-  }
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float rinv = 0.f;  // NORM: inverse RMS of this lane's B row
-  unsigned fw = 0;   // NORM: this lane's norm-weight fragment base (bytes)
-  auto consume = [&](int j) {
-    const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
-    const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
-    if (k0 + kUnit > K) {  // K tail: zero the entries fetched past K
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (k0 + wch[i] >= K) ds_zero16(ring0 + so + (unsigned)(i * kWave + lane) * 16u);
-#pragma unroll
-      for (int i = 0; i < BR / 4; ++i)
-        if (k0 + xch[i] >= K) ds_zero16(ring0 + so + (unsigned)(256 + i * kWave + lane) * 16u);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    u32x4 a[4], b[4];
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      a[s2] = ds_read16(fa[s2] + so);
-      b[s2] = ds_read16(fb[s2] + so);
-    }
-    if constexpr (NORM) {
-      u32x4 c[8];  // norm weight of fragment s2: floats k0 + (4 s2 + g) * 8 .. + 8
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {
-        const unsigned wa = fw + (unsigned)(k0 + s2 * 32) * 4u;
-        c[2 * s2] = ds_read16(wa);
-        c[2 * s2 + 1] = ds_read16(wa + 16u);
-      }
-      wait_lds(a, b, c);
-#pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) b[s2] = norm_frag<T>(b[s2], rinv, c[2 * s2], c[2 * s2 + 1]);
-    } else {
-      wait_lds(a, b);
-    }
-#pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) acc = mfma16(__builtin_bit_cast(V8, a[s2]), __builtin_bit_cast(V8, b[s2]), acc);
-  };
-  const int pre = mine < D ? mine : D;
-  // wave 0 writes the tile: its cos/sin loads go out first, so they complete
-  // under the main loop's first wait instead of after the loop
-  TileAngles ang{};
-  if constexpr (ROPE)
-    if (wave == 0 && tr.rotated()) ang = tile_angles(rp, tr, lane, M);
-  if constexpr (NORM) {
-    float* wl = norm_lds;
-    float* inv = norm_lds + units * kUnit;
-    stage_norm_w(wl, nwp, nw_dtype, K, units * kUnit);
-    for (int j = 0; j < pre; ++j) issue(j);
-    row_inv_rms<T, BR>(inv, inv + 16, x, sxm, M, K, eps);
-    rinv = inv[rb];
-    fw = lds_addr(wl) + (unsigned)(g * 8) * 4u;
-  } else {
-    for (int j = 0; j < pre; ++j) issue(j);
-  }
-  int j = 0;
-  for (; j + D <= mine; ++j) {  // D units in flight: the D-1 after unit j may stay outstanding
-    wait_vm<OPS * (D - 1)>();
-    consume(j);
-    if (j + D < mine) issue(j + D);
-  }
-  wait_vm<0>();
-  for (; j < mine; ++j) consume(j);
-  part[wave * kWave + lane] = acc;
-  __syncthreads();
-  if (threadIdx.x < kWave) {
-    f32x4 s = part[threadIdx.x];
-    for (int i = 1; i < NW; ++i) s += part[i * kWave + threadIdx.x];
-    mfma_tile_out<T, ROPE>(y, s, threadIdx.x, n0, tr, e, ang, NoScale{}, M, N, sym, syn);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -704,63 +545,10 @@ void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, i
   }
 }
 
-// LDS of one DMA MFMA workgroup: its ring and the cross-wave partial sums.
-constexpr size_t dma_lds(int nw, int d, int br) {
-  return (size_t)nw * d * (256 + br * 16) * 16 + (size_t)nw * kWave * 16;
-}
-
-// Activation rows a DMA MFMA launch stages: M rounded up to 4, 8 or 16.
-inline int dma_rows(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
-
 // Shapes of the DMA MFMA GEMV a tile may name: waves 2, 4 or 8, units in flight
 // 1-3, within the LDS of one CU.
 inline bool dma_shape_ok(int nw, int d, int M) {
   return (nw == 2 || nw == 4 || nw == 8) && d >= 1 && d <= 3 && dma_lds(nw, d, dma_rows(M)) <= kMaxLds;
-}
-
-// The RMSNorm folded into a DMA MFMA launch (x = raw activations, normalised in
-// the kernel with norm_w / eps).
-struct FoldNorm {
-  const void* w;
-  int dtype;
-  float eps;
-};
-
-// Dynamic LDS of a NORM launch: the float32 norm weight over whole K units, the
-// 16 inverse RMS values and the reduction scratch.
-inline size_t norm_dma_lds(int K) {
-  return sizeof(float) * ((size_t)((K + kUnit - 1) / kUnit) * kUnit + 16 + kMaxWaves * 16);
-}
-
-template <typename T, int NW, int D, int BR, bool ROPE, bool NORM>
-int launch_dma(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
-               int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Rope& r,
-               const FoldNorm& fn, hipStream_t st) {
-  if constexpr (dma_lds(NW, D, BR) <= kMaxLds) {
-    const size_t dyn = NORM ? norm_dma_lds(K) : 0;
-    auto kernel = gemv_mfma_dma_kernel<T, NW, D, BR, ROPE, NORM>;
-    if (dma_lds(NW, D, BR) + dyn > kMaxLds)
-      return set_error(FD_EUNSUPPORTED, "K too large for the folded RMSNorm's LDS stage");
-    if (!allow_lds(kernel, dyn))
-      return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", dyn);
-    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(NW * kWave), dyn, st, static_cast<T*>(y),
-                       static_cast<const T*>(x), static_cast<const T*>(w), M, N, K, sxm, swn, sym,
-                       syn, e, r, fn.w, fn.dtype, fn.eps);
-    return FD_OK;
-  }
-  return set_error(FD_EINVAL, "MFMA tile beyond the LDS of a CU");
-}
-
-template <typename T, int NW, int D, bool ROPE, bool NORM>
-int launch_dma_rows(unsigned blocks, void* y, const void* x, const void* w, int M, int N, int K,
-                    int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-                    const Rope& r, const FoldNorm& fn, hipStream_t st) {
-  const int br = dma_rows(M);
-  if (br == 4)
-    return launch_dma<T, NW, D, 4, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
-  if (br == 8)
-    return launch_dma<T, NW, D, 8, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
-  return launch_dma<T, NW, D, 16, ROPE, NORM>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, fn, st);
 }
 
 // Default shape: four waves (fewer when K has fewer units) with two units in
@@ -780,20 +568,15 @@ int launch_mfma(int M, void* y, const void* x, const void* w, int N, int K, int6
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
   const Rope& r = rp ? *rp : none;
-  if (fold) {  // the fused QKV from kMfmaMinM rows: RoPE epilogue, RMSNorm folded in
-    return nw >= 4 ? launch_dma_rows<T, 4, 2, true, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
-                                                          *fold, st)
-                   : launch_dma_rows<T, 2, 2, true, true>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
-                                                          *fold, st);
-  }
-  if (rp) {
-    return nw >= 4 ? launch_dma_rows<T, 4, 2, true, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
-                                                           nofold, st)
-                   : launch_dma_rows<T, 2, 2, true, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r,
-                                                           nofold, st);
-  }
-#define FD_DMA(NW, D) \
-  return launch_dma_rows<T, NW, D, false, false>(blocks, y, x, w, M, N, K, sxm, swn, sym, syn, e, r, nofold, st)
+  if (fold)  // the fused QKV from kMfmaMinM rows: RoPE epilogue, RMSNorm folded in
+    return launch_dma_default<T, T, EPI_ROPE, true>(blocks, y, x, w, nullptr, M, N, K, sxm, swn, sym, syn, e,
+                                                    r, *fold, st);
+  if (rp)
+    return launch_dma_default<T, T, EPI_ROPE, false>(blocks, y, x, w, nullptr, M, N, K, sxm, swn, sym, syn,
+                                                     e, r, nofold, st);
+#define FD_DMA(NW, D)                                                                                        \
+  return launch_dma_rows<T, T, NW, D, EPI_PLAIN, false>(blocks, y, x, w, nullptr, M, N, K, sxm, swn, sym, syn, \
+                                                        e, r, nofold, st)
   if (nw <= 2) {
     if (d == 1) FD_DMA(2, 1); else if (d == 2) FD_DMA(2, 2); else FD_DMA(2, 3);
   } else if (nw <= 4) {
@@ -1047,12 +830,17 @@ int mlp_check(void* mid, const void* hidden, const void* norm_w, int norm_w_dtyp
 // Whether the gate/up launch of this call needs the [M, H] `normed` buffer
 // (the MFMA form normalises in a separate row kernel).
 bool mlp_needs_normed(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
+bool mlp_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
 
 int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
                 const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
                 int act_dtype, hipStream_t st) {
   int rc;
   if (mlp_needs_normed(M, kind)) {
+    // The relayout kernel (register loads, 16 gate and 16 up rows per workgroup
+    // against one B tile), not the DMA form: Llama-3-8B widths, M=8, whole MLP
+    // 63.5 us against 72.9 for DMA workgroups of the same two tiles, 69.9 for
+    // DMA tiles of 8 gate + 8 up rows, 77.7 for those with the norm folded in.
     rc = rms_rows(normed, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
     if (rc != FD_OK) return rc;
     rc = act_dtype == FD_F16
@@ -1192,7 +980,7 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
   using namespace fd;
   if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
     return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
-  const bool mfma = mlp_needs_normed(M, kind);
+  const bool mfma = mlp_mfma(M, kind);
   Epi e;
   Rope rp;
   bool empty = false;

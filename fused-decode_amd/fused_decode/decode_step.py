@@ -160,7 +160,7 @@ class DecodeStep:
         mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
         mlp = 3 if mfma else 2
         if self.fp8:  # the fp8 kernels take the MFMA forms from 5 rows whatever the kind
-            return (2 if self.m >= _MFMA_MIN_M else 1) + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
+            return 1 + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
         if self.fused:
             return 1 + 1 + mlp
         return 4 + mlp

@@ -211,11 +211,8 @@ def pre_attn_qkv_fp8(
             h2 = h2.contiguous()
         nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
         b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
-        normed = None
-        if m >= _FP8_MFMA_MIN_M:
-            normed = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
         status = native().pre_attn_qkv_fp8(
-            out.data_ptr(), normed.data_ptr() if normed is not None else None, h2.data_ptr(),
+            out.data_ptr(), None, h2.data_ptr(),
             nw.data_ptr(), DTYPE_CODE[nw.dtype], w_qkv.data_ptr(), scale.contiguous().data_ptr(),
             b.data_ptr() if b is not None else None,
             DTYPE_CODE[b.dtype] if b is not None else DTYPE_CODE[hidden.dtype],

@@ -261,9 +261,9 @@ int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* nor
  * fd_pre_attn_qkv with FP8 weights: w_qkv8 [N,H] E4M3 codes (contiguous) with
  * per-row float32 scales w_scale [N]; the projection is fd_linear_fp8's product
  * and everything else (RMSNorm, bias, rounding, RoPE of the first rope_cols
- * columns, cos/sin layout) is fd_pre_attn_qkv's. One launch up to M = 4; from
- * M = 5 the RMSNorm runs first into `normed` ([M,H], 16-byte aligned; unused and
- * may be NULL below that) and the products run on MFMA. H % 16 == 0 and
+ * columns, cos/sin layout) is fd_pre_attn_qkv's. One launch at every M (from
+ * M = 5 the MFMA form, with the RMSNorm folded in); `normed` is unused and may
+ * be NULL (kept for the fp16 entry point's signature). H % 16 == 0 and
  * head_dim % 16 == 0 (else FD_EUNSUPPORTED). No reference counterpart (see
  * fd_linear_fp8 and fd_pre_attn_qkv).
  */

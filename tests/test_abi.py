@@ -176,7 +176,9 @@ def test_fp8_entry_points_reject(L):
     assert qkv(h=72) == L.FD_EUNSUPPORTED                  # H % 16
     assert qkv(head_dim=24, rope_cols=48) == L.FD_EUNSUPPORTED
     assert qkv(rope_cols=48) == L.FD_EINVAL                # not a multiple of head_dim
-    assert qkv(m=5) == L.FD_EINVAL                         # the MFMA form needs `normed`
+    # the MFMA form (from 5 rows) folds the norm in: a null `normed` passes the
+    # checks (without a GPU only the launch fails)
+    assert qkv(m=5) not in (L.FD_EINVAL, L.FD_EUNSUPPORTED)
     assert qkv(m=0) == L.FD_OK
 
 

@@ -269,7 +269,7 @@ def test_decode_step_fp8_matches_oracle_and_graph(m):
         out = ds.replay()
         torch.cuda.synchronize()
         torch.testing.assert_close(out, eager, rtol=0, atol=0)
-    assert ds.launches_per_layer == (4 if m < 5 else 6)
+    assert ds.launches_per_layer == (4 if m < 5 else 5)
 
 
 # ---------------------------------------------------------------- fused QKV
@@ -375,8 +375,9 @@ def test_pre_attn_qkv_fp8_llama3_8b(dtype, m):
 
 
 def test_pre_attn_qkv_fp8_entry_point_and_rejects():
-    """fd_pre_attn_qkv_fp8 through the C ABI: from 5 rows it needs `normed`, H not
-    a multiple of 16 is FD_EUNSUPPORTED; the Python checks of pre_attn_qkv hold."""
+    """fd_pre_attn_qkv_fp8 through the C ABI: from 5 rows the MFMA form folds the
+    RMSNorm in (`normed` may be null and is left untouched), H not a multiple of 16
+    is FD_EUNSUPPORTED; the Python checks of pre_attn_qkv hold."""
     import fused_decode as fd
     from fused_decode import _lib as L
 
@@ -389,11 +390,15 @@ def test_pre_attn_qkv_fp8_entry_point_and_rejects():
     args = lambda nrm, hh: (  # noqa: E731
         y.data_ptr(), nrm, hd.data_ptr(), nwd.data_ptr(), L.FD_F16, q.data_ptr(), s.data_ptr(), None,
         L.FD_F16, cd.data_ptr(), sd.data_ptr(), L.FD_F32, 64, 8, hh, n, rc, 64, 1e-5, L.FD_F16, st)
-    assert L.lib().fd_pre_attn_qkv_fp8(*args(None, 256)) == L.FD_EINVAL
     assert L.lib().fd_pre_attn_qkv_fp8(*args(normed.data_ptr(), 248)) == L.FD_EUNSUPPORTED
-    L.check("fd_pre_attn_qkv_fp8", L.lib().fd_pre_attn_qkv_fp8(*args(normed.data_ptr(), 256)))
     ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+    L.check("fd_pre_attn_qkv_fp8", L.lib().fd_pre_attn_qkv_fp8(*args(None, 256)))
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    normed.fill_(7.0)
+    y.zero_()
+    L.check("fd_pre_attn_qkv_fp8", L.lib().fd_pre_attn_qkv_fp8(*args(normed.data_ptr(), 256)))
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    assert bool((normed == 7.0).all()), "normed must be left untouched"
     with pytest.raises(TypeError, match="float8_e4m3fn"):
         fd.pre_attn_qkv_fp8(hd, nwd, q.float(), s, cd, sd, rope_cols=rc)
     with pytest.raises(ValueError, match="scale"):
