@@ -181,6 +181,28 @@ def copy_roof_gbs(torch) -> float:
     return 2 * n / (us * 1e-6) / 1e9
 
 
+def read_roof_gbs(torch) -> float:
+    """The read roof: fd_read streaming 1 GiB (the copy's load pattern, no stores)."""
+    from fused_decode.kernels import launch_read
+
+    n = 1 << 30
+    src = torch.zeros(n, dtype=torch.uint8, device="cuda")
+    hit = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for _ in range(3):
+        launch_read(src, hit)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    iters = 20
+    start.record()
+    for _ in range(iters):
+        launch_read(src, hit)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / iters
+    del src, hit
+    return n / (us * 1e-6) / 1e9
+
+
 def pmc_traffic() -> int | None:
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE passes (profiles/mlp_gate_up_m1_pmc.md), or None."""
@@ -318,6 +340,7 @@ def main() -> None:
                                         "hipGraphLaunch adds an idle gap before its first kernel"},
         "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
         "copy_roof_gbs": round(roof, 1),
+        "read_roof_gbs": round(read_roof_gbs(torch), 1),
         "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
         "target_us": round(1.25 * weights / (roof * 1e9) * 1e6, 2),
         "roofline": {
@@ -361,6 +384,10 @@ def main() -> None:
             f"eager {row['eager_us']} us, {row['pct_copy_roof']}% of copy roof, max_abs {row['max_abs_vs_fp32']:.3g}"))
         line["ops_note"] = ("dev_us: one HIP graph over rotated buffer sets (HBM reads); eager_us: allocating calls "
                             "back to back; gbs and pct_* from dev_us and the reference's useful bytes; "
+                            "same_size_us: the roof kernel moving the op's bytes the same way (fd_copy of half "
+                            "each way for the norms and RoPE, fd_triad for SwiGLU, fd_read of all for the GEMVs) "
+                            "timed like dev_us, "
+                            "pct_same_size = same_size_us / dev_us; "
                             "max_abs_vs_fp32 against the reference's formulas in float32, rounded once")
         torch.cuda.empty_cache()
     if not args.no_cpu:

@@ -249,9 +249,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   if constexpr (NORM) {
     float* wl = norm_lds;
     float* inv = norm_lds + units * kUnit;
-    stage_norm_w(wl, nwp, nw_dtype, K, units * kUnit);
     for (int j = 0; j < pre; ++j) issue(j);
-    row_inv_rms<T, BR>(inv, inv + 16, x, sxm, M, K, eps);
+    norm_prologue<T, BR>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps);
     rinv = inv[rb];
     fw = lds_addr(wl) + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
   } else {

@@ -116,49 +116,78 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
 // in LDS as float32 (zeros from H to `hp`, a whole number of K units) and the
 // inverse RMS of every activation row (inv[m], zero for rows past M); each B
 // fragment of raw activations is then normalised as the row kernels do it,
-// round(x * inv[m] * w[k]) (norm.hip). The caller issues its first DMAs
-// between the two steps, so the weight stream is in flight while the rows are
-// reduced.
-__device__ __forceinline__ void stage_norm_w(float* wl, const void* nwp, int nw_dtype, int H, int hp) {
-  for (int k = threadIdx.x * 8; k < hp; k += block_threads() * 8) {
-    float f[8];
-    if (k < H) {
-      load8_norm_w(nwp, nw_dtype, k, f);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) f[i] = 0.f;
-    }
-    reinterpret_cast<f32x4*>(wl + k)[0] = f32x4{f[0], f[1], f[2], f[3]};
-    reinterpret_cast<f32x4*>(wl + k)[1] = f32x4{f[4], f[5], f[6], f[7]};
+// round(x * inv[m] * w[k]) (norm.hip).
+//
+// One memory round trip: a thread's first two 16-byte chunks of the norm
+// weight and its first 8-element slice of every row are all loaded before
+// either is used (every load unconditional, indices clamped), after the
+// caller's first DMAs, so the three streams are in flight together. Wider rows
+// take further passes. H % 8 == 0; `scratch` holds kMaxWaves * pow2_ceil(MMAX)
+// floats. Ends with a barrier (wl and inv are then visible).
+__device__ __forceinline__ void store_norm_chunk(float* wl, const u32x4& v, int c, int dtype) {
+  if (dtype == FD_F32) {
+    reinterpret_cast<f32x4*>(wl)[c] = __builtin_bit_cast(f32x4, v);
+    return;
   }
+  float f[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t u = v[j];
+    if (dtype == FD_BF16) {
+      f[2 * j] = __builtin_bit_cast(float, u << 16);
+      f[2 * j + 1] = __builtin_bit_cast(float, u & 0xffff0000u);
+    } else {
+      f[2 * j] = (float)__builtin_bit_cast(f16, (unsigned short)(u & 0xffffu));
+      f[2 * j + 1] = (float)__builtin_bit_cast(f16, (unsigned short)(u >> 16));
+    }
+  }
+  reinterpret_cast<f32x4*>(wl)[2 * c] = f32x4{f[0], f[1], f[2], f[3]};
+  reinterpret_cast<f32x4*>(wl)[2 * c + 1] = f32x4{f[4], f[5], f[6], f[7]};
 }
 
-// inv[m] = rsqrt(mean(x[m]^2) + eps) for m < M (0 up to MMAX), every thread of
-// the workgroup; `scratch` holds kMaxWaves * pow2_ceil(MMAX) floats. Ends with
-// a barrier (inv and the caller's staged norm weight are then visible).
 template <typename T, int MMAX>
-__device__ __forceinline__ void row_inv_rms(float* inv, float* scratch, const T* x, int64_t sxm,
-                                            int M, int H, float eps) {
+__device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scratch, const void* nwp,
+                                              int nw_dtype, const T* x, int64_t sxm, int M, int H,
+                                              int hp, float eps) {
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nt = block_threads(), nwv = nt / kWave;
+  const int wchunks = H / (nw_dtype == FD_F32 ? 4 : 8);  // 16-byte chunks of the weight
+  const u32x4* wsrc = static_cast<const u32x4*>(nwp);
+  u32x4 wr[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + i * nt;
+    wr[i] = wsrc[c < wchunks ? c : 0];
+  }
+  const int k0 = tid * 8;
+  V8 h[MMAX];
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k0 < H ? k0 : 0));
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + i * nt;
+    if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
+  }
+  for (int c = tid + 2 * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
+  for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
   float ss[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
-  for (int k = tid * 8; k < H; k += nt * 8) {
-    // every load unconditional (rows past M re-read the last row, masked below):
-    // a load under a branch would make the compiler wait for all outstanding
-    // loads, the caller's in-flight DMAs included, before each use
-    V8 h[MMAX];
-#pragma unroll
-    for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
+  auto add = [&](int k) {
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
-      const float keep = m < M ? 1.f : 0.f;
+      const float keep = m < M && k < H ? 1.f : 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss[m] += keep * (to_f32(h[m][i]) * to_f32(h[m][i]));
     }
+  };
+  add(k0);
+  for (int k = k0 + nt * 8; k < H; k += nt * 8) {
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
+    add(k);
   }
   butterfly_sum<MP>(ss, lane);
   if (butterfly_writer<MP>(lane)) scratch[wave * MP + butterfly_index<MP>(lane)] = ss[0];

@@ -111,6 +111,7 @@ static int (*p_pre_attn_qkv_fp8)(void*, void*, const void*, const void*, int, co
                                  void*);
 static int (*p_copy)(void*, const void*, int64_t, void*);
 static int (*p_triad)(void*, const void*, const void*, float, int64_t, int, void*);
+static int (*p_read)(const void*, int64_t, int, void*, void*);
 
 #define NEED_BOUND()                                                           \
   if (!g_handle) {                                                             \
@@ -165,6 +166,7 @@ WRAP(pre_attn_qkv_fp8, "ppppipppippillllllfis",
                         a[15].l, a[16].l, a[17].l, a[18].f, a[19].i, a[20].p))
 WRAP(copy, "ppls", p_copy(a[0].p, a[1].p, a[2].l, a[3].p))
 WRAP(triad, "pppflis", p_triad(a[0].p, a[1].p, a[2].p, a[3].f, a[4].l, a[5].i, a[6].p))
+WRAP(read, "plips", p_read(a[0].p, a[1].l, a[2].i, a[3].p, a[4].p))
 
 static PyObject* w_last_error(PyObject* self, PyObject* unused) {
   (void)self;
@@ -214,6 +216,7 @@ static PyObject* w_bind(PyObject* self, PyObject* arg) {
   RESOLVE(p_pre_attn_qkv_fp8, "fd_pre_attn_qkv_fp8");
   RESOLVE(p_copy, "fd_copy");
   RESOLVE(p_triad, "fd_triad");
+  RESOLVE(p_read, "fd_read");
   g_handle = h;
   Py_RETURN_NONE;
 }
@@ -236,6 +239,7 @@ static PyMethodDef methods[] = {
     FAST(pre_attn_qkv_fp8),
     FAST(copy),
     FAST(triad),
+    FAST(read),
     {NULL, NULL, 0, NULL},
 };
 

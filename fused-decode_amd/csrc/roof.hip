@@ -1,5 +1,7 @@
-// In-process bandwidth roofs: a 16-byte-vector copy and a STREAM-style triad.
-// Every percent-of-roof figure divides by the copy measured with these.
+// In-process bandwidth roofs: a 16-byte-vector copy, a read of the same layout
+// and a STREAM-style triad. Every percent-of-roof figure divides by the copy
+// measured with these; the read is the ceiling of a kernel that only streams
+// (the decode GEMVs, whose outputs are a few KiB).
 // Also the library's version and error entry points.
 #include "fd_device.h"
 #include "fd_host.h"
@@ -27,6 +29,26 @@ __global__ __launch_bounds__(kRoofThreads) void copy_vec_kernel(u32x4* dst, cons
     const int64_t e = base + i * kRoofThreads;
     if (e < nvec) __builtin_nontemporal_store(v[i], dst + e);
   }
+}
+
+// The copy's loads alone: each thread xors its kRoofUnroll vectors, a wave
+// combines its lanes, and the flag is set where a wave's result equals `key`,
+// so no load can be dropped and the stores are one per 64 KiB at most.
+__global__ __launch_bounds__(kRoofThreads) void read_vec_kernel(const u32x4* src, int64_t nvec,
+                                                                uint32_t key, uint32_t* hit) {
+  const int64_t base = (int64_t)blockIdx.x * (kRoofThreads * kRoofUnroll) + threadIdx.x;
+  u32x4 v[kRoofUnroll];
+#pragma unroll
+  for (int i = 0; i < kRoofUnroll; ++i) {
+    const int64_t e = base + i * kRoofThreads;
+    v[i] = e < nvec ? __builtin_nontemporal_load(src + e) : u32x4{0u, 0u, 0u, 0u};
+  }
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < kRoofUnroll; ++i) acc ^= v[i][0] ^ v[i][1] ^ v[i][2] ^ v[i][3];
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off);
+  if ((threadIdx.x & (kWave - 1)) == 0 && acc == key) atomicOr(hit, 1u);
 }
 
 __global__ __launch_bounds__(kRoofThreads) void copy_byte_kernel(uint8_t* dst, const uint8_t* src,
@@ -100,6 +122,22 @@ extern "C" int fd_copy(void* dst, const void* src, int64_t bytes, void* stream) 
     hipLaunchKernelGGL(copy_byte_kernel, dim3((unsigned)blocks), dim3(kRoofThreads), 0, st,
                        (uint8_t*)dst, (const uint8_t*)src, bytes);
   }
+  return check_launch();
+}
+
+extern "C" int fd_read(const void* src, int64_t bytes, int key, void* hit, void* stream) {
+  if (bytes < 0) return set_error(FD_EINVAL, "bytes must be >= 0");
+  if (bytes == 0) return FD_OK;
+  if (!src || !hit) return set_error(FD_EINVAL, "null pointer argument");
+  if (!aligned16(src) || bytes % 16 != 0)
+    return set_error(FD_EUNSUPPORTED, "the read roof needs a 16-byte aligned source and bytes %% 16 == 0");
+  if ((uintptr_t)hit % 4 != 0) return set_error(FD_EINVAL, "hit must be 4-byte aligned");
+  const int64_t nvec = bytes / 16;
+  const int64_t blocks = (nvec + kRoofThreads * kRoofUnroll - 1) / (kRoofThreads * kRoofUnroll);
+  if (blocks > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "read too large");
+  hipLaunchKernelGGL(read_vec_kernel, dim3((unsigned)blocks), dim3(kRoofThreads), 0,
+                     static_cast<hipStream_t>(stream), (const u32x4*)src, nvec, (uint32_t)key,
+                     static_cast<uint32_t*>(hit));
   return check_launch();
 }
 

@@ -79,6 +79,7 @@ SIGNATURES: dict[str, list] = {
                             _l, _f, _i, _p],
     "fd_copy": [_p, _p, _l, _p],
     "fd_triad": [_p, _p, _p, _f, _l, _i, _p],
+    "fd_read": [_p, _l, _i, _p, _p],
 }
 
 _LIB: ctypes.CDLL | None = None

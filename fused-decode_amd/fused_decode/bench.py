@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib, kernels
-from .kernels import launch_copy, launch_triad
+from .kernels import launch_copy, launch_read, launch_triad
 from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope, swiglu
 
 LLAMA_H = 4096
@@ -490,6 +490,8 @@ def _compact(op, shape, dtype, nbytes, dev_us, eager_us, roof, max_abs, **extra)
            "pct_copy_roof": round(100.0 * gbs / roof, 1), "pct_8tbs": round(100.0 * gbs / DATASHEET_GBS, 1),
            "max_abs_vs_fp32": max_abs}
     row.update({k: (round(v, 2) if isinstance(v, float) else v) for k, v in extra.items()})
+    if extra.get("same_size_us"):
+        row["pct_same_size"] = round(100.0 * extra["same_size_us"] / dev_us, 1)
     return row
 
 
@@ -508,6 +510,37 @@ def ops_block(roof: float, log=print) -> list[dict]:
         eager = time_us(call, iters=iters or max(30, 2 * k), warmup=5, rounds=3)
         return dev, eager
 
+    roofs: dict = {}
+
+    def same_size(kind: str, nbytes: int) -> dict:
+        """The roof kernel moving an op's bytes the same way, timed like its
+        dev_us (a HIP graph over rotated buffers): a copy of half each way for
+        ops that read and write as much, a triad for two reads and a write, a
+        read of all of them for the GEMVs."""
+        key = (kind, nbytes)
+        if key not in roofs:
+            if kind == "triad":  # two reads and one write, fp16
+                n = max(8, nbytes // 6 // 8 * 8)
+                k = copies_for(6 * n)
+                src = [torch.zeros(n, dtype=torch.float16, device="cuda") for _ in range(3 * k)]
+                roofs[key] = graph_us(lambda i: launch_triad(src[3 * (i % k)], src[3 * (i % k) + 1],
+                                                             src[3 * (i % k) + 2], 1.0), k)
+            elif kind == "copy":
+                half = max(16, nbytes // 2 // 16 * 16)
+                k = copies_for(2 * half)
+                src = [torch.zeros(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
+                dst = [torch.empty(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
+                roofs[key] = graph_us(lambda i: launch_copy(dst[i % k], src[i % k]), k)
+            else:
+                n = max(16, nbytes // 16 * 16)
+                k = copies_for(n)
+                src = [torch.zeros(n, dtype=torch.uint8, device="cuda") for _ in range(k)]
+                hit = torch.zeros(1, dtype=torch.int32, device="cuda")
+                roofs[key] = graph_us(lambda i: launch_read(src[i % k], hit), k)
+            del src
+            torch.cuda.empty_cache()
+        return {"same_size_kind": kind, "same_size_us": roofs[key]}
+
     # norms: x, residual ~N(0,1), weight ~N(1, 0.1), eps 1e-5, residual_out in place
     for r in (8192, 1):
         dt, h = torch.float16, LLAMA_H
@@ -518,13 +551,15 @@ def ops_block(roof: float, log=print) -> list[dict]:
         w = _gen((h,), dt, g, 0.1, 1.0)
         err = _max_abs(rms_norm(xs[0], w, eps), fp32_rms(xs[0], w, eps)[0])
         dev, eager = timed(lambda i: rms_norm(xs[i % k], w, eps), k)
-        rows.append(_compact("rms_norm", (r, h), dt, (2 * r * h + h) * e, dev, eager, roof, err))
+        rows.append(_compact("rms_norm", (r, h), dt, (2 * r * h + h) * e, dev, eager, roof, err,
+                             **same_size("copy", (2 * r * h + h) * e)))
         y_ref, ro_ref = fp32_rms(xs[0], w, eps, rs[0])
         r0 = rs[0].clone()
         y, ro = add_rms_norm(xs[0], r0, w, eps, residual_out=r0)
         err = max(_max_abs(y, y_ref), _max_abs(ro, ro_ref))
         dev, eager = timed(lambda i: add_rms_norm(xs[i % k], rs[i % k], w, eps, residual_out=rs[i % k]), k)
-        rows.append(_compact("add_rms_norm", (r, h), dt, (4 * r * h + h) * e, dev, eager, roof, err))
+        rows.append(_compact("add_rms_norm", (r, h), dt, (4 * r * h + h) * e, dev, eager, roof, err,
+                             **same_size("copy", (4 * r * h + h) * e)))
         log(rows[-2]), log(rows[-1])
         del xs, rs
     # SwiGLU: gate, up ~N(0, 2)
@@ -536,7 +571,8 @@ def ops_block(roof: float, log=print) -> list[dict]:
             us_ = [_gen((r, n), dt, g, 2.0) for _ in range(k)]
             err = _max_abs(swiglu(gs[0], us_[0]), fp32_swiglu(gs[0], us_[0]))
             dev, eager = timed(lambda i: swiglu(gs[i % k], us_[i % k]), k)
-            rows.append(_compact("swiglu", (r, n), dt, 3 * r * n * 2, dev, eager, roof, err))
+            rows.append(_compact("swiglu", (r, n), dt, 3 * r * n * 2, dev, eager, roof, err,
+                                 **same_size("triad", 3 * r * n * 2)))
             log(rows[-1])
             del gs, us_
     # RoPE with Llama-3 tables (theta 500000), cos/sin [2048, 128] viewed [2048, 1, 128]
@@ -551,7 +587,7 @@ def ops_block(roof: float, log=print) -> list[dict]:
             xs = [_gen(xshape, dt, g) for _ in range(k)]
             err = _max_abs(rope(xs[0], c, s_), fp32_rope(xs[0], c, s_))
             dev, eager = timed(lambda i: rope(xs[i % k], c, s_), k)
-            rows.append(_compact("rope", xshape, dt, nbytes, dev, eager, roof, err))
+            rows.append(_compact("rope", xshape, dt, nbytes, dev, eager, roof, err, **same_size("copy", nbytes)))
             log(rows[-1])
             del xs
     # decode GEMV: x ~N(0,1), W ~N(0, 1/sqrt(K)), bias and row_add in the error check
@@ -568,7 +604,7 @@ def ops_block(roof: float, log=print) -> list[dict]:
                 for kind in kinds:
                     err = _max_abs(linear_decode(x, wf, bias, row_add=ra, kind=kind), ref)
                     dev, eager = timed(lambda i: linear_decode(x, ws[i % k], kind=kind), k)
-                    extra = {"kind": kind}
+                    extra = {"kind": kind, **same_size("read", (m * kk + n * kk + m * n) * 2)}
                     if hip is not None:
                         extra["hipblaslt_dev_us"] = hip
                     rows.append(_compact("linear_decode", (m, n, kk), dt, (m * kk + n * kk + m * n) * 2, dev, eager,

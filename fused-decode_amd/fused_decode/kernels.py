@@ -334,6 +334,15 @@ def launch_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
         fail("fd_copy", status)
 
 
+def launch_read(src: torch.Tensor, hit: torch.Tensor, key: int = 0x2545F491) -> None:
+    """Read roof: stream ``src`` (contiguous, 16-byte multiple) and set bit 0 of
+    the int32 ``hit`` where the xor of a wave's words equals ``key``."""
+    nbytes = src.numel() * src.element_size()
+    status = native().read(src.data_ptr(), nbytes, int(key), hit.data_ptr(), stream_of(src))
+    if status:
+        fail("fd_read", status)
+
+
 def launch_triad(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor, scale: float = 1.0) -> None:
     """``c = a + b * scale`` over contiguous tensors of one dtype."""
     status = native().triad(

@@ -283,6 +283,16 @@ int fd_copy(void* dst, const void* src, int64_t bytes, void* stream);
 int fd_triad(void* c, const void* a, const void* b, float scale, int64_t n, int dtype,
              void* stream);
 
+/*
+ * Read roof: streams `bytes` bytes from src (16-byte aligned, bytes % 16 == 0,
+ * else FD_EUNSUPPORTED) with the copy's load pattern and stores nothing but a
+ * flag: *hit (a device word, 4-byte aligned) gets bit 0 set where the xor of
+ * the words one wave read equals `key`, so the loads cannot be elided. The
+ * ceiling of a kernel that only streams, as the decode GEMVs do. No reference
+ * counterpart (its bench has the copy and the triad).
+ */
+int fd_read(const void* src, int64_t bytes, int key, void* hit, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,18 @@ def test_version_and_error_string(L):
     assert lib.fd_copy(None, None, 0, None) == L.FD_OK  # empty copy: nothing to do
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="host-only argument checks")
+def test_read_rejects(L):
+    lib = L.lib()
+    assert lib.fd_read(0x1000, -16, 0, 0x2000, None) == L.FD_EINVAL
+    assert lib.fd_read(None, 0, 0, None, None) == L.FD_OK        # nothing to read
+    assert lib.fd_read(None, 16, 0, 0x2000, None) == L.FD_EINVAL
+    assert lib.fd_read(0x1000, 16, 0, None, None) == L.FD_EINVAL
+    assert lib.fd_read(0x1008, 16, 0, 0x2000, None) == L.FD_EUNSUPPORTED  # misaligned source
+    assert lib.fd_read(0x1000, 24, 0, 0x2000, None) == L.FD_EUNSUPPORTED  # not whole vectors
+    assert lib.fd_read(0x1000, 16, 0, 0x2002, None) == L.FD_EINVAL        # misaligned flag
+
+
 # Argument checks below return before any HIP call; the pointers are never
 # dereferenced. Skipped where a GPU is present so no launch can ever see them.
 nogpu = pytest.mark.skipif(torch.cuda.is_available(), reason="host-only argument checks")

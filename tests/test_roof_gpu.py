@@ -1,7 +1,9 @@
 """The bandwidth roofs every "% of copy roof" figure divides by: fd_copy must
 copy exactly the bytes it is given (vector path for 16-byte aligned sizes and
 pointers, byte path otherwise) and touch nothing past them; fd_triad must
-compute c = a + b * scale in float32 with one rounding to the element type.
+compute c = a + b * scale in float32 with one rounding to the element type;
+fd_read must read every word it is given (its flag follows the xor of each
+wave's words) and nothing past them.
 The launchers of the reference's kernels.py:833-858 (launch_copy,
 launch_triad) are exercised through the same calls."""
 
@@ -87,3 +89,56 @@ def test_launch_triad_wrapper(L):
     launch_triad(a, b, c, -0.5)
     torch.cuda.synchronize()
     torch.testing.assert_close(c.cpu(), _triad_expected(a, b, -0.5), rtol=8e-3, atol=1e-6)
+
+
+def _wave_xors(words: torch.Tensor) -> list[int]:
+    """The xor of the 32-bit words each wave of fd_read's kernel reads: wave w of
+    block b takes 16-byte vectors b*1024 + 64w + j + 256i (j < 64, i < 4)."""
+    nvec = words.numel() // 4
+    vec = words.view(nvec, 4).cpu().numpy().astype("uint32")
+    out = []
+    blocks = (nvec + 1023) // 1024
+    for b in range(blocks):
+        for w in range(4):
+            acc = 0
+            for i in range(4):
+                lo = b * 1024 + 256 * i + 64 * w
+                for row in vec[lo: min(lo + 64, nvec)]:
+                    for x in row:
+                        acc ^= int(x)
+            out.append(acc)
+    return out
+
+
+@pytest.mark.parametrize("nvec", [1, 64, 1024, 1024 + 320, 5000])
+def test_read_flags_exactly_the_matching_wave(L, nvec):
+    g = torch.Generator().manual_seed(nvec)
+    words = torch.zeros(nvec * 4 + 64, dtype=torch.int32)  # 64 trailing words, never read
+    words[nvec * 4:] = 0x5A5A5A5A
+    pos = int(torch.randint(0, nvec * 4, (1,), generator=g))
+    words[pos] = 0x1234567
+    src = words.to(DEV)
+    xors = _wave_xors(words[: nvec * 4])
+    hit = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for key, expect in ((0x1234567, 1), (0x7777777, 0), (0x5A5A5A5A, 0)):
+        hit.zero_()
+        L.check("fd_read", L.lib().fd_read(src.data_ptr(), nvec * 16, key, hit.data_ptr(), _stream()))
+        torch.cuda.synchronize()
+        assert int(hit.item()) == expect, (key, expect)
+        assert (key in xors) == bool(expect)  # the model of the waves agrees
+    # all-zero data: every wave's xor is 0
+    zero = torch.zeros(nvec * 4, dtype=torch.int32, device=DEV)
+    hit.zero_()
+    L.check("fd_read", L.lib().fd_read(zero.data_ptr(), nvec * 16, 0, hit.data_ptr(), _stream()))
+    torch.cuda.synchronize()
+    assert int(hit.item()) == 1
+
+
+def test_read_launcher(L):
+    from fused_decode.kernels import launch_read
+
+    src = torch.zeros(1 << 16, dtype=torch.float16, device=DEV)
+    hit = torch.zeros(1, dtype=torch.int32, device=DEV)
+    launch_read(src, hit, key=0)
+    torch.cuda.synchronize()
+    assert int(hit.item()) == 1
