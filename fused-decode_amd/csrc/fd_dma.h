@@ -25,7 +25,7 @@
 //
 // Epilogues. EPI_PLAIN: tile rows n0..n0+15, bias / row_add / rounding as the
 // GEMV. EPI_ROPE (fused QKV): rows placed by TileRows<16>, rotated tiles rotate
-// their rounded outputs (cos/sin loaded before the main loop). E4M3 sums are
+// their rounded outputs (cos/sin staged through LDS, see angle_loads). E4M3 sums are
 // multiplied by the row's channel scale first.
 //
 // With NORM, x is the raw activation and the kernel applies the RMSNorm itself:
@@ -88,6 +88,16 @@ __device__ __forceinline__ void wait_lds_all(u32x4 (&v)[NR]) {
   else
     static_assert(NR == 6, "no register list for this fragment count");
 }
+template <int N1, int N2>
+__device__ __forceinline__ void wait_lds_all(u32x4 (&a)[N1], u32x4 (&b)[N2]) {
+  if constexpr (N1 == 2 && N2 == 4)
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])::"memory");
+  else if constexpr (N1 == 1 && N2 == 2)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(a[0]), "+v"(b[0]), "+v"(b[1])::"memory");
+  else
+    static_assert(N1 == 2 && N2 == 4, "no register list for these counts");
+}
 #undef FD_V1
 #undef FD_V6
 #undef FD_V8
@@ -122,11 +132,12 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   constexpr bool F8 = sizeof(W) == 1;
   constexpr DmaGeom G = dma_geom(sizeof(W));
   constexpr int NA = F8 ? 2 : 4;               // A reads per unit per lane
-  constexpr int NR = NA + 4 + (NORM ? 8 : 0);  // ds_read16 results per unit
+  constexpr int NR = NA + 4 + (NORM && BR > 8 ? 8 : 0);  // fragment reads per unit
   constexpr int SLOT = G.ae + BR * 16;         // 16-byte entries: the A tile, then the B rows
   constexpr int OPS = G.aops + BR / 4;         // DMA instructions per unit
   __shared__ u32x4 ring[NW][D][SLOT];
   __shared__ f32x4 part[NW * kWave];
+  __shared__ float ang_lds[EPI == EPI_ROPE ? kTileAngles : 1];  // ROPE: the tile's cos/sin
   extern __shared__ float norm_lds[];  // NORM: w [units * 128], inv [16], scratch
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform, so the unit indices, the K-tail tests and the ring addresses
@@ -191,8 +202,10 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     fb[s2] = ring0 + (unsigned)(G.ae + rb * 16 + (cb ^ rb)) * 16u;
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float rinv = 0.f;  // NORM: inverse RMS of this lane's B row
-  unsigned fw = 0;   // NORM: this lane's norm-weight base (bytes)
+  float rinv = 0.f;       // NORM, BR = 16: inverse RMS of this lane's B row
+  unsigned fw = 0;        // NORM, BR = 16: this lane's norm-weight fragment base (bytes)
+  float rinv_e[BR / 4];   // NORM, BR <= 8: inverse RMS of the rows this lane's DMAs fill
+  unsigned fwl = 0;       // NORM: the staged norm weight (bytes)
   auto consume = [&](int j) {
     const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
     const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
@@ -205,13 +218,30 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
         if (k0 + xch[i] >= K) ds_zero16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    // v: [NA] A reads, [4] B fragments, NORM: [8] norm weight
+    if constexpr (NORM && BR <= 8) {
+      // normalise the unit's B rows in place, each element once: this lane's
+      // BR/4 entries are the ones its own DMAs filled (row 4i + g, chunk xch[i])
+      u32x4 raw[BR / 4], wv[BR / 2];
+#pragma unroll
+      for (int i = 0; i < BR / 4; ++i) {
+        raw[i] = ds_read16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u);
+        const unsigned wa = fwl + (unsigned)(k0 + xch[i]) * 4u;
+        wv[2 * i] = ds_read16(wa);
+        wv[2 * i + 1] = ds_read16(wa + 16u);
+      }
+      wait_lds_all(raw, wv);
+#pragma unroll
+      for (int i = 0; i < BR / 4; ++i)
+        ds_write16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u,
+                   norm_frag<T>(raw[i], rinv_e[i], wv[2 * i], wv[2 * i + 1]));
+    }
+    // v: [NA] A reads, [4] B fragments, NORM (BR = 16): [8] norm weight
     u32x4 v[NR];
 #pragma unroll
     for (int t = 0; t < NA; ++t) v[t] = ds_read16(fa[t] + so);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) v[NA + s2] = ds_read16(fb[s2] + so);
-    if constexpr (NORM) {
+    if constexpr (NORM && BR > 8) {
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {  // 8 floats at fragment s2's k
         const unsigned wa = fw + (unsigned)(k0 + s2 * (F8 ? 8 : 32)) * 4u;
@@ -223,7 +253,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     u32x4 b[4];
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
-      if constexpr (NORM)
+      if constexpr (NORM && BR > 8)
         b[s2] = norm_frag<T>(v[NA + s2], rinv, v[NA + 4 + 2 * s2], v[NA + 5 + 2 * s2]);
       else
         b[s2] = v[NA + s2];
@@ -243,16 +273,19 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   const int pre = mine < D ? mine : D;
   // wave 0 writes the tile: its cos/sin loads go out first, so they complete
   // under the main loop's first wait instead of after the loop
-  TileAngles ang{};
-  if constexpr (EPI == EPI_ROPE)
-    if (wave == 0 && tr.rotated()) ang = tile_angles(rp, tr, lane, M);
+  constexpr int APER = (kTileAngles + NW * kWave - 1) / (NW * kWave);
+  AngleLoads<APER> ang{};
+  if constexpr (EPI == EPI_ROPE) ang = angle_loads<APER>(rp, tr, M, wrow[0]);
   if constexpr (NORM) {
     float* wl = norm_lds;
     float* inv = norm_lds + units * kUnit;
     for (int j = 0; j < pre; ++j) issue(j);
     norm_prologue<T, BR>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps);
     rinv = inv[rb];
-    fw = lds_addr(wl) + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
+#pragma unroll
+    for (int i = 0; i < BR / 4; ++i) rinv_e[i] = inv[4 * i + g];
+    fwl = lds_addr(wl);
+    fw = fwl + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
   } else {
     for (int j = 0; j < pre; ++j) issue(j);
   }
@@ -264,15 +297,17 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   }
   wait_vm<0>();
   for (; j < mine; ++j) consume(j);
+  if constexpr (EPI == EPI_ROPE) angle_store<APER>(ang_lds, ang, rp, tr, M);
   part[wave * kWave + lane] = acc;
   __syncthreads();
   if (threadIdx.x < kWave) {
     f32x4 s = part[threadIdx.x];
     for (int i = 1; i < NW; ++i) s += part[i * kWave + threadIdx.x];
     if constexpr (F8)
-      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang, RowScale{wscale}, M, N, sym, syn);
+      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, RowScale{wscale}, M, N, sym,
+                                          syn);
     else
-      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang, NoScale{}, M, N, sym, syn);
+      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, NoScale{}, M, N, sym, syn);
   }
 }
 
@@ -291,7 +326,7 @@ template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
 int launch_dma(unsigned blocks, void* y, const void* x, const void* w, const float* ws, int M,
                int N, int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
                const Rope& r, const FoldNorm& fn, hipStream_t st) {
-  constexpr size_t lds = dma_lds(NW, D, BR, sizeof(W));
+  constexpr size_t lds = dma_lds(NW, D, BR, sizeof(W)) + (EPI == EPI_ROPE ? kTileAngles * sizeof(float) : 0);
   if constexpr (lds <= kMaxLds) {
     const size_t dyn = NORM ? norm_dma_lds(K) : 0;
     auto kernel = gemv_mfma_dma_kernel<T, W, NW, D, BR, EPI, NORM>;

@@ -57,27 +57,16 @@ __device__ __forceinline__ void ds_zero16(unsigned addr) {
   asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(z) : "memory");
 }
 
+__device__ __forceinline__ void ds_write16(unsigned addr, const u32x4& v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+
 __device__ __forceinline__ u32x4 ds_read16(unsigned addr) {
   u32x4 v;
   asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
   return v;
 }
 
-// Make twelve ds_read16 results usable (the norm-weight fragments as well).
-__device__ __forceinline__ void wait_lds(u32x4 (&a)[4], u32x4 (&b)[4], u32x4 (&c)[8]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]),
-                 "+v"(b[3]), "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]), "+v"(c[4]), "+v"(c[5]),
-                 "+v"(c[6]), "+v"(c[7])::"memory");
-}
-
-// Make eight ds_read16 results usable: wait for the wave's LDS reads, tying the
-// wait to the registers so no use is scheduled ahead of it.
-__device__ __forceinline__ void wait_lds(u32x4 (&a)[4], u32x4 (&b)[4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]),
-                 "+v"(b[3])::"memory");
-}
 
 constexpr int pow2_ceil(int v) {
   int p = 1;
@@ -119,11 +108,23 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
 // round(x * inv[m] * w[k]) (norm.hip).
 //
 // One memory round trip: a thread's first two 16-byte chunks of the norm
-// weight and its first 8-element slice of every row are all loaded before
-// either is used (every load unconditional, indices clamped), after the
-// caller's first DMAs, so the three streams are in flight together. Wider rows
-// take further passes. H % 8 == 0; `scratch` holds kMaxWaves * pow2_ceil(MMAX)
+// weight and its first two 8-element slices of every row (one up to 8 rows)
+// are all loaded before any is used (every load unconditional, indices
+// clamped), after the caller's first DMAs, so the three streams are in flight
+// together. Wider rows take further passes. H % 8 == 0; `scratch` holds kMaxWaves * pow2_ceil(MMAX)
 // floats. Ends with a barrier (wl and inv are then visible).
+// acc + the squares of the two T values packed in `pair`, in float32.
+template <typename T>
+__device__ __forceinline__ float sq_dot2(uint32_t pair, float acc) {
+  if constexpr (std::is_same<T, f16>::value) {
+    const f16x2 v = __builtin_bit_cast(f16x2, pair);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  } else {
+    const bf16x2 v = __builtin_bit_cast(bf16x2, pair);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  }
+}
+
 __device__ __forceinline__ void store_norm_chunk(float* wl, const u32x4& v, int c, int dtype) {
   if (dtype == FD_F32) {
     reinterpret_cast<f32x4*>(wl)[c] = __builtin_bit_cast(f32x4, v);
@@ -161,10 +162,14 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
     const int c = tid + i * nt;
     wr[i] = wsrc[c < wchunks ? c : 0];
   }
-  const int k0 = tid * 8;
-  V8 h[MMAX];
+  const int k0 = tid * 8, k1 = k0 + nt * 8;
+  V8 h[MMAX], h1[MMAX <= 8 ? MMAX : 1];
 #pragma unroll
   for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k0 < H ? k0 : 0));
+  if constexpr (MMAX <= 8) {  // the second pass's loads in the same round trip
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) h1[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k1 < H ? k1 : 0));
+  }
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int c = tid + i * nt;
@@ -175,16 +180,27 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
   float ss[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+  // x^2 two at a time with v_dot2_f32_f16 / _bf16 (no conversions); a slice past
+  // H keeps the old sums, and rows past M get inv = 0 whatever they summed
   auto add = [&](int k) {
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
-      const float keep = m < M && k < H ? 1.f : 0.f;
+      const u32x4 p = __builtin_bit_cast(u32x4, h[m]);
+      float s = ss[m];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss[m] += keep * (to_f32(h[m][i]) * to_f32(h[m][i]));
+      for (int j = 0; j < 4; ++j) s = sq_dot2<T>(p[j], s);
+      ss[m] = k < H ? s : ss[m];
     }
   };
   add(k0);
-  for (int k = k0 + nt * 8; k < H; k += nt * 8) {
+  int k = k1;
+  if constexpr (MMAX <= 8) {
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) h[m] = h1[m];
+    add(k1);
+    k += nt * 8;
+  }
+  for (; k < H; k += nt * 8) {
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
     add(k);
@@ -524,35 +540,82 @@ struct TileRows {
   __device__ __forceinline__ int64_t row(int s) const { return rotated() ? base + col(s) : base + s; }
 };
 
+
+// Table loads without a branch on the table's dtype: the raw bits of element
+// i as two halfword loads (the same halfword twice for fp16/bf16, both halves
+// of a float32), combined and converted only where the value is used. A dtype
+// switch around the loads makes the compiler wait for each load where it
+// converts it.
+struct TableBits {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ TableBits load_table_bits(const void* p, int dtype, int64_t i) {
+  const unsigned short* h = static_cast<const unsigned short*>(p);
+  const int64_t lo = dtype == FD_F32 ? 2 * i : i;
+  const int64_t hi = dtype == FD_F32 ? 2 * i + 1 : i;
+  return TableBits{h[lo], h[hi]};
+}
+__device__ __forceinline__ float table_value(TableBits b, int dtype) {
+  if (dtype == FD_F32) return __builtin_bit_cast(float, b.lo | (b.hi << 16));
+  if (dtype == FD_BF16) return __builtin_bit_cast(float, b.lo << 16);
+  return (float)__builtin_bit_cast(f16, (unsigned short)b.lo);
+}
+
+// The cos/sin of a rotated 16-row MFMA tile, staged in LDS once per workgroup:
+// value v = (t * rows + r) * 16 + j is table t (0 cos, 1 sin) at row r (rows =
+// 1 when every token shares one table row, else M) and the tile's slot j
+// (TileRows<16>::col(j): slots 8-15 are the partners dim/2 further on). A
+// workgroup loads its values before its main loop, PER per thread, so they wait
+// under it, and stores them to LDS before its epilogue barrier. The loads are
+// unconditional: a thread without a value (or any thread of an unrotated
+// tile) reads `own`, an address of its own that the kernel reads anyway.
+// Loads under a branch get their registers merged at its end, which waits for
+// them; and every lane of every wave reading the table itself queued the whole
+// launch on the same few L2 lines (together 1.9 us of 16.4 in the fused QKV at
+// M = 8).
+constexpr int kTileAngles = 2 * 16 * 16;  // cos and sin, 16 slots, up to 16 rows
+template <int PER>
+struct AngleLoads {
+  TableBits b[PER];
+};
+template <int PER>
+__device__ __forceinline__ AngleLoads<PER> angle_loads(const Rope& rp, const TileRows<16>& tr, int M,
+                                                       const void* own) {
+  AngleLoads<PER> a;
+  const int rows = rp.rs == 0 ? 1 : M;
+  const int nt = block_threads();
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int v = (int)threadIdx.x + p * nt;
+    const bool use = tr.rotated() && v < 32 * rows;
+    const int t = v / (16 * rows), r = (v / 16) % rows, j = v % 16;
+    const void* base = use ? (t ? rp.sin : rp.cos) : own;
+    a.b[p] = load_table_bits(base, rp.dtype, use ? (int64_t)r * rp.rs + tr.col(j) : 0);
+  }
+  return a;
+}
+template <int PER>
+__device__ __forceinline__ void angle_store(float* lds, const AngleLoads<PER>& a, const Rope& rp,
+                                            const TileRows<16>& tr, int M) {
+  const int rows = rp.rs == 0 ? 1 : M;
+  const int nt = block_threads();
+#pragma unroll
+  for (int p = 0; p < PER; ++p) {
+    const int v = (int)threadIdx.x + p * nt;
+    if (tr.rotated() && v < 32 * rows) lds[v] = table_value(a.b[p], rp.dtype);
+  }
+}
+
 // Rotate one pair in float32 from the rounded projection outputs x1 (first
-// half, head column d) and x2 (second half, column d + dim/2), as the rope op.
+// half, head column d) and x2 (second half, column d + dim/2), as the rope op;
+// the four table loads are issued before any is converted (load_table_bits).
 __device__ __forceinline__ void rope_pair(const Rope& rp, int64_t m, int d, float x1, float x2,
                                           float& o1, float& o2) {
   const int64_t c = m * rp.rs + d, h = rp.dim >> 1;
-  o1 = x1 * load_any(rp.cos, rp.dtype, c) - x2 * load_any(rp.sin, rp.dtype, c);
-  o2 = x2 * load_any(rp.cos, rp.dtype, c + h) + x1 * load_any(rp.sin, rp.dtype, c + h);
-}
-
-// cos/sin of the four outputs one MFMA-epilogue lane rotates in a rotated tile
-// (lane l: column m = l%16, slots nb..nb+3 with nb = 4*(l/16); slots below 8
-// are first-half columns, the rest their partners dim/2 further on), so the
-// loads can be issued before a kernel's main loop and wait under it.
-struct TileAngles {
-  float c[4], s[4];
-};
-__device__ __forceinline__ TileAngles tile_angles(const Rope& rp, const TileRows<16>& tr, int lane,
-                                                  int M) {
-  TileAngles a;
-  const int m = lane & 15, nb = (lane >> 4) * 4;
-  const bool first = nb < 8;
-  const int64_t row = (int64_t)(m < M ? m : M - 1) * rp.rs;  // rows past M: never stored
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t c = row + tr.col(first ? nb + i : nb + i - 8) + (first ? 0 : rp.dim >> 1);
-    a.c[i] = load_any(rp.cos, rp.dtype, c);
-    a.s[i] = load_any(rp.sin, rp.dtype, c);
-  }
-  return a;
+  const TableBits c1 = load_table_bits(rp.cos, rp.dtype, c), s1 = load_table_bits(rp.sin, rp.dtype, c);
+  const TableBits c2 = load_table_bits(rp.cos, rp.dtype, c + h), s2 = load_table_bits(rp.sin, rp.dtype, c + h);
+  o1 = x1 * table_value(c1, rp.dtype) - x2 * table_value(s1, rp.dtype);
+  o2 = x2 * table_value(c2, rp.dtype) + x1 * table_value(s2, rp.dtype);
 }
 
 // Per-row factor applied to a GEMV sum before the epilogue: none for fp16/bf16
@@ -570,12 +633,13 @@ struct RowScale {
 // With ROPE the rows follow TileRows<16>, and a rotated tile rotates its rounded
 // outputs: lanes 0-31 hold slots 0-7 and lanes 32-63 their partners 8-15 (same
 // m), one lane-xor-32 exchange apart, so every lane of the wave must call this;
-// `ang` is tile_angles() of the lane (read in rotated tiles only).
+// `ang` is the tile's staged cos/sin (angle_store) and `ang_rs` the table's row
+// stride (0: one row for every m); read in rotated tiles only.
 template <typename T, bool ROPE, typename Scale>
 __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, int64_t n0,
                                               const TileRows<16>& tr, const Epi& e,
-                                              const TileAngles& ang, const Scale& sc, int M,
-                                              int N, int64_t sym, int64_t syn) {
+                                              const float* ang, int64_t ang_rs, const Scale& sc,
+                                              int M, int N, int64_t sym, int64_t syn) {
   const int m = lane & 15;
   const int nb = (lane >> 4) * 4;
   if (ROPE && tr.rotated()) {
@@ -592,7 +656,9 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
       for (int i = 0; i < 4; ++i) {
         // the rope op's pair rotation: x1 cos - x2 sin (first half), x2 cos + x1 sin
         const float x1 = first ? v[i] : pv[i], x2 = first ? pv[i] : v[i];
-        const float o = first ? x1 * ang.c[i] - x2 * ang.s[i] : x2 * ang.c[i] + x1 * ang.s[i];
+        const int rows = ang_rs == 0 ? 1 : M, r = ang_rs == 0 ? 0 : m;
+        const float c = ang[r * 16 + nb + i], sn = ang[(rows + r) * 16 + nb + i];
+        const float o = first ? x1 * c - x2 * sn : x2 * c + x1 * sn;
         y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(o);
       }
     }
