@@ -500,10 +500,15 @@ int launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const 
   if ((K + kUnit - 1) / kUnit < 4)
     return launch_dma_rows<T, uint8_t, 2, 2, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
                                                                e, none, nofold, st);
-  // Three units in flight where the tiles fit on the chip in two rounds or
-  // fewer, two on wide layers (Llama-3-8B widths, M=8: N=4096 K=14336 14.5 us
-  // against 17.0 for two; N=28672 K=4096 26.4 against 27.6 for three; the
-  // relayout kernel this replaced: 15.6 and 29.8).
+  // One tile per CU or fewer (N = 4096): eight waves, two units in flight each,
+  // so every SIMD has two waves; up to two rounds: four waves, three units in
+  // flight; wider layers: four waves, two units (Llama-3-8B widths, M=8:
+  // N=4096 K=14336 14.4 us against 14.9 for 4 x 3 and 17.0 for 4 x 2; N=6144
+  // 9.5 with 4 x 3; N=28672 K=4096 26.6 against 27.6 for 4 x 3; the relayout
+  // kernel this replaced: 15.6, 11.0 and 29.8).
+  if (blocks <= (unsigned)device_cus())
+    return launch_dma_rows<T, uint8_t, 8, 2, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
+                                                               e, none, nofold, st);
   if (blocks <= 2u * (unsigned)device_cus())
     return launch_dma_rows<T, uint8_t, 4, 3, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
                                                                e, none, nofold, st);
