@@ -111,6 +111,23 @@ def test_post_attn_mlp_fp8_matches_oracle(dtype, m):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 8])
+def test_post_attn_mlp_fp8_norm_weight_in_other_dtypes(dtype, m):
+    import fused_decode as fd
+
+    h, i = 256, 512
+    other = torch.bfloat16 if dtype == torch.float16 else torch.float16
+    gq, gs, gqn, gsn = quant(rnd(2 * i, h, seed=33, scale=h ** -0.5))
+    dq, ds, dqn, dsn = quant(rnd(h, i, seed=34, scale=i ** -0.5))
+    for j, nw_dtype in enumerate((torch.float32, other)):
+        hid = rnd(m, h, seed=35 + m + j, dtype=dtype)
+        nw = rnd(h, seed=37 + j, dtype=nw_dtype, scale=0.3, mean=1.0)
+        y = fd.post_attn_mlp_fp8(hid.to(DEV), nw.to(DEV), gq, gs, dq, ds, 1e-5)
+        ref = O.post_attn_mlp_fp8(npf(hid), npf(nw), gqn, gsn, dqn, dsn, 1e-5, tag(dtype))
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_post_attn_mlp_fp8_several_tiles_per_workgroup(m):
     """I = 6144 with 4-row tiles: 1536 tiles over two workgroups per CU, so each
@@ -311,6 +328,20 @@ def test_pre_attn_qkv_fp8_matches_oracle(dtype, m):
     y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
     ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, dtype)
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [1, 5, 8, 16])
+def test_pre_attn_qkv_fp8_norm_weight_in_other_dtypes(dtype, m):
+    """A float32 or other-half-type norm weight: the folded MFMA path (5+ rows)
+    converts it while staging each K chunk, the SIMT path per element."""
+    other = torch.bfloat16 if dtype == torch.float16 else torch.float16
+    for j, nw_dtype in enumerate((torch.float32, other)):
+        hidden, _, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 512, 4, 2, 64, dtype, seed=80 + m, bias=j == 0)
+        nw = rnd(512, seed=95 + m + j, dtype=nw_dtype, scale=0.3, mean=1.0)
+        y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+        ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, dtype)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
 @pytest.mark.parametrize("m", [1, 3])

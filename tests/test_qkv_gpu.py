@@ -85,6 +85,22 @@ def test_pre_attn_qkv_matches_oracle(dtype, kind, m):
                                **tol(dtype))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("kind", ["dot", "simt"])
+@pytest.mark.parametrize("m", [1, 5, 8, 16])
+def test_pre_attn_qkv_norm_weight_in_other_dtypes(dtype, kind, m):
+    """The norm weight may be float32 or the other half type; the folded MFMA
+    path (kind "dot", 5+ rows) converts it while staging each K chunk, the
+    others per element. A float32 weight carries bits no half type holds."""
+    other = torch.bfloat16 if dtype == torch.float16 else torch.float16
+    for j, nw_dtype in enumerate((torch.float32, other)):
+        hidden, _, w, b, cos, sin, rc = case(m, 512, 4, 2, 64, dtype, seed=70 + m, bias=j == 1)
+        nw = randn(512, gen=torch.Generator().manual_seed(90 + m + j), dtype=nw_dtype, scale=0.3, mean=1.0)
+        y = run(hidden, nw, w, b, cos, sin, rc, kind)
+        ref = oracle(hidden, nw, w, b, cos, sin, rc, dtype)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
 @pytest.mark.parametrize("kind", ["dot", "simt"])
 @pytest.mark.parametrize("m", [1, 8])
 def test_pre_attn_qkv_bias_shared_angles_half_precision_angles(kind, m):
