@@ -127,7 +127,7 @@ template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
 __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     T* y, const T* x, const W* w, const float* wscale, int M, int N, int K, int64_t sxm,
     int64_t swn, int64_t sym, int64_t syn, Epi e, Rope rp, const void* nwp, int nw_dtype,
-    float eps) {
+    float eps, RowSq rq) {
   typedef typename Vec8<T>::type V8;
   constexpr bool F8 = sizeof(W) == 1;
   constexpr DmaGeom G = dma_geom(sizeof(W));
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     float* wl = norm_lds;
     float* inv = norm_lds + units * kUnit;
     for (int j = 0; j < pre; ++j) issue(j);
-    norm_prologue<T, BR>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps);
+    norm_prologue<T, BR>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps, rq);
     rinv = inv[rb];
 #pragma unroll
     for (int i = 0; i < BR / 4; ++i) rinv_e[i] = inv[4 * i + g];
@@ -320,6 +320,7 @@ struct FoldNorm {
   const void* w;
   int dtype;
   float eps;
+  RowSq sq = {nullptr, 0};  // the producer's row sums of squares of x, if it wrote them
 };
 
 template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
@@ -336,7 +337,7 @@ int launch_dma(unsigned blocks, void* y, const void* x, const void* w, const flo
       return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", dyn);
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(NW * kWave), dyn, st, static_cast<T*>(y),
                        static_cast<const T*>(x), static_cast<const W*>(w), ws, M, N, K, sxm, swn,
-                       sym, syn, e, r, fn.w, fn.dtype, fn.eps);
+                       sym, syn, e, r, fn.w, fn.dtype, fn.eps, fn.sq);
     return FD_OK;
   }
   return set_error(FD_EINVAL, "MFMA tile beyond the LDS of a CU");

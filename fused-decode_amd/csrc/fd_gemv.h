@@ -83,6 +83,10 @@ struct Epi {
   const void* row;
   int row_dtype;
   int64_t srm, srn;
+  // MFMA plain tiles only: each tile t also writes ss[t*16 + m], the float32 sum
+  // of its rounded outputs squared in row m (zero for m >= M), for the RMSNorm
+  // of a kernel that reads this output next
+  float* ss = nullptr;
 };
 
 __device__ __forceinline__ float epilogue(const Epi& e, float acc, int64_t m, int64_t n) {
@@ -146,10 +150,19 @@ __device__ __forceinline__ void store_norm_chunk(float* wl, const u32x4& v, int 
   reinterpret_cast<f32x4*>(wl)[2 * c + 1] = f32x4{f[4], f[5], f[6], f[7]};
 }
 
-template <typename T, int MMAX>
+// Row sums of squares a producer kernel wrote for this kernel's input (Epi::ss
+// layout: `parts` tiles of 16 floats), or p == nullptr to derive them from x.
+struct RowSq {
+  const float* p;
+  int parts;
+};
+
+// FROM_X false: only the RowSq form is compiled (rq.p must be set), which keeps
+// the x passes' registers out of a kernel that never runs them.
+template <typename T, int MMAX, bool FROM_X = true>
 __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scratch, const void* nwp,
                                               int nw_dtype, const T* x, int64_t sxm, int M, int H,
-                                              int hp, float eps) {
+                                              int hp, float eps, const RowSq& rq) {
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -162,48 +175,72 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
     const int c = tid + i * nt;
     wr[i] = wsrc[c < wchunks ? c : 0];
   }
-  const int k0 = tid * 8, k1 = k0 + nt * 8;
-  V8 h[MMAX], h1[MMAX <= 8 ? MMAX : 1];
+  auto stage_w = [&]() {
 #pragma unroll
-  for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k0 < H ? k0 : 0));
-  if constexpr (MMAX <= 8) {  // the second pass's loads in the same round trip
-#pragma unroll
-    for (int m = 0; m < MMAX; ++m) h1[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k1 < H ? k1 : 0));
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + i * nt;
-    if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
-  }
-  for (int c = tid + 2 * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
-  for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + i * nt;
+      if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
+    }
+    for (int c = tid + 2 * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
+    for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
+  };
   float ss[MP];
 #pragma unroll
   for (int m = 0; m < MP; ++m) ss[m] = 0.f;
-  // x^2 two at a time with v_dot2_f32_f16 / _bf16 (no conversions); a slice past
-  // H keeps the old sums, and rows past M get inv = 0 whatever they summed
-  auto add = [&](int k) {
+  bool from_sq = true;
+  if constexpr (FROM_X) from_sq = rq.p != nullptr;
+  if (from_sq) {
+    // the producer's tile sums: thread tid adds tiles tid, tid + nt, ... (rows
+    // past M are added too and discarded below)
+    constexpr int MQ = (MMAX + 3) / 4;
+    auto tile_rows = [&](int t, f32x4 (&q)[MQ]) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(rq.p + (int64_t)(t < rq.parts ? t : 0) * 16);
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) {
-      const u32x4 p = __builtin_bit_cast(u32x4, h[m]);
-      float s = ss[m];
+      for (int i = 0; i < MQ; ++i) q[i] = src[i];
+    };
+    f32x4 q[MQ];
+    tile_rows(tid, q);
+    stage_w();
+    for (int t = tid; t < rq.parts; t += nt) {
+      if (t != tid) tile_rows(t, q);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) s = sq_dot2<T>(p[j], s);
-      ss[m] = k < H ? s : ss[m];
+      for (int m = 0; m < MMAX; ++m) ss[m] += q[m / 4][m % 4];
     }
-  };
-  add(k0);
-  int k = k1;
-  if constexpr (MMAX <= 8) {
+  } else if constexpr (FROM_X) {
+    const int k0 = tid * 8, k1 = k0 + nt * 8;
+    V8 h[MMAX], h1[MMAX <= 8 ? MMAX : 1];
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) h[m] = h1[m];
-    add(k1);
-    k += nt * 8;
-  }
-  for (; k < H; k += nt * 8) {
+    for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k0 < H ? k0 : 0));
+    if constexpr (MMAX <= 8) {  // the second pass's loads in the same round trip
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
-    add(k);
+      for (int m = 0; m < MMAX; ++m) h1[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k1 < H ? k1 : 0));
+    }
+    stage_w();
+    // x^2 two at a time with v_dot2_f32_f16 / _bf16 (no conversions); a slice past
+    // H keeps the old sums, and rows past M get inv = 0 whatever they summed
+    auto add = [&](int k) {
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) {
+        const u32x4 p = __builtin_bit_cast(u32x4, h[m]);
+        float s = ss[m];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s = sq_dot2<T>(p[j], s);
+        ss[m] = k < H ? s : ss[m];
+      }
+    };
+    add(k0);
+    int k = k1;
+    if constexpr (MMAX <= 8) {
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) h[m] = h1[m];
+      add(k1);
+      k += nt * 8;
+    }
+    for (; k < H; k += nt * 8) {
+#pragma unroll
+      for (int m = 0; m < MMAX; ++m) h[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + k);
+      add(k);
+    }
   }
   butterfly_sum<MP>(ss, lane);
   if (butterfly_writer<MP>(lane)) scratch[wave * MP + butterfly_index<MP>(lane)] = ss[0];
@@ -495,6 +532,14 @@ __device__ __forceinline__ T swiglu_out(float g, float u) {
 
 constexpr int kNormScratch = kMaxWaves * 16 + 16;
 
+// Relayout gate/up kernels that normalise from a producer's row sums (SS): at
+// most this many waves, and their dynamic LDS for H columns (the norm weight
+// as float32 in whole K units, inv[16], and the reduction scratch of `waves`).
+constexpr int kSsWaves = 4;
+__host__ __device__ constexpr size_t relayout_ss_lds(int H, int waves) {
+  return ((size_t)(H + kUnit - 1) / kUnit * kUnit + 16 + (size_t)waves * 16) * sizeof(float);
+}
+
 constexpr bool kNtWeights = true;           // nontemporal weight loads (measured +10-20%)
 constexpr size_t kMaxLds = 160 * 1024;       // LDS per CU on gfx950
 
@@ -662,11 +707,25 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
         y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(o);
       }
     }
-  } else if (m < M) {
+  } else {
+    float q = 0.f;
+    if (m < M) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
-      if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, sc(s[i], n), m, n));
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
+        if (n < N) {
+          const T o = from_f32<T>(epilogue(e, sc(s[i], n), m, n));
+          y[m * sym + n * syn] = o;
+          if (!ROPE && e.ss) q += to_f32(o) * to_f32(o);
+        }
+      }
+    }
+    if constexpr (!ROPE) {
+      if (e.ss) {  // lanes m, m+16, m+32, m+48 hold row m's four column groups
+        q = xlane_sum<32>(q);
+        q = xlane_sum<16>(q);
+        if (lane < 16) e.ss[(n0 >> 4) * 16 + lane] = q;
+      }
     }
   }
 }

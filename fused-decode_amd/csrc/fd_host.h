@@ -88,6 +88,24 @@ inline bool rows_vectorizable(const void* p, const fd_rows& l, int elem_bytes) {
   return true;
 }
 
+// Row sums of squares handed between launches (a producer GEMV's per-tile sums
+// of its squared outputs, read by the next RMSNorm): the checks of a *_sumsq
+// entry point's `ss_in` (ceil(H/16) tiles of the norm input's width H) and
+// `ss_out`. `mfma`: whether this call runs the MFMA kernels that read or write
+// them.
+inline int check_sumsq(bool mfma, const float* ss_in, int64_t ss_tiles, int64_t H, const float* ss_out) {
+  if (!mfma)
+    return set_error(FD_EUNSUPPORTED, "row sums of squares are for the MFMA kernels (kind=dot, M >= 5)");
+  if (ss_in) {
+    if (ss_tiles != (H + 15) / 16)
+      return set_error(FD_EINVAL, "ss_tiles must be ceil(H / 16) = %lld, got %lld", (long long)((H + 15) / 16),
+                       (long long)ss_tiles);
+    if (!aligned16(ss_in)) return set_error(FD_EUNSUPPORTED, "ss_in must be 16-byte aligned");
+  }
+  if (ss_out && !aligned16(ss_out)) return set_error(FD_EUNSUPPORTED, "ss_out must be 16-byte aligned");
+  return FD_OK;
+}
+
 inline int check_launch() {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(FD_ELAUNCH, "HIP launch failed: %s", hipGetErrorString(e));

@@ -395,12 +395,20 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
 
 // Gate/up + SwiGLU in the same form: 16 gate and the matching 16 up rows per
 // workgroup, B = the normalised activations written by the row kernel.
-template <typename T>
-__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_kernel(
-    T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I) {
+// With SS, x is the raw hidden state, normalised in the kernel from its
+// producer's row sums of squares as in mlp_gate_up_relayout_kernel (gemv.hip).
+// The SS form runs two waves per workgroup, held to the VGPRs of three waves
+// per SIMD (six workgroups per CU).
+constexpr int kFp8SsWaves = 2;
+template <typename T, bool SS>
+__global__ __launch_bounds__(SS ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS ? 3 : 1) void mlp_gate_up_fp8_relayout_kernel(
+    T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I, const void* nwp,
+    int nw_dtype, float eps, RowSq rq) {
   typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * kWave];
-  __shared__ u32x4 tiles[kMaxWaves][256];
+  constexpr int LW = SS ? kFp8SsWaves : kMaxWaves;
+  __shared__ f32x4 part[LW * kWave];
+  __shared__ u32x4 tiles[LW][256];
+  extern __shared__ float norm_lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = block_threads() / kWave;
@@ -422,6 +430,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   const int off = sweep_offset(units);
   auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, H); };
+  float rinv = 0.f;
   auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
@@ -429,13 +438,25 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_fp8_relayout_ke
     stage_unit8<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
-      const V8 b = unit_b(q.b[s2], u, s2, g, H);
+      V8 xb = q.b[s2];
+      if constexpr (SS) {
+        const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
+        xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
+                                                 __builtin_bit_cast(u32x4, wk[0]),
+                                                 __builtin_bit_cast(u32x4, wk[1])));
+      }
+      const V8 b = unit_b(xb, u, s2, g, H);
       ag = mfma16(a[s2], b, ag);
       au = mfma16(c[s2], b, au);
     }
   };
   UnitRegs8<T, 2> qa, qb;
   if (mine > 0) issue(qa, 0);
+  if constexpr (SS) {  // the first unit's loads fly while the prologue runs
+    float* inv = norm_lds + units * kUnit;
+    norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
+    rinv = inv[r];
+  }
   stream_steps(mine, qa, qb, issue, consume);
   part[wave * kWave + lane] = ag;
   __syncthreads();
@@ -627,12 +648,13 @@ int launch_qkv_fp8_m(int M, void* y, const void* hidden, const void* nw, int nw_
 }  // namespace
 }  // namespace fd
 
-extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
-                             const void* bias, int bias_dtype, const void* row_add, int row_dtype,
-                             int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn,
-                             int64_t sb, int64_t srm, int64_t srn, int64_t sym, int64_t syn,
-                             int act_dtype, void* stream) {
-  using namespace fd;
+namespace fd {
+namespace {
+
+int linear_fp8_entry(void* y, const void* x, const void* w8, const float* w_scale, const void* bias,
+                     int bias_dtype, const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+                     int64_t sxm, int64_t swn, int64_t sb, int64_t srm, int64_t srn, int64_t sym, int64_t syn,
+                     int act_dtype, float* ss_out, void* stream) {
   if (!check_act_dtype(act_dtype)) return FD_EINVAL;
   if (M < 0 || N < 0 || K < 0) return set_error(FD_EINVAL, "negative size");
   if (M > 16) return set_error(FD_EINVAL, "the fp8 GEMV covers M <= 16");
@@ -656,6 +678,7 @@ extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float
   e.row_dtype = row_dtype;
   e.srm = srm;
   e.srn = srn;
+  e.ss = ss_out;  // the MFMA form writes it (the caller checked M)
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w8);
   const int rc = act_dtype == FD_F16
@@ -665,12 +688,38 @@ extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float
   return check_launch();
 }
 
-extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* norm_w,
-                                    int norm_w_dtype, const void* w_gate_up8,
-                                    const float* gate_up_scale, const void* w_down8,
-                                    const float* down_scale, int64_t M, int64_t H, int64_t I,
-                                    float eps, int act_dtype, void* stream) {
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
+                             const void* bias, int bias_dtype, const void* row_add, int row_dtype,
+                             int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn,
+                             int64_t sb, int64_t srm, int64_t srn, int64_t sym, int64_t syn,
+                             int act_dtype, void* stream) {
+  return fd::linear_fp8_entry(y, x, w8, w_scale, bias, bias_dtype, row_add, row_dtype, M, N, K, sxm, swn, sb,
+                              srm, srn, sym, syn, act_dtype, nullptr, stream);
+}
+
+extern "C" int fd_linear_fp8_sumsq(void* y, const void* x, const void* w8, const float* w_scale,
+                                   const void* bias, int bias_dtype, const void* row_add, int row_dtype,
+                                   int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn, int64_t sb,
+                                   int64_t srm, int64_t srn, int64_t sym, int64_t syn, int act_dtype,
+                                   float* ss_out, void* stream) {
   using namespace fd;
+  if (!ss_out) return set_error(FD_EINVAL, "null pointer argument");
+  const int rc = check_sumsq(M >= kFp8MfmaMinM && M <= 16, nullptr, 0, 0, ss_out);
+  if (rc != FD_OK) return rc;
+  return linear_fp8_entry(y, x, w8, w_scale, bias, bias_dtype, row_add, row_dtype, M, N, K, sxm, swn, sb, srm,
+                          srn, sym, syn, act_dtype, ss_out, stream);
+}
+
+namespace fd {
+namespace {
+
+int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+                            const void* w_gate_up8, const float* gate_up_scale, const void* w_down8,
+                            const float* down_scale, int64_t M, int64_t H, int64_t I, float eps, int act_dtype,
+                            const RowSq* rq, float* ss_out, void* stream) {
   if (!check_act_dtype(act_dtype) || !check_any_dtype(norm_w_dtype, "norm_w_dtype"))
     return FD_EINVAL;
   if (M < 0 || M > 16) return set_error(FD_EINVAL, "M must be in [0, 16]");
@@ -688,7 +737,24 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* wgu = static_cast<const uint8_t*>(w_gate_up8);
   int rc;
-  if (M >= kFp8MfmaMinM) {
+  if (rq) {  // the MFMA gate/up normalising from the producer's row sums
+    const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : kFp8SsWaves;
+    const size_t lds = relayout_ss_lds((int)H, kFp8SsWaves);
+    if (lds + (size_t)(kFp8SsWaves * kWave + kFp8SsWaves * 256) * 16 > kMaxLds)
+      return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
+    auto launch = [&](auto kernel, auto* out, auto* in) {
+      if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+      hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, out, in, wgu,
+                         gate_up_scale, (int)M, (int)H, (int)I, norm_w, norm_w_dtype, eps, *rq);
+      return (int)FD_OK;
+    };
+    rc = act_dtype == FD_F16
+             ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true>, static_cast<f16*>(mid),
+                      static_cast<const f16*>(hidden))
+             : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true>, static_cast<bf16*>(mid),
+                      static_cast<const bf16*>(hidden));
+    if (rc != FD_OK) return rc;
+  } else if (M >= kFp8MfmaMinM) {
     // y doubles as the normed buffer: the down projection writes it last
     rc = rms_rows(y, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
     if (rc != FD_OK) return rc;
@@ -697,13 +763,15 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
     // (M=8: 26.4 us against 29.5 for four waves and 32.5 for eight).
     const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : 2;
     if (act_dtype == FD_F16)
-      hipLaunchKernelGGL(mlp_gate_up_fp8_relayout_kernel<f16>, dim3((unsigned)((I + 15) / 16)),
+      hipLaunchKernelGGL((mlp_gate_up_fp8_relayout_kernel<f16, false>), dim3((unsigned)((I + 15) / 16)),
                          dim3(nwv * kWave), 0, st, static_cast<f16*>(mid),
-                         static_cast<const f16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I);
+                         static_cast<const f16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I, nullptr,
+                         FD_F32, 0.f, RowSq{nullptr, 0});
     else
-      hipLaunchKernelGGL(mlp_gate_up_fp8_relayout_kernel<bf16>, dim3((unsigned)((I + 15) / 16)),
+      hipLaunchKernelGGL((mlp_gate_up_fp8_relayout_kernel<bf16, false>), dim3((unsigned)((I + 15) / 16)),
                          dim3(nwv * kWave), 0, st, static_cast<bf16*>(mid),
-                         static_cast<const bf16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I);
+                         static_cast<const bf16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I, nullptr,
+                         FD_F32, 0.f, RowSq{nullptr, 0});
   } else {
     rc = act_dtype == FD_F16
              ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
@@ -720,6 +788,7 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
   e.row_dtype = act_dtype;
   e.srm = H;
   e.srn = 1;
+  e.ss = ss_out;
   const uint8_t* wd = static_cast<const uint8_t*>(w_down8);
   rc = act_dtype == FD_F16
            ? launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st)
@@ -728,13 +797,39 @@ extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, cons
   return check_launch();
 }
 
-extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* norm_w,
-                                   int norm_w_dtype, const void* w_qkv8, const float* w_scale,
-                                   const void* bias, int bias_dtype, const void* cos,
-                                   const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
-                                   int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim,
-                                   float eps, int act_dtype, void* stream) {
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* norm_w,
+                                    int norm_w_dtype, const void* w_gate_up8,
+                                    const float* gate_up_scale, const void* w_down8,
+                                    const float* down_scale, int64_t M, int64_t H, int64_t I,
+                                    float eps, int act_dtype, void* stream) {
+  return fd::post_attn_mlp_fp8_entry(y, mid, hidden, norm_w, norm_w_dtype, w_gate_up8, gate_up_scale, w_down8,
+                                     down_scale, M, H, I, eps, act_dtype, nullptr, nullptr, stream);
+}
+
+extern "C" int fd_post_attn_mlp_fp8_sumsq(void* y, void* mid, const void* hidden, const void* norm_w,
+                                          int norm_w_dtype, const void* w_gate_up8, const float* gate_up_scale,
+                                          const void* w_down8, const float* down_scale, int64_t M, int64_t H,
+                                          int64_t I, float eps, int act_dtype, const float* ss_in,
+                                          int64_t ss_tiles, float* ss_out, void* stream) {
   using namespace fd;
+  const int rc = check_sumsq(M >= kFp8MfmaMinM && M <= 16, ss_in, ss_tiles, H, ss_out);
+  if (rc != FD_OK) return rc;
+  const RowSq rq{ss_in, (int)ss_tiles};
+  return post_attn_mlp_fp8_entry(y, mid, hidden, norm_w, norm_w_dtype, w_gate_up8, gate_up_scale, w_down8,
+                                 down_scale, M, H, I, eps, act_dtype, ss_in ? &rq : nullptr, ss_out, stream);
+}
+
+namespace fd {
+namespace {
+
+int pre_attn_qkv_fp8_entry(void* y, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
+                           const void* w_qkv8, const float* w_scale, const void* bias, int bias_dtype,
+                           const void* cos, const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
+                           int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim, float eps, int act_dtype,
+                           const RowSq* rq, void* stream) {
   const bool mfma = M >= kFp8MfmaMinM;
   Epi e;
   Rope rp;
@@ -749,7 +844,8 @@ extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, co
   const uint8_t* w = static_cast<const uint8_t*>(w_qkv8);
   if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
-    const FoldNorm fn{norm_w, norm_w_dtype, eps};
+    FoldNorm fn{norm_w, norm_w_dtype, eps};
+    if (rq) fn.sq = *rq;
     const int rc = act_dtype == FD_F16
                        ? launch_gemv_fp8_mfma<f16>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1,
                                                    e, st, &rp, &fn)
@@ -765,4 +861,34 @@ extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, co
     if (rc != FD_OK) return rc;
   }
   return check_launch();
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* norm_w,
+                                   int norm_w_dtype, const void* w_qkv8, const float* w_scale,
+                                   const void* bias, int bias_dtype, const void* cos,
+                                   const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
+                                   int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim,
+                                   float eps, int act_dtype, void* stream) {
+  return fd::pre_attn_qkv_fp8_entry(y, normed, hidden, norm_w, norm_w_dtype, w_qkv8, w_scale, bias, bias_dtype,
+                                    cos, sin, cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim, eps,
+                                    act_dtype, nullptr, stream);
+}
+
+extern "C" int fd_pre_attn_qkv_fp8_sumsq(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
+                                         const void* w_qkv8, const float* w_scale, const void* bias,
+                                         int bias_dtype, const void* cos, const void* sin, int cs_dtype,
+                                         int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
+                                         int64_t rope_cols, int64_t head_dim, float eps, int act_dtype,
+                                         const float* ss_in, int64_t ss_tiles, void* stream) {
+  using namespace fd;
+  if (!ss_in) return set_error(FD_EINVAL, "null pointer argument");
+  const int rc = check_sumsq(M >= kFp8MfmaMinM && M <= 16, ss_in, ss_tiles, H, nullptr);
+  if (rc != FD_OK) return rc;
+  const RowSq rq{ss_in, (int)ss_tiles};
+  return pre_attn_qkv_fp8_entry(y, nullptr, hidden, norm_w, norm_w_dtype, w_qkv8, w_scale, bias, bias_dtype, cos,
+                                sin, cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim, eps, act_dtype, &rq,
+                                stream);
 }

@@ -424,12 +424,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
 // 16 gate rows and the matching 16 up rows per workgroup with the row-contiguous
 // load + LDS relayout of gemv_mfma_relayout_kernel. B operand: the normalised
 // activations from global memory (L2-resident, [M, H]).
-template <typename T, bool NTW>
-__global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel(
-    T* mid, const T* x, const T* wgu, int M, int H, int I) {
+//
+// With SS, x is the raw hidden state and the kernel normalises it itself from
+// the row sums of squares its producer wrote (RowSq): the prologue stages the
+// norm weight as float32 in LDS and derives inv[m] from those sums, and every B
+// fragment becomes round(x * inv[m] * w[k]) before its MFMA -- the row kernel's
+// arithmetic, without its launch. Launched with at most kSsWaves waves, and
+// held to the VGPRs of three waves per SIMD (the form without SS needs as
+// many).
+
+template <typename T, bool NTW, bool SS>
+__global__ __launch_bounds__(SS ? kSsWaves * kWave : kMaxWaves * kWave, SS ? 3 : 1) void mlp_gate_up_relayout_kernel(
+    T* mid, const T* x, const T* wgu, int M, int H, int I, const void* nwp, int nw_dtype, float eps,
+    RowSq rq) {
   typedef typename Vec8<T>::type V8;
-  __shared__ f32x4 part[kMaxWaves * kWave];
-  __shared__ u32x4 tiles[kMaxWaves][256];
+  constexpr int LW = SS ? kSsWaves : kMaxWaves;
+  __shared__ f32x4 part[LW * kWave];
+  __shared__ u32x4 tiles[LW][256];
+  extern __shared__ float norm_lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = block_threads() / kWave;
@@ -453,6 +465,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
   auto issue = [&](UnitRegs16<T, 2>& q, int i) {
     load_unit16<T, 2, NTW>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, H);
   };
+  float rinv = 0.f;
   auto consume = [&](const UnitRegs16<T, 2>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
@@ -460,13 +473,25 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void mlp_gate_up_relayout_kernel
     stage_unit16<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
 #pragma unroll
     for (int s2 = 0; s2 < 4; ++s2) {
-      const V8 b = unit_b(q.b[s2], u, s2, g, H);
+      V8 xb = q.b[s2];
+      if constexpr (SS) {
+        const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
+        xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
+                                                 __builtin_bit_cast(u32x4, wk[0]),
+                                                 __builtin_bit_cast(u32x4, wk[1])));
+      }
+      const V8 b = unit_b(xb, u, s2, g, H);
       ag = mfma16(a[s2], b, ag);
       au = mfma16(c[s2], b, au);
     }
   };
   UnitRegs16<T, 2> qa, qb;
   if (mine > 0) issue(qa, 0);
+  if constexpr (SS) {  // the first unit's loads fly while the prologue runs
+    float* inv = norm_lds + units * kUnit;
+    norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
+    rinv = inv[r];
+  }
   stream_steps(mine, qa, qb, issue, consume);
   // two-phase reduction through one buffer: gate sums, then up sums
   part[wave * kWave + lane] = ag;
@@ -684,9 +709,27 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   // 39.3 us against 41.2 for eight waves and 39.8 for the one-unit loop).
   const int units = (H + kUnit - 1) / kUnit;
   const int nwv = units < 4 ? units : 4;
-  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, true>), dim3((unsigned)((I + 15) / 16)),
+  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, true, false>), dim3((unsigned)((I + 15) / 16)),
                      dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
-                     static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I);
+                     static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I, nullptr,
+                     FD_F32, 0.f, RowSq{nullptr, 0});
+  return FD_OK;
+}
+
+// The same gate/up from the raw hidden state and its producer's row sums of
+// squares (the RMSNorm inside the kernel, no row kernel first).
+template <typename T>
+int launch_mlp_relayout_ss(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
+                           const void* wgu, int H, int I, float eps, const RowSq& rq, hipStream_t st) {
+  const int units = (H + kUnit - 1) / kUnit;
+  const int nwv = units < kSsWaves ? units : kSsWaves;
+  const size_t lds = relayout_ss_lds(H, kSsWaves);
+  auto kernel = mlp_gate_up_relayout_kernel<T, true, true>;
+  if (lds + (size_t)(kSsWaves * kWave + kSsWaves * 256) * 16 > kMaxLds)
+    return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
+  if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
+                     static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps, rq);
   return FD_OK;
 }
 
@@ -725,6 +768,8 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
                     (N == 1 || swn % 8 == 0) && (M == 1 || sxm % 8 == 0) && N <= 0x7fffffffLL &&
                     K <= 0x7fffffffLL;
   if (!fast) {
+    if (e.ss)
+      return set_error(FD_EUNSUPPORTED, "row sums of squares need the vector GEMV's operand layout");
     if (N > 0x7fffffffLL) return set_error(FD_EUNSUPPORTED, "N too large");
     if (act_dtype == FD_F16)
       hipLaunchKernelGGL(gemv_gen_kernel<f16>, dim3((unsigned)N), dim3(256), 0, st, (f16*)y,
@@ -736,6 +781,8 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
     return FD_OK;
   }
   const bool mfma = linear_uses_mfma(M, kind, t);
+  if (e.ss && !mfma)
+    return set_error(FD_EUNSUPPORTED, "row sums of squares come from the MFMA GEMV (kind=dot, M >= 5)");
   if (act_dtype == FD_F16) {
     if (mfma)
       return launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
@@ -753,12 +800,14 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
 
 using namespace fd;
 
-extern "C" int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias,
-                               int bias_dtype, const void* row_add, int row_dtype, int64_t M,
-                               int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swn,
-                               int64_t swk, int64_t sb, int64_t srm, int64_t srn, int64_t sym,
-                               int64_t syn, const fd_tile* tile, int kind, int act_dtype,
-                               void* stream) {
+namespace fd {
+namespace {
+
+int linear_entry(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+                 const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
+                 int64_t sxk, int64_t swn, int64_t swk, int64_t sb, int64_t srm, int64_t srn,
+                 int64_t sym, int64_t syn, const fd_tile* tile, int kind, int act_dtype,
+                 float* ss_out, void* stream) {
   if (!check_act_dtype(act_dtype)) return FD_EINVAL;
   if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
     return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
@@ -789,10 +838,37 @@ extern "C" int fd_linear_tiled(void* y, const void* x, const void* w, const void
   e.row_dtype = row_dtype;
   e.srm = srm;
   e.srn = srn;
+  e.ss = ss_out;
   const int rc = linear_dispatch(y, x, w, e, M, N, K, sxm, sxk, swn, swk, sym, syn, kind,
                                  act_dtype, static_cast<hipStream_t>(stream), t);
   if (rc != FD_OK) return rc;
   return check_launch();
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias,
+                               int bias_dtype, const void* row_add, int row_dtype, int64_t M,
+                               int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swn,
+                               int64_t swk, int64_t sb, int64_t srm, int64_t srn, int64_t sym,
+                               int64_t syn, const fd_tile* tile, int kind, int act_dtype,
+                               void* stream) {
+  return linear_entry(y, x, w, bias, bias_dtype, row_add, row_dtype, M, N, K, sxm, sxk, swn, swk, sb,
+                      srm, srn, sym, syn, tile, kind, act_dtype, nullptr, stream);
+}
+
+extern "C" int fd_linear_sumsq(void* y, const void* x, const void* w, const void* bias,
+                               int bias_dtype, const void* row_add, int row_dtype, int64_t M,
+                               int64_t N, int64_t K, int64_t sxm, int64_t sxk, int64_t swn,
+                               int64_t swk, int64_t sb, int64_t srm, int64_t srn, int64_t sym,
+                               int64_t syn, int kind, int act_dtype, float* ss_out, void* stream) {
+  if (!ss_out) return set_error(FD_EINVAL, "null pointer argument");
+  if (!aligned16(ss_out)) return set_error(FD_EUNSUPPORTED, "ss_out must be 16-byte aligned");
+  if (!(kind == FD_KIND_DOT && M >= kMfmaMinM && M <= 16))
+    return set_error(FD_EUNSUPPORTED, "row sums of squares come from the MFMA GEMV (kind=dot, M >= 5)");
+  return linear_entry(y, x, w, bias, bias_dtype, row_add, row_dtype, M, N, K, sxm, sxk, swn, swk, sb,
+                      srm, srn, sym, syn, nullptr, kind, act_dtype, ss_out, stream);
 }
 
 extern "C" int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
@@ -834,9 +910,15 @@ bool mlp_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMin
 
 int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
                 const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
-                int act_dtype, hipStream_t st) {
+                int act_dtype, hipStream_t st, const RowSq* rq = nullptr) {
   int rc;
-  if (mlp_needs_normed(M, kind)) {
+  if (rq) {  // MFMA form, normalised inside the kernel from the producer's row sums
+    rc = act_dtype == FD_F16
+             ? launch_mlp_relayout_ss<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
+                                           (int)I, eps, *rq, st)
+             : launch_mlp_relayout_ss<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
+                                            (int)I, eps, *rq, st);
+  } else if (mlp_needs_normed(M, kind)) {
     // The relayout kernel (register loads, 16 gate and 16 up rows per workgroup
     // against one B tile), not the DMA form: Llama-3-8B widths, M=8, whole MLP
     // 63.5 us against 72.9 for DMA workgroups of the same two tiles, 69.9 for
@@ -873,10 +955,13 @@ extern "C" int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const
                      act_dtype, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
-                                int norm_w_dtype, const void* w_gate_up, const void* w_down,
-                                int64_t M, int64_t H, int64_t I, float eps, int kind,
-                                int act_dtype, void* stream) {
+namespace fd {
+namespace {
+
+int post_attn_mlp_entry(void* y, void* mid, const void* hidden, const void* norm_w, int norm_w_dtype,
+                        const void* w_gate_up, const void* w_down, int64_t M, int64_t H, int64_t I,
+                        float eps, int kind, int act_dtype, const RowSq* rq, float* ss_out,
+                        void* stream) {
   int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
   if (rc != FD_OK || M == 0) return rc;
   if (!y || !w_down) return set_error(FD_EINVAL, "null pointer argument");
@@ -888,7 +973,7 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   // y doubles as the normed buffer of the MFMA form: the down projection, which
   // writes y, runs after the gate/up launch has consumed it.
   rc = mlp_gate_up(mid, y, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind,
-                   act_dtype, st);
+                   act_dtype, st, rq);
   if (rc != FD_OK) return rc;
   Epi e;
   e.bias = nullptr;
@@ -898,9 +983,33 @@ extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const vo
   e.row_dtype = act_dtype;
   e.srm = H;
   e.srn = 1;
+  e.ss = ss_out;
   rc = linear_dispatch(y, mid, w_down, e, M, H, I, I, 1, I, 1, H, 1, kind, act_dtype, st);
   if (rc != FD_OK) return rc;
   return check_launch();
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
+                                int norm_w_dtype, const void* w_gate_up, const void* w_down,
+                                int64_t M, int64_t H, int64_t I, float eps, int kind,
+                                int act_dtype, void* stream) {
+  return post_attn_mlp_entry(y, mid, hidden, norm_w, norm_w_dtype, w_gate_up, w_down, M, H, I, eps, kind,
+                             act_dtype, nullptr, nullptr, stream);
+}
+
+extern "C" int fd_post_attn_mlp_sumsq(void* y, void* mid, const void* hidden, const void* norm_w,
+                                      int norm_w_dtype, const void* w_gate_up, const void* w_down,
+                                      int64_t M, int64_t H, int64_t I, float eps, int kind,
+                                      int act_dtype, const float* ss_in, int64_t ss_tiles,
+                                      float* ss_out, void* stream) {
+  const int rc = check_sumsq(kind == FD_KIND_DOT && M >= kMfmaMinM, ss_in, ss_tiles, H, ss_out);
+  if (rc != FD_OK) return rc;
+  const RowSq rq{ss_in, (int)ss_tiles};
+  return post_attn_mlp_entry(y, mid, hidden, norm_w, norm_w_dtype, w_gate_up, w_down, M, H, I, eps, kind,
+                             act_dtype, ss_in ? &rq : nullptr, ss_out, stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -971,13 +1080,13 @@ extern "C" int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void*
                           kind, act_dtype, stream);
 }
 
-extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_w,
-                               int norm_w_dtype, const void* w_qkv, const void* bias,
-                               int bias_dtype, const void* cos, const void* sin, int cs_dtype,
-                               int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
-                               int64_t rope_cols, int64_t head_dim, float eps, int kind,
-                               int act_dtype, void* stream) {
-  using namespace fd;
+namespace fd {
+namespace {
+
+int pre_attn_qkv_entry(void* y, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
+                       const void* w_qkv, const void* bias, int bias_dtype, const void* cos, const void* sin,
+                       int cs_dtype, int64_t cs_row_stride, int64_t M, int64_t H, int64_t N, int64_t rope_cols,
+                       int64_t head_dim, float eps, int kind, int act_dtype, const RowSq* rq, void* stream) {
   if (kind != FD_KIND_DOT && kind != FD_KIND_SIMT)
     return set_error(FD_EINVAL, "kind must be FD_KIND_DOT or FD_KIND_SIMT");
   const bool mfma = mlp_mfma(M, kind);
@@ -994,7 +1103,8 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
   int rc;
   if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
-    const FoldNorm fn{norm_w, norm_w_dtype, eps};
+    FoldNorm fn{norm_w, norm_w_dtype, eps};
+    if (rq) fn.sq = *rq;
     rc = act_dtype == FD_F16
              ? launch_mfma<f16>((int)M, y, hidden, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp, nullptr, &fn)
              : launch_mfma<bf16>((int)M, y, hidden, w_qkv, (int)N, (int)H, H, H, N, 1, e, st, &rp, nullptr, &fn);
@@ -1008,4 +1118,33 @@ extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const 
     if (rc != FD_OK) return rc;
   }
   return check_launch();
+}
+
+}  // namespace
+}  // namespace fd
+
+extern "C" int fd_pre_attn_qkv(void* y, void* normed, const void* hidden, const void* norm_w,
+                               int norm_w_dtype, const void* w_qkv, const void* bias,
+                               int bias_dtype, const void* cos, const void* sin, int cs_dtype,
+                               int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
+                               int64_t rope_cols, int64_t head_dim, float eps, int kind,
+                               int act_dtype, void* stream) {
+  return pre_attn_qkv_entry(y, normed, hidden, norm_w, norm_w_dtype, w_qkv, bias, bias_dtype, cos, sin,
+                            cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim, eps, kind, act_dtype,
+                            nullptr, stream);
+}
+
+extern "C" int fd_pre_attn_qkv_sumsq(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
+                                     const void* w_qkv, const void* bias, int bias_dtype, const void* cos,
+                                     const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
+                                     int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim, float eps,
+                                     int kind, int act_dtype, const float* ss_in, int64_t ss_tiles,
+                                     void* stream) {
+  if (!ss_in) return set_error(FD_EINVAL, "null pointer argument");
+  const int rc = check_sumsq(kind == FD_KIND_DOT && M >= kMfmaMinM, ss_in, ss_tiles, H, nullptr);
+  if (rc != FD_OK) return rc;
+  const RowSq rq{ss_in, (int)ss_tiles};
+  return pre_attn_qkv_entry(y, nullptr, hidden, norm_w, norm_w_dtype, w_qkv, bias, bias_dtype, cos, sin,
+                            cs_dtype, cs_row_stride, M, H, N, rope_cols, head_dim, eps, kind, act_dtype, &rq,
+                            stream);
 }

@@ -77,6 +77,15 @@ SIGNATURES: dict[str, list] = {
                         _i, _p],
     "fd_pre_attn_qkv_fp8": [_p, _p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l,
                             _l, _f, _i, _p],
+    "fd_linear_sumsq": [_p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _i,
+                        _p, _p],
+    "fd_post_attn_mlp_sumsq": [_p, _p, _p, _p, _i, _p, _p, _l, _l, _l, _f, _i, _i, _p, _l, _p, _p],
+    "fd_pre_attn_qkv_sumsq": [_p, _p, _p, _i, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i, _i, _p,
+                              _l, _p],
+    "fd_linear_fp8_sumsq": [_p, _p, _p, _p, _p, _i, _p, _i, _l, _l, _l, _l, _l, _l, _l, _l, _l, _l, _i, _p, _p],
+    "fd_post_attn_mlp_fp8_sumsq": [_p, _p, _p, _p, _i, _p, _p, _p, _p, _l, _l, _l, _f, _i, _p, _l, _p, _p],
+    "fd_pre_attn_qkv_fp8_sumsq": [_p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i,
+                                  _p, _l, _p],
     "fd_copy": [_p, _p, _l, _p],
     "fd_triad": [_p, _p, _p, _f, _l, _i, _p],
     "fd_read": [_p, _l, _i, _p, _p],

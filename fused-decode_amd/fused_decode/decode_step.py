@@ -10,9 +10,14 @@ fused form (the default):
     h    = linear_decode(attn, w_o, row_add=x)           # O-proj with the residual fused
     x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
 
-That is four launches per layer at M < 5 (five from 5 rows with kind "dot",
-where the MLP's RMSNorm runs as a row kernel ahead of its MFMA gate/up). The unfused form
-composes the reference's operators instead, six launches per layer (seven):
+That is four launches per layer at M < 5. From 5 rows with kind "dot" the
+projections run on MFMA and the layer hands row sums of squares along (rowsq.py):
+the O-proj writes them for h, the MLP's gate/up normalises h from them inside its
+kernel (no RMSNorm row kernel), its down projection writes them for the next x,
+and the next layer's QKV takes its norm from those -- four launches again
+(five with rowsq=False, where the MLP's RMSNorm runs as a row kernel ahead of
+its MFMA gate/up). The unfused form composes the reference's operators instead,
+six launches per layer (seven from 5 rows):
 
     normed, stream = add_rms_norm(x, zero, attn_norm_w)   # stream <- x, normed <- rms(x)
     qkv  = linear_decode(normed, w_qkv)                  # [M, 6144]
@@ -26,7 +31,8 @@ points. The whole step is captured once and replayed.
 
 With weights="fp8" the four projections hold E4M3 codes with per-row scales
 (quantize_fp8) and the layer runs as pre_attn_qkv_fp8, linear_decode_fp8 (O-proj
-with the residual) and post_attn_mlp_fp8: four launches per layer at M < 5.
+with the residual) and post_attn_mlp_fp8: four launches per layer, with the same
+row-sum handoff from 5 rows.
 
 Weights per layer: 436,207,616 bytes in fp16 (13.96 GB for 32 layers), half that
 plus the scales in fp8, random with the benchmark distributions (no checkpoint
@@ -43,6 +49,8 @@ import torch
 from .kernels import _MFMA_MIN_M
 from .fp8 import linear_decode_fp8, post_attn_mlp_fp8, pre_attn_qkv_fp8, quantize_fp8
 from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rope
+from .rowsq import (linear_fp8_sumsq, linear_sumsq, post_attn_mlp_fp8_sumsq, post_attn_mlp_sumsq,
+                    pre_attn_qkv_fp8_sumsq, pre_attn_qkv_sumsq, sumsq_buffer)
 
 H, I, HEADS, KV_HEADS, HEAD_DIM = 4096, 14336, 32, 8, 128
 QKV = (HEADS + 2 * KV_HEADS) * HEAD_DIM  # 6144
@@ -62,11 +70,15 @@ class DecodeStep:
 
     def __init__(self, m: int = 1, layers: int = 32, dtype=torch.float16, device="cuda",
                  seed: int = 0, h: int = H, i: int = I, kind: str | None = None, position: int = 1024,
-                 fused: bool = True, weights: str = "fp16"):
+                 fused: bool = True, weights: str = "fp16", rowsq: bool = True):
         if weights not in ("fp16", "fp8"):
             raise ValueError("weights must be 'fp16' (the activation dtype) or 'fp8'")
         self.m, self.layers, self.dtype, self.kind, self.fused = m, layers, dtype, kind, fused
         self.fp8 = weights == "fp8"
+        # the row-sum handoff needs the MFMA kernels (the fp8 forms take them from
+        # 5 rows whatever the kind)
+        mfma = m >= _MFMA_MIN_M and (self.fp8 or (kind or "dot") == "dot")
+        self.rowsq = rowsq and fused and mfma
         self.h, self.i = h, i
         heads = h // HEAD_DIM
         kv = max(1, heads // 4)
@@ -100,6 +112,10 @@ class DecodeStep:
         self.qkv = torch.empty(m, self.qkv_n, device=device, dtype=dtype)
         self.hbuf = torch.empty(m, h, device=device, dtype=dtype)
         self.out = torch.empty(m, h, device=device, dtype=dtype)
+        if self.rowsq:
+            self.xbuf = torch.empty(m, h, device=device, dtype=dtype)
+            self.mid = torch.empty(m, i, device=device, dtype=dtype)
+            self.ss_h, self.ss_x = sumsq_buffer(h, device), sumsq_buffer(h, device)
         self.graph = None
 
     @property
@@ -113,9 +129,42 @@ class DecodeStep:
         return per * self.layers
 
     def step(self) -> torch.Tensor:
+        if self.rowsq:
+            return self._step_rowsq()
         if self.fp8:
             return self._step_fp8()
         return self._step_fused() if self.fused else self._step_composed()
+
+    def _step_rowsq(self) -> torch.Tensor:
+        """The fused layer with row sums of squares handed to each RMSNorm (the
+        first layer's QKV, whose input no launch of the step wrote, normalises
+        itself)."""
+        x = self.x_in
+        rope_cols = self.qk_heads * HEAD_DIM
+        for li, w in enumerate(self.w):
+            if self.fp8:
+                if li == 0:
+                    pre_attn_qkv_fp8(x, w["attn_norm"], *w["qkv"], self.cos, self.sin, 1e-5,
+                                     rope_cols=rope_cols, out=self.qkv)
+                else:
+                    pre_attn_qkv_fp8_sumsq(x, w["attn_norm"], *w["qkv"], self.cos, self.sin, 1e-5,
+                                           rope_cols=rope_cols, ss_in=self.ss_x, out=self.qkv)
+                linear_fp8_sumsq(w["attn_out"], *w["o"], row_add=x, out=self.hbuf, ss_out=self.ss_h)
+                post_attn_mlp_fp8_sumsq(self.hbuf, w["mlp_norm"], *w["gate_up"], *w["down"], 1e-5, out=self.xbuf,
+                                        ss_in=self.ss_h, ss_out=self.ss_x, mid=self.mid)
+            else:
+                if li == 0:
+                    pre_attn_qkv(x, w["attn_norm"], w["qkv"], self.cos, self.sin, 1e-5, rope_cols=rope_cols,
+                                 out=self.qkv, kind=self.kind)
+                else:
+                    pre_attn_qkv_sumsq(x, w["attn_norm"], w["qkv"], self.cos, self.sin, 1e-5,
+                                       rope_cols=rope_cols, ss_in=self.ss_x, out=self.qkv)
+                linear_sumsq(w["attn_out"], w["o"], row_add=x, out=self.hbuf, ss_out=self.ss_h)
+                post_attn_mlp_sumsq(self.hbuf, w["mlp_norm"], w["gate_up"], w["down"], 1e-5, out=self.xbuf,
+                                    ss_in=self.ss_h, ss_out=self.ss_x, mid=self.mid)
+            x = self.xbuf
+        self.out.copy_(x)
+        return self.out
 
     def _step_fp8(self) -> torch.Tensor:
         """The fused layer with E4M3 projections: pre_attn_qkv_fp8, fp8 O-proj with
@@ -158,6 +207,8 @@ class DecodeStep:
         """HIP launches one layer issues (the MFMA MLP at kind "dot" from 5 rows adds
         a row kernel for its RMSNorm; the fused QKV folds its norm in at every M)."""
         mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
+        if self.rowsq:  # the MLP's RMSNorm runs inside its gate/up kernel
+            return 1 + 1 + 2
         mlp = 3 if mfma else 2
         if self.fp8:  # the fp8 kernels take the MFMA forms from 5 rows whatever the kind
             return 1 + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
@@ -208,10 +259,12 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 5)")
     ap.add_argument("--weights", choices=["fp16", "fp8"], default="fp16", help="projection weights (fp8: E4M3 + row scales)")
+    ap.add_argument("--no-rowsq", action="store_true", help="no row-sum handoff (the MLP's RMSNorm as a row kernel from 5 rows)")
     args = ap.parse_args()
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     for m in args.m:
-        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused, weights=args.weights)
+        ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused, weights=args.weights,
+                        rowsq=not args.no_rowsq)
         eager = time_step(ds, args.steps, args.warmup, graph=False)
         graph = time_step(ds, args.steps, args.warmup, graph=True)
         wb = ds.weight_bytes

@@ -275,6 +275,62 @@ int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* n
                         void* stream);
 
 /*
+ * Row sums of squares handed from a producer launch to the next RMSNorm
+ * (decode-step chaining; the MFMA kernels only: kind FD_KIND_DOT, or the fp8
+ * forms, with 5 <= M <= 16, else FD_EUNSUPPORTED). A producer that writes an
+ * [M,N] activation also writes `ss_out`: ceil(N/16) tiles of 16 floats,
+ * ss_out[t*16 + m] = sum over the tile's columns n of round(y[m,n])^2 in float32
+ * (0 for m >= M). A consumer whose RMSNorm input is that activation (width H)
+ * takes `ss_in` (ss_tiles = ceil(H/16), else FD_EINVAL) and derives
+ * rsqrt(mean(x^2) + eps) from it instead of re-reading the rows: the MLP's
+ * RMSNorm then runs inside the gate/up kernel (no row kernel), the QKV kernel
+ * skips its pass over x. Results are the operators' (the same float32 sum of
+ * squares, added in another order). ss_in must hold the sums of exactly the
+ * `hidden` passed with it; ss_in/ss_out are 16-byte aligned (FD_EUNSUPPORTED).
+ * No reference counterpart: the reference's operators each normalise their own
+ * input (ops.py:72-88, composed at ops.py:312-315).
+ *
+ * fd_linear_sumsq: fd_linear plus ss_out (non-NULL).
+ * fd_post_attn_mlp_sumsq: fd_post_attn_mlp; ss_in may be NULL (the row kernel
+ *   then normalises as in fd_post_attn_mlp), ss_out may be NULL.
+ * fd_pre_attn_qkv_sumsq: fd_pre_attn_qkv without `normed`, ss_in non-NULL.
+ * The _fp8 forms are the same over fd_linear_fp8, fd_post_attn_mlp_fp8 and
+ * fd_pre_attn_qkv_fp8.
+ */
+int fd_linear_sumsq(void* y, const void* x, const void* w, const void* bias, int bias_dtype,
+                    const void* row_add, int row_dtype, int64_t M, int64_t N, int64_t K,
+                    int64_t sxm, int64_t sxk, int64_t swn, int64_t swk, int64_t sb, int64_t srm,
+                    int64_t srn, int64_t sym, int64_t syn, int kind, int act_dtype, float* ss_out,
+                    void* stream);
+int fd_post_attn_mlp_sumsq(void* y, void* mid, const void* hidden, const void* norm_w,
+                           int norm_w_dtype, const void* w_gate_up, const void* w_down, int64_t M,
+                           int64_t H, int64_t I, float eps, int kind, int act_dtype,
+                           const float* ss_in, int64_t ss_tiles, float* ss_out, void* stream);
+int fd_pre_attn_qkv_sumsq(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
+                          const void* w_qkv, const void* bias, int bias_dtype, const void* cos,
+                          const void* sin, int cs_dtype, int64_t cs_row_stride, int64_t M,
+                          int64_t H, int64_t N, int64_t rope_cols, int64_t head_dim, float eps,
+                          int kind, int act_dtype, const float* ss_in, int64_t ss_tiles,
+                          void* stream);
+int fd_linear_fp8_sumsq(void* y, const void* x, const void* w8, const float* w_scale,
+                        const void* bias, int bias_dtype, const void* row_add, int row_dtype,
+                        int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t swn, int64_t sb,
+                        int64_t srm, int64_t srn, int64_t sym, int64_t syn, int act_dtype,
+                        float* ss_out, void* stream);
+int fd_post_attn_mlp_fp8_sumsq(void* y, void* mid, const void* hidden, const void* norm_w,
+                               int norm_w_dtype, const void* w_gate_up8,
+                               const float* gate_up_scale, const void* w_down8,
+                               const float* down_scale, int64_t M, int64_t H, int64_t I,
+                               float eps, int act_dtype, const float* ss_in, int64_t ss_tiles,
+                               float* ss_out, void* stream);
+int fd_pre_attn_qkv_fp8_sumsq(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
+                              const void* w_qkv8, const float* w_scale, const void* bias,
+                              int bias_dtype, const void* cos, const void* sin, int cs_dtype,
+                              int64_t cs_row_stride, int64_t M, int64_t H, int64_t N,
+                              int64_t rope_cols, int64_t head_dim, float eps, int act_dtype,
+                              const float* ss_in, int64_t ss_tiles, void* stream);
+
+/*
  * Bandwidth roofs. dst = src over `bytes` bytes (any size; 16-byte aligned
  * pointers take the vector path). c = a + b*scale over n elements of dtype.
  * Replace kernels.py:833-858 (`launch_copy`, `launch_triad`).

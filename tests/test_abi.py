@@ -249,3 +249,48 @@ def test_python_binding_matches_the_header():
     assert wrapped, "no wrappers found"
     for name, fmt in wrapped.items():
         assert sigs["fd_" + name] == fmt, name
+
+
+def test_ctypes_signatures_match_the_header(L):
+    """Every ctypes argtypes list has the header's argument count and kinds."""
+    import ctypes
+
+    kinds = {ctypes.c_void_p: "p", ctypes.c_int: "i", ctypes.c_int64: "l", ctypes.c_float: "f"}
+    for name, fmt in _header_signatures().items():
+        if name not in L.SIGNATURES:
+            continue
+        got = "".join(kinds.get(t, "r" if "FdRows" in str(t) else "t" if "FdTile" in str(t) else "p")
+                      for t in L.SIGNATURES[name])
+        assert got == fmt.replace("s", "p"), name
+
+
+@nogpu
+def test_sumsq_entry_points_reject(L):
+    """The row-sum handoff runs on the MFMA kernels only (kind=dot, 5..16 rows),
+    with ceil(H/16) tiles and 16-byte aligned sums; every check returns before a
+    launch."""
+    lib = L.lib()
+    F, ss = FAKE, 0x4000
+    lin = lambda m, kind, out: lib.fd_linear_sumsq(F, F, F, None, 0, None, 0, m, 64, 64, 64, 1, 64, 1, 0, 0,  # noqa: E731
+                                                   0, 64, 1, kind, 0, out, None)
+    assert lin(4, 0, ss) == L.FD_EUNSUPPORTED and b"MFMA" in lib.fd_last_error()
+    assert lin(8, 1, ss) == L.FD_EUNSUPPORTED
+    assert lin(8, 0, None) == L.FD_EINVAL
+    assert lin(8, 0, ss + 8) == L.FD_EUNSUPPORTED
+    mlp = lambda m, tiles, sin, sout: lib.fd_post_attn_mlp_sumsq(  # noqa: E731
+        F, 0x10000, 0x20000, F, 0, F, F, m, 256, 512, 1e-5, 0, 0, sin, tiles, sout, None)
+    assert mlp(4, 16, ss, None) == L.FD_EUNSUPPORTED
+    assert mlp(8, 15, ss, None) == L.FD_EINVAL and b"ss_tiles" in lib.fd_last_error()
+    assert mlp(8, 16, ss + 4, None) == L.FD_EUNSUPPORTED
+    assert mlp(8, 16, ss, ss + 4) == L.FD_EUNSUPPORTED
+    qkv = lambda m, sin, tiles: lib.fd_pre_attn_qkv_sumsq(  # noqa: E731
+        F, F, F, 0, F, None, 0, F, F, 2, 0, m, 256, 256, 128, 64, 1e-5, 0, 0, sin, tiles, None)
+    assert qkv(8, None, 16) == L.FD_EINVAL
+    assert qkv(3, ss, 16) == L.FD_EUNSUPPORTED
+    assert qkv(8, ss, 17) == L.FD_EINVAL
+    assert lib.fd_linear_fp8_sumsq(F, F, F, F, None, 0, None, 0, 2, 64, 64, 64, 64, 0, 0, 0, 64, 1, 0, ss,
+                                   None) == L.FD_EUNSUPPORTED
+    assert lib.fd_post_attn_mlp_fp8_sumsq(F, 0x10000, 0x20000, F, 0, F, F, F, F, 8, 256, 512, 1e-5, 0, ss, 3,
+                                          None, None) == L.FD_EINVAL
+    assert lib.fd_pre_attn_qkv_fp8_sumsq(F, F, F, 0, F, F, None, 0, F, F, 2, 0, 4, 256, 256, 128, 64, 1e-5, 0,
+                                         ss, 16, None) == L.FD_EUNSUPPORTED
