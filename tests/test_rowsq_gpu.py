@@ -113,6 +113,36 @@ def test_post_attn_mlp_sumsq_chain_matches_oracle(dtype, m, nw_dtype):
     torch.testing.assert_close(ss_x.cpu(), tile_sums(out), rtol=2e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("weights", ["fp16", "fp8"])
+@pytest.mark.parametrize("m", [5, 8])
+def test_post_attn_mlp_sumsq_ragged_widths(weights, m):
+    """H not a whole number of 128-element units (its last tile of sums half
+    full, the norm weight's LDS stage zero-padded) and I not a whole tile."""
+    from fused_decode.rowsq import (linear_fp8_sumsq, linear_sumsq, post_attn_mlp_fp8_sumsq,
+                                    post_attn_mlp_sumsq, sumsq_buffer)
+
+    fp8 = weights == "fp8"
+    h, i = (272, 528) if fp8 else (264, 520)
+    attn, x = rnd(m, h, seed=60 + m), rnd(m, h, seed=61 + m)
+    nw = rnd(h, seed=62, dtype=torch.float32, scale=0.3, mean=1.0)
+    wo = rnd(h, h, seed=63, scale=h ** -0.5)
+    wgu, wd = rnd(2 * i, h, seed=64, scale=h ** -0.5), rnd(h, i, seed=65, scale=i ** -0.5)
+    hbuf, out = (torch.empty(m, h, device=DEV, dtype=torch.float16) for _ in range(2))
+    ss_h, ss_x = sumsq_buffer(h, DEV), sumsq_buffer(h, DEV)
+    if fp8:
+        (oq, os_, _, _), (gq, gs, gqn, gsn), (dq, ds, dqn, dsn) = quant(wo), quant(wgu), quant(wd)
+        linear_fp8_sumsq(attn.to(DEV), oq, os_, row_add=x.to(DEV), out=hbuf, ss_out=ss_h)
+        post_attn_mlp_fp8_sumsq(hbuf, nw.to(DEV), gq, gs, dq, ds, 1e-5, out=out, ss_in=ss_h, ss_out=ss_x)
+        ref = O.post_attn_mlp_fp8(npf(hbuf), npf(nw), gqn, gsn, dqn, dsn, 1e-5, "f16")
+    else:
+        linear_sumsq(attn.to(DEV), wo.to(DEV), row_add=x.to(DEV), out=hbuf, ss_out=ss_h)
+        post_attn_mlp_sumsq(hbuf, nw.to(DEV), wgu.to(DEV), wd.to(DEV), 1e-5, out=out, ss_in=ss_h, ss_out=ss_x)
+        ref = O.post_attn_mlp(npf(hbuf), npf(nw), npf(wgu), npf(wd), 1e-5, "f16")
+    torch.testing.assert_close(ss_h.cpu(), tile_sums(hbuf), rtol=2e-6, atol=1e-6)
+    torch.testing.assert_close(out.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    torch.testing.assert_close(ss_x.cpu(), tile_sums(out), rtol=2e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m", [5, 8, 16])
 def test_pre_attn_qkv_sumsq_matches_oracle(dtype, m):
