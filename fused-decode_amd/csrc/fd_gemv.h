@@ -506,6 +506,31 @@ __device__ __forceinline__ void stream_steps(int total, Buf& a, Buf& b, Issue&& 
   }
 }
 
+// Half-B form of the relayout kernels' activation fragments, for M <= 8 (MFMA
+// columns 8-15 are padding): a lane of row r < 8 loads fragment 2p of x row r,
+// a lane of row r >= 8 fragment 2p+1 of x row 15-r (half_b_row), and after any
+// per-lane transform mirror16 (DPP row_mirror: lane r <-> 15-r, k group kept)
+// hands each low lane its partner's fragment. Two loads and two transforms per
+// unit then give the four B fragments lanes 0-7 need.
+__device__ __forceinline__ int half_b_row(int r) { return r < 8 ? r : 15 - r; }
+
+template <typename T>
+__device__ __forceinline__ void load_b_half(typename Vec8<T>::type (&b)[4], const T* xh, int u, int g, int hi,
+                                            int K) {
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int kb = u * kUnit + ((2 * p + hi) * 4 + g) * 8;
+    b[p] = load8<T>(xh + (kb < K ? kb : 0));
+  }
+}
+
+__device__ __forceinline__ u32x4 mirror16(const u32x4& v) {
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (unsigned)__builtin_amdgcn_mov_dpp((int)v[i], XlaneDpp<8>::ctrl, 0xf, 0xf, false);
+  return o;
+}
+
 // B fragment s2 of MFMA unit u for lane group g (x[m][k .. k+8), k = u*128 +
 // (4*s2 + g)*8), zeroed past K; the MFMA forms load it unconditionally.
 __device__ __forceinline__ f16x8 unit_b(const f16x8& b, int u, int s2, int g, int K) {

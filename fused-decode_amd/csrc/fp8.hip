@@ -274,7 +274,7 @@ struct UnitRegs8 {
 // row's first 16 codes instead (masked when staged), a B fragment past K its x
 // row's first fragment (masked in unit_b). `wl` are code row bases (rows past N
 // clamped by the caller to row 0), `xr` the lane's x row.
-template <typename T, int S>
+template <typename T, int S, bool LOADB = true>
 __device__ __forceinline__ void load_unit8(UnitRegs8<T, S>& q, const uint8_t* const (&wl)[S][2],
                                            const T* xr, int u, int lchunk, int g, int K) {
   const int k = u * kUnit + lchunk * 16;
@@ -283,10 +283,12 @@ __device__ __forceinline__ void load_unit8(UnitRegs8<T, S>& q, const uint8_t* co
   for (int s = 0; s < S; ++s)
 #pragma unroll
     for (int j = 0; j < 2; ++j) q.v[s][j] = load16_nt(wl[s][j] + kc);
+  if constexpr (LOADB) {
 #pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2) {
-    const int kb = u * kUnit + (s2 * 4 + g) * 8;
-    q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int kb = u * kUnit + (s2 * 4 + g) * 8;
+      q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
+    }
   }
 }
 
@@ -400,8 +402,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
 // The SS form runs two waves per workgroup, held to the VGPRs of three waves
 // per SIMD (six workgroups per CU).
 constexpr int kFp8SsWaves = 2;
-template <typename T, bool SS>
-__global__ __launch_bounds__(SS ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS ? 3 : 1) void mlp_gate_up_fp8_relayout_kernel(
+// HALF (M <= 8): the activation fragments in the half-B form (load_b_half).
+template <typename T, bool SS, bool HALF>
+__global__ __launch_bounds__(SS || HALF ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_fp8_relayout_kernel(
     T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I, const void* nwp,
     int nw_dtype, float eps, RowSq rq) {
   typedef typename Vec8<T>::type V8;
@@ -414,7 +417,8 @@ __global__ __launch_bounds__(SS ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS ? 
   const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored
+  const int hi = r >= 8, xrow = HALF ? half_b_row(r) : r;
+  const T* xr = x + (xrow < M ? xrow : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;
   const uint8_t* wl[2][2];  // [gate, up][row lrow, lrow + 8] bases
 #pragma unroll
@@ -429,25 +433,45 @@ __global__ __launch_bounds__(SS ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS ? 
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   const int off = sweep_offset(units);
-  auto issue = [&](UnitRegs8<T, 2>& q, int i) { load_unit8<T, 2>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, H); };
+  auto issue = [&](UnitRegs8<T, 2>& q, int i) {
+    const int u = sweep_unit(wave, i, nw, off, units);
+    load_unit8<T, 2, !HALF>(q, wl, xr, u, lchunk, g, H);
+    if constexpr (HALF) load_b_half<T>(q.b, xr, u, g, hi, H);
+  };
   float rinv = 0.f;
+  // fragment s2's B: the activations, normalised in the SS form, zero past K
+  auto frag = [&](const V8& raw, int u, int s2) {
+    V8 xb = raw;
+    if constexpr (SS) {
+      const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
+      xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
+                                               __builtin_bit_cast(u32x4, wk[0]),
+                                               __builtin_bit_cast(u32x4, wk[1])));
+    }
+    return unit_b(xb, u, s2, g, H);
+  };
   auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
     stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
     stage_unit8<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
+    if constexpr (HALF) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      V8 xb = q.b[s2];
-      if constexpr (SS) {
-        const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
-        xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
-                                                 __builtin_bit_cast(u32x4, wk[0]),
-                                                 __builtin_bit_cast(u32x4, wk[1])));
+      for (int p = 0; p < 2; ++p) {
+        const V8 own = frag(q.b[p], u, 2 * p + hi);
+        const V8 oth = __builtin_bit_cast(V8, mirror16(__builtin_bit_cast(u32x4, own)));
+        ag = mfma16(a[2 * p], own, ag);
+        au = mfma16(c[2 * p], own, au);
+        ag = mfma16(a[2 * p + 1], oth, ag);
+        au = mfma16(c[2 * p + 1], oth, au);
       }
-      const V8 b = unit_b(xb, u, s2, g, H);
-      ag = mfma16(a[s2], b, ag);
-      au = mfma16(c[s2], b, au);
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const V8 b = frag(q.b[s2], u, s2);
+        ag = mfma16(a[s2], b, ag);
+        au = mfma16(c[s2], b, au);
+      }
     }
   };
   UnitRegs8<T, 2> qa, qb;
@@ -455,7 +479,7 @@ __global__ __launch_bounds__(SS ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS ? 
   if constexpr (SS) {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
     norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
-    rinv = inv[r];
+    rinv = inv[xrow];
   }
   stream_steps(mine, qa, qb, issue, consume);
   part[wave * kWave + lane] = ag;
@@ -748,11 +772,18 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
                          gate_up_scale, (int)M, (int)H, (int)I, norm_w, norm_w_dtype, eps, *rq);
       return (int)FD_OK;
     };
-    rc = act_dtype == FD_F16
-             ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true>, static_cast<f16*>(mid),
-                      static_cast<const f16*>(hidden))
-             : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true>, static_cast<bf16*>(mid),
-                      static_cast<const bf16*>(hidden));
+    if (M <= 8)
+      rc = act_dtype == FD_F16
+               ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true, true>, static_cast<f16*>(mid),
+                        static_cast<const f16*>(hidden))
+               : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true, true>, static_cast<bf16*>(mid),
+                        static_cast<const bf16*>(hidden));
+    else
+      rc = act_dtype == FD_F16
+               ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true, false>, static_cast<f16*>(mid),
+                        static_cast<const f16*>(hidden))
+               : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true, false>, static_cast<bf16*>(mid),
+                        static_cast<const bf16*>(hidden));
     if (rc != FD_OK) return rc;
   } else if (M >= kFp8MfmaMinM) {
     // y doubles as the normed buffer: the down projection writes it last
@@ -762,16 +793,23 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
     // of them at 130 VGPRs), each wave with two of its 16 units in flight
     // (M=8: 26.4 us against 29.5 for four waves and 32.5 for eight).
     const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : 2;
-    if (act_dtype == FD_F16)
-      hipLaunchKernelGGL((mlp_gate_up_fp8_relayout_kernel<f16, false>), dim3((unsigned)((I + 15) / 16)),
-                         dim3(nwv * kWave), 0, st, static_cast<f16*>(mid),
-                         static_cast<const f16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I, nullptr,
-                         FD_F32, 0.f, RowSq{nullptr, 0});
-    else
-      hipLaunchKernelGGL((mlp_gate_up_fp8_relayout_kernel<bf16, false>), dim3((unsigned)((I + 15) / 16)),
-                         dim3(nwv * kWave), 0, st, static_cast<bf16*>(mid),
-                         static_cast<const bf16*>(y), wgu, gate_up_scale, (int)M, (int)H, (int)I, nullptr,
-                         FD_F32, 0.f, RowSq{nullptr, 0});
+    auto launch = [&](auto kernel, auto* out, auto* in) {
+      hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), 0, st, out, in, wgu,
+                         gate_up_scale, (int)M, (int)H, (int)I, nullptr, FD_F32, 0.f, RowSq{nullptr, 0});
+    };
+    if (act_dtype == FD_F16) {
+      if (M <= 8)
+        launch(mlp_gate_up_fp8_relayout_kernel<f16, false, true>, static_cast<f16*>(mid), static_cast<const f16*>(y));
+      else
+        launch(mlp_gate_up_fp8_relayout_kernel<f16, false, false>, static_cast<f16*>(mid), static_cast<const f16*>(y));
+    } else {
+      if (M <= 8)
+        launch(mlp_gate_up_fp8_relayout_kernel<bf16, false, true>, static_cast<bf16*>(mid),
+               static_cast<const bf16*>(y));
+      else
+        launch(mlp_gate_up_fp8_relayout_kernel<bf16, false, false>, static_cast<bf16*>(mid),
+               static_cast<const bf16*>(y));
+    }
   } else {
     rc = act_dtype == FD_F16
              ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,

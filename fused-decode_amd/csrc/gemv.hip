@@ -165,7 +165,7 @@ struct UnitRegs16 {
 // row's first chunk instead (zeroed when staged), a B fragment past K its x
 // row's first fragment (zeroed by unit_b). `wl` are weight row bases (rows past
 // N clamped by the caller to row 0), `xr` the lane's x row.
-template <typename T, int S, bool NTW>
+template <typename T, int S, bool NTW, bool LOADB = true>
 __device__ __forceinline__ void load_unit16(UnitRegs16<T, S>& q, const T* const (&wl)[S][4],
                                             const T* xr, int u, int lchunk, int g, int K) {
   const int k = u * kUnit + lchunk * 8;
@@ -177,10 +177,12 @@ __device__ __forceinline__ void load_unit16(UnitRegs16<T, S>& q, const T* const 
       const u32x4* p = reinterpret_cast<const u32x4*>(wl[s][i] + kc);
       q.v[s][i] = NTW ? __builtin_nontemporal_load(p) : *p;
     }
+  if constexpr (LOADB) {
 #pragma unroll
-  for (int s2 = 0; s2 < 4; ++s2) {
-    const int kb = u * kUnit + (s2 * 4 + g) * 8;
-    q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int kb = u * kUnit + (s2 * 4 + g) * 8;
+      q.b[s2] = load8<T>(xr + (kb < K ? kb : 0));
+    }
   }
 }
 
@@ -433,8 +435,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
 // held to the VGPRs of three waves per SIMD (the form without SS needs as
 // many).
 
-template <typename T, bool NTW, bool SS>
-__global__ __launch_bounds__(SS ? kSsWaves * kWave : kMaxWaves * kWave, SS ? 3 : 1) void mlp_gate_up_relayout_kernel(
+//
+// HALF (M <= 8): the activation fragments in the half-B form (load_b_half).
+template <typename T, bool NTW, bool SS, bool HALF>
+__global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_relayout_kernel(
     T* mid, const T* x, const T* wgu, int M, int H, int I, const void* nwp, int nw_dtype, float eps,
     RowSq rq) {
   typedef typename Vec8<T>::type V8;
@@ -447,7 +451,8 @@ __global__ __launch_bounds__(SS ? kSsWaves * kWave : kMaxWaves * kWave, SS ? 3 :
   const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int64_t j0 = (int64_t)blockIdx.x * 16;
-  const T* xr = x + (r < M ? r : 0) * (int64_t)H;  // rows past M: columns never stored
+  const int hi = r >= 8, xrow = HALF ? half_b_row(r) : r;
+  const T* xr = x + (xrow < M ? xrow : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 4, lchunk = lane & 15;
   const T* wl[2][4];  // [gate, up][row 4i + lrow] bases
 #pragma unroll
@@ -463,26 +468,44 @@ __global__ __launch_bounds__(SS ? kSsWaves * kWave : kMaxWaves * kWave, SS ? 3 :
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   const int off = sweep_offset(units);
   auto issue = [&](UnitRegs16<T, 2>& q, int i) {
-    load_unit16<T, 2, NTW>(q, wl, xr, sweep_unit(wave, i, nw, off, units), lchunk, g, H);
+    const int u = sweep_unit(wave, i, nw, off, units);
+    load_unit16<T, 2, NTW, !HALF>(q, wl, xr, u, lchunk, g, H);
+    if constexpr (HALF) load_b_half<T>(q.b, xr, u, g, hi, H);
   };
   float rinv = 0.f;
+  // fragment s2's B: the activations, normalised in the SS form, zero past K
+  auto frag = [&](const V8& raw, int u, int s2) {
+    V8 xb = raw;
+    if constexpr (SS) {
+      const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
+      xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
+                                               __builtin_bit_cast(u32x4, wk[0]),
+                                               __builtin_bit_cast(u32x4, wk[1])));
+    }
+    return unit_b(xb, u, s2, g, H);
+  };
   auto consume = [&](const UnitRegs16<T, 2>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
     stage_unit16<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
     stage_unit16<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
+    if constexpr (HALF) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      V8 xb = q.b[s2];
-      if constexpr (SS) {
-        const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
-        xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
-                                                 __builtin_bit_cast(u32x4, wk[0]),
-                                                 __builtin_bit_cast(u32x4, wk[1])));
+      for (int p = 0; p < 2; ++p) {
+        const V8 own = frag(q.b[p], u, 2 * p + hi);
+        const V8 oth = __builtin_bit_cast(V8, mirror16(__builtin_bit_cast(u32x4, own)));
+        ag = mfma16(a[2 * p], own, ag);
+        au = mfma16(c[2 * p], own, au);
+        ag = mfma16(a[2 * p + 1], oth, ag);
+        au = mfma16(c[2 * p + 1], oth, au);
       }
-      const V8 b = unit_b(xb, u, s2, g, H);
-      ag = mfma16(a[s2], b, ag);
-      au = mfma16(c[s2], b, au);
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        const V8 b = frag(q.b[s2], u, s2);
+        ag = mfma16(a[s2], b, ag);
+        au = mfma16(c[s2], b, au);
+      }
     }
   };
   UnitRegs16<T, 2> qa, qb;
@@ -490,7 +513,7 @@ __global__ __launch_bounds__(SS ? kSsWaves * kWave : kMaxWaves * kWave, SS ? 3 :
   if constexpr (SS) {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
     norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
-    rinv = inv[r];
+    rinv = inv[xrow];
   }
   stream_steps(mine, qa, qb, issue, consume);
   // two-phase reduction through one buffer: gate sums, then up sums
@@ -709,10 +732,13 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   // 39.3 us against 41.2 for eight waves and 39.8 for the one-unit loop).
   const int units = (H + kUnit - 1) / kUnit;
   const int nwv = units < 4 ? units : 4;
-  hipLaunchKernelGGL((mlp_gate_up_relayout_kernel<T, true, false>), dim3((unsigned)((I + 15) / 16)),
-                     dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
-                     static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I, nullptr,
-                     FD_F32, 0.f, RowSq{nullptr, 0});
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
+                       static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I, nullptr, FD_F32, 0.f,
+                       RowSq{nullptr, 0});
+  };
+  // (the half-B form would spill here: 168 VGPRs and 20 bytes of scratch)
+  launch(mlp_gate_up_relayout_kernel<T, true, false, false>);
   return FD_OK;
 }
 
@@ -724,13 +750,16 @@ int launch_mlp_relayout_ss(int M, void* mid, const void* hidden, const void* nw,
   const int units = (H + kUnit - 1) / kUnit;
   const int nwv = units < kSsWaves ? units : kSsWaves;
   const size_t lds = relayout_ss_lds(H, kSsWaves);
-  auto kernel = mlp_gate_up_relayout_kernel<T, true, true>;
   if (lds + (size_t)(kSsWaves * kWave + kSsWaves * 256) * 16 > kMaxLds)
     return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
-  if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
-  hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
-                     static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps, rq);
-  return FD_OK;
+  auto launch = [&](auto kernel) {
+    if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
+                       static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps, rq);
+    return (int)FD_OK;
+  };
+  return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true>)
+                : launch(mlp_gate_up_relayout_kernel<T, true, true, false>);
 }
 
 // The kernel a call runs: a tile's row count names it (16 = MFMA, which needs
