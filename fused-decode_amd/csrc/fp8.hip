@@ -395,20 +395,21 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
   stream_steps(p.total, a, b, issue, consume);
 }
 
-// Gate/up + SwiGLU in the same form: 16 gate and the matching 16 up rows per
-// workgroup, B = the normalised activations written by the row kernel.
-// With SS, x is the raw hidden state, normalised in the kernel from its
-// producer's row sums of squares as in mlp_gate_up_relayout_kernel (gemv.hip).
-// The SS form runs two waves per workgroup, held to the VGPRs of three waves
-// per SIMD (six workgroups per CU).
-constexpr int kFp8SsWaves = 2;
+// Gate/up + SwiGLU in the same form (M >= 5): 16 gate and the matching 16 up
+// rows per workgroup, x the raw hidden state, normalised inside the kernel as
+// in mlp_gate_up_relayout_kernel's SS form (gemv.hip): the norm weight staged
+// in LDS, inv[m] from the producer's row sums of squares (RowSq) or, with FX,
+// from a pass over x in the prologue, each B fragment round(x * inv * w).
+// Two waves per workgroup, held to the VGPRs of three waves per SIMD (six
+// workgroups per CU: all 896 of Llama-3-8B's resident at once).
 // HALF (M <= 8): the activation fragments in the half-B form (load_b_half).
-template <typename T, bool SS, bool HALF>
-__global__ __launch_bounds__(SS || HALF ? kFp8SsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_fp8_relayout_kernel(
+constexpr int kFp8SsWaves = 2;
+template <typename T, bool HALF, bool FX>
+__global__ __launch_bounds__(kFp8SsWaves * kWave, 3) void mlp_gate_up_fp8_relayout_kernel(
     T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I, const void* nwp,
     int nw_dtype, float eps, RowSq rq) {
   typedef typename Vec8<T>::type V8;
-  constexpr int LW = SS ? kFp8SsWaves : kMaxWaves;
+  constexpr int LW = kFp8SsWaves;
   __shared__ f32x4 part[LW * kWave];
   __shared__ u32x4 tiles[LW][256];
   extern __shared__ float norm_lds[];
@@ -439,15 +440,12 @@ __global__ __launch_bounds__(SS || HALF ? kFp8SsWaves * kWave : kMaxWaves * kWav
     if constexpr (HALF) load_b_half<T>(q.b, xr, u, g, hi, H);
   };
   float rinv = 0.f;
-  // fragment s2's B: the activations, normalised in the SS form, zero past K
+  // fragment s2's B: the normalised activations, zero past K
   auto frag = [&](const V8& raw, int u, int s2) {
-    V8 xb = raw;
-    if constexpr (SS) {
-      const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
-      xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xb), rinv,
-                                               __builtin_bit_cast(u32x4, wk[0]),
-                                               __builtin_bit_cast(u32x4, wk[1])));
-    }
+    const f32x4* wk = reinterpret_cast<const f32x4*>(norm_lds + u * kUnit + (s2 * 4 + g) * 8);
+    const V8 xb = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, raw), rinv,
+                                                      __builtin_bit_cast(u32x4, wk[0]),
+                                                      __builtin_bit_cast(u32x4, wk[1])));
     return unit_b(xb, u, s2, g, H);
   };
   auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
@@ -476,9 +474,10 @@ __global__ __launch_bounds__(SS || HALF ? kFp8SsWaves * kWave : kMaxWaves * kWav
   };
   UnitRegs8<T, 2> qa, qb;
   if (mine > 0) issue(qa, 0);
-  if constexpr (SS) {  // the first unit's loads fly while the prologue runs
+  {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
-    norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
+    norm_prologue<T, HALF ? 8 : 16, FX>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps,
+                                        rq);
     rinv = inv[xrow];
   }
   stream_steps(mine, qa, qb, issue, consume);
@@ -761,55 +760,35 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* wgu = static_cast<const uint8_t*>(w_gate_up8);
   int rc;
-  if (rq) {  // the MFMA gate/up normalising from the producer's row sums
+  if (M >= kFp8MfmaMinM) {
+    // the MFMA gate/up normalising inside the kernel: row sums from the producer,
+    // or from a pass over x (one launch instead of the row kernel + gate/up)
     const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : kFp8SsWaves;
     const size_t lds = relayout_ss_lds((int)H, kFp8SsWaves);
     if (lds + (size_t)(kFp8SsWaves * kWave + kFp8SsWaves * 256) * 16 > kMaxLds)
       return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
+    const RowSq sq = rq ? *rq : RowSq{nullptr, 0};
     auto launch = [&](auto kernel, auto* out, auto* in) {
       if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
       hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, out, in, wgu,
-                         gate_up_scale, (int)M, (int)H, (int)I, norm_w, norm_w_dtype, eps, *rq);
+                         gate_up_scale, (int)M, (int)H, (int)I, norm_w, norm_w_dtype, eps, sq);
       return (int)FD_OK;
     };
-    if (M <= 8)
-      rc = act_dtype == FD_F16
-               ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true, true>, static_cast<f16*>(mid),
-                        static_cast<const f16*>(hidden))
-               : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true, true>, static_cast<bf16*>(mid),
-                        static_cast<const bf16*>(hidden));
-    else
-      rc = act_dtype == FD_F16
-               ? launch(mlp_gate_up_fp8_relayout_kernel<f16, true, false>, static_cast<f16*>(mid),
-                        static_cast<const f16*>(hidden))
-               : launch(mlp_gate_up_fp8_relayout_kernel<bf16, true, false>, static_cast<bf16*>(mid),
-                        static_cast<const bf16*>(hidden));
-    if (rc != FD_OK) return rc;
-  } else if (M >= kFp8MfmaMinM) {
-    // y doubles as the normed buffer: the down projection writes it last
-    rc = rms_rows(y, hidden, norm_w, norm_w_dtype, M, H, eps, act_dtype, st);
-    if (rc != FD_OK) return rc;
-    // Two waves per workgroup: every workgroup resident at once (I = 14336: 896
-    // of them at 130 VGPRs), each wave with two of its 16 units in flight
-    // (M=8: 26.4 us against 29.5 for four waves and 32.5 for eight).
-    const int nwv = pick_waves((H + kUnit - 1) / kUnit) < 2 ? 1 : 2;
-    auto launch = [&](auto kernel, auto* out, auto* in) {
-      hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), 0, st, out, in, wgu,
-                         gate_up_scale, (int)M, (int)H, (int)I, nullptr, FD_F32, 0.f, RowSq{nullptr, 0});
+    auto run = [&](auto k16, auto kb16) {
+      return act_dtype == FD_F16 ? launch(k16, static_cast<f16*>(mid), static_cast<const f16*>(hidden))
+                                 : launch(kb16, static_cast<bf16*>(mid), static_cast<const bf16*>(hidden));
     };
-    if (act_dtype == FD_F16) {
-      if (M <= 8)
-        launch(mlp_gate_up_fp8_relayout_kernel<f16, false, true>, static_cast<f16*>(mid), static_cast<const f16*>(y));
-      else
-        launch(mlp_gate_up_fp8_relayout_kernel<f16, false, false>, static_cast<f16*>(mid), static_cast<const f16*>(y));
-    } else {
-      if (M <= 8)
-        launch(mlp_gate_up_fp8_relayout_kernel<bf16, false, true>, static_cast<bf16*>(mid),
-               static_cast<const bf16*>(y));
-      else
-        launch(mlp_gate_up_fp8_relayout_kernel<bf16, false, false>, static_cast<bf16*>(mid),
-               static_cast<const bf16*>(y));
-    }
+    if (rq)
+      rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, false>,
+                        mlp_gate_up_fp8_relayout_kernel<bf16, true, false>)
+                  : run(mlp_gate_up_fp8_relayout_kernel<f16, false, false>,
+                        mlp_gate_up_fp8_relayout_kernel<bf16, false, false>);
+    else
+      rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, true>,
+                        mlp_gate_up_fp8_relayout_kernel<bf16, true, true>)
+                  : run(mlp_gate_up_fp8_relayout_kernel<f16, false, true>,
+                        mlp_gate_up_fp8_relayout_kernel<bf16, false, true>);
+    if (rc != FD_OK) return rc;
   } else {
     rc = act_dtype == FD_F16
              ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,

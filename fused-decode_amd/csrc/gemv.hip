@@ -30,8 +30,9 @@
 // LDS), streams matching gate row j and up row I+j, and writes only
 // mid = round(silu(round(g)) * round(u)). Launch 2 is the down GEMV with the
 // residual fused as row_add. Weights are read once; gate_up never exists in HBM.
-// From 5 rows (kind=dot) the norm runs as a row kernel and both launches use
-// the MFMA form.
+// From 5 rows (kind=dot) both launches use the MFMA form; up to 8 rows the
+// gate/up kernel still normalises x itself, from 9 a row kernel writes the
+// normalised rows first.
 //
 // Fused QKV (qkv_simt_kernel, and the MFMA kernel with ROPE): the same prologue
 // and weight stream with tiles placed so that both halves of every rotate-half
@@ -420,12 +421,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   stream_steps(p.total, a, b, issue, consume);
 }
 
-// MFMA form of the gate/up launch for M >= kMfmaMinM (M padded to 16): the RMSNorm of
-// hidden is written by a separate row kernel (into the caller's output buffer,
-// which the down projection overwrites last), and this kernel streams a tile of
-// 16 gate rows and the matching 16 up rows per workgroup with the row-contiguous
-// load + LDS relayout of gemv_mfma_relayout_kernel. B operand: the normalised
-// activations from global memory (L2-resident, [M, H]).
+// MFMA form of the gate/up launch for M >= kMfmaMinM (M padded to 16): a tile of
+// 16 gate rows and the matching 16 up rows per workgroup, streamed with the
+// row-contiguous load + LDS relayout of gemv_mfma_relayout_kernel. B operand:
+// the activations from global memory (L2-resident, [M, H]). Without SS they
+// are the normalised rows a separate row kernel wrote (into the caller's output
+// buffer, which the down projection overwrites last; from 9 rows).
 //
 // With SS, x is the raw hidden state and the kernel normalises it itself from
 // the row sums of squares its producer wrote (RowSq): the prologue stages the
@@ -437,7 +438,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
 
 //
 // HALF (M <= 8): the activation fragments in the half-B form (load_b_half).
-template <typename T, bool NTW, bool SS, bool HALF>
+// FX (with SS): no producer sums; the prologue derives the row sums from x
+// (up to 8 rows: every workgroup reads the rows from L2 once more, which costs
+// less than the row kernel's launch).
+template <typename T, bool NTW, bool SS, bool HALF, bool FX = false>
 __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_relayout_kernel(
     T* mid, const T* x, const T* wgu, int M, int H, int I, const void* nwp, int nw_dtype, float eps,
     RowSq rq) {
@@ -512,7 +516,8 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
   if (mine > 0) issue(qa, 0);
   if constexpr (SS) {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
-    norm_prologue<T, 16, false>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps, rq);
+    norm_prologue<T, HALF ? 8 : 16, FX>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps,
+                                        rq);
     rinv = inv[xrow];
   }
   stream_steps(mine, qa, qb, issue, consume);
@@ -742,11 +747,12 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   return FD_OK;
 }
 
-// The same gate/up from the raw hidden state and its producer's row sums of
-// squares (the RMSNorm inside the kernel, no row kernel first).
+// The same gate/up from the raw hidden state, the RMSNorm inside the kernel
+// (no row kernel first): its row sums from the producer (rq), or, with rq
+// null, from a pass over hidden in the prologue.
 template <typename T>
 int launch_mlp_relayout_ss(int M, void* mid, const void* hidden, const void* nw, int nw_dtype,
-                           const void* wgu, int H, int I, float eps, const RowSq& rq, hipStream_t st) {
+                           const void* wgu, int H, int I, float eps, const RowSq* rq, hipStream_t st) {
   const int units = (H + kUnit - 1) / kUnit;
   const int nwv = units < kSsWaves ? units : kSsWaves;
   const size_t lds = relayout_ss_lds(H, kSsWaves);
@@ -755,11 +761,15 @@ int launch_mlp_relayout_ss(int M, void* mid, const void* hidden, const void* nw,
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
     hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
-                       static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps, rq);
+                       static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps,
+                       rq ? *rq : RowSq{nullptr, 0});
     return (int)FD_OK;
   };
-  return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true>)
-                : launch(mlp_gate_up_relayout_kernel<T, true, true, false>);
+  if (rq)
+    return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true>)
+                  : launch(mlp_gate_up_relayout_kernel<T, true, true, false>);
+  return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true, true>)
+                : launch(mlp_gate_up_relayout_kernel<T, true, true, false, true>);
 }
 
 // The kernel a call runs: a tile's row count names it (16 = MFMA, which needs
@@ -932,21 +942,26 @@ int mlp_check(void* mid, const void* hidden, const void* norm_w, int norm_w_dtyp
   return FD_OK;
 }
 
-// Whether the gate/up launch of this call needs the [M, H] `normed` buffer
-// (the MFMA form normalises in a separate row kernel).
-bool mlp_needs_normed(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
 bool mlp_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
+// Whether the gate/up launch of this call needs the [M, H] `normed` buffer:
+// the MFMA form from 9 rows normalises in a separate row kernel (up to 8 rows
+// it normalises inside the gate/up kernel).
+bool mlp_needs_normed(int64_t M, int kind) { return mlp_mfma(M, kind) && M > 8; }
 
 int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
                 const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
                 int act_dtype, hipStream_t st, const RowSq* rq = nullptr) {
   int rc;
-  if (rq) {  // MFMA form, normalised inside the kernel from the producer's row sums
+  if (rq || (mlp_mfma(M, kind) && !mlp_needs_normed(M, kind))) {
+    // MFMA form, normalised inside the kernel: row sums from the producer, or from
+    // a pass over x (up to 8 rows; from 9 its registers would spill: 168 VGPRs
+    // and 12 bytes of scratch), one launch instead of the row kernel + gate/up
+    // (Llama-3-8B widths, M=8: whole MLP 69.3 -> 66.3 us eager)
     rc = act_dtype == FD_F16
              ? launch_mlp_relayout_ss<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
-                                           (int)I, eps, *rq, st)
+                                           (int)I, eps, rq, st)
              : launch_mlp_relayout_ss<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
-                                            (int)I, eps, *rq, st);
+                                            (int)I, eps, rq, st);
   } else if (mlp_needs_normed(M, kind)) {
     // The relayout kernel (register loads, 16 gate and 16 up rows per workgroup
     // against one B tile), not the DMA form: Llama-3-8B widths, M=8, whole MLP

@@ -10,14 +10,14 @@ fused form (the default):
     h    = linear_decode(attn, w_o, row_add=x)           # O-proj with the residual fused
     x    = post_attn_mlp(h, mlp_norm_w, w_gate_up, w_down)
 
-That is four launches per layer at M < 5. From 5 rows with kind "dot" the
-projections run on MFMA and the layer hands row sums of squares along (rowsq.py):
-the O-proj writes them for h, the MLP's gate/up normalises h from them inside its
-kernel (no RMSNorm row kernel), its down projection writes them for the next x,
-and the next layer's QKV takes its norm from those -- four launches again
-(five with rowsq=False, where the MLP's RMSNorm runs as a row kernel ahead of
-its MFMA gate/up). The unfused form composes the reference's operators instead,
-six launches per layer (seven from 5 rows):
+That is four launches per layer. From 5 rows with kind "dot" the projections
+run on MFMA and the layer hands row sums of squares along (rowsq.py): the O-proj
+writes them for h, the MLP's gate/up normalises h from them inside its kernel,
+its down projection writes them for the next x, and the next layer's QKV takes
+its norm from those. With rowsq=False each norm derives its sums from its own
+input (from 9 rows the MLP's RMSNorm runs as a row kernel, five launches). The
+unfused form composes the reference's operators instead, six launches per layer
+(seven from 9 rows):
 
     normed, stream = add_rms_norm(x, zero, attn_norm_w)   # stream <- x, normed <- rms(x)
     qkv  = linear_decode(normed, w_qkv)                  # [M, 6144]
@@ -204,15 +204,12 @@ class DecodeStep:
 
     @property
     def launches_per_layer(self) -> int:
-        """HIP launches one layer issues (the MFMA MLP at kind "dot" from 5 rows adds
-        a row kernel for its RMSNorm; the fused QKV folds its norm in at every M)."""
-        mfma = (self.kind or "dot") == "dot" and self.m >= _MFMA_MIN_M
-        if self.rowsq:  # the MLP's RMSNorm runs inside its gate/up kernel
-            return 1 + 1 + 2
-        mlp = 3 if mfma else 2
-        if self.fp8:  # the fp8 kernels take the MFMA forms from 5 rows whatever the kind
-            return 1 + 1 + (3 if self.m >= _MFMA_MIN_M else 2)
-        if self.fused:
+        """HIP launches one layer issues (the fused QKV folds its norm in at every M;
+        the MLP is two launches, three where its fp16/bf16 MFMA form from 9 rows runs
+        a row kernel for its RMSNorm)."""
+        row_kernel = (self.kind or "dot") == "dot" and self.m > 8 and not self.fp8 and not self.rowsq
+        mlp = 3 if row_kernel else 2
+        if self.fp8 or self.fused:
             return 1 + 1 + mlp
         return 4 + mlp
 
@@ -259,7 +256,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 5)")
     ap.add_argument("--weights", choices=["fp16", "fp8"], default="fp16", help="projection weights (fp8: E4M3 + row scales)")
-    ap.add_argument("--no-rowsq", action="store_true", help="no row-sum handoff (the MLP's RMSNorm as a row kernel from 5 rows)")
+    ap.add_argument("--no-rowsq", action="store_true", help="no row-sum handoff (each RMSNorm derives its sums from its own input)")
     args = ap.parse_args()
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
     for m in args.m:

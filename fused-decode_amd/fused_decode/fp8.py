@@ -148,7 +148,7 @@ def post_attn_mlp_fp8(
     """``post_attn_mlp`` with E4M3 weights (``w_gate_up [2I, H]``, ``w_down [H, I]``)
     and their float32 per-row scales: the same four rounding points (reference
     reference.py:66-79), each projection as ``linear_decode_fp8``. Two HIP launches
-    up to 4 rows, three up to 16 (the RMSNorm runs first as a row kernel);
+    up to 16 rows (from 5 the MFMA gate/up normalises inside its kernel);
     otherwise composed from the operators."""
     a = check("post_attn_mlp_fp8", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up,
               gate_up_scale=gate_up_scale, w_down=w_down, down_scale=down_scale, eps=eps)
@@ -195,9 +195,9 @@ def pre_attn_qkv_fp8(
     """``pre_attn_qkv`` with E4M3 ``w_qkv [N, H]`` and its float32 per-row
     ``scale [N]``: RMSNorm, the projection as ``linear_decode_fp8``'s product (plus
     ``bias``), rounding, then RoPE of the first ``rope_cols`` columns, with the
-    argument rules of ``pre_attn_qkv``. One HIP launch up to 4 rows, two up to 16
-    (the norm runs as a row kernel ahead of the MFMA form); otherwise, or for
-    shapes the kernels do not take, composed from the operators."""
+    argument rules of ``pre_attn_qkv``. One HIP launch up to 16 rows (from 5 the
+    MFMA form with the norm folded in); otherwise, or for shapes the kernels do
+    not take, composed from the operators."""
     a0 = check("pre_attn_qkv_fp8", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, scale=scale,
                eps=eps, bias=bias)
     n, h = w_qkv.shape

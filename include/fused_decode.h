@@ -154,8 +154,9 @@ int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias, int
  * w_gate_up is [2I,H] (gate rows above up rows), w_down is [H,I], both contiguous.
  * `mid` is caller-owned scratch of M*I activation elements. y, mid and hidden must
  * not share memory (FD_EINVAL): hidden is read as the residual after y and mid are
- * written. Two launches (three for kind FD_KIND_DOT at M >= 5, whose RMSNorm runs
- * as its own row kernel into y).
+ * written. Two launches (three for kind FD_KIND_DOT at M >= 9, whose RMSNorm runs
+ * as its own row kernel into y; from 5 to 8 rows the MFMA gate/up kernel
+ * normalises hidden itself).
  * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
  * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
  */
@@ -185,7 +186,7 @@ int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w, in
 /*
  * The gate/up half of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u))
  * with g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
- * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 5 the RMSNorm is
+ * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 9 the RMSNorm is
  * written to `normed` ([M,H] activation scratch, 16-byte aligned) by a row kernel
  * before the MFMA gate/up kernel reads it; otherwise `normed` is unused (may be
  * NULL) and a single kernel normalises in its prologue. For callers that run their
@@ -245,10 +246,9 @@ int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
  * fd_post_attn_mlp with FP8 weights: w_gate_up8 [2I,H] and w_down8 [H,I] E4M3
  * codes (contiguous) with per-row float32 scales gate_up_scale [2I] and
  * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
- * rounding points as fd_post_attn_mlp. Two launches up to M = 4 (fused RMSNorm +
- * gate/up + SwiGLU, then down + residual), three from M = 5 (the RMSNorm runs
- * first as a row kernel into y, then the MFMA gate/up and the down projection);
- * `mid` is caller scratch of M*I activations. y, mid and hidden must not share
+ * rounding points as fd_post_attn_mlp. Two launches at every M (fused RMSNorm +
+ * gate/up + SwiGLU, from M = 5 on MFMA, then down + residual); `mid` is caller
+ * scratch of M*I activations. y, mid and hidden must not share
  * memory (FD_EINVAL). H % 16 == 0 and I % 16 == 0. No reference counterpart (see
  * fd_linear_fp8).
  */
@@ -291,8 +291,8 @@ int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* n
  * input (ops.py:72-88, composed at ops.py:312-315).
  *
  * fd_linear_sumsq: fd_linear plus ss_out (non-NULL).
- * fd_post_attn_mlp_sumsq: fd_post_attn_mlp; ss_in may be NULL (the row kernel
- *   then normalises as in fd_post_attn_mlp), ss_out may be NULL.
+ * fd_post_attn_mlp_sumsq: fd_post_attn_mlp; ss_in may be NULL (the MLP then
+ *   normalises as in fd_post_attn_mlp), ss_out may be NULL.
  * fd_pre_attn_qkv_sumsq: fd_pre_attn_qkv without `normed`, ss_in non-NULL.
  * The _fp8 forms are the same over fd_linear_fp8, fd_post_attn_mlp_fp8 and
  * fd_pre_attn_qkv_fp8.

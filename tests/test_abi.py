@@ -115,8 +115,8 @@ def test_mlp_rejects(L):
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 0, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 2, 60, 128, 1e-6, 0, 0, None) == L.FD_EUNSUPPORTED
     assert lib.fd_post_attn_mlp(FAKE, FAKE, FAKE, FAKE, 0, FAKE, FAKE, 0, 64, 128, 1e-6, 0, 0, None) == L.FD_OK
-    # kind=dot takes the MFMA route (RMSNorm row kernel into `normed`) from 5 rows
-    assert lib.fd_mlp_gate_up(FAKE, None, FAKE, FAKE, 0, FAKE, 5, 64, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
+    # kind=dot from 9 rows runs the RMSNorm as a row kernel into `normed`
+    assert lib.fd_mlp_gate_up(FAKE, None, FAKE, FAKE, 0, FAKE, 9, 64, 128, 1e-6, 0, 0, None) == L.FD_EINVAL
 
 
 @nogpu

@@ -547,7 +547,9 @@ def _oracle_decode_step(ds, tagd):
 @pytest.mark.parametrize("m", [1, 3, 5, 8, 16])
 def test_decode_step_small_matches_oracle_and_graph(m, fused):
     """Both forms of the layer, below and above the MFMA switch at 5 rows (where
-    the RMSNorms run as row kernels), against the oracle, then graph replays."""
+    the fused form hands row sums of squares to each norm and the composed one
+    runs the MLP's norm inside its gate/up, or as a row kernel from 9 rows),
+    against the oracle, then graph replays."""
     from fused_decode.decode_step import DecodeStep
 
     ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=5, fused=fused)
@@ -604,7 +606,7 @@ def test_mlp_gate_up_entry_point(m, kind):
         mid.data_ptr(), normed.data_ptr(), hd.data_ptr(), nwd.data_ptr(), L.FD_F16, wgd.data_ptr(),
         m, h, i, 1e-5, L.KIND_CODE[kind], L.FD_F16, st))
     check(mid, ref, torch.float16, "linear")
-    if kind == "dot" and m >= 5:
+    if kind == "dot" and m >= 9:
         check(normed, hn, torch.float16)  # the row kernel's output is the staged input
         assert L.lib().fd_mlp_gate_up(mid.data_ptr(), None, hd.data_ptr(), nwd.data_ptr(), L.FD_F16,
                                       wgd.data_ptr(), m, h, i, 1e-5, L.FD_KIND_DOT, L.FD_F16, st) == L.FD_EINVAL

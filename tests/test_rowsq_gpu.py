@@ -212,15 +212,16 @@ def test_fp8_sumsq_chain_matches_oracle(dtype, m):
 @pytest.mark.parametrize("weights", ["fp16", "fp8"])
 @pytest.mark.parametrize("m", [5, 8, 16])
 def test_decode_step_rowsq_matches_row_kernel_form(weights, m):
-    """The decode step with and without the handoff: four launches per layer
-    against five, the same values within the GEMV tolerance (the norms' sums are
+    """The decode step with and without the handoff (four launches per layer;
+    five without it where the fp16 MLP from 9 rows runs its norm as a row
+    kernel), the same values within the GEMV tolerance (the norms' sums are
     added in another order), graph replays identical to eager."""
     from fused_decode.decode_step import DecodeStep
 
     a = DecodeStep(m=m, layers=3, h=256, i=512, seed=25, weights=weights)
     b = DecodeStep(m=m, layers=3, h=256, i=512, seed=25, weights=weights, rowsq=False)
     assert a.rowsq and not b.rowsq
-    assert (a.launches_per_layer, b.launches_per_layer) == (4, 5)
+    assert (a.launches_per_layer, b.launches_per_layer) == (4, 5 if weights == "fp16" and m > 8 else 4)
     ya, yb = a.step().clone(), b.step().clone()
     torch.testing.assert_close(ya, yb, **tol(torch.float16))
     torch.testing.assert_close(a.qkv, b.qkv, **tol(torch.float16))
