@@ -943,16 +943,20 @@ int mlp_check(void* mid, const void* hidden, const void* norm_w, int norm_w_dtyp
 }
 
 bool mlp_mfma(int64_t M, int kind) { return kind == FD_KIND_DOT && M >= kMfmaMinM; }
-// Whether the gate/up launch of this call needs the [M, H] `normed` buffer:
-// the MFMA form from 9 rows normalises in a separate row kernel (up to 8 rows
-// it normalises inside the gate/up kernel).
-bool mlp_needs_normed(int64_t M, int kind) { return mlp_mfma(M, kind) && M > 8; }
+// Whether the MFMA gate/up normalises x inside the kernel with no producer
+// sums: up to 8 rows, while the norm weight's LDS stage fits (H up to about
+// 35,000); otherwise the MFMA form runs a row kernel into `normed` first.
+bool mlp_fold(int64_t M, int64_t H) {
+  return M <= 8 && relayout_ss_lds((int)H, kSsWaves) + (size_t)(kSsWaves * kWave + kSsWaves * 256) * 16 <= kMaxLds;
+}
+// Whether the gate/up launch of this call needs the [M, H] `normed` buffer.
+bool mlp_needs_normed(int64_t M, int64_t H, int kind) { return mlp_mfma(M, kind) && !mlp_fold(M, H); }
 
 int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w, int norm_w_dtype,
                 const void* w_gate_up, int64_t M, int64_t H, int64_t I, float eps, int kind,
                 int act_dtype, hipStream_t st, const RowSq* rq = nullptr) {
   int rc;
-  if (rq || (mlp_mfma(M, kind) && !mlp_needs_normed(M, kind))) {
+  if (rq || (mlp_mfma(M, kind) && mlp_fold(M, H))) {
     // MFMA form, normalised inside the kernel: row sums from the producer, or from
     // a pass over x (up to 8 rows; from 9 its registers would spill: 168 VGPRs
     // and 12 bytes of scratch), one launch instead of the row kernel + gate/up
@@ -962,7 +966,7 @@ int mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm_w,
                                            (int)I, eps, rq, st)
              : launch_mlp_relayout_ss<bf16>((int)M, mid, hidden, norm_w, norm_w_dtype, w_gate_up, (int)H,
                                             (int)I, eps, rq, st);
-  } else if (mlp_needs_normed(M, kind)) {
+  } else if (mlp_needs_normed(M, H, kind)) {
     // The relayout kernel (register loads, 16 gate and 16 up rows per workgroup
     // against one B tile), not the DMA form: Llama-3-8B widths, M=8, whole MLP
     // 63.5 us against 72.9 for DMA workgroups of the same two tiles, 69.9 for
@@ -991,8 +995,8 @@ extern "C" int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const
                               int64_t I, float eps, int kind, int act_dtype, void* stream) {
   int rc = mlp_check(mid, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind, act_dtype);
   if (rc != FD_OK || M == 0) return rc;
-  if (mlp_needs_normed(M, kind)) {
-    if (!normed) return set_error(FD_EINVAL, "kind=dot with M >= 5 needs the normed buffer");
+  if (mlp_needs_normed(M, H, kind)) {
+    if (!normed) return set_error(FD_EINVAL, "kind=dot with M >= 9 needs the normed buffer");
     if (!aligned16(normed)) return set_error(FD_EUNSUPPORTED, "operands must be 16-byte aligned");
   }
   return mlp_gate_up(mid, normed, hidden, norm_w, norm_w_dtype, w_gate_up, M, H, I, eps, kind,

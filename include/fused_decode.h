@@ -156,7 +156,7 @@ int fd_linear_tiled(void* y, const void* x, const void* w, const void* bias, int
  * not share memory (FD_EINVAL): hidden is read as the residual after y and mid are
  * written. Two launches (three for kind FD_KIND_DOT at M >= 9, whose RMSNorm runs
  * as its own row kernel into y; from 5 to 8 rows the MFMA gate/up kernel
- * normalises hidden itself).
+ * normalises hidden itself, for H up to about 35,000).
  * Replaces the composition at ops.py:283-315 (`post_attn_mlp`), which runs four
  * launches (rms_norm, linear_decode, swiglu, linear_decode with row_add).
  */
@@ -186,7 +186,8 @@ int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w, in
 /*
  * The gate/up half of fd_post_attn_mlp alone: mid = round(silu(round(g)) * round(u))
  * with g,u = round(round(rms_norm(hidden)) @ w_gate_up.T) split at I. Same operand
- * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 9 the RMSNorm is
+ * rules as fd_post_attn_mlp. With kind FD_KIND_DOT and M >= 9 (or H above about
+ * 35,000 from M = 5) the RMSNorm is
  * written to `normed` ([M,H] activation scratch, 16-byte aligned) by a row kernel
  * before the MFMA gate/up kernel reads it; otherwise `normed` is unused (may be
  * NULL) and a single kernel normalises in its prologue. For callers that run their
@@ -247,8 +248,9 @@ int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
  * codes (contiguous) with per-row float32 scales gate_up_scale [2I] and
  * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
  * rounding points as fd_post_attn_mlp. Two launches at every M (fused RMSNorm +
- * gate/up + SwiGLU, from M = 5 on MFMA, then down + residual); `mid` is caller
- * scratch of M*I activations. y, mid and hidden must not share
+ * gate/up + SwiGLU, from M = 5 on MFMA with the norm weight staged in LDS, which
+ * takes H up to about 38,000: FD_EUNSUPPORTED beyond, then down + residual);
+ * `mid` is caller scratch of M*I activations. y, mid and hidden must not share
  * memory (FD_EINVAL). H % 16 == 0 and I % 16 == 0. No reference counterpart (see
  * fd_linear_fp8).
  */

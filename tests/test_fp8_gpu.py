@@ -128,6 +128,30 @@ def test_post_attn_mlp_fp8_norm_weight_in_other_dtypes(dtype, m):
         torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+def test_post_attn_mlp_fp8_wide_hidden_composes():
+    """H = 39936 at M = 8: beyond the width the MFMA gate/up's norm-weight LDS
+    stage takes, the library declines (FD_EUNSUPPORTED) and the operator
+    composes rms_norm, the fp8 GEMVs and swiglu; same result."""
+    import fused_decode as fd
+    from fused_decode import _lib as L
+
+    h, i, m = 39936, 64, 8
+    hid = rnd(m, h, seed=70)
+    nw = rnd(h, seed=71, scale=0.1, mean=1.0)
+    gq, gs, gqn, gsn = quant(rnd(2 * i, h, seed=72, scale=h ** -0.5))
+    dq, ds, dqn, dsn = quant(rnd(h, i, seed=73, scale=i ** -0.5))
+    hd, nwd = hid.to(DEV), nw.to(DEV)
+    y_c = torch.empty(m, h, device=DEV, dtype=torch.float16)
+    mid = torch.empty(m, i, device=DEV, dtype=torch.float16)
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.lib().fd_post_attn_mlp_fp8(y_c.data_ptr(), mid.data_ptr(), hd.data_ptr(), nwd.data_ptr(), L.FD_F16,
+                                        gq.data_ptr(), gs.data_ptr(), dq.data_ptr(), ds.data_ptr(), m, h, i, 1e-5,
+                                        L.FD_F16, st) == L.FD_EUNSUPPORTED
+    y = fd.post_attn_mlp_fp8(hd, nwd, gq, gs, dq, ds, 1e-5)
+    ref = O.post_attn_mlp_fp8(npf(hid), npf(nw), gqn, gsn, dqn, dsn, 1e-5, "f16")
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_post_attn_mlp_fp8_several_tiles_per_workgroup(m):
     """I = 6144 with 4-row tiles: 1536 tiles over two workgroups per CU, so each

@@ -384,6 +384,21 @@ def test_post_attn_mlp():
         check(y, ref, dtype, "linear")
 
 
+@pytest.mark.parametrize("m", [5, 8])
+def test_post_attn_mlp_wide_hidden_row_kernel_form(m):
+    """H = 36864: the norm weight's float32 LDS stage no longer fits beside the
+    gate/up kernel's tiles, so from 5 rows the MLP runs its norm as a row kernel
+    first (three launches) instead of inside the gate/up kernel."""
+    h, i = 36864, 64
+    g = torch.Generator().manual_seed(95 + m)
+    x = randn(m, h, gen=g)
+    nw = randn(h, gen=g, scale=0.1, mean=1.0)
+    w_gu = randn(2 * i, h, gen=g, scale=h ** -0.5)
+    w_d = randn(h, i, gen=g, scale=i ** -0.5)
+    y = fd().post_attn_mlp(x.to(DEV), nw.to(DEV), w_gu.to(DEV), w_d.to(DEV), 1e-5, kind="dot")
+    check(y, O.post_attn_mlp(npf(x), npf(nw), npf(w_gu), npf(w_d), 1e-5, "f16"), torch.float16, "linear")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_post_attn_mlp_every_m_and_fp32_norm_weight(dtype):
     h, i = 256, 384
