@@ -276,6 +276,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   constexpr int APER = (kTileAngles + NW * kWave - 1) / (NW * kWave);
   AngleLoads<APER> ang{};
   if constexpr (EPI == EPI_ROPE) ang = angle_loads<APER>(rp, tr, M, wrow[0]);
+  TileEpi tep{};
+  if constexpr (EPI == EPI_PLAIN) tep = tile_epi_loads<F8>(e, wscale, wrow[0], lane, n0, M, N);
   if constexpr (NORM) {
     float* wl = norm_lds;
     float* inv = norm_lds + units * kUnit;
@@ -303,11 +305,12 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   if (threadIdx.x < kWave) {
     f32x4 s = part[threadIdx.x];
     for (int i = 1; i < NW; ++i) s += part[i * kWave + threadIdx.x];
-    if constexpr (F8)
-      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, RowScale{wscale}, M, N, sym,
-                                          syn);
+    if constexpr (EPI == EPI_PLAIN)
+      mfma_tile_out_plain<T, F8>(y, s, threadIdx.x, n0, e, tep, M, N, sym, syn);
+    else if constexpr (F8)
+      mfma_tile_out<T, true>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, RowScale{wscale}, M, N, sym, syn);
     else
-      mfma_tile_out<T, EPI == EPI_ROPE>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, NoScale{}, M, N, sym, syn);
+      mfma_tile_out<T, true>(y, s, threadIdx.x, n0, tr, e, ang_lds, rp.rs, NoScale{}, M, N, sym, syn);
   }
 }
 

@@ -698,6 +698,67 @@ struct RowScale {
   __device__ __forceinline__ float operator()(float s, int64_t n) const { return s * scale[n]; }
 };
 
+// The epilogue operands of a plain 16-row MFMA tile for one lane of the wave
+// that writes it (lane l: column m = l%16, rows nb..nb+3 with nb = 4*(l/16)):
+// bias, row_add and (E4M3) channel scale, loaded before the main loop so their
+// latency hides under it instead of adding to every workgroup's end. Loads are
+// unconditional and branch-free (halfword pairs, see load_table_bits): absent
+// operands and out-of-range lanes read the start of `own`, an address of the
+// lane's own that the kernel reads anyway (one shared address would queue every
+// lane of the launch on one L2 line).
+struct TileEpi {
+  TableBits b[4], r[4];
+  float ws[4];
+};
+template <bool F8>
+__device__ __forceinline__ TileEpi tile_epi_loads(const Epi& e, const float* wscale, const void* own, int lane,
+                                                  int64_t n0, int M, int N) {
+  const int m = lane & 15, nb = (lane >> 4) * 4;
+  const void* bp = e.bias ? e.bias : own;
+  const void* rp = e.row ? e.row : own;
+  const int bdt = e.bias ? e.bias_dtype : FD_F16, rdt = e.row ? e.row_dtype : FD_F16;
+  TileEpi t;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + nb + i;
+    const bool in = n < N, mn = in && m < M;
+    t.b[i] = load_table_bits(bp, bdt, e.bias && in ? n * e.sb : 0);
+    t.r[i] = load_table_bits(rp, rdt, e.row && mn ? m * e.srm + n * e.srn : 0);
+    if constexpr (F8) t.ws[i] = wscale[in ? n : 0];
+  }
+  return t;
+}
+
+// Plain tile output from the early-loaded operands: bias, then row_add, then
+// one rounding (the order of `epilogue`); with Epi::ss also the tile's row sums
+// of the squared rounded outputs.
+template <typename T, bool F8>
+__device__ __forceinline__ void mfma_tile_out_plain(T* y, const f32x4& s, int lane, int64_t n0, const Epi& e,
+                                                    const TileEpi& t, int M, int N, int64_t sym, int64_t syn) {
+  const int m = lane & 15;
+  const int nb = (lane >> 4) * 4;
+  float q = 0.f;
+  if (m < M) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + nb + i;
+      if (n < N) {
+        float acc = F8 ? s[i] * t.ws[i] : s[i];
+        if (e.bias) acc += table_value(t.b[i], e.bias_dtype);
+        if (e.row) acc += table_value(t.r[i], e.row_dtype);
+        const T o = from_f32<T>(acc);
+        y[m * sym + n * syn] = o;
+        if (e.ss) q += to_f32(o) * to_f32(o);
+      }
+    }
+  }
+  if (e.ss) {  // lanes m, m+16, m+32, m+48 hold row m's four column groups
+    q = xlane_sum<32>(q);
+    q = xlane_sum<16>(q);
+    if (lane < 16) e.ss[(n0 >> 4) * 16 + lane] = q;
+  }
+}
+
 // Output of one 16-row MFMA tile, from the 64 lanes of one wave holding the
 // cross-wave sums: lane l has rows nb..nb+3 (nb = 4*(l/16)) of column m = l%16.
 // With ROPE the rows follow TileRows<16>, and a rotated tile rotates its rounded
@@ -732,25 +793,11 @@ __device__ __forceinline__ void mfma_tile_out(T* y, const f32x4& s, int lane, in
         y[m * sym + tr.row(nb + i) * syn] = from_f32<T>(o);
       }
     }
-  } else {
-    float q = 0.f;
-    if (m < M) {
+  } else if (m < M) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
-        if (n < N) {
-          const T o = from_f32<T>(epilogue(e, sc(s[i], n), m, n));
-          y[m * sym + n * syn] = o;
-          if (!ROPE && e.ss) q += to_f32(o) * to_f32(o);
-        }
-      }
-    }
-    if constexpr (!ROPE) {
-      if (e.ss) {  // lanes m, m+16, m+32, m+48 hold row m's four column groups
-        q = xlane_sum<32>(q);
-        q = xlane_sum<16>(q);
-        if (lane < 16) e.ss[(n0 >> 4) * 16 + lane] = q;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = ROPE ? tr.row(nb + i) : n0 + nb + i;
+      if (n < N) y[m * sym + n * syn] = from_f32<T>(epilogue(e, sc(s[i], n), m, n));
     }
   }
 }
