@@ -30,8 +30,9 @@
 //
 // With NORM, x is the raw activation and the kernel applies the RMSNorm itself:
 // the norm weight (float32) and the rows' inverse RMS are staged in dynamic LDS
-// (norm_dma_lds bytes) by a prologue that runs while the first units' DMAs are
-// in flight, and every B fragment is normalised after its LDS read.
+// (norm_dma_lds bytes) by a prologue whose loads go out just before the first
+// units' DMAs and which runs while those are in flight, and every B fragment is
+// normalised after its LDS read.
 #pragma once
 
 #include "fd_gemv.h"
@@ -281,8 +282,10 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   if constexpr (NORM) {
     float* wl = norm_lds;
     float* inv = norm_lds + units * kUnit;
-    for (int j = 0; j < pre; ++j) issue(j);
-    norm_prologue<T, BR>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps, rq);
+    norm_prologue<T, BR, true, NW * kWave>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps, rq,
+                                           [&] {
+                                             for (int j = 0; j < pre; ++j) issue(j);
+                                           });
     rinv = inv[rb];
 #pragma unroll
     for (int i = 0; i < BR / 4; ++i) rinv_e[i] = inv[4 * i + g];

@@ -105,18 +105,6 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
     load8_f32<f16>(static_cast<const f16*>(p) + k, f);
 }
 
-// RMSNorm folded into a DMA MFMA kernel. The workgroup stages the norm weight
-// in LDS as float32 (zeros from H to `hp`, a whole number of K units) and the
-// inverse RMS of every activation row (inv[m], zero for rows past M); each B
-// fragment of raw activations is then normalised as the row kernels do it,
-// round(x * inv[m] * w[k]) (norm.hip).
-//
-// One memory round trip: a thread's first two 16-byte chunks of the norm
-// weight and its first two 8-element slices of every row (one up to 8 rows)
-// are all loaded before any is used (every load unconditional, indices
-// clamped), after the caller's first DMAs, so the three streams are in flight
-// together. Wider rows take further passes. H % 8 == 0; `scratch` holds kMaxWaves * pow2_ceil(MMAX)
-// floats. Ends with a barrier (wl and inv are then visible).
 // acc + the squares of the two T values packed in `pair`, in float32.
 template <typename T>
 __device__ __forceinline__ float sq_dot2(uint32_t pair, float acc) {
@@ -157,31 +145,53 @@ struct RowSq {
   int parts;
 };
 
+// RMSNorm folded into an MFMA kernel. The workgroup stages the norm weight in
+// LDS as float32 (wl; zeros from H to `hp`, a whole number of K units) and the
+// inverse RMS of every activation row (inv[m] = 1/sqrt(mean(x[m]^2) + eps),
+// zero for rows past M), from the producer's row sums (rq) or from x; each B
+// fragment of raw activations is then normalised as the row kernels do it,
+// round(x * inv[m] * w[k]) (norm.hip).
+//
+// One memory round trip: a thread's first 16-byte chunks of the norm weight and
+// its first producer tiles, or its first two 8-element slices of every row (one
+// up to 8 rows), are all loaded before any is used (every load unconditional,
+// indices clamped). `after_loads()` runs once, right after those loads are
+// issued: a caller that issues its weight stream there queues it behind them,
+// and since vector-memory loads complete in issue order, waiting for the
+// prologue's data then never waits for the weights. NTMAX, the launch's
+// largest block size, sizes that first round to 512 weight chunks and 256
+// producer tiles (H up to 4096 with a 16-bit weight); wider rows take further
+// rounds after after_loads(). H % 8 == 0; `scratch` holds kMaxWaves *
+// pow2_ceil(MMAX) floats. Ends with a barrier (wl and inv are then visible).
 // FROM_X false: only the RowSq form is compiled (rq.p must be set), which keeps
 // the x passes' registers out of a kernel that never runs them.
-template <typename T, int MMAX, bool FROM_X = true>
+template <typename T, int MMAX, bool FROM_X, int NTMAX, typename AfterLoads>
 __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scratch, const void* nwp,
                                               int nw_dtype, const T* x, int64_t sxm, int M, int H,
-                                              int hp, float eps, const RowSq& rq) {
+                                              int hp, float eps, const RowSq& rq, AfterLoads&& after_loads) {
   typedef typename Vec8<T>::type V8;
   constexpr int MP = pow2_ceil(MMAX);
+  // weight chunks per thread in the first round (two where an x pass of more
+  // than 8 rows holds its registers)
+  constexpr int WR = NTMAX >= 256 || (FROM_X && MMAX > 8) ? 2 : 512 / NTMAX;
+  constexpr int TQ = NTMAX >= 256 ? 1 : 256 / NTMAX;  // producer tiles per thread in the first round
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int nt = block_threads(), nwv = nt / kWave;
   const int wchunks = H / (nw_dtype == FD_F32 ? 4 : 8);  // 16-byte chunks of the weight
   const u32x4* wsrc = static_cast<const u32x4*>(nwp);
-  u32x4 wr[2];
+  u32x4 wr[WR];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < WR; ++i) {
     const int c = tid + i * nt;
     wr[i] = wsrc[c < wchunks ? c : 0];
   }
   auto stage_w = [&]() {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < WR; ++i) {
       const int c = tid + i * nt;
       if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
     }
-    for (int c = tid + 2 * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
+    for (int c = tid + WR * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
     for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
   };
   float ss[MP];
@@ -198,13 +208,21 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
 #pragma unroll
       for (int i = 0; i < MQ; ++i) q[i] = src[i];
     };
-    f32x4 q[MQ];
-    tile_rows(tid, q);
-    stage_w();
-    for (int t = tid; t < rq.parts; t += nt) {
-      if (t != tid) tile_rows(t, q);
+    auto add_tile = [&](const f32x4 (&q)[MQ]) {
 #pragma unroll
       for (int m = 0; m < MMAX; ++m) ss[m] += q[m / 4][m % 4];
+    };
+    f32x4 q[TQ][MQ];
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) tile_rows(tid + i * nt, q[i]);
+    after_loads();
+    stage_w();
+#pragma unroll
+    for (int i = 0; i < TQ; ++i)
+      if (tid + i * nt < rq.parts) add_tile(q[i]);
+    for (int t = tid + TQ * nt; t < rq.parts; t += nt) {
+      tile_rows(t, q[0]);
+      add_tile(q[0]);
     }
   } else if constexpr (FROM_X) {
     const int k0 = tid * 8, k1 = k0 + nt * 8;
@@ -215,6 +233,7 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
 #pragma unroll
       for (int m = 0; m < MMAX; ++m) h1[m] = load8<T>(x + (m < M ? m : M - 1) * sxm + (k1 < H ? k1 : 0));
     }
+    after_loads();
     stage_w();
     // x^2 two at a time with v_dot2_f32_f16 / _bf16 (no conversions); a slice past
     // H keeps the old sums, and rows past M get inv = 0 whatever they summed
@@ -502,6 +521,33 @@ __device__ __forceinline__ void stream_steps(int total, Buf& a, Buf& b, Issue&& 
     consume(a, s);
     consume(b, s + 1);
   } else if (s < total) {
+    consume(a, s);
+  }
+}
+
+// stream_steps for a caller that issued both step 0 (into `a`) and step 1 (into
+// `b`, when total > 1) before a prologue, so the prologue overlaps two steps'
+// loads. Same two buffers, same order of loads and math after that.
+template <typename Buf, typename Issue, typename Consume>
+__device__ __forceinline__ void stream_steps_issued2(int total, Buf& a, Buf& b, Issue&& issue,
+                                                     Consume&& consume) {
+  int s = 0;
+  for (; s + 3 < total; s += 2) {
+    consume(a, s);
+    issue(a, s + 2);
+    consume(b, s + 1);
+    issue(b, s + 3);
+  }
+  const int left = total - s;
+  if (left == 3) {
+    consume(a, s);
+    issue(a, s + 2);
+    consume(b, s + 1);
+    consume(a, s + 2);
+  } else if (left == 2) {
+    consume(a, s);
+    consume(b, s + 1);
+  } else if (left == 1) {
     consume(a, s);
   }
 }

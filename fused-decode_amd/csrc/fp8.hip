@@ -473,14 +473,16 @@ __global__ __launch_bounds__(kFp8SsWaves * kWave, 3) void mlp_gate_up_fp8_relayo
     }
   };
   UnitRegs8<T, 2> qa, qb;
-  if (mine > 0) issue(qa, 0);
-  {  // the first unit's loads fly while the prologue runs
+  {  // the first two units' loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
-    norm_prologue<T, HALF ? 8 : 16, FX>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps,
-                                        rq);
+    norm_prologue<T, HALF ? 8 : 16, FX, kFp8SsWaves * kWave>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H,
+                                                             units * kUnit, eps, rq, [&] {
+                                                               if (mine > 0) issue(qa, 0);
+                                                               if (mine > 1) issue(qb, 1);
+                                                             });
     rinv = inv[xrow];
   }
-  stream_steps(mine, qa, qb, issue, consume);
+  stream_steps_issued2(mine, qa, qb, issue, consume);
   part[wave * kWave + lane] = ag;
   __syncthreads();
   f32x4 sg = {0.f, 0.f, 0.f, 0.f};

@@ -513,12 +513,15 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
     }
   };
   UnitRegs16<T, 2> qa, qb;
-  if (mine > 0) issue(qa, 0);
   if constexpr (SS) {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
-    norm_prologue<T, HALF ? 8 : 16, FX>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H, units * kUnit, eps,
-                                        rq);
+    norm_prologue<T, HALF ? 8 : 16, FX, kSsWaves * kWave>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H,
+                                                         units * kUnit, eps, rq, [&] {
+                                                           if (mine > 0) issue(qa, 0);
+                                                         });
     rinv = inv[xrow];
+  } else {
+    if (mine > 0) issue(qa, 0);
   }
   stream_steps(mine, qa, qb, issue, consume);
   // two-phase reduction through one buffer: gate sums, then up sums

@@ -27,11 +27,11 @@ import torch
 from . import _lib
 from ._checks import check
 from ._lib import DTYPE_CODE, fail, native, stream_of
-from .ops import _check_out, _qkv_args, _rope_qkv_heads, _row_add_rows, rms_norm, swiglu
+from .ops import _FP8_ROWS, _PLANS, _check_out, _plan_qkv, _remember, _row_add_rows, _sig, rms_norm, swiglu
 
 FP8_MAX = 448.0
 FP8_DTYPE = torch.float8_e4m3fn
-_HAND_LIMIT = 16
+_HAND_LIMIT = _FP8_ROWS
 _FP8_MFMA_MIN_M = 5  # rows from which the fp8 kernels run on MFMA (fp8.hip)
 _warned: set[str] = set()
 
@@ -198,35 +198,16 @@ def pre_attn_qkv_fp8(
     argument rules of ``pre_attn_qkv``. One HIP launch up to 16 rows (from 5 the
     MFMA form with the norm folded in); otherwise, or for shapes the kernels do
     not take, composed from the operators."""
-    a0 = check("pre_attn_qkv_fp8", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, scale=scale,
-               eps=eps, bias=bias)
-    n, h = w_qkv.shape
-    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
-    out, m = a.out, a.m
-    if m == 0 or n == 0:
-        return out
-    if m <= _HAND_LIMIT and w_qkv.is_contiguous() and h % 16 == 0:
-        h2 = hidden.reshape(m, h)
-        if not h2.is_contiguous():
-            h2 = h2.contiguous()
-        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
-        b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
-        status = native().pre_attn_qkv_fp8(
-            out.data_ptr(), None, h2.data_ptr(),
-            nw.data_ptr(), DTYPE_CODE[nw.dtype], w_qkv.data_ptr(), scale.contiguous().data_ptr(),
-            b.data_ptr() if b is not None else None,
-            DTYPE_CODE[b.dtype] if b is not None else DTYPE_CODE[hidden.dtype],
-            a.cos.data_ptr(), a.sin.data_ptr(), DTYPE_CODE[a.cos.dtype], a.cs_row_stride, m, h, n,
-            a.rope_cols, a.d, a.eps, DTYPE_CODE[hidden.dtype], stream_of(hidden),
-        )
-        if status != _lib.FD_EUNSUPPORTED:
-            if status:
-                fail("fd_pre_attn_qkv_fp8", status)
-            return out
-    normed = rms_norm(hidden, norm_weight, eps=a.eps)
-    linear_decode_fp8(normed, w_qkv, scale, bias, out=out)
-    _rope_qkv_heads(a)
-    return out
+    try:
+        key = ("qkv_fp8", _sig(hidden), _sig(norm_weight), _sig(w_qkv), _sig(scale), _sig(cos), _sig(sin), eps,
+               rope_cols, _sig(bias), _sig(out))
+        plan = _PLANS.get(key)
+    except (AttributeError, TypeError):  # a non-tensor or unhashable argument: checked below
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_qkv(hidden, norm_weight, w_qkv, scale, cos, sin, eps, rope_cols, bias, out,
+                                        None))
+    return plan(hidden, norm_weight, w_qkv, scale, cos, sin, bias, out)
 
 
 __all__ = ["FP8_MAX", "dequantize_fp8", "linear_decode_fp8", "post_attn_mlp_fp8", "pre_attn_qkv_fp8",

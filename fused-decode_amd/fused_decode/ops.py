@@ -57,6 +57,7 @@ from .kernels import (
 # up to 14 rows), so the HIP GEMV is the default over the whole hand range.
 DECODE_LINEAR_MAX_M = 16
 _FORCED_LIMIT = 16  # rows the GEMV takes when the caller names a kind
+_FP8_ROWS = 16  # rows the E4M3 kernels take
 
 __all__ = [
     "DECODE_LINEAR_MAX_M",
@@ -646,26 +647,90 @@ def pre_attn_qkv(
     No reference counterpart as one call; it composes ops.py:72-88, :212-280 and
     :138-160.
     """
-    a0 = check("pre_attn_qkv", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, eps=eps, kind=kind,
-               bias=bias)
-    n, h = w_qkv.shape
+    try:
+        key = ("qkv", _sig(hidden), _sig(norm_weight), _sig(w_qkv), _sig(cos), _sig(sin), eps, rope_cols,
+               _sig(bias), _sig(out), kind, _env("FUSED_DECODE_LINEAR_KIND"))
+        plan = _PLANS.get(key)
+    except (AttributeError, TypeError):  # a non-tensor or unhashable argument: checked below
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_qkv(hidden, norm_weight, w_qkv, None, cos, sin, eps, rope_cols, bias, out,
+                                        kind))
+    return plan(hidden, norm_weight, w_qkv, None, cos, sin, bias, out)
+
+
+def _plan_qkv(hidden, norm_weight, w_qkv, scale, cos, sin, eps, rope_cols, bias, out, kind) -> Plan:
+    """Launch plan of ``pre_attn_qkv`` (``scale`` None) or ``pre_attn_qkv_fp8``
+    for one argument signature: every check runs here once; the plan's calls
+    only take the pointers. cos/sin already in the kernel's ``[1 or M, D]``
+    contiguous rows of one dtype are passed as they are, others are gathered
+    per call."""
+    fp8 = scale is not None
+    if fp8:
+        a0 = check("pre_attn_qkv_fp8", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, scale=scale,
+                   eps=eps, bias=bias)
+    else:
+        a0 = check("pre_attn_qkv", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, eps=eps, kind=kind,
+                   bias=bias)
+    n, h = (int(v) for v in w_qkv.shape)
     a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
-    out, m, eps = a.out, a.m, a.eps
+    m, d, rc, rs, eps = a.m, a.d, a.rope_cols, a.cs_row_stride, a.eps
+    lead, expected = tuple(hidden.shape[:-1]), tuple(a.out.shape)
+
+    def angles(c, s):
+        cr, sr = _token_angles(c, lead, "cos"), _token_angles(s, lead, "sin")
+        return (cr, sr) if cr.dtype == sr.dtype else (cr.float(), sr.float())
+
+    def composed(x, nw, w, sc, c, s, b, o):
+        y = o if o is not None else x.new_empty(expected)
+        cr, sr = angles(c, s)
+        normed = rms_norm(x, nw, eps=eps)
+        if fp8:
+            from .fp8 import linear_decode_fp8
+
+            linear_decode_fp8(normed, w, sc, b, out=y)
+        else:
+            linear_decode(normed, w, b, out=y, kind=kind)
+        _rope_qkv_heads(_QkvArgs(m, n, h, d, rc, eps, cr, sr, rs, y))
+        return y
+
     if m == 0 or n == 0:
-        return out
-    limit = _FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
-    kind_r = resolve_kind(kind)
-    if m <= limit and w_qkv.is_contiguous():
-        h2 = hidden.reshape(m, h)
-        if not h2.is_contiguous():
-            h2 = h2.contiguous()
-        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
-        b = bias if bias is None or bias.is_contiguous() else bias.contiguous()
-        status = pre_attn_qkv_out(h2, nw, w_qkv, b, a.cos, a.sin, a.cs_row_stride, a.rope_cols,
-                                  a.d, eps, out.view(m, n), None, kind_r)
-        if status == _lib.FD_OK:
-            return out
-    normed = rms_norm(hidden, norm_weight, eps=eps)
-    linear_decode(normed, w_qkv, bias, out=out, kind=kind)
-    _rope_qkv_heads(a)
-    return out
+        return lambda x, nw, w, sc, c, s, b, o: o if o is not None else x.new_empty(expected)
+    if fp8:
+        fits = m <= _FP8_ROWS and w_qkv.is_contiguous() and h % 16 == 0
+    else:
+        fits = m <= (_FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M) and w_qkv.is_contiguous()
+    if not fits:
+        return composed
+    direct = (a.cos.data_ptr() == cos.data_ptr() and a.sin.data_ptr() == sin.data_ptr()
+              and cos.dtype == sin.dtype)
+    dense_h, dense_nw = _dense(hidden), _dense(norm_weight)
+    dense_b = bias is None or _dense(bias)
+    dense_sc = not fp8 or _dense(scale)
+    act, nwc, csc, dev = (DTYPE_CODE[hidden.dtype], DTYPE_CODE[norm_weight.dtype], DTYPE_CODE[a.cos.dtype],
+                          hidden.device.index)
+    bc = DTYPE_CODE[bias.dtype] if bias is not None else act
+    call = native().pre_attn_qkv_fp8 if fp8 else native().pre_attn_qkv
+    kcode = None if fp8 else KIND_CODE[resolve_kind(kind)]
+    name = "fd_pre_attn_qkv_fp8" if fp8 else "fd_pre_attn_qkv"
+
+    def fused(x, nw, w, sc, c, s, b, o):
+        y = o if o is not None else x.new_empty(expected)
+        cr, sr = (c, s) if direct else angles(c, s)
+        x2 = x if dense_h else x.contiguous()
+        nw2 = nw if dense_nw else nw.contiguous()
+        bp = None if b is None else (b if dense_b else b.contiguous()).data_ptr()
+        if fp8:
+            sp = (sc if dense_sc else sc.contiguous()).data_ptr()
+            status = call(y.data_ptr(), None, x2.data_ptr(), nw2.data_ptr(), nwc, w.data_ptr(), sp, bp, bc,
+                          cr.data_ptr(), sr.data_ptr(), csc, rs, m, h, n, rc, d, eps, act, _raw_stream(dev))
+        else:
+            status = call(y.data_ptr(), None, x2.data_ptr(), nw2.data_ptr(), nwc, w.data_ptr(), bp, bc,
+                          cr.data_ptr(), sr.data_ptr(), csc, rs, m, h, n, rc, d, eps, kcode, act,
+                          _raw_stream(dev))
+        if status == FD_EUNSUPPORTED:  # a shape the fused kernels do not take: the operators
+            return composed(x, nw, w, sc, c, s, b, y)
+        if status:
+            fail(name, status)
+        return y
+    return fused

@@ -429,6 +429,25 @@ def test_pre_attn_qkv_fp8_llama3_8b(dtype, m):
     torch.testing.assert_close(y[:1].float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+@pytest.mark.parametrize("m", [2, 8])
+def test_pre_attn_qkv_fp8_plan_reuse(m):
+    """A second call with the same argument signature (the cached plan) on new
+    operands, and angles gathered per call ([M, 1, D] views), match the oracle."""
+    from fused_decode import ops
+
+    ops.clear_plans()
+    for seed in (41, 42):
+        hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 256, 4, 2, 64, torch.float16, seed=seed, bias=True)
+        y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+        ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    for seed in (43, 44):
+        hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 256, 4, 2, 64, torch.float16, seed=seed)
+        y = qkv_run(hidden, nw, q, s, None, cos.unsqueeze(1), sin.unsqueeze(1), rc)
+        ref = qkv_oracle(hidden, nw, qn, sn, None, cos, sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 def test_pre_attn_qkv_fp8_entry_point_and_rejects():
     """fd_pre_attn_qkv_fp8 through the C ABI: from 5 rows the MFMA form folds the
     RMSNorm in (`normed` may be null and is left untouched), H not a multiple of 16

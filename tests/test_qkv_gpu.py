@@ -206,6 +206,30 @@ def test_pre_attn_qkv_rejects():
         fd.pre_attn_qkv(hd, nwd, wd, cd, sd, rope_cols=rc, kind="mfma")
 
 
+@pytest.mark.parametrize("m", [2, 8])
+def test_pre_attn_qkv_plan_reuse(m):
+    """Calls that share an argument signature reuse one cached launch plan: new
+    operands of that signature give their own results, and angles that need
+    gathering ([M, 1, D] float16 cos beside float32 sin) are gathered on every
+    call, also when the plan is reused."""
+    import fused_decode as fd
+    from fused_decode import ops
+
+    ops.clear_plans()
+    for seed in (31, 32):
+        hidden, nw, w, b, cos, sin, rc = case(m, 256, 4, 2, 64, torch.float16, seed=seed, bias=True)
+        y = run(hidden, nw, w, b, cos, sin, rc, kind="dot")
+        ref = oracle(hidden, nw, w, b, cos, sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+    for seed in (33, 34):
+        hidden, nw, w, b, cos, sin, rc = case(m, 256, 4, 2, 64, torch.float16, seed=seed)
+        c16 = cos.half()
+        y = fd.pre_attn_qkv(hidden.to(DEV), nw.to(DEV), w.to(DEV), c16.unsqueeze(1).to(DEV),
+                            sin.unsqueeze(1).to(DEV), 1e-5, rope_cols=rc)
+        ref = oracle(hidden, nw, w, None, c16.float(), sin, rc, torch.float16)
+        torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
+
+
 def test_pre_attn_qkv_entry_point_normed_and_status():
     """fd_pre_attn_qkv through the C ABI at 8 rows (the MFMA form): `normed` may
     be NULL; an unsupported head_dim is FD_EUNSUPPORTED, not a launch."""
