@@ -26,8 +26,9 @@ import torch
 
 from . import _lib
 from ._checks import check
-from ._lib import DTYPE_CODE, fail, native, stream_of
-from .ops import _FP8_ROWS, _PLANS, _check_out, _plan_qkv, _remember, _row_add_rows, _sig, rms_norm, swiglu
+from ._lib import DTYPE_CODE, fail, native
+from .ops import (_FP8_ROWS, _PLANS, _check_out, _dense, _empty, _plan_qkv, _raw_stream, _remember, _row_add_rows,
+                  _sig, rms_norm, swiglu)
 
 FP8_MAX = 448.0
 FP8_DTYPE = torch.float8_e4m3fn
@@ -42,7 +43,7 @@ def _slow_path(why: str) -> None:
         _warned.add(why)
         warnings.warn(f"linear_decode_fp8: {why}; computing a float32 product of the decoded weights "
                       "(same values, about 4x the weight traffic of the fp8 kernels)", RuntimeWarning,
-                      stacklevel=3)
+                      stacklevel=5)  # _slow_path, the plan's helper, the plan, linear_decode_fp8, its caller
 
 
 def quantize_fp8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -66,12 +67,6 @@ def dequantize_fp8(codes: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return codes.float() * scale.float()[:, None]
 
 
-def _kernel_rows_ok(weight: torch.Tensor) -> bool:
-    """Codes the fp8 kernels stream: unit K stride, K % 16 == 0, 16-byte rows."""
-    return weight.stride(1) == 1 and (weight.shape[0] == 1 or weight.stride(0) % 16 == 0) \
-        and weight.shape[1] % 16 == 0 and weight.data_ptr() % 16 == 0
-
-
 def linear_decode_fp8(
     x: torch.Tensor,
     weight: torch.Tensor,
@@ -87,53 +82,83 @@ def linear_decode_fp8(
     ``K % 16 == 0`` this is the HIP fp8 GEMV; other shapes compute a float32
     product of the decoded weights (same values, several times the traffic: a
     RuntimeWarning says so once per reason)."""
+    try:
+        key = ("linear_fp8", _sig(x), _sig(weight), _sig(scale), _sig(bias), _sig(row_add), _sig(out))
+        plan = _PLANS.get(key)
+    except AttributeError:  # a non-tensor argument: checked below
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_linear_fp8(x, weight, scale, bias, row_add, out))
+    return plan(x, weight, scale, bias, row_add, out)
+
+
+def _plan_linear_fp8(x, weight, scale, bias, row_add, out):
+    """Launch plan of ``linear_decode_fp8`` for one argument signature: the
+    contract's checks and the shape rules of the kernel run once; each call
+    checks only the two pointers whose alignment the signature leaves open."""
     check("linear_decode_fp8", x=x, weight=weight, scale=scale, bias=bias, row_add=row_add)
     n, k = (int(d) for d in weight.shape)
     m = 1 if x.ndim == 1 else math.prod(x.shape[:-1])
     expected = (n,) if x.ndim == 1 else (*x.shape[:-1], n)
     ra = None if row_add is None else _row_add_rows(row_add, m, n, expected)
-    if out is None:
-        out = torch.empty(expected, device=x.device, dtype=x.dtype)
-    else:
+    if out is not None:
         _check_out(out, expected, x)
-    y2 = out.view(m, n)
+    alloc = _empty(expected, x)
     if m == 0 or n == 0:
-        return out
-    x2 = x.reshape(m, k)
-    if x2.stride(1) != 1:
-        x2 = x2.contiguous()
+        return lambda x, w, sc, b, r, o: alloc(x) if o is None else o
+
+    def slow(x2, w, sc, b, r, y, why):
+        _slow_path(why)
+        p = (x2.float() @ w.float().t()) * sc
+        if b is not None:
+            p = p + b.float()
+        if r is not None:
+            p = p + r.expand(expected).reshape(m, n).float()
+        y.view(m, n).copy_(p.to(x2.dtype))
+        return y
+
+    x2p = x.reshape(m, k)
+    x_copy = x2p.stride(1) != 1  # gathered per call into contiguous rows
     why = None
     if m > _HAND_LIMIT:
         why = f"{m} rows is above the kernels' {_HAND_LIMIT}"
-    elif not _kernel_rows_ok(weight):
+    elif not (weight.stride(1) == 1 and (n == 1 or weight.stride(0) % 16 == 0) and k % 16 == 0):
         why = "the codes are not 16-byte rows with K % 16 == 0"
-    elif x2.stride(1) != 1 or (m > 1 and x2.stride(0) % 8 != 0) or x2.data_ptr() % 16 != 0:
+    elif not x_copy and m > 1 and x2p.stride(0) % 8 != 0:
         why = "x rows are not 16-byte aligned with unit stride"
     if why is not None:
-        _slow_path(why)
-        y = (x2.float() @ weight.float().t()) * scale
-        if bias is not None:
-            y = y + bias.float()
-        if row_add is not None:
-            y = y + row_add.expand(expected).reshape(m, n).float()
-        y2.copy_(y.to(x.dtype))
-        return out
-    act = DTYPE_CODE[x.dtype]
-    r2, srm, srn = None, 0, 0
-    if row_add is not None:  # indexed in place through (srm, srn), or copied when its dims do not merge
-        srm, srn, flat = ra
-        r2 = row_add.expand(expected).reshape(m, n) if flat else row_add
-    sc = scale if scale.is_contiguous() else scale.contiguous()
-    status = native().linear_fp8(
-        y2.data_ptr(), x2.data_ptr(), weight.data_ptr(), sc.data_ptr(),
-        None if bias is None else bias.data_ptr(), act if bias is None else DTYPE_CODE[bias.dtype],
-        None if r2 is None else r2.data_ptr(), act if r2 is None else DTYPE_CODE[r2.dtype],
-        m, n, k, int(x2.stride(0)), int(weight.stride(0)), 0 if bias is None else int(bias.stride(0)),
-        srm, srn, int(y2.stride(0)), int(y2.stride(1)), act, stream_of(x),
-    )
-    if status:
-        fail("fd_linear_fp8", status)
-    return out
+        def fallback(x, w, sc, b, r, o):
+            x2 = x.reshape(m, k)
+            return slow(x2.contiguous() if x_copy else x2, w, sc, b, r, alloc(x) if o is None else o, why)
+        return fallback
+
+    act, dev = DTYPE_CODE[x.dtype], x.device.index
+    bcode = act if bias is None else DTYPE_CODE[bias.dtype]
+    sb = 0 if bias is None else int(bias.stride(0))
+    rcode = act if row_add is None else DTYPE_CODE[row_add.dtype]
+    srm, srn, r_flat = ra if ra is not None else (0, 0, False)
+    dense_sc = _dense(scale)
+    sxm = k if x_copy else int(x2p.stride(0))
+    call = native().linear_fp8
+
+    def run(x, w, sc, b, r, o):
+        y = alloc(x) if o is None else o
+        x2 = x.reshape(m, k)
+        if x_copy:
+            x2 = x2.contiguous()
+        if w.data_ptr() % 16:
+            return slow(x2, w, sc, b, r, y, "the codes are not 16-byte rows with K % 16 == 0")
+        if x2.data_ptr() % 16:
+            return slow(x2, w, sc, b, r, y, "x rows are not 16-byte aligned with unit stride")
+        if r is not None and r_flat:  # indexed in place through (srm, srn), or copied when its dims do not merge
+            r = r.expand(expected).reshape(m, n)
+        status = call(y.data_ptr(), x2.data_ptr(), w.data_ptr(), (sc if dense_sc else sc.contiguous()).data_ptr(),
+                      None if b is None else b.data_ptr(), bcode, None if r is None else r.data_ptr(), rcode,
+                      m, n, k, sxm, int(w.stride(0)), sb, srm, srn, n, 1, act, _raw_stream(dev))
+        if status:
+            fail("fd_linear_fp8", status)
+        return y
+    return run
 
 
 def post_attn_mlp_fp8(
@@ -150,33 +175,53 @@ def post_attn_mlp_fp8(
     reference.py:66-79), each projection as ``linear_decode_fp8``. Two HIP launches
     up to 16 rows (from 5 the MFMA gate/up normalises inside its kernel);
     otherwise composed from the operators."""
+    try:
+        key = ("mlp_fp8", _sig(hidden), _sig(norm_weight), _sig(w_gate_up), _sig(gate_up_scale), _sig(w_down),
+               _sig(down_scale), eps)
+        plan = _PLANS.get(key)
+    except (AttributeError, TypeError):  # a non-tensor or unhashable argument: checked below
+        key, plan = None, None
+    if plan is None:
+        plan = _remember(key, _plan_mlp_fp8(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps))
+    return plan(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale)
+
+
+def _plan_mlp_fp8(hidden, norm_weight, w_gate_up, gate_up_scale, w_down, down_scale, eps):
+    """Launch plan of ``post_attn_mlp_fp8`` for one argument signature."""
     a = check("post_attn_mlp_fp8", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up,
               gate_up_scale=gate_up_scale, w_down=w_down, down_scale=down_scale, eps=eps)
     eps = a["eps"]
     h, i = int(w_gate_up.shape[1]), int(w_down.shape[1])
     m = hidden.numel() // h if h else 0
-    if 0 < m <= _HAND_LIMIT and w_gate_up.is_contiguous() and w_down.is_contiguous() \
-            and h % 16 == 0 and i % 16 == 0:
-        h2 = hidden.reshape(m, h)
-        if not h2.is_contiguous():
-            h2 = h2.contiguous()
-        nw = norm_weight if norm_weight.is_contiguous() else norm_weight.contiguous()
-        y = torch.empty((m, h), device=hidden.device, dtype=hidden.dtype)
-        mid = torch.empty((m, i), device=hidden.device, dtype=hidden.dtype)
-        status = native().post_attn_mlp_fp8(
-            y.data_ptr(), mid.data_ptr(), h2.data_ptr(), nw.data_ptr(), DTYPE_CODE[nw.dtype],
-            w_gate_up.data_ptr(), gate_up_scale.contiguous().data_ptr(), w_down.data_ptr(),
-            down_scale.contiguous().data_ptr(), m, h, i, eps, DTYPE_CODE[hidden.dtype],
-            stream_of(hidden),
-        )
-        if status != _lib.FD_EUNSUPPORTED:
-            if status:
-                fail("fd_post_attn_mlp_fp8", status)
-            return y.view(hidden.shape)
-    normed = rms_norm(hidden, norm_weight, eps=eps)
-    gate_up = linear_decode_fp8(normed, w_gate_up, gate_up_scale)
-    gate, up = gate_up.split(i, dim=-1)
-    return linear_decode_fp8(swiglu(gate, up), w_down, down_scale, row_add=hidden)
+
+    def composed(x, nw, wgu, sgu, wd, sd):
+        normed = rms_norm(x, nw, eps=eps)
+        gate, up = linear_decode_fp8(normed, wgu, sgu).split(i, dim=-1)
+        return linear_decode_fp8(swiglu(gate, up), wd, sd, row_add=x)
+
+    if not (0 < m <= _HAND_LIMIT and w_gate_up.is_contiguous() and w_down.is_contiguous()
+            and h % 16 == 0 and i % 16 == 0):
+        return composed
+    shape = tuple(hidden.shape)
+    dense_h, dense_nw, dense_s = _dense(hidden), _dense(norm_weight), _dense(gate_up_scale) and _dense(down_scale)
+    call, act, nwc, dev = (native().post_attn_mlp_fp8, DTYPE_CODE[hidden.dtype], DTYPE_CODE[norm_weight.dtype],
+                           hidden.device.index)
+
+    def fused(x, nw, wgu, sgu, wd, sd):
+        x2 = x if dense_h else x.contiguous()
+        nw2 = nw if dense_nw else nw.contiguous()
+        if not dense_s:
+            sgu, sd = sgu.contiguous(), sd.contiguous()
+        y = x2.new_empty((m, h))
+        mid = x2.new_empty((m, i))
+        status = call(y.data_ptr(), mid.data_ptr(), x2.data_ptr(), nw2.data_ptr(), nwc, wgu.data_ptr(),
+                      sgu.data_ptr(), wd.data_ptr(), sd.data_ptr(), m, h, i, eps, act, _raw_stream(dev))
+        if status == _lib.FD_EUNSUPPORTED:  # e.g. an unaligned operand or a hidden width beyond the LDS
+            return composed(x, nw, wgu, sgu, wd, sd)
+        if status:
+            fail("fd_post_attn_mlp_fp8", status)
+        return y.view(shape)
+    return fused
 
 
 def pre_attn_qkv_fp8(

@@ -89,11 +89,30 @@ def test_linear_fp8_llama_shapes(dtype, nk):
 def test_linear_fp8_fallback_shapes():
     import fused_decode as fd
 
+    from fused_decode import fp8 as F8
+
     x = rnd(24, 200, seed=9)  # 24 rows > 16 and K % 16 != 0: the float32 path
     q, s, qn, sn = quant(rnd(48, 200, seed=10, scale=0.1))
-    y = fd.linear_decode_fp8(x.to(DEV), q, s)
+    F8._warned.clear()
+    with pytest.warns(RuntimeWarning, match="float32 product"):
+        y = fd.linear_decode_fp8(x.to(DEV), q, s)
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(O.linear_fp8(npf(x), qn, sn, dtype="f16")),
                                **tol(torch.float16))
+    # codes at an address that is not 16-byte aligned, after a call that cached the
+    # plan of the same signature on aligned codes: the float32 path, same values
+    x = rnd(4, 256, seed=11)
+    q, s, qn, sn = quant(rnd(32, 256, seed=12, scale=0.1))
+    raw = torch.empty(32 * 256 + 8, dtype=torch.uint8, device=DEV)
+    mis = raw[8:].view(32, 256)
+    mis.copy_(q.view(torch.uint8))
+    qm = mis.view(q.dtype)
+    assert qm.stride() == q.stride() and qm.data_ptr() % 16 == 8
+    ref = torch.from_numpy(O.linear_fp8(npf(x), qn, sn, dtype="f16"))
+    y = fd.linear_decode_fp8(x.to(DEV), q, s)
+    torch.testing.assert_close(y.float().cpu(), ref, **tol(torch.float16))
+    with pytest.warns(RuntimeWarning, match="16-byte rows"):
+        y1 = fd.linear_decode_fp8(x.to(DEV), qm, s)
+    torch.testing.assert_close(y1.float().cpu(), ref, **tol(torch.float16))
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
