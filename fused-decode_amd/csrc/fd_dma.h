@@ -32,7 +32,8 @@
 // the norm weight (float32) and the rows' inverse RMS are staged in dynamic LDS
 // (norm_dma_lds bytes) by a prologue whose loads go out just before the first
 // units' DMAs and which runs while those are in flight, and every B fragment is
-// normalised after its LDS read.
+// normalised after its LDS read (up to 8 rows in the half-B form: each lane
+// normalises two fragments and swaps them with its row-mirror partner).
 #pragma once
 
 #include "fd_gemv.h"
@@ -74,7 +75,8 @@ inline int dma_rows(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 #define FD_V1(i) "+v"(v[i])
 #define FD_V6 FD_V1(0), FD_V1(1), FD_V1(2), FD_V1(3), FD_V1(4), FD_V1(5)
 #define FD_V8 FD_V6, FD_V1(6), FD_V1(7)
-#define FD_V14 FD_V8, FD_V1(8), FD_V1(9), FD_V1(10), FD_V1(11), FD_V1(12), FD_V1(13)
+#define FD_V10 FD_V8, FD_V1(8), FD_V1(9)
+#define FD_V14 FD_V10, FD_V1(10), FD_V1(11), FD_V1(12), FD_V1(13)
 #define FD_V16 FD_V14, FD_V1(14), FD_V1(15)
 template <int NR>
 __device__ __forceinline__ void wait_lds_all(u32x4 (&v)[NR]) {
@@ -82,6 +84,8 @@ __device__ __forceinline__ void wait_lds_all(u32x4 (&v)[NR]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V6::"memory");
   else if constexpr (NR == 8)
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V8::"memory");
+  else if constexpr (NR == 10)
+    asm volatile("s_waitcnt lgkmcnt(0)" : FD_V10::"memory");
   else if constexpr (NR == 14)
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V14::"memory");
   else if constexpr (NR == 16)
@@ -102,6 +106,7 @@ __device__ __forceinline__ void wait_lds_all(u32x4 (&a)[N1], u32x4 (&b)[N2]) {
 #undef FD_V1
 #undef FD_V6
 #undef FD_V8
+#undef FD_V10
 #undef FD_V14
 #undef FD_V16
 
@@ -133,7 +138,11 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   constexpr bool F8 = sizeof(W) == 1;
   constexpr DmaGeom G = dma_geom(sizeof(W));
   constexpr int NA = F8 ? 2 : 4;               // A reads per unit per lane
-  constexpr int NR = NA + 4 + (NORM && BR > 8 ? 8 : 0);  // fragment reads per unit
+  // NORM up to 8 rows: the half-B form (half_b_row / mirror16): a lane reads and
+  // normalises two B fragments, steps 2p + hi, and the row mirror hands each
+  // low lane its partner's; from 9 rows a lane normalises all four it reads
+  constexpr bool NHALF = NORM && BR <= 8;
+  constexpr int NR = NA + (NHALF ? 2 + 4 : 4 + (NORM ? 8 : 0));  // LDS reads per unit
   constexpr int SLOT = G.ae + BR * 16;         // 16-byte entries: the A tile, then the B rows
   constexpr int OPS = G.aops + BR / 4;         // DMA instructions per unit
   __shared__ u32x4 ring[NW][D][SLOT];
@@ -202,11 +211,17 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     const int cb = F8 ? g * 4 + s2 : s2 * 4 + g;
     fb[s2] = ring0 + (unsigned)(G.ae + rb * 16 + (cb ^ rb)) * 16u;
   }
+  const int hi = r >= 8, hrow = half_b_row(r) % BR;  // NHALF: this lane's B row
+  if constexpr (NHALF) {  // fb[p]: fragment 2p + hi of row hrow
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int s2 = 2 * p + hi, cb = F8 ? g * 4 + s2 : s2 * 4 + g;
+      fb[p] = ring0 + (unsigned)(G.ae + hrow * 16 + (cb ^ hrow)) * 16u;
+    }
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float rinv = 0.f;       // NORM, BR = 16: inverse RMS of this lane's B row
-  unsigned fw = 0;        // NORM, BR = 16: this lane's norm-weight fragment base (bytes)
-  float rinv_e[BR / 4];   // NORM, BR <= 8: inverse RMS of the rows this lane's DMAs fill
-  unsigned fwl = 0;       // NORM: the staged norm weight (bytes)
+  float rinv = 0.f;       // NORM: inverse RMS of this lane's B row
+  unsigned fw = 0;        // NORM: this lane's norm-weight fragment base (bytes)
   auto consume = [&](int j) {
     const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
     const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
@@ -219,45 +234,39 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
         if (k0 + xch[i] >= K) ds_zero16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    if constexpr (NORM && BR <= 8) {
-      // normalise the unit's B rows in place, each element once: this lane's
-      // BR/4 entries are the ones its own DMAs filled (row 4i + g, chunk xch[i])
-      u32x4 raw[BR / 4], wv[BR / 2];
-#pragma unroll
-      for (int i = 0; i < BR / 4; ++i) {
-        raw[i] = ds_read16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u);
-        const unsigned wa = fwl + (unsigned)(k0 + xch[i]) * 4u;
-        wv[2 * i] = ds_read16(wa);
-        wv[2 * i + 1] = ds_read16(wa + 16u);
-      }
-      wait_lds_all(raw, wv);
-#pragma unroll
-      for (int i = 0; i < BR / 4; ++i)
-        ds_write16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u,
-                   norm_frag<T>(raw[i], rinv_e[i], wv[2 * i], wv[2 * i + 1]));
-    }
-    // v: [NA] A reads, [4] B fragments, NORM (BR = 16): [8] norm weight
+    // v: [NA] A reads, then NHALF: [2] B fragments, [4] norm weight; else [4] B
+    // fragments, NORM: [8] norm weight
     u32x4 v[NR];
 #pragma unroll
     for (int t = 0; t < NA; ++t) v[t] = ds_read16(fa[t] + so);
+    constexpr int NB = NHALF ? 2 : 4;
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) v[NA + s2] = ds_read16(fb[s2] + so);
-    if constexpr (NORM && BR > 8) {
+    for (int t = 0; t < NB; ++t) v[NA + t] = ds_read16(fb[t] + so);
+    if constexpr (NORM) {
 #pragma unroll
-      for (int s2 = 0; s2 < 4; ++s2) {  // 8 floats at fragment s2's k
+      for (int t = 0; t < NB; ++t) {  // 8 floats at the k of fragment t's step
+        const int s2 = NHALF ? 2 * t + hi : t;
         const unsigned wa = fw + (unsigned)(k0 + s2 * (F8 ? 8 : 32)) * 4u;
-        v[NA + 4 + 2 * s2] = ds_read16(wa);
-        v[NA + 5 + 2 * s2] = ds_read16(wa + 16u);
+        v[NA + NB + 2 * t] = ds_read16(wa);
+        v[NA + NB + 2 * t + 1] = ds_read16(wa + 16u);
       }
     }
     wait_lds_all(v);
     u32x4 b[4];
+    if constexpr (NHALF) {
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      if constexpr (NORM && BR > 8)
-        b[s2] = norm_frag<T>(v[NA + s2], rinv, v[NA + 4 + 2 * s2], v[NA + 5 + 2 * s2]);
-      else
-        b[s2] = v[NA + s2];
+      for (int p = 0; p < 2; ++p) {
+        b[2 * p] = norm_frag<T>(v[NA + p], rinv, v[NA + 2 + 2 * p], v[NA + 3 + 2 * p]);
+        b[2 * p + 1] = mirror16(b[2 * p]);
+      }
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 4; ++s2) {
+        if constexpr (NORM)
+          b[s2] = norm_frag<T>(v[NA + s2], rinv, v[NA + 4 + 2 * s2], v[NA + 5 + 2 * s2]);
+        else
+          b[s2] = v[NA + s2];
+      }
     }
     u32x4 af[4];
     if constexpr (F8) {
@@ -286,11 +295,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
                                            [&] {
                                              for (int j = 0; j < pre; ++j) issue(j);
                                            });
-    rinv = inv[rb];
-#pragma unroll
-    for (int i = 0; i < BR / 4; ++i) rinv_e[i] = inv[4 * i + g];
-    fwl = lds_addr(wl);
-    fw = fwl + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
+    rinv = inv[NHALF ? hrow : rb];
+    fw = lds_addr(wl) + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
   } else {
     for (int j = 0; j < pre; ++j) issue(j);
   }
