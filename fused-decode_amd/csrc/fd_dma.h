@@ -42,6 +42,12 @@ namespace fd {
 
 enum DmaEpi { EPI_PLAIN = 0, EPI_ROPE = 1 };
 
+// How a launch applies the folded RMSNorm: not at all; with the norm weight
+// staged in LDS as float32 by the prologue (any weight dtype); or with the
+// weight (in the activation type) streamed with each unit like the activations,
+// so the prologue waits only for the row sums.
+enum DmaNorm { NORM_NONE = 0, NORM_STAGED = 1, NORM_STREAMED = 2 };
+
 // Ring geometry of one unit's 16-row weight tile for weights of `bytes` bytes.
 struct DmaGeom {
   int cpr;   // 16-byte chunks per 128-element row: 16 or 8
@@ -55,16 +61,19 @@ __host__ __device__ constexpr DmaGeom dma_geom(int bytes) {
                  kWave / (kUnit * bytes / 16)};
 }
 
-// Static LDS of a DMA launch: the ring (NW waves x D slots of the weight tile
-// and the B rows) and the partial sums.
-__host__ __device__ constexpr size_t dma_lds(int nw, int d, int br, int wbytes = 2) {
-  return (size_t)nw * d * (dma_geom(wbytes).ae + br * 16) * 16 + (size_t)nw * kWave * 16;
+// Static LDS of a DMA launch: the ring (NW waves x D slots of the weight tile,
+// the B rows and, streaming the norm weight, its 16 entries) and the partial
+// sums.
+__host__ __device__ constexpr size_t dma_lds(int nw, int d, int br, int wbytes = 2, bool ws = false) {
+  return (size_t)nw * d * (dma_geom(wbytes).ae + br * 16 + (ws ? 16 : 0)) * 16 + (size_t)nw * kWave * 16;
 }
 
-// Dynamic LDS of a NORM launch: the float32 norm weight over whole K units, the
-// 16 inverse RMS values and the prologue's reduction scratch.
-inline size_t norm_dma_lds(int K) {
-  return sizeof(float) * ((size_t)((K + kUnit - 1) / kUnit) * kUnit + 16 + kMaxWaves * 16);
+// Dynamic LDS of a NORM launch: NORM_STAGED the float32 norm weight over whole
+// K units; both modes the 16 inverse RMS values and the prologue's reduction
+// scratch.
+inline size_t norm_dma_lds(int K, int mode) {
+  const size_t w = mode == NORM_STAGED ? (size_t)((K + kUnit - 1) / kUnit) * kUnit : 0;
+  return sizeof(float) * (w + 16 + kMaxWaves * 16);
 }
 
 // Activation rows a DMA MFMA launch stages: M rounded up to 4, 8 or 16.
@@ -76,7 +85,8 @@ inline int dma_rows(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 #define FD_V6 FD_V1(0), FD_V1(1), FD_V1(2), FD_V1(3), FD_V1(4), FD_V1(5)
 #define FD_V8 FD_V6, FD_V1(6), FD_V1(7)
 #define FD_V10 FD_V8, FD_V1(8), FD_V1(9)
-#define FD_V14 FD_V10, FD_V1(10), FD_V1(11), FD_V1(12), FD_V1(13)
+#define FD_V12 FD_V10, FD_V1(10), FD_V1(11)
+#define FD_V14 FD_V12, FD_V1(12), FD_V1(13)
 #define FD_V16 FD_V14, FD_V1(14), FD_V1(15)
 template <int NR>
 __device__ __forceinline__ void wait_lds_all(u32x4 (&v)[NR]) {
@@ -86,6 +96,8 @@ __device__ __forceinline__ void wait_lds_all(u32x4 (&v)[NR]) {
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V8::"memory");
   else if constexpr (NR == 10)
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V10::"memory");
+  else if constexpr (NR == 12)
+    asm volatile("s_waitcnt lgkmcnt(0)" : FD_V12::"memory");
   else if constexpr (NR == 14)
     asm volatile("s_waitcnt lgkmcnt(0)" : FD_V14::"memory");
   else if constexpr (NR == 16)
@@ -107,6 +119,7 @@ __device__ __forceinline__ void wait_lds_all(u32x4 (&a)[N1], u32x4 (&b)[N2]) {
 #undef FD_V6
 #undef FD_V8
 #undef FD_V10
+#undef FD_V12
 #undef FD_V14
 #undef FD_V16
 
@@ -129,7 +142,7 @@ __device__ __forceinline__ void fp8x16_decode(const u32x4& w, u32x4& c0, u32x4& 
   c1 = u32x4{h[4], h[5], h[6], h[7]};
 }
 
-template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
+template <typename T, typename W, int NW, int D, int BR, int EPI, int NORM>
 __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     T* y, const T* x, const W* w, const float* wscale, int M, int N, int K, int64_t sxm,
     int64_t swn, int64_t sym, int64_t syn, Epi e, Rope rp, const void* nwp, int nw_dtype,
@@ -142,13 +155,19 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   // normalises two B fragments, steps 2p + hi, and the row mirror hands each
   // low lane its partner's; from 9 rows a lane normalises all four it reads
   constexpr bool NHALF = NORM && BR <= 8;
-  constexpr int NR = NA + (NHALF ? 2 + 4 : 4 + (NORM ? 8 : 0));  // LDS reads per unit
-  constexpr int SLOT = G.ae + BR * 16;         // 16-byte entries: the A tile, then the B rows
-  constexpr int OPS = G.aops + BR / 4;         // DMA instructions per unit
+  constexpr bool WS = NORM == NORM_STREAMED;
+  constexpr int NB = NHALF ? 2 : 4;                                    // B fragment reads per unit
+  constexpr int NWR = NORM == NORM_STAGED ? 2 * NB : WS ? NB : 0;      // norm-weight reads per unit
+  constexpr int NR = NA + NB + NWR;                                    // LDS reads per unit
+  // 16-byte entries: the A tile, the B rows, WS: the unit's 128 norm weights
+  // (16 entries, filled by lanes 0-15 of one DMA instruction)
+  constexpr int WOFF = G.ae + BR * 16;
+  constexpr int SLOT = WOFF + (WS ? 16 : 0);
+  constexpr int OPS = G.aops + BR / 4 + (WS ? 1 : 0);  // DMA instructions per unit
   __shared__ u32x4 ring[NW][D][SLOT];
   __shared__ f32x4 part[NW * kWave];
   __shared__ float ang_lds[EPI == EPI_ROPE ? kTileAngles : 1];  // ROPE: the tile's cos/sin
-  extern __shared__ float norm_lds[];  // NORM: w [units * 128], inv [16], scratch
+  extern __shared__ float norm_lds[];  // NORM_STAGED: w [units * 128]; NORM: inv [16], scratch
   const int lane = threadIdx.x & (kWave - 1);
   // wave-uniform, so the unit indices, the K-tail tests and the ring addresses
   // are scalar (a per-lane value here turns the tail test into exec-masked
@@ -177,6 +196,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   const int units = (K + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + NW - 1) / NW : 0;
   const int off = sweep_offset(units);
+  const T* nwt = static_cast<const T*>(nwp);  // WS: the norm weight, in T
+  const int wsc = (lane & 15) * 8;            // WS: this lane's chunk of a unit's norm weights
   auto issue = [&](int j) {
     const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
     u32x4* slot = ring[wave][j % D];
@@ -185,6 +206,8 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
       for (int i = 0; i < G.aops; ++i) dma16(wrow[i] + k0 + wch[i], slot + i * kWave);
 #pragma unroll
       for (int i = 0; i < BR / 4; ++i) dma16(xrow[i] + k0 + xch[i], slot + G.ae + i * kWave);
+      if constexpr (WS)
+        if (lane < 16) dma16(nwt + k0 + wsc, slot + WOFF);
     } else {  // the same instruction count, chunks past K clamped to the row's first
 #pragma unroll
       for (int i = 0; i < G.aops; ++i) {
@@ -195,6 +218,10 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
       for (int i = 0; i < BR / 4; ++i) {
         const int k = k0 + xch[i];
         dma16(xrow[i] + (k < K ? k : 0), slot + G.ae + i * kWave);
+      }
+      if constexpr (WS) {
+        const int k = k0 + wsc;
+        if (lane < 16) dma16(nwt + (k < K ? k : 0), slot + WOFF);
       }
     }
   };
@@ -221,7 +248,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   float rinv = 0.f;       // NORM: inverse RMS of this lane's B row
-  unsigned fw = 0;        // NORM: this lane's norm-weight fragment base (bytes)
+  unsigned fwl = 0;       // NORM_STAGED: the staged norm weight (bytes)
   auto consume = [&](int j) {
     const unsigned so = (unsigned)(j % D) * (SLOT * 16u);
     const int k0 = sweep_unit(wave, j, NW, off, units) * kUnit;
@@ -232,38 +259,50 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
 #pragma unroll
       for (int i = 0; i < BR / 4; ++i)
         if (k0 + xch[i] >= K) ds_zero16(ring0 + so + (unsigned)(G.ae + i * kWave + lane) * 16u);
+      if constexpr (WS)
+        if (lane < 16 && k0 + wsc >= K) ds_zero16(ring0 + so + (unsigned)(WOFF + lane) * 16u);
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    // v: [NA] A reads, then NHALF: [2] B fragments, [4] norm weight; else [4] B
-    // fragments, NORM: [8] norm weight
+    // v: [NA] A reads, [NB] B fragments, then the norm weight at their k:
+    // NORM_STAGED 8 floats each (two reads), WS 8 T values each (one read)
     u32x4 v[NR];
 #pragma unroll
     for (int t = 0; t < NA; ++t) v[t] = ds_read16(fa[t] + so);
-    constexpr int NB = NHALF ? 2 : 4;
 #pragma unroll
     for (int t = 0; t < NB; ++t) v[NA + t] = ds_read16(fb[t] + so);
     if constexpr (NORM) {
 #pragma unroll
-      for (int t = 0; t < NB; ++t) {  // 8 floats at the k of fragment t's step
+      for (int t = 0; t < NB; ++t) {
         const int s2 = NHALF ? 2 * t + hi : t;
-        const unsigned wa = fw + (unsigned)(k0 + s2 * (F8 ? 8 : 32)) * 4u;
-        v[NA + NB + 2 * t] = ds_read16(wa);
-        v[NA + NB + 2 * t + 1] = ds_read16(wa + 16u);
+        const int kl = F8 ? 32 * g + 8 * s2 : 32 * s2 + 8 * g;  // fragment t's first k in the unit
+        if constexpr (WS) {
+          v[NA + NB + t] = ds_read16(ring0 + so + (unsigned)(WOFF + kl / 8) * 16u);
+        } else {
+          const unsigned wa = fwl + (unsigned)(k0 + kl) * 4u;
+          v[NA + NB + 2 * t] = ds_read16(wa);
+          v[NA + NB + 2 * t + 1] = ds_read16(wa + 16u);
+        }
       }
     }
     wait_lds_all(v);
+    auto normed = [&](int t) {
+      if constexpr (WS)
+        return norm_frag_w<T>(v[NA + t], rinv, v[NA + NB + t]);
+      else
+        return norm_frag<T>(v[NA + t], rinv, v[NA + NB + 2 * t], v[NA + NB + 2 * t + 1]);
+    };
     u32x4 b[4];
     if constexpr (NHALF) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
-        b[2 * p] = norm_frag<T>(v[NA + p], rinv, v[NA + 2 + 2 * p], v[NA + 3 + 2 * p]);
+        b[2 * p] = normed(p);
         b[2 * p + 1] = mirror16(b[2 * p]);
       }
     } else {
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         if constexpr (NORM)
-          b[s2] = norm_frag<T>(v[NA + s2], rinv, v[NA + 4 + 2 * s2], v[NA + 5 + 2 * s2]);
+          b[s2] = normed(s2);
         else
           b[s2] = v[NA + s2];
       }
@@ -290,13 +329,13 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   if constexpr (EPI == EPI_PLAIN) tep = tile_epi_loads<F8>(e, wscale, wrow[0], lane, n0, M, N);
   if constexpr (NORM) {
     float* wl = norm_lds;
-    float* inv = norm_lds + units * kUnit;
-    norm_prologue<T, BR, true, NW * kWave>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps, rq,
-                                           [&] {
-                                             for (int j = 0; j < pre; ++j) issue(j);
-                                           });
+    float* inv = norm_lds + (WS ? 0 : units * kUnit);
+    norm_prologue<T, BR, true, NW * kWave, !WS>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps,
+                                                rq, [&] {
+                                                  for (int j = 0; j < pre; ++j) issue(j);
+                                                });
     rinv = inv[NHALF ? hrow : rb];
-    fw = lds_addr(wl) + (unsigned)(g * (F8 ? 32 : 8)) * 4u;
+    fwl = lds_addr(wl);
   } else {
     for (int j = 0; j < pre; ++j) issue(j);
   }
@@ -335,14 +374,15 @@ struct FoldNorm {
   RowSq sq = {nullptr, 0};  // the producer's row sums of squares of x, if it wrote them
 };
 
-template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
-int launch_dma(unsigned blocks, void* y, const void* x, const void* w, const float* ws, int M,
-               int N, int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
-               const Rope& r, const FoldNorm& fn, hipStream_t st) {
-  constexpr size_t lds = dma_lds(NW, D, BR, sizeof(W)) + (EPI == EPI_ROPE ? kTileAngles * sizeof(float) : 0);
+template <typename T, typename W, int NW, int D, int BR, int EPI, int MODE>
+int launch_dma_mode(unsigned blocks, void* y, const void* x, const void* w, const float* ws, int M,
+                    int N, int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+                    const Rope& r, const FoldNorm& fn, hipStream_t st) {
+  constexpr size_t lds = dma_lds(NW, D, BR, sizeof(W), MODE == NORM_STREAMED) +
+                         (EPI == EPI_ROPE ? kTileAngles * sizeof(float) : 0);
   if constexpr (lds <= kMaxLds) {
-    const size_t dyn = NORM ? norm_dma_lds(K) : 0;
-    auto kernel = gemv_mfma_dma_kernel<T, W, NW, D, BR, EPI, NORM>;
+    const size_t dyn = MODE ? norm_dma_lds(K, MODE) : 0;
+    auto kernel = gemv_mfma_dma_kernel<T, W, NW, D, BR, EPI, MODE>;
     if (lds + dyn > kMaxLds)
       return set_error(FD_EUNSUPPORTED, "K too large for the folded RMSNorm's LDS stage");
     if (!allow_lds(kernel, dyn))
@@ -353,6 +393,24 @@ int launch_dma(unsigned blocks, void* y, const void* x, const void* w, const flo
     return FD_OK;
   }
   return set_error(FD_EINVAL, "MFMA tile beyond the LDS of a CU");
+}
+
+// NORM: the norm weight streams with the units when it has the activations'
+// dtype (one 16-byte read per B fragment, nothing staged before the first unit),
+// else the prologue stages it as float32.
+template <typename T, typename W, int NW, int D, int BR, int EPI, bool NORM>
+int launch_dma(unsigned blocks, void* y, const void* x, const void* w, const float* ws, int M,
+               int N, int K, int64_t sxm, int64_t swn, int64_t sym, int64_t syn, const Epi& e,
+               const Rope& r, const FoldNorm& fn, hipStream_t st) {
+  if constexpr (NORM) {
+    if (fn.dtype == (std::is_same<T, f16>::value ? FD_F16 : FD_BF16))
+      return launch_dma_mode<T, W, NW, D, BR, EPI, NORM_STREAMED>(blocks, y, x, w, ws, M, N, K, sxm, swn, sym,
+                                                                  syn, e, r, fn, st);
+    return launch_dma_mode<T, W, NW, D, BR, EPI, NORM_STAGED>(blocks, y, x, w, ws, M, N, K, sxm, swn, sym, syn,
+                                                              e, r, fn, st);
+  }
+  return launch_dma_mode<T, W, NW, D, BR, EPI, NORM_NONE>(blocks, y, x, w, ws, M, N, K, sxm, swn, sym, syn, e, r,
+                                                          fn, st);
 }
 
 template <typename T, typename W, int NW, int D, int EPI, bool NORM>

@@ -164,8 +164,9 @@ struct RowSq {
 // rounds after after_loads(). H % 8 == 0; `scratch` holds kMaxWaves *
 // pow2_ceil(MMAX) floats. Ends with a barrier (wl and inv are then visible).
 // FROM_X false: only the RowSq form is compiled (rq.p must be set), which keeps
-// the x passes' registers out of a kernel that never runs them.
-template <typename T, int MMAX, bool FROM_X, int NTMAX, typename AfterLoads>
+// the x passes' registers out of a kernel that never runs them. STAGE false:
+// the caller reads the norm weight itself; wl is left untouched.
+template <typename T, int MMAX, bool FROM_X, int NTMAX, bool STAGE = true, typename AfterLoads>
 __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scratch, const void* nwp,
                                               int nw_dtype, const T* x, int64_t sxm, int M, int H,
                                               int hp, float eps, const RowSq& rq, AfterLoads&& after_loads) {
@@ -180,19 +181,23 @@ __device__ __forceinline__ void norm_prologue(float* wl, float* inv, float* scra
   const int wchunks = H / (nw_dtype == FD_F32 ? 4 : 8);  // 16-byte chunks of the weight
   const u32x4* wsrc = static_cast<const u32x4*>(nwp);
   u32x4 wr[WR];
-#pragma unroll
-  for (int i = 0; i < WR; ++i) {
-    const int c = tid + i * nt;
-    wr[i] = wsrc[c < wchunks ? c : 0];
-  }
-  auto stage_w = [&]() {
+  if constexpr (STAGE) {
 #pragma unroll
     for (int i = 0; i < WR; ++i) {
       const int c = tid + i * nt;
-      if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
+      wr[i] = wsrc[c < wchunks ? c : 0];
     }
-    for (int c = tid + WR * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
-    for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
+  }
+  auto stage_w = [&]() {
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int i = 0; i < WR; ++i) {
+        const int c = tid + i * nt;
+        if (c < wchunks) store_norm_chunk(wl, wr[i], c, nw_dtype);
+      }
+      for (int c = tid + WR * nt; c < wchunks; c += nt) store_norm_chunk(wl, wsrc[c], c, nw_dtype);
+      for (int k = H + tid; k < hp; k += nt) wl[k] = 0.f;
+    }
   };
   float ss[MP];
 #pragma unroll
@@ -311,6 +316,40 @@ __device__ __forceinline__ u32x4 norm_frag(const u32x4& raw, float inv, const u3
     o[i] = from_f32<T>(to_f32(h[i]) * inv * wa[i]);
     o[i + 4] = from_f32<T>(to_f32(h[i + 4]) * inv * wb[i]);
   }
+  return __builtin_bit_cast(u32x4, o);
+}
+
+// a * w in float32 for the low / high f16 of the packed pair `w`: the same
+// v_fma_mix_f32 form (the f16 converted exactly, the product rounded once).
+__device__ __forceinline__ float mul_f32_lo_f16(float a, unsigned w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w));
+  return r;
+}
+__device__ __forceinline__ float mul_f32_hi_f16(float a, unsigned w) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, neg(0) op_sel:[0,1,0] op_sel_hi:[0,1,0]" : "=v"(r) : "v"(a), "v"(w));
+  return r;
+}
+
+// norm_frag with the 8 norm weights in T (`wt`, exact in float32): the same
+// float32 products, so the same rounded results.
+template <typename T>
+__device__ __forceinline__ u32x4 norm_frag_w(const u32x4& raw, float inv, const u32x4& wt) {
+  if constexpr (std::is_same<T, f16>::value) {
+    f16x8 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      o[2 * j] = (f16)mul_f32_lo_f16(mul_lo_f16(raw[j], inv), wt[j]);
+      o[2 * j + 1] = (f16)mul_f32_hi_f16(mul_hi_f16(raw[j], inv), wt[j]);
+    }
+    return __builtin_bit_cast(u32x4, o);
+  }
+  typedef typename Vec8<T>::type V8;
+  const V8 h = __builtin_bit_cast(V8, raw), wv = __builtin_bit_cast(V8, wt);
+  V8 o;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(to_f32(h[i]) * inv * to_f32(wv[i]));
   return __builtin_bit_cast(u32x4, o);
 }
 

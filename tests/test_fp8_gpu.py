@@ -448,6 +448,20 @@ def test_pre_attn_qkv_fp8_llama3_8b(dtype, m):
     torch.testing.assert_close(y[:1].float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [5, 8, 12])
+@pytest.mark.parametrize("nw_dtype", ["act", torch.float32])
+def test_pre_attn_qkv_fp8_ragged_hidden(dtype, m, nw_dtype):
+    """E4M3 QKV over a hidden width with a partial last K unit (272), the norm
+    weight streamed (activations' dtype) or staged (float32)."""
+    hidden, nw, q, s, qn, sn, b, cos, sin, rc = qkv_case(m, 272, 4, 2, 64, dtype, seed=95 + m, bias=True)
+    if nw_dtype != "act":
+        nw = nw.to(nw_dtype)
+    y = qkv_run(hidden, nw, q, s, b, cos, sin, rc)
+    ref = qkv_oracle(hidden, nw, qn, sn, b, cos, sin, rc, dtype)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
 @pytest.mark.parametrize("m", [2, 8])
 def test_pre_attn_qkv_fp8_plan_reuse(m):
     """A second call with the same argument signature (the cached plan) on new

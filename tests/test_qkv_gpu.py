@@ -206,6 +206,22 @@ def test_pre_attn_qkv_rejects():
         fd.pre_attn_qkv(hd, nwd, wd, cd, sd, rope_cols=rc, kind="mfma")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [5, 8, 12])
+@pytest.mark.parametrize("nw_dtype", ["act", torch.float32])
+def test_pre_attn_qkv_ragged_hidden(dtype, m, nw_dtype):
+    """A hidden width that is not a whole number of 128-wide K units (264): the
+    last unit's activations and norm weights past H read as zero, whether the
+    norm weight streams with the units (the activations' dtype) or is staged as
+    float32."""
+    hidden, nw, w, b, cos, sin, rc = case(m, 264, 4, 2, 64, dtype, seed=90 + m, bias=True)
+    if nw_dtype != "act":
+        nw = nw.to(nw_dtype)
+    y = run(hidden, nw, w, b, cos, sin, rc, kind="dot")
+    ref = oracle(hidden, nw, w, b, cos, sin, rc, dtype)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
 @pytest.mark.parametrize("m", [2, 8])
 def test_pre_attn_qkv_plan_reuse(m):
     """Calls that share an argument signature reuse one cached launch plan: new
