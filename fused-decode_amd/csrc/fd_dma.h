@@ -327,7 +327,45 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
   if constexpr (EPI == EPI_ROPE) ang = angle_loads<APER>(rp, tr, M, wrow[0]);
   TileEpi tep{};
   if constexpr (EPI == EPI_PLAIN) tep = tile_epi_loads<F8>(e, wscale, wrow[0], lane, n0, M, N);
-  if constexpr (NORM) {
+  bool wave_sums = false;
+  if constexpr (WS && !F8) wave_sums = rq.p != nullptr;
+  if (wave_sums) {
+    // streamed norm weight and the producer's row sums: each wave adds all the
+    // tiles' sums itself (its lanes take tiles lane, lane + 64, ...), so no
+    // workgroup barrier stands between the sums and the first unit (fp16/bf16
+    // weights, QKV at M=8: 14.0 -> 13.7 us; with E4M3 weights, whose units
+    // arrive twice as fast, the four waves' extra reads of the sums cost more:
+    // 11.5 -> 11.7 us, so those keep the workgroup prologue)
+    constexpr int MP = pow2_ceil(BR), MQ = BR / 4, TQ = 4;
+    float ss[MP];
+#pragma unroll
+    for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+    f32x4 q[TQ][MQ];
+    auto tile_rows = [&](int t, f32x4 (&d)[MQ]) {
+      const f32x4* src = reinterpret_cast<const f32x4*>(rq.p + (int64_t)(t < rq.parts ? t : 0) * 16);
+#pragma unroll
+      for (int i = 0; i < MQ; ++i) d[i] = src[i];
+    };
+    auto add_tile = [&](const f32x4 (&d)[MQ]) {
+#pragma unroll
+      for (int m = 0; m < BR; ++m) ss[m] += d[m / 4][m % 4];
+    };
+#pragma unroll
+    for (int i = 0; i < TQ; ++i) tile_rows(lane + i * kWave, q[i]);
+    for (int j = 0; j < pre; ++j) issue(j);  // behind the sums' loads, which complete first
+#pragma unroll
+    for (int i = 0; i < TQ; ++i)
+      if (lane + i * kWave < rq.parts) add_tile(q[i]);
+    for (int t = lane + TQ * kWave; t < rq.parts; t += kWave) {
+      tile_rows(t, q[0]);
+      add_tile(q[0]);
+    }
+    butterfly_sum<MP>(ss, lane);  // lane l: the sum of row butterfly_index<MP>(l)
+    const int row = butterfly_index<MP>(lane);
+    const float il = row < M ? rsqrtf(ss[0] / (float)K + eps) : 0.f;
+    const int want = (NHALF ? hrow : rb) * (kWave / MP);  // a lane holding this lane's row
+    rinv = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(want << 2, __builtin_bit_cast(int, il)));
+  } else if constexpr (NORM) {
     float* wl = norm_lds;
     float* inv = norm_lds + (WS ? 0 : units * kUnit);
     norm_prologue<T, BR, true, NW * kWave, !WS>(wl, inv, inv + 16, nwp, nw_dtype, x, sxm, M, K, units * kUnit, eps,
