@@ -210,7 +210,9 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
  * multiple of head_dim (0: no rotation); this build needs head_dim % 16 == 0 and
  * H % 8 == 0 (FD_EUNSUPPORTED otherwise: compose fd_rms_norm, fd_linear, fd_rope).
  * With kind FD_KIND_DOT from M = 5 the projection runs on MFMA with the RMSNorm
- * folded into the kernel (H up to about 30,000); below that, or with
+ * folded into the kernel (any H when norm_w has act_dtype, which streams with
+ * the weights; another norm_w dtype is staged in LDS as float32, which takes H
+ * up to about 22,000, FD_EUNSUPPORTED beyond); below that, or with
  * FD_KIND_SIMT, a SIMT kernel normalises in its prologue. `normed` is unused at
  * every M and may be NULL (it stays in the signature for callers written against
  * earlier builds).

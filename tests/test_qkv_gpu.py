@@ -271,6 +271,33 @@ def test_pre_attn_qkv_entry_point_normed_and_status():
     assert bool((normed == 7.0).all())
 
 
+def test_pre_attn_qkv_wide_hidden_streams_the_norm_weight():
+    """H = 32768 at 8 rows: a norm weight in the activations' dtype streams with
+    the weight tiles (one launch at any H), a float32 one is staged in LDS and
+    does not fit (FD_EUNSUPPORTED, so the Python operator composes); both match
+    the oracle."""
+    import fused_decode as fd
+    from fused_decode import _lib as L
+
+    h = 32768
+    hidden, nw, w, b, cos, sin, rc = case(8, h, 2, 1, 64, torch.float16, seed=14)
+    hd, wd, cd, sd = (t.to(DEV) for t in (hidden, w, cos, sin))
+    n = w.shape[0]
+    st = torch.cuda.current_stream().cuda_stream
+    for nw_t, code, want in ((nw, L.FD_F16, L.FD_OK), (nw.float(), L.FD_F32, L.FD_EUNSUPPORTED)):
+        nwd = nw_t.to(DEV)
+        y = torch.zeros(8, n, device=DEV, dtype=torch.float16)
+        status = L.lib().fd_pre_attn_qkv(y.data_ptr(), None, hd.data_ptr(), nwd.data_ptr(), code, wd.data_ptr(),
+                                         None, L.FD_F16, cd.data_ptr(), sd.data_ptr(), L.FD_F32, 64, 8, h, n, rc,
+                                         64, 1e-5, L.FD_KIND_DOT, L.FD_F16, st)
+        assert status == want
+        ref = torch.from_numpy(oracle(hidden, nw_t, w, b, cos, sin, rc, torch.float16))
+        if status == L.FD_OK:
+            torch.testing.assert_close(y.float().cpu(), ref, **tol(torch.float16))
+        out = fd.pre_attn_qkv(hd, nwd, wd, cd, sd, 1e-5, rope_cols=rc, kind="dot")
+        torch.testing.assert_close(out.float().cpu(), ref, **tol(torch.float16))
+
+
 @pytest.mark.parametrize("m", [1, 3, 8])
 def test_decode_step_fused_matches_composed_and_graph(m):
     from fused_decode.decode_step import DecodeStep
