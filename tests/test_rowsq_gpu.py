@@ -145,8 +145,12 @@ def test_post_attn_mlp_sumsq_ragged_widths(weights, m):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m", [5, 8, 16])
-def test_pre_attn_qkv_sumsq_matches_oracle(dtype, m):
-    """The QKV kernel's norm from a producer's sums (MLP down projection)."""
+@pytest.mark.parametrize("nw_kind", ["other", "act"])
+def test_pre_attn_qkv_sumsq_matches_oracle(dtype, m, nw_kind):
+    """The QKV kernel's norm from a producer's sums (MLP down projection), with
+    a norm weight of the other 16-bit dtype (staged in LDS, the workgroup adds
+    the sums) and of the activations' dtype (streamed with the units, each wave
+    adds the sums)."""
     from fused_decode.rowsq import post_attn_mlp_sumsq, pre_attn_qkv_sumsq, sumsq_buffer
 
     h, i, d, heads, kv = 256, 512, 64, 4, 2
@@ -154,7 +158,8 @@ def test_pre_attn_qkv_sumsq_matches_oracle(dtype, m):
     x = rnd(m, h, seed=30 + m, dtype=dtype)
     nw_mlp = rnd(h, seed=31, dtype=dtype, scale=0.1, mean=1.0)
     wgu, wd = rnd(2 * i, h, seed=32, dtype=dtype, scale=h ** -0.5), rnd(h, i, seed=33, dtype=dtype, scale=i ** -0.5)
-    nw = rnd(h, seed=34, dtype=torch.bfloat16 if dtype == torch.float16 else torch.float16, scale=0.3, mean=1.0)
+    other = torch.bfloat16 if dtype == torch.float16 else torch.float16
+    nw = rnd(h, seed=34, dtype=other if nw_kind == "other" else dtype, scale=0.3, mean=1.0)
     w = rnd(n, h, seed=35, dtype=dtype, scale=h ** -0.5)
     b = rnd(n, seed=36, dtype=torch.float32, scale=0.5)
     pos = torch.arange(700, 700 + m, dtype=torch.float64)
