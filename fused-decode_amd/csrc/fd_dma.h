@@ -28,12 +28,15 @@
 // their rounded outputs (cos/sin staged through LDS, see angle_loads). E4M3 sums are
 // multiplied by the row's channel scale first.
 //
-// With NORM, x is the raw activation and the kernel applies the RMSNorm itself:
-// the norm weight (float32) and the rows' inverse RMS are staged in dynamic LDS
-// (norm_dma_lds bytes) by a prologue whose loads go out just before the first
-// units' DMAs and which runs while those are in flight, and every B fragment is
-// normalised after its LDS read (up to 8 rows in the half-B form: each lane
-// normalises two fragments and swaps them with its row-mirror partner).
+// With NORM, x is the raw activation and the kernel applies the RMSNorm itself.
+// A prologue whose loads go out just before the first units' DMAs derives the
+// rows' inverse RMS, from x or from the producer's row sums (with those and a
+// streamed weight, in every wave, with no workgroup barrier). The norm weight
+// streams with the units when it has the activations' dtype (NORM_STREAMED), or
+// the prologue stages it in dynamic LDS as float32 (NORM_STAGED, norm_dma_lds
+// bytes). Every B fragment is normalised after its LDS read (up to 8 rows in the
+// half-B form: each lane normalises two fragments and swaps them with its
+// row-mirror partner).
 #pragma once
 
 #include "fd_gemv.h"
