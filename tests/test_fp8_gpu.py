@@ -304,7 +304,7 @@ def test_fp8_rejects():
         fd.linear_decode_fp8(x[:, :32], q, s)
 
 
-@pytest.mark.parametrize("m", [2, 8])
+@pytest.mark.parametrize("m", [2, 8, 16])
 def test_decode_step_fp8_matches_oracle_and_graph(m):
     """The fp8 layer below and above the MFMA switch at 5 rows."""
     from fused_decode.decode_step import HEAD_DIM, DecodeStep

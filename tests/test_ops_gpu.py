@@ -581,6 +581,24 @@ def test_decode_step_small_matches_oracle_and_graph(m, fused):
         _ = (ds.x_in.float() * 2).sum().item()  # unrelated eager work between replays
 
 
+@pytest.mark.parametrize("m", [1, 5, 8, 16])
+def test_decode_step_small_bf16_matches_oracle(m):
+    """The fused layer in bfloat16 (the norm weights bfloat16 too, so from 5 rows
+    the QKV streams its norm weight and adds the producer's row sums per wave, and
+    the gate/up normalises from them) against the oracle, then a graph replay."""
+    from fused_decode.decode_step import DecodeStep
+
+    ds = DecodeStep(m=m, layers=2, h=256, i=512, seed=9, dtype=torch.bfloat16)
+    eager = ds.step().clone()
+    qkv = ds.qkv.clone()
+    ref, ref_qkv = _oracle_decode_step(ds, "bf16")
+    check(eager, ref, torch.bfloat16, "linear")
+    check(qkv, ref_qkv, torch.bfloat16, "linear")
+    ds.capture()
+    ds.out.zero_()
+    torch.testing.assert_close(ds.replay(), eager, rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("m", [1, 8])
 def test_decode_step_llama3_8b_matches_oracle(m):
     """Two layers at full Llama-3-8B widths (H=4096, 32 q + 8 kv heads of 128,
