@@ -24,28 +24,29 @@ def L():
     return lib
 
 
-def _case(m, h, i, seed):
+def _case(m, h, i, seed, dtype=torch.float16):
     g = torch.Generator().manual_seed(seed)
-    r = lambda *s, scale=1.0, mean=0.0: (torch.randn(*s, generator=g) * scale + mean).half()  # noqa: E731
+    r = lambda *s, scale=1.0, mean=0.0: (torch.randn(*s, generator=g) * scale + mean).to(dtype)  # noqa: E731
     return r(m, h), r(h, scale=0.1, mean=1.0), r(2 * i, h, scale=h ** -0.5), r(h, i, scale=i ** -0.5)
 
 
-def _run_both(L, m, h, i, kind, seed):
-    hidden, nw, wgu, wd = _case(m, h, i, seed)
+def _run_both(L, m, h, i, kind, seed, dtype=torch.float16):
+    hidden, nw, wgu, wd = _case(m, h, i, seed, dtype)
     hd, nwd, wgud, wdd = (t.to(DEV) for t in (hidden, nw, wgu, wd))
+    code = L.DTYPE_CODE[dtype]
     st = torch.cuda.current_stream().cuda_stream
-    y_ref = torch.empty(m, h, device=DEV, dtype=torch.float16)
-    mid = torch.empty(m, i, device=DEV, dtype=torch.float16)
+    y_ref = torch.empty(m, h, device=DEV, dtype=dtype)
+    mid = torch.empty(m, i, device=DEV, dtype=dtype)
     L.check("fd_post_attn_mlp", L.lib().fd_post_attn_mlp(
-        y_ref.data_ptr(), mid.data_ptr(), hd.data_ptr(), nwd.data_ptr(), L.FD_F16, wgud.data_ptr(),
-        wdd.data_ptr(), m, h, i, 1e-5, kind, L.FD_F16, st))
-    y = torch.full((m, h), float("nan"), device=DEV, dtype=torch.float16)
+        y_ref.data_ptr(), mid.data_ptr(), hd.data_ptr(), nwd.data_ptr(), code, wgud.data_ptr(),
+        wdd.data_ptr(), m, h, i, 1e-5, kind, code, st))
+    y = torch.full((m, h), float("nan"), device=DEV, dtype=dtype)
     L.check("fd_post_attn_mlp_noalloc", L.lib().fd_post_attn_mlp_noalloc(
-        y.data_ptr(), hd.data_ptr(), nwd.data_ptr(), L.FD_F16, wgud.data_ptr(), wdd.data_ptr(),
-        m, h, i, 1e-5, kind, L.FD_F16, st))
+        y.data_ptr(), hd.data_ptr(), nwd.data_ptr(), code, wgud.data_ptr(), wdd.data_ptr(),
+        m, h, i, 1e-5, kind, code, st))
     torch.cuda.synchronize()
     f = lambda t: t.float().numpy()  # noqa: E731
-    ref = O.post_attn_mlp(f(hidden), f(nw), f(wgu), f(wd), 1e-5, "f16")
+    ref = O.post_attn_mlp(f(hidden), f(nw), f(wgu), f(wd), 1e-5, "f16" if dtype == torch.float16 else "bf16")
     return y, y_ref, ref, (hd, nwd, wgud, wdd)
 
 
@@ -60,6 +61,20 @@ def test_noalloc_matches_the_allocating_entry_point(L):
     y, y_ref, ref, _ = _run_both(L, 3, 256, 512, L.FD_KIND_SIMT, seed=2)
     torch.testing.assert_close(y, y_ref, rtol=0, atol=0)
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), rtol=2e-2, atol=2e-2)
+
+
+def test_noalloc_bfloat16(L):
+    """bfloat16 activations and weights, two calls in a row (8 rows on the MFMA
+    route, then 2 rows on the SIMT route), against the allocating entry point;
+    oracle tolerance for bfloat16 GEMVs rtol=atol=4e-2 (tests/test_ops.py:27-35)."""
+    print("[noalloc] bf16 m=8 h=512 i=2048 dot", flush=True)
+    y, y_ref, ref, _ = _run_both(L, 8, 512, 2048, L.FD_KIND_DOT, seed=4, dtype=torch.bfloat16)
+    torch.testing.assert_close(y, y_ref, rtol=0, atol=0)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), rtol=4e-2, atol=4e-2)
+    print("[noalloc] bf16 m=2 h=256 i=384 simt", flush=True)
+    y, y_ref, ref, _ = _run_both(L, 2, 256, 384, L.FD_KIND_SIMT, seed=5, dtype=torch.bfloat16)
+    torch.testing.assert_close(y, y_ref, rtol=0, atol=0)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), rtol=4e-2, atol=4e-2)
 
 
 def test_noalloc_llama3_8b_widths_and_graph_capture(L):
