@@ -3,6 +3,8 @@
 // launch-shape helpers.
 #pragma once
 
+#include <atomic>
+
 #include "fd_device.h"
 #include "fd_host.h"
 
@@ -943,19 +945,20 @@ inline bool allow_lds(F kernel, size_t bytes) {
                              (int)bytes) == hipSuccess;
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; host threads may race
+// to fill an entry, and all of them store the same value).
 inline int device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (!cus) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         cus <= 0)
       cus = 256;
-    cached[dev] = cus;
+    cached[dev].store(cus, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cus;
 }
 
 // Dynamic LDS of a fused kernel: the staged activations and the reduction scratch.
