@@ -5,7 +5,9 @@
 // ... of a sweep that starts at the workgroup's XCD offset (sweep_unit). A unit
 // is 128 K elements: the 16-row weight tile (4 KiB of fp16/bf16, 2 KiB of E4M3
 // codes) and the BR-row activation tile (BR = M rounded up to 4, 8 or 16),
-// moved by global_load_lds_dwordx4 instructions into one of the wave's D ring
+// moved by global_load_lds_dwordx4 instructions (nontemporal for the weights,
+// which are read once; cached for the activations, which every workgroup
+// re-reads) into one of the wave's D ring
 // slots, D units in flight. Lane L of an instruction
 // fills ring entry 16*L of it; the lane picks its source chunk so that the slot
 // holds every row XOR-swizzled (chunk c of row r at position c ^ (r mod
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
     u32x4* slot = ring[wave][j % D];
     if (k0 + kUnit <= K) {  // a whole unit (every unit but a K tail): no clamps
 #pragma unroll
-      for (int i = 0; i < G.aops; ++i) dma16(wrow[i] + k0 + wch[i], slot + i * kWave);
+      for (int i = 0; i < G.aops; ++i) dma16_nt(wrow[i] + k0 + wch[i], slot + i * kWave);
 #pragma unroll
       for (int i = 0; i < BR / 4; ++i) dma16(xrow[i] + k0 + xch[i], slot + G.ae + i * kWave);
       if constexpr (WS)
@@ -215,7 +217,7 @@ __global__ __launch_bounds__(NW * kWave) void gemv_mfma_dma_kernel(
 #pragma unroll
       for (int i = 0; i < G.aops; ++i) {
         const int k = k0 + wch[i];
-        dma16(wrow[i] + (k < K ? k : 0), slot + i * kWave);
+        dma16_nt(wrow[i] + (k < K ? k : 0), slot + i * kWave);
       }
 #pragma unroll
       for (int i = 0; i < BR / 4; ++i) {
