@@ -21,9 +21,15 @@ roofline: the dominant kernel, the fused RMSNorm + gate/up GEMV + SwiGLU
 launch, timed alone with HIP events on the stream it is launched on;
 achieved = its algorithmic bytes / its average duration.
 
-ops: one compact row per norm, SwiGLU, RoPE and decode-GEMV benchmark
-configuration (device and eager microseconds, GB/s, % of the copy roof and of
-8 TB/s, and the largest deviation from the reference's float32 formulas).
+mlp: the same post_attn_mlp timings in fp16 and bf16 at M = 1 and 8.
+
+ops: every norm, SwiGLU, RoPE and decode-GEMV benchmark configuration (device
+and eager microseconds, GB/s, % of the copy roof and of 8 TB/s, and the
+largest deviation from the reference's float32 formulas), one full row each,
+is written to --ops-out; the headline line carries a summary of them (device
+microseconds, % of the copy roof and of the same-size roof kernel, max error)
+and stays under LINE_LIMIT bytes, so a reader that keeps only the last 8 KB of
+stdout still sees all of it.
 
 cpu_baseline: the reference's eager formula of the same block
 (src/fused_decode/bench.py:395-398: F.rms_norm, F.linear, F.silu, F.linear + residual)
@@ -61,6 +67,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-decode-step", action="store_true", help="skip the 32-layer decode step")
     ap.add_argument("--no-ops", action="store_true", help="skip the per-op block")
+    ap.add_argument("--ops-out", default="gpurun_out/bench_ops.json",
+                    help="file for the full per-op rows (the headline line carries their summary)")
     return ap.parse_args()
 
 
@@ -203,6 +211,13 @@ def read_roof_gbs(torch) -> float:
     return n / (us * 1e-6) / 1e9
 
 
+OPS_NOTE = ("dev_us: one HIP graph over rotated buffer sets (HBM reads); eager_us: allocating calls back to "
+            "back; gbs and pct_* from dev_us and the reference's useful bytes; same_size_us: the roof kernel "
+            "moving the op's bytes the same way (fd_copy of half each way for the norms and RoPE, fd_triad for "
+            "SwiGLU, fd_read of all for the GEMVs) timed like dev_us, pct_same_size = same_size_us / dev_us; "
+            "max_abs_vs_fp32 against the reference's formulas in float32, rounded once")
+
+
 def pmc_traffic() -> int | None:
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE passes (profiles/mlp_gate_up_m1_pmc.md), or None."""
@@ -274,6 +289,81 @@ def progress(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+LINE_LIMIT = 6000  # bytes: the headline line stays well inside an 8 KB stdout window
+_DT = {"float16": "f16", "bfloat16": "bf16"}
+
+
+def headline(*, steps: int, warmup: int, kind: str, mlp: dict, gate_us: float, roof: float, read_roof: float,
+             traffic: int | None, decode: dict | None = None, ops_rows: list | None = None,
+             ops_path: str | None = None, cpu: dict | None = None) -> dict:
+    """The one JSON object bench.py prints last. ``mlp[dtype][m]`` holds the
+    post_attn_mlp timings (eager_us, graph_us, graph_per_call_us) for dtype
+    "f16"/"bf16" and m 1/8; ``value`` is fp16 M=1 eager. The full per-op rows go
+    to ``ops_path``; the line carries their summary (fused_decode.bench.summarize_ops)."""
+    us1 = mlp["f16"][1]["eager_us"]
+    weights = 3 * H * I * 2
+    mlp_bytes = (3 * H * I + 2 * 1 * H + H) * 2
+    gate_bytes = (2 * I * H + 1 * H + H + 1 * I) * 2  # weights, hidden, norm_w, mid write
+    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
+    line = {
+        "metric": "post_attn_mlp us @M=1 (Llama-3-8B widths); M=8 in m8_us",
+        "value": round(us1, 3),
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(us1 / 1000.0, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: random-init weights ~N(0,1/sqrt(K)), hidden ~N(0,1), 4 rotating weight sets",
+        "config": {
+            "workload": "post_attn_mlp Llama-3-8B H=4096 I=14336 M=1, fp16, cold weights (4 rotating sets)",
+            "kind": kind,
+            "m": 1,
+        },
+        "m8_us": round(mlp["f16"][8]["eager_us"], 3),
+        "mlp": {
+            "cols": "[eager_us, graph_us (one graph of 100 steps), graph_per_call_us (one graph per call)]",
+            **{dt: {f"m{m}": [round(r["eager_us"], 2), round(r["graph_us"], 2), round(r["graph_per_call_us"], 2)]
+                    for m, r in sorted(per_m.items())} for dt, per_m in mlp.items()},
+        },
+        "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
+        "copy_roof_gbs": round(roof, 1),
+        "read_roof_gbs": round(read_roof, 1),
+        "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
+        "target_us": round(1.25 * weights / (roof * 1e9) * 1e6, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mlp_gate_up (RMSNorm + gate/up GEMV + SwiGLU), M=1",
+            "achieved": round(gate_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+            "avg_us": round(gate_us, 3),
+            "algorithmic_bytes": gate_bytes,
+            "traffic": traffic,
+            "traffic_source": "profiles/mlp_gate_up_m1_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE, copy-calibrated)",
+        },
+    }
+    if decode is not None:
+        line["decode_step"] = decode
+    if ops_rows is not None:
+        from fused_decode.bench import summarize_ops
+
+        line["ops"] = summarize_ops(ops_rows)
+        line["ops_file"] = ops_path
+    if cpu is not None:
+        line["cpu_baseline"] = cpu
+    return line
+
+
+def render(line: dict) -> str:
+    """The headline as one compact JSON line."""
+    return json.dumps(line, separators=(",", ":"))
+
+
 def main() -> None:
     args = parse()
     if args.gpus != 1:
@@ -288,112 +378,73 @@ def main() -> None:
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda:0")
-    dtype = torch.float16
     kind = resolve_kind(None)
     roof = copy_roof_gbs(torch)
 
-    results = {}
-    for m in (1, 8):
-        sets = make_sets(torch, m, dtype, dev)
-        graph_us, graph_per_call_us = time_graph_steps(torch, fd, sets, args.steps, args.warmup, None)
-        results[m] = {
-            "graph_us": graph_us,
-            "graph_per_call_us": graph_per_call_us,
-            "eager_us": time_eager_steps(torch, fd, sets, args.steps, args.warmup, None),
-        }
-        if m == 1:
-            gate_us = time_gate_up_kernel(torch, lib(), sets, m, max(args.steps, 50), KIND_CODE[kind])
-        progress(f"post_attn_mlp M={m}: eager {results[m]['eager_us']:.2f} us, graph {results[m]['graph_us']:.2f} us, "
-                 f"one graph per call {results[m]['graph_per_call_us']:.2f} us")
-        del sets
-        torch.cuda.empty_cache()
+    mlp: dict = {}
+    gate_us = None
+    for dtype in (torch.float16, torch.bfloat16):
+        dt = _DT[str(dtype).replace("torch.", "")]
+        mlp[dt] = {}
+        for m in (1, 8):
+            sets = make_sets(torch, m, dtype, dev)
+            graph_us, graph_per_call_us = time_graph_steps(torch, fd, sets, args.steps, args.warmup, None)
+            r = mlp[dt][m] = {
+                "graph_us": graph_us,
+                "graph_per_call_us": graph_per_call_us,
+                "eager_us": time_eager_steps(torch, fd, sets, args.steps, args.warmup, None),
+            }
+            if m == 1 and dtype == torch.float16:
+                gate_us = time_gate_up_kernel(torch, lib(), sets, m, max(args.steps, 50), KIND_CODE[kind])
+            progress(f"post_attn_mlp {dt} M={m}: eager {r['eager_us']:.2f} us, graph {r['graph_us']:.2f} us, "
+                     f"one graph per call {r['graph_per_call_us']:.2f} us")
+            del sets
+            torch.cuda.empty_cache()
 
-    us1 = results[1]["eager_us"]
-    weights = 3 * H * I * 2
-    mlp_bytes = (3 * H * I + 2 * 1 * H + H) * 2
-    gate_bytes = (2 * I * H + 1 * H + H + 1 * I) * 2  # weights, hidden, norm_w, mid write
-    gate_gbs = gate_bytes / (gate_us * 1e-6) / 1e9
-    line = {
-        "metric": "post_attn_mlp us @M=1 (Llama-3-8B widths); M=8 in m8_us",
-        "value": round(us1, 3),
-        "unit": "us",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(us1 / 1000.0, 6),
-        "higher_is_better": False,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "fp16",
-        "data": "synthetic: random-init weights ~N(0,1/sqrt(K)), hidden ~N(0,1), 4 rotating weight sets",
-        "config": {
-            "workload": "post_attn_mlp Llama-3-8B H=4096 I=14336 M=1, fp16, cold weights (4 rotating sets)",
-            "kind": kind,
-            "m": 1,
-        },
-        "m8_us": round(results[8]["eager_us"], 3),
-        "graph_us": {"m1": round(results[1]["graph_us"], 3), "m8": round(results[8]["graph_us"], 3),
-                     "method": "one HIP graph holding 100 steps (25 rotations of the 4 weight sets), per step"},
-        "graph_per_call_us": {"m1": round(results[1]["graph_per_call_us"], 3),
-                              "m8": round(results[8]["graph_per_call_us"], 3),
-                              "method": "one HIP graph per call (the reference's _graph_time): each "
-                                        "hipGraphLaunch adds an idle gap before its first kernel"},
-        "mlp_gbs": round(mlp_bytes / (us1 * 1e-6) / 1e9, 1),
-        "copy_roof_gbs": round(roof, 1),
-        "read_roof_gbs": round(read_roof_gbs(torch), 1),
-        "pct_copy_roof": round(100.0 * mlp_bytes / (us1 * 1e-6) / 1e9 / roof, 1),
-        "target_us": round(1.25 * weights / (roof * 1e9) * 1e6, 2),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "mlp_gate_up (RMSNorm + gate/up GEMV + SwiGLU), M=1",
-            "achieved": round(gate_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-            "avg_us": round(gate_us, 3),
-            "algorithmic_bytes": gate_bytes,
-            "traffic": pmc_traffic(),
-            "traffic_source": "profiles/mlp_gate_up_m1_pmc.md (FETCH_SIZE x2.0 + WRITE_SIZE, copy-calibrated)",
-        },
-    }
+    decode = None
     if not args.no_decode_step:
         from fused_decode.decode_step import DecodeStep, time_step
 
-        line["decode_step"] = {}
+        decode = {"workload": "32-layer Llama-3-8B decode step minus attention, hipGraph, fp16; fused = "
+                              "pre_attn_qkv + O-proj + post_attn_mlp, unfused = the reference's operators, "
+                              "fp8 = fused with E4M3 weights; gbs over each form's weight bytes"}
         for m in (1, 8):
             for form in ("fused", "unfused", "fp8"):
-                ds = DecodeStep(m=m, layers=32, dtype=dtype, fused=form != "unfused",
+                ds = DecodeStep(m=m, layers=32, dtype=torch.float16, fused=form != "unfused",
                                 weights="fp8" if form == "fp8" else "fp16")
                 g_us = time_step(ds, 10, 2, graph=True)
                 key = f"m{m}" if form == "fused" else f"m{m}_{form}"
-                line["decode_step"][f"{key}_us"] = round(g_us, 1)
-                line["decode_step"][f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
-                line["decode_step"][f"{key}_launches_per_layer"] = ds.launches_per_layer
+                decode[f"{key}_us"] = round(g_us, 1)
+                decode[f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
+                decode[f"{key}_launches"] = ds.launches_per_layer
                 progress(f"decode step {key}: {g_us:.1f} us")
                 del ds
                 torch.cuda.empty_cache()
-        line["decode_step"]["workload"] = (
-            "32-layer Llama-3-8B decode step minus attention, hipGraph; fused = pre_attn_qkv + "
-            "O-proj with residual + post_attn_mlp, unfused = the reference's operators composed, "
-            "fp8 = the fused layer with E4M3 projection weights (gbs over its own weight bytes)")
+    ops_rows = None
     if not args.no_ops:
         from fused_decode.bench import ops_block
 
-        line["ops"] = ops_block(roof, log=lambda row: progress(
+        ops_rows = ops_block(roof, log=lambda row: progress(
             f"{row['op']} {row['shape']} {row['dtype']} {row.get('kind', '')}: dev {row['dev_us']} us, "
             f"eager {row['eager_us']} us, {row['pct_copy_roof']}% of copy roof, max_abs {row['max_abs_vs_fp32']:.3g}"))
-        line["ops_note"] = ("dev_us: one HIP graph over rotated buffer sets (HBM reads); eager_us: allocating calls "
-                            "back to back; gbs and pct_* from dev_us and the reference's useful bytes; "
-                            "same_size_us: the roof kernel moving the op's bytes the same way (fd_copy of half "
-                            "each way for the norms and RoPE, fd_triad for SwiGLU, fd_read of all for the GEMVs) "
-                            "timed like dev_us, "
-                            "pct_same_size = same_size_us / dev_us; "
-                            "max_abs_vs_fp32 against the reference's formulas in float32, rounded once")
+        out = Path(args.ops_out)
+        out.parent.mkdir(parents=True, exist_ok=True)
+        out.write_text(json.dumps({"note": OPS_NOTE, "copy_roof_gbs": roof, "rows": ops_rows}, indent=1))
+        progress(f"{len(ops_rows)} op rows written to {out}")
         torch.cuda.empty_cache()
+    cpu = None
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
+        cpu = cpu_baseline(torch, args.cpu_seconds)
         progress("cpu baseline done")
-    print(json.dumps(line), flush=True)
+    line = headline(steps=args.steps, warmup=args.warmup, kind=kind, mlp=mlp, gate_us=gate_us, roof=roof,
+                    read_roof=read_roof_gbs(torch), traffic=pmc_traffic(), decode=decode, ops_rows=ops_rows,
+                    ops_path=args.ops_out if ops_rows is not None else None, cpu=cpu)
+    text = render(line)
+    if len(text) > LINE_LIMIT:
+        progress(f"headline line is {len(text)} bytes (limit {LINE_LIMIT}): the ops summary is left out")
+        line.pop("ops", None)
+        text = render(line)
+    print(text, flush=True)
 
 
 if __name__ == "__main__":

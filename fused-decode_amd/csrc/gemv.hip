@@ -1108,6 +1108,23 @@ int scratch_ptr(int device, void** out) {
 }  // namespace
 }  // namespace fd
 
+extern "C" int fd_init(void) {
+  using namespace fd;
+  int count = 0;
+  const hipError_t e = hipGetDeviceCount(&count);
+  if (e == hipErrorNoDevice || (e == hipSuccess && count == 0)) {
+    (void)hipGetLastError();  // no GPU: nothing to set up
+    return FD_OK;
+  }
+  if (e != hipSuccess) return set_error(FD_ELAUNCH, "hipGetDeviceCount failed: %s", hipGetErrorString(e));
+  for (int d = 0; d < count && d < kMaxDevices; ++d) {
+    void* p = nullptr;
+    const int rc = scratch_ptr(d, &p);
+    if (rc != FD_OK) return rc;
+  }
+  return FD_OK;
+}
+
 extern "C" int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w,
                                         int norm_w_dtype, const void* w_gate_up,
                                         const void* w_down, int64_t M, int64_t H, int64_t I,

@@ -275,6 +275,116 @@ def output_like(name: str, ref: str) -> Rule:
     return like(name, ref, optional=True)
 
 
+# ------------------------------------------------- row-sum (sumsq) entry points
+#
+# The row-sum forms call C entry points that take bare pointers with no extents
+# and, for the MLP and QKV weights, no strides: every operand's layout is fixed
+# here, before any launch, so a mis-shaped tensor raises instead of becoming an
+# out-of-bounds read or write on the GPU.
+
+SUMSQ_MIN_ROWS = 5  # the MFMA kernels that write and read the sums run from this many rows
+
+
+def decode_rows(name: str, lo: int = SUMSQ_MIN_ROWS, hi: int = 16) -> Rule:
+    """A contiguous rank-2 ``[M, K]`` activation with ``lo <= M <= hi``."""
+
+    def rule(a: dict) -> None:
+        t = a[name]
+        if t.ndim != 2 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous [M, K] tensor, got shape {tuple(t.shape)} "
+                             f"strides {t.stride()}")
+        if not lo <= t.shape[0] <= hi:
+            raise ValueError(f"row sums of squares run on the MFMA kernels: {name} needs {lo} to {hi} rows, "
+                             f"got {t.shape[0]}")
+
+    return rule
+
+
+def unit_k_stride(name: str) -> Rule:
+    """A weight whose K (last) dim is dense: element stride 1."""
+
+    def rule(a: dict) -> None:
+        w = a[name]
+        if w.shape[-1] > 1 and w.stride(-1) != 1:
+            raise ValueError(f"{name} must have unit stride along K, got strides {w.stride()}")
+
+    return rule
+
+
+def dense(*names: str) -> Rule:
+    """Contiguous tensors (kernels that take no strides for them)."""
+
+    def rule(a: dict) -> None:
+        for name in names:
+            t = a.get(name)
+            if isinstance(t, torch.Tensor) and not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous, got shape {tuple(t.shape)} strides {t.stride()}")
+
+    return rule
+
+
+def matrix_for(name: str, ref: str, rows: Callable[[dict], int], cols: Callable[[dict], int], *,
+               optional: bool = False, dtypes=None) -> Rule:
+    """A contiguous ``[rows, cols]`` tensor on ``ref``'s device, in ``ref``'s dtype
+    (or one of ``dtypes``): an output, scratch or addend the kernel indexes as
+    dense rows."""
+
+    def rule(a: dict) -> None:
+        t, r = a.get(name), a[ref]
+        if t is None:
+            if optional:
+                return
+            raise ValueError(f"{name} is required")
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor, got {type(t).__name__}")
+        if t.device != r.device:
+            raise ValueError(f"{name} is on {t.device} but {ref} is on {r.device}")
+        ok = (r.dtype,) if dtypes is None else dtypes
+        if t.dtype not in ok:
+            raise TypeError(f"{name} must be {_names(ok)}, got {t.dtype}")
+        shape = (rows(a), cols(a))
+        if tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous {list(shape)} tensor, got shape {tuple(t.shape)} "
+                             f"strides {t.stride()}")
+
+    return rule
+
+
+def sums_buffer(name: str, ref: str, width: Callable[[dict], int], *, optional: bool = False) -> Rule:
+    """Float32 tile sums of squares for a ``width``-column activation: a
+    contiguous buffer of ``ceil(width / 16) * 16`` values on ``ref``'s device
+    (``sumsq_buffer``)."""
+
+    def rule(a: dict) -> None:
+        t = a.get(name)
+        if t is None:
+            if optional:
+                return
+            raise ValueError(f"{name} is required")
+        w = width(a)
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a tensor, got {type(t).__name__}")
+        if t.device != a[ref].device:
+            raise ValueError(f"{name} is on {t.device} but {ref} is on {a[ref].device}")
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.numel() != (w + 15) // 16 * 16:
+            raise ValueError(f"{name} must be a contiguous float32 tensor of ceil({w}/16)*16 values "
+                             f"(sumsq_buffer), got {t.dtype} shape {tuple(t.shape)}")
+
+    return rule
+
+
+def _m(ref: str) -> Callable[[dict], int]:
+    return lambda a: a[ref].shape[0]
+
+
+def _rows_of(weight: str) -> Callable[[dict], int]:
+    return lambda a: a[weight].shape[0]
+
+
+def _cols_of(weight: str) -> Callable[[dict], int]:
+    return lambda a: a[weight].shape[1]
+
+
 # ------------------------------------------------------------------ contract
 
 CONTRACT: dict[str, tuple[Rule, ...]] = {
@@ -304,6 +414,46 @@ CONTRACT: dict[str, tuple[Rule, ...]] = {
                          vector_for("norm_weight", "hidden", label="weight"), finite_eps(),
                          bias_for("bias", "hidden", "w_qkv")),
 }
+
+
+
+def dot_kind_if(*sums: str, name: str = "kind") -> Rule:
+    """The row sums come from the MFMA kernel, which kind "dot" selects: required
+    when any of the ``sums`` buffers is passed."""
+
+    def rule(a: dict) -> None:
+        if any(a.get(s) is not None for s in sums) and a[name] != "dot":
+            raise ValueError(f"row sums of squares come from the MFMA GEMV: kind must be 'dot', got {a[name]!r}")
+
+    return rule
+
+
+def _h(a: dict) -> int:
+    return a["hidden"].shape[1]
+
+
+_SUMSQ_LINEAR = (decode_rows("x"), unit_k_stride("weight"),
+                 matrix_for("out", "x", _m("x"), _rows_of("weight")),
+                 matrix_for("row_add", "x", _m("x"), _rows_of("weight"), optional=True, dtypes=FLOAT),
+                 sums_buffer("ss_out", "x", _rows_of("weight")))
+_SUMSQ_MLP = (decode_rows("hidden"), dense("norm_weight", "w_gate_up", "w_down"),
+              matrix_for("out", "hidden", _m("hidden"), _h),
+              matrix_for("mid", "hidden", _m("hidden"), _cols_of("w_down"), optional=True),
+              sums_buffer("ss_in", "hidden", _h, optional=True), sums_buffer("ss_out", "hidden", _h, optional=True))
+_SUMSQ_QKV = (decode_rows("hidden"), dense("norm_weight", "w_qkv"), sums_buffer("ss_in", "hidden", _h),
+              matrix_for("out", "hidden", _m("hidden"), _rows_of("w_qkv")))
+
+# The row-sum forms (rowsq.py): their plain operator's rules, then the layout the
+# bare-pointer entry points assume.
+CONTRACT.update({
+    "linear_sumsq": (*CONTRACT["linear_decode"], dot_kind_if("ss_out"), *_SUMSQ_LINEAR),
+    "post_attn_mlp_sumsq": (*CONTRACT["post_attn_mlp"], dot_kind_if("ss_in", "ss_out"), *_SUMSQ_MLP),
+    "pre_attn_qkv_sumsq": (*CONTRACT["pre_attn_qkv"], dot_kind_if("ss_in"), *_SUMSQ_QKV),
+    "linear_fp8_sumsq": (*CONTRACT["linear_decode_fp8"], *_SUMSQ_LINEAR),
+    "post_attn_mlp_fp8_sumsq": (*CONTRACT["post_attn_mlp_fp8"], dense("gate_up_scale", "down_scale"),
+                                *_SUMSQ_MLP),
+    "pre_attn_qkv_fp8_sumsq": (*CONTRACT["pre_attn_qkv_fp8"], dense("scale"), *_SUMSQ_QKV),
+})
 
 
 def check(op: str, **args) -> dict:

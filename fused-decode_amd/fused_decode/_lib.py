@@ -60,6 +60,7 @@ _rows = ctypes.POINTER(FdRows)
 # name -> argument types; every entry point returns an int status.
 SIGNATURES: dict[str, list] = {
     "fd_version": [],
+    "fd_init": [],
     "fd_runtime_version": [ctypes.POINTER(ctypes.c_int)],
     "fd_rms_norm": [_p, _p, _p, _i, _l, _rows, _rows, _f, _i, _p],
     "fd_add_rms_norm": [_p, _p, _p, _p, _p, _i, _l, _rows, _rows, _rows, _rows, _f, _i, _p],
@@ -119,7 +120,21 @@ def lib() -> ctypes.CDLL:
         handle.fd_last_error.argtypes = []
         handle.fd_last_error.restype = ctypes.c_char_p
         _LIB = handle
+        _init()
     return _LIB
+
+
+_INITIALISED = False
+
+
+def _init() -> None:
+    """fd_init once per process where a GPU is visible (the library's per-device
+    set-up, done before any caller can be capturing a graph)."""
+    global _INITIALISED
+    if _INITIALISED or not torch.cuda.is_available():
+        return
+    _INITIALISED = True
+    check("fd_init", lib().fd_init())
 
 
 def check(func: str, status: int) -> None:
@@ -149,6 +164,7 @@ def native():
             ) from exc
         _fdcall.bind(str(LIB_PATH))
         _NATIVE = _fdcall
+        _init()
     return _NATIVE
 
 

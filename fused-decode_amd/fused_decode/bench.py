@@ -482,6 +482,66 @@ def _max_abs(a, b) -> float:
     return float((a.float() - b.float()).abs().max().item())
 
 
+# The benchmark configurations of the ops block (the norms at one width in fp16;
+# SwiGLU, RoPE and the GEMVs in both activation dtypes; the GEMV at every decode
+# weight shape, row count and kind).
+NORM_ROWS = (8192, 1)
+SWIGLU_ROWS = (2048, 1)
+ROPE_X_SHAPES = ((1, 2048, 32, 128), (1, 1, 32, 128))
+GEMV_SHAPES = ((4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096))
+GEMV_MS = (1, 2, 4, 8, 16)
+GEMV_KINDS = ("dot", "simt")
+OPS_DTYPES = (torch.float16, torch.bfloat16)
+
+
+def ops_configs() -> list[tuple]:
+    """(op, shape, dtype, kind) of every row ``ops_block`` produces, in its order."""
+    cfg = []
+    for r in NORM_ROWS:
+        cfg += [("rms_norm", (r, LLAMA_H), torch.float16, None), ("add_rms_norm", (r, LLAMA_H), torch.float16, None)]
+    cfg += [("swiglu", (r, LLAMA_I), dt, None) for dt in OPS_DTYPES for r in SWIGLU_ROWS]
+    cfg += [("rope", s, dt, None) for dt in OPS_DTYPES for s in ROPE_X_SHAPES]
+    cfg += [("linear_decode", (m, n, k), dt, kind) for dt in OPS_DTYPES for n, k in GEMV_SHAPES for m in GEMV_MS
+            for kind in GEMV_KINDS]
+    return cfg
+
+
+_SHORT = {"float16": "f16", "bfloat16": "bf16"}
+
+
+def _g3(v: float) -> float:
+    """Three significant digits (error columns)."""
+    return float(f"{v:.3g}")
+
+
+OPS_SUMMARY_COLS = ("[dev_us, pct_copy_roof, pct_same_size, max_abs_vs_fp32] per op; GEMV groups "
+                    "[dev_us per M, pct_copy_roof per M, pct_same_size per M, max max_abs] for M=1,2,4,8,16; "
+                    "F.linear: hipBLASLt dev_us per M")
+
+
+def summarize_ops(rows: list[dict]) -> dict:
+    """The ops rows in a few KB for the headline line: one entry per norm, SwiGLU
+    and RoPE configuration, one per GEMV (dtype, kind, N x K) with a value per
+    row count, and F.linear's device time per (dtype, N x K) beside them."""
+    out: dict = {"cols": OPS_SUMMARY_COLS}
+    for r in rows:
+        dt = _SHORT.get(r["dtype"], r["dtype"])
+        same = r.get("pct_same_size")
+        if r["op"] == "linear_decode":
+            _, n, k = r["shape"]
+            grp = out.setdefault(f"gemv {dt} {r['kind']} {n}x{k}", [[], [], [], 0.0])
+            grp[0].append(r["dev_us"])
+            grp[1].append(round(r["pct_copy_roof"]))
+            grp[2].append(round(same) if same else None)
+            grp[3] = max(grp[3], _g3(r["max_abs_vs_fp32"]))
+            if r.get("hipblaslt_dev_us") and r["kind"] == GEMV_KINDS[0]:
+                out.setdefault(f"F.linear {dt} {n}x{k}", []).append(round(r["hipblaslt_dev_us"], 2))
+        else:
+            key = f"{r['op']} {'x'.join(str(v) for v in r['shape'])} {dt}"
+            out[key] = [r["dev_us"], r["pct_copy_roof"], same, _g3(r["max_abs_vs_fp32"])]
+    return out
+
+
 def _compact(op, shape, dtype, nbytes, dev_us, eager_us, roof, max_abs, **extra) -> dict:
     gbs = nbytes / (dev_us * 1e-6) / 1e9
     row = {"op": op, "shape": list(shape), "dtype": str(dtype).replace("torch.", ""), "bytes": nbytes,
@@ -542,7 +602,7 @@ def ops_block(roof: float, log=print) -> list[dict]:
         return {"same_size_kind": kind, "same_size_us": roofs[key]}
 
     # norms: x, residual ~N(0,1), weight ~N(1, 0.1), eps 1e-5, residual_out in place
-    for r in (8192, 1):
+    for r in NORM_ROWS:
         dt, h = torch.float16, LLAMA_H
         e = 2
         k = copies_for(4 * r * h * e)
@@ -563,8 +623,8 @@ def ops_block(roof: float, log=print) -> list[dict]:
         log(rows[-2]), log(rows[-1])
         del xs, rs
     # SwiGLU: gate, up ~N(0, 2)
-    for dt in (torch.float16, torch.bfloat16):
-        for r in (2048, 1):
+    for dt in OPS_DTYPES:
+        for r in SWIGLU_ROWS:
             n = LLAMA_I
             k = copies_for(3 * r * n * 2)
             gs = [_gen((r, n), dt, g, 2.0) for _ in range(k)]
@@ -578,10 +638,12 @@ def ops_block(roof: float, log=print) -> list[dict]:
     # RoPE with Llama-3 tables (theta 500000), cos/sin [2048, 128] viewed [2048, 1, 128]
     inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float64, device="cuda") / 128))
     emb = torch.cat([torch.outer(torch.arange(2048, dtype=torch.float64, device="cuda"), inv)] * 2, -1)
-    for dt in (torch.float16, torch.bfloat16):
+    for dt in OPS_DTYPES:
         cos_t, sin_t = emb.cos().to(dt), emb.sin().to(dt)
-        for xshape, c, s_ in (((1, 2048, 32, 128), cos_t.view(2048, 1, 128), sin_t.view(2048, 1, 128)),
-                              ((1, 1, 32, 128), cos_t[1024].view(1, 1, 128), sin_t[1024].view(1, 1, 128))):
+        for xshape in ROPE_X_SHAPES:
+            t = xshape[1]  # all 2048 positions, or the one token at position 1024
+            pos = slice(0, t) if t > 1 else slice(1024, 1025)
+            c, s_ = cos_t[pos].view(t, 1, 128), sin_t[pos].view(t, 1, 128)
             nbytes = 2 * math.prod(xshape) * 2 + 2 * c.numel() * 2
             k = copies_for(nbytes)
             xs = [_gen(xshape, dt, g) for _ in range(k)]
@@ -591,17 +653,17 @@ def ops_block(roof: float, log=print) -> list[dict]:
             log(rows[-1])
             del xs
     # decode GEMV: x ~N(0,1), W ~N(0, 1/sqrt(K)), bias and row_add in the error check
-    for dt, kinds in ((torch.float16, ("dot", "simt")), (torch.bfloat16, ("dot",))):
-        for n, kk in ((4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)):
+    for dt in OPS_DTYPES:
+        for n, kk in GEMV_SHAPES:
             k = copies_for(n * kk * 2)
             ws = [_gen((n, kk), dt, g, kk ** -0.5) for _ in range(k)]
             bias, wf = _gen((n,), dt, g), ws[0]
-            for m in (1, 2, 4, 8, 16):
+            for m in GEMV_MS:
                 x = _gen((m, kk), dt, g)
                 ra = _gen((m, n), dt, g)
                 ref = fp32_linear(x, wf, bias, ra)
-                hip = graph_us(lambda i: F.linear(x, ws[i % k]), k) if dt == torch.float16 else None
-                for kind in kinds:
+                hip = graph_us(lambda i: F.linear(x, ws[i % k]), k)
+                for kind in GEMV_KINDS:
                     err = _max_abs(linear_decode(x, wf, bias, row_add=ra, kind=kind), ref)
                     dev, eager = timed(lambda i: linear_decode(x, ws[i % k], kind=kind), k)
                     extra = {"kind": kind, **same_size("read", (m * kk + n * kk + m * n) * 2)}

@@ -30,10 +30,10 @@ import ctypes
 
 import torch
 
+from . import _checks
+from ._checks import SUMSQ_MIN_ROWS as MIN_ROWS
 from ._lib import DTYPE_CODE, KIND_CODE, check, lib, stream_of
 from .ops import _qkv_args
-
-MIN_ROWS = 5  # the MFMA kernels that write and read the sums run from this M
 
 
 def sumsq_buffer(width: int, device) -> torch.Tensor:
@@ -46,23 +46,6 @@ def _p(t: torch.Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
-def _rows(x: torch.Tensor, what: str) -> tuple[int, int]:
-    if x.ndim != 2 or not x.is_contiguous():
-        raise ValueError(f"{what} must be a contiguous [M, K] tensor")
-    m, k = x.shape
-    if not MIN_ROWS <= m <= 16:
-        raise ValueError(f"row sums of squares run on the MFMA kernels: {what} needs {MIN_ROWS} to 16 rows, got {m}")
-    return m, k
-
-
-def _sums(ss: torch.Tensor | None, width: int, what: str) -> None:
-    if ss is None:
-        return
-    if ss.dtype != torch.float32 or not ss.is_contiguous() or ss.numel() != (width + 15) // 16 * 16:
-        raise ValueError(f"{what} must be a contiguous float32 tensor of ceil({width}/16)*16 values "
-                         "(sumsq_buffer)")
-
-
 def linear_sumsq(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor, ss_out: torch.Tensor,
                  bias: torch.Tensor | None = None, row_add: torch.Tensor | None = None,
                  kind: str = "dot") -> torch.Tensor:
@@ -70,18 +53,14 @@ def linear_sumsq(x: torch.Tensor, weight: torch.Tensor, *, out: torch.Tensor, ss
     contiguous ``x [M, K]``, ``weight [N, K]``, ``out [M, N]`` and ``row_add``
     ``[M, N]``, also writing ``ss_out`` (``sumsq_buffer(N)``) for the norm that reads
     ``out`` next."""
-    m, k = _rows(x, "x")
-    n = weight.shape[0]
-    _sums(ss_out, n, "ss_out")
-    if tuple(out.shape) != (m, n) or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous [{m}, {n}] tensor")
-    if row_add is not None and (tuple(row_add.shape) != (m, n) or not row_add.is_contiguous()):
-        raise ValueError(f"row_add must be a contiguous [{m}, {n}] tensor")
+    _checks.check("linear_sumsq", x=x, weight=weight, bias=bias, row_add=row_add, kind=kind, out=out,
+                  ss_out=ss_out)
+    (m, k), n = x.shape, weight.shape[0]
     code = DTYPE_CODE[x.dtype]
     check("fd_linear_sumsq", lib().fd_linear_sumsq(
         _p(out), _p(x), _p(weight), _p(bias), DTYPE_CODE[bias.dtype] if bias is not None else code,
         _p(row_add), DTYPE_CODE[row_add.dtype] if row_add is not None else code, m, n, k, k, 1,
-        int(weight.stride(0)), 1, int(bias.stride(0)) if bias is not None else 0,
+        int(weight.stride(0)), int(weight.stride(1)), int(bias.stride(0)) if bias is not None else 0,
         n if row_add is not None else 0, 1 if row_add is not None else 0, n, 1, KIND_CODE[kind], code,
         _p(ss_out), ctypes.c_void_p(stream_of(x))))
     return out
@@ -94,10 +73,9 @@ def post_attn_mlp_sumsq(hidden: torch.Tensor, norm_weight: torch.Tensor, w_gate_
     """``post_attn_mlp`` for a contiguous ``hidden [M, H]``: with ``ss_in`` (the sums
     of ``hidden``) the RMSNorm runs inside the gate/up kernel; with ``ss_out`` the
     down projection writes the sums of ``out`` for the next norm."""
-    m, h = _rows(hidden, "hidden")
-    i = w_down.shape[1]
-    _sums(ss_in, h, "ss_in")
-    _sums(ss_out, h, "ss_out")
+    a = _checks.check("post_attn_mlp_sumsq", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up,
+                      w_down=w_down, eps=eps, kind=kind, out=out, mid=mid, ss_in=ss_in, ss_out=ss_out)
+    (m, h), i, eps = hidden.shape, w_down.shape[1], a["eps"]
     if mid is None:
         mid = torch.empty(m, i, device=hidden.device, dtype=hidden.dtype)
     check("fd_post_attn_mlp_sumsq", lib().fd_post_attn_mlp_sumsq(
@@ -112,10 +90,10 @@ def pre_attn_qkv_sumsq(hidden: torch.Tensor, norm_weight: torch.Tensor, w_qkv: t
                        bias: torch.Tensor | None = None, kind: str = "dot") -> torch.Tensor:
     """``pre_attn_qkv`` for a contiguous ``hidden [M, H]`` whose RMSNorm takes its
     row sums from ``ss_in`` (written by the launch that wrote ``hidden``)."""
-    m, h = _rows(hidden, "hidden")
-    n = w_qkv.shape[0]
-    _sums(ss_in, h, "ss_in")
-    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    a0 = _checks.check("pre_attn_qkv_sumsq", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv, eps=eps,
+                       kind=kind, bias=bias, ss_in=ss_in, out=out)
+    (m, h), n = hidden.shape, w_qkv.shape[0]
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
     code = DTYPE_CODE[hidden.dtype]
     check("fd_pre_attn_qkv_sumsq", lib().fd_pre_attn_qkv_sumsq(
         _p(a.out), _p(hidden), _p(norm_weight), DTYPE_CODE[norm_weight.dtype], _p(w_qkv), _p(bias),
@@ -130,13 +108,9 @@ def linear_fp8_sumsq(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor,
                      row_add: torch.Tensor | None = None) -> torch.Tensor:
     """``linear_decode_fp8`` (E4M3 ``weight [N, K]``, float32 ``scale [N]``) for a
     contiguous ``x [M, K]``, also writing ``ss_out`` for the next norm."""
-    m, k = _rows(x, "x")
-    n = weight.shape[0]
-    _sums(ss_out, n, "ss_out")
-    if tuple(out.shape) != (m, n) or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous [{m}, {n}] tensor")
-    if row_add is not None and (tuple(row_add.shape) != (m, n) or not row_add.is_contiguous()):
-        raise ValueError(f"row_add must be a contiguous [{m}, {n}] tensor")
+    _checks.check("linear_fp8_sumsq", x=x, weight=weight, scale=scale, bias=bias, row_add=row_add, out=out,
+                  ss_out=ss_out)
+    (m, k), n = x.shape, weight.shape[0]
     code = DTYPE_CODE[x.dtype]
     check("fd_linear_fp8_sumsq", lib().fd_linear_fp8_sumsq(
         _p(out), _p(x), _p(weight), _p(scale), _p(bias), DTYPE_CODE[bias.dtype] if bias is not None else code,
@@ -152,10 +126,10 @@ def post_attn_mlp_fp8_sumsq(hidden: torch.Tensor, norm_weight: torch.Tensor, w_g
                             ss_out: torch.Tensor | None = None, mid: torch.Tensor | None = None) -> torch.Tensor:
     """``post_attn_mlp_fp8`` for a contiguous ``hidden [M, H]`` with the row sums
     of ``post_attn_mlp_sumsq``."""
-    m, h = _rows(hidden, "hidden")
-    i = w_down.shape[1]
-    _sums(ss_in, h, "ss_in")
-    _sums(ss_out, h, "ss_out")
+    a = _checks.check("post_attn_mlp_fp8_sumsq", hidden=hidden, norm_weight=norm_weight, w_gate_up=w_gate_up,
+                      gate_up_scale=gate_up_scale, w_down=w_down, down_scale=down_scale, eps=eps, out=out,
+                      mid=mid, ss_in=ss_in, ss_out=ss_out)
+    (m, h), i, eps = hidden.shape, w_down.shape[1], a["eps"]
     if mid is None:
         mid = torch.empty(m, i, device=hidden.device, dtype=hidden.dtype)
     check("fd_post_attn_mlp_fp8_sumsq", lib().fd_post_attn_mlp_fp8_sumsq(
@@ -171,10 +145,10 @@ def pre_attn_qkv_fp8_sumsq(hidden: torch.Tensor, norm_weight: torch.Tensor, w_qk
                            bias: torch.Tensor | None = None) -> torch.Tensor:
     """``pre_attn_qkv_fp8`` for a contiguous ``hidden [M, H]`` whose RMSNorm takes
     its row sums from ``ss_in``."""
-    m, h = _rows(hidden, "hidden")
-    n = w_qkv.shape[0]
-    _sums(ss_in, h, "ss_in")
-    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, eps, rope_cols, bias, out)
+    a0 = _checks.check("pre_attn_qkv_fp8_sumsq", hidden=hidden, norm_weight=norm_weight, w_qkv=w_qkv,
+                       scale=scale, eps=eps, bias=bias, ss_in=ss_in, out=out)
+    (m, h), n = hidden.shape, w_qkv.shape[0]
+    a = _qkv_args(hidden, norm_weight, n, h, cos, sin, a0["eps"], rope_cols, bias, out)
     code = DTYPE_CODE[hidden.dtype]
     check("fd_pre_attn_qkv_fp8_sumsq", lib().fd_pre_attn_qkv_fp8_sumsq(
         _p(a.out), _p(hidden), _p(norm_weight), DTYPE_CODE[norm_weight.dtype], _p(w_qkv), _p(scale), _p(bias),

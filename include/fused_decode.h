@@ -64,6 +64,17 @@ int fd_runtime_version(int* version);
 const char* fd_last_error(void);
 
 /*
+ * Set-up, once per process, before any graph capture: resolves the library's
+ * per-device state on every visible device (the device address of the no-alloc
+ * entry point's array, which must not be looked up while a stream is being
+ * captured). Makes each device current in turn and restores the caller's
+ * device. FD_OK with no visible device; safe to call again (cheap). The Python
+ * loaders call it when they load the library on a machine with a GPU.
+ * No counterpart in the reference (its launchers need no set-up).
+ */
+int fd_init(void);
+
+/*
  * y = x * rsqrt(mean(x^2) + eps) * w, per row, float32 reduction.
  * Replaces kernels.py:343-414 (`rms_out` without residual), launched from
  * ops.py:72-88 (`rms_norm`). w has n elements at stride w_stride, dtype w_dtype
@@ -176,8 +187,9 @@ int fd_post_attn_mlp(void* y, void* mid, const void* hidden, const void* norm_w,
  * GPU's array: calls that may overlap on one GPU (different streams, or host
  * threads) race and must be serialised by the caller. Nothing in the array needs
  * to start at zero (the gate/up launch writes all M*I values before the down
- * projection reads them). The array's address is looked up on the first call on
- * each device (the stream's device).
+ * projection reads them). The array's address is resolved per device by fd_init;
+ * a caller that skipped fd_init gets it looked up on its first call on each
+ * device (the stream's device), which must then not be under graph capture.
  */
 int fd_post_attn_mlp_noalloc(void* y, const void* hidden, const void* norm_w, int norm_w_dtype,
                              const void* w_gate_up, const void* w_down, int64_t M, int64_t H,

@@ -2,7 +2,9 @@
 
 Every rule of fused_decode._checks.CONTRACT is broken once and must raise the
 reference's exception type with a message naming the argument (the reference
-tests match "CUDA", "weight", "even", tests/test_ops.py:174-187). Then the plan
+tests match "CUDA", "weight", "even", tests/test_ops.py:174-187); the row-sum
+forms (fused_decode.rowsq), whose C entry points see no tensor extents, break
+each of their rules too and must raise before anything is launched. Then the plan
 cache: repeated calls with one signature and new values, signatures that differ
 only in strides, environment variables that change between calls with an
 unchanged signature, and the row_add / flattening forms linear_decode accepts,
@@ -112,6 +114,183 @@ def test_every_rule_rejects_with_its_keyword(case):
     _, call, exc, word = next(c for c in BAD if c[0] == case)
     with pytest.raises(exc, match=word):
         call(fd(), _tensors())
+
+
+def _sumsq_tensors():
+    """M=8 rows (the row-sum kernels run from 5), H=64, I=128, a 32-row linear
+    weight and a 3x16-column QKV with 16-wide heads; every argument valid."""
+    from fused_decode import rowsq
+
+    m, h, i = 8, 64, 128
+    t = dict(x=r(m, h, seed=30), hidden=r(m, h, seed=31), nw=r(h, seed=32, scale=0.1, mean=1.0),
+             W=r(32, h, seed=33, scale=h ** -0.5), wgu=r(2 * i, h, seed=34, scale=h ** -0.5),
+             wd=r(h, i, seed=35, scale=i ** -0.5), wqkv=r(48, h, seed=36, scale=h ** -0.5),
+             cs=r(1, 16, seed=37), out32=torch.zeros(m, 32, device=DEV, dtype=F16),
+             outh=torch.zeros(m, h, device=DEV, dtype=F16), out48=torch.zeros(m, 48, device=DEV, dtype=F16),
+             ss32=rowsq.sumsq_buffer(32, DEV).zero_(), ssh=rowsq.sumsq_buffer(h, DEV).fill_(float(h)),
+             ssh2=rowsq.sumsq_buffer(h, DEV).zero_())
+    t["q8"], t["s8"] = fd().quantize_fp8(t["W"])
+    t["q8gu"], t["s8gu"] = fd().quantize_fp8(t["wgu"])
+    t["q8d"], t["s8d"] = fd().quantize_fp8(t["wd"])
+    t["q8qkv"], t["s8qkv"] = fd().quantize_fp8(t["wqkv"])
+    return t
+
+
+def _rs():
+    from fused_decode import rowsq
+
+    return rowsq
+
+
+def _lin(t, **kw):
+    a = dict(out=t["out32"], ss_out=t["ss32"])
+    a.update(kw)
+    return _rs().linear_sumsq(a.pop("x", t["x"]), a.pop("weight", t["W"]), **a)
+
+
+def _mlp(t, **kw):
+    a = dict(hidden=t["hidden"], norm_weight=t["nw"], w_gate_up=t["wgu"], w_down=t["wd"], eps=1e-5,
+             out=t["outh"], ss_in=t["ssh"], ss_out=t["ssh2"])
+    a.update(kw)
+    return _rs().post_attn_mlp_sumsq(a.pop("hidden"), a.pop("norm_weight"), a.pop("w_gate_up"), a.pop("w_down"),
+                                     a.pop("eps"), **a)
+
+
+def _qkv(t, **kw):
+    a = dict(hidden=t["hidden"], norm_weight=t["nw"], w_qkv=t["wqkv"], cos=t["cs"], sin=t["cs"], eps=1e-5,
+             rope_cols=32, ss_in=t["ssh"], out=t["out48"])
+    a.update(kw)
+    return _rs().pre_attn_qkv_sumsq(a.pop("hidden"), a.pop("norm_weight"), a.pop("w_qkv"), a.pop("cos"),
+                                    a.pop("sin"), a.pop("eps"), **a)
+
+
+def _lin8(t, **kw):
+    a = dict(weight=t["q8"], scale=t["s8"], out=t["out32"], ss_out=t["ss32"])
+    a.update(kw)
+    return _rs().linear_fp8_sumsq(a.pop("x", t["x"]), a.pop("weight"), a.pop("scale"), **a)
+
+
+def _mlp8(t, **kw):
+    a = dict(hidden=t["hidden"], norm_weight=t["nw"], w_gate_up=t["q8gu"], gate_up_scale=t["s8gu"],
+             w_down=t["q8d"], down_scale=t["s8d"], eps=1e-5, out=t["outh"], ss_in=t["ssh"], ss_out=t["ssh2"])
+    a.update(kw)
+    return _rs().post_attn_mlp_fp8_sumsq(a.pop("hidden"), a.pop("norm_weight"), a.pop("w_gate_up"),
+                                         a.pop("gate_up_scale"), a.pop("w_down"), a.pop("down_scale"),
+                                         a.pop("eps"), **a)
+
+
+def _qkv8(t, **kw):
+    a = dict(hidden=t["hidden"], norm_weight=t["nw"], w_qkv=t["q8qkv"], scale=t["s8qkv"], cos=t["cs"],
+             sin=t["cs"], eps=1e-5, rope_cols=32, ss_in=t["ssh"], out=t["out48"])
+    a.update(kw)
+    return _rs().pre_attn_qkv_fp8_sumsq(a.pop("hidden"), a.pop("norm_weight"), a.pop("w_qkv"), a.pop("scale"),
+                                        a.pop("cos"), a.pop("sin"), a.pop("eps"), **a)
+
+
+def _strided_k(w):
+    """``w``'s values with K stride 2 (every other column of a twice-wide copy)."""
+    wide = torch.zeros(w.shape[0], 2 * w.shape[1], device=w.device, dtype=w.dtype)
+    wide[:, ::2] = w
+    return wide[:, ::2]
+
+
+def _transposed(w):
+    """``w``'s values in a non-contiguous (column-major) layout."""
+    return w.t().contiguous().t()
+
+
+# (case, call on the tensors t, exception, keyword): one case per rule of the
+# six row-sum forms' contracts, each raised before any launch
+BAD_SUMSQ = [
+    # linear_sumsq
+    ("lin x on the CPU", lambda t: _lin(t, x=t["x"].cpu()), ValueError, "CUDA"),
+    ("lin weight dtype", lambda t: _lin(t, weight=t["W"].bfloat16()), ValueError, "weight"),
+    ("lin K", lambda t: _lin(t, x=t["x"][:, :32].contiguous()), ValueError, "K"),
+    ("lin kind name", lambda t: _lin(t, kind="mfma"), ValueError, "kind"),
+    ("lin kind simt", lambda t: _lin(t, kind="simt"), ValueError, "'dot'"),
+    ("lin bias shape", lambda t: _lin(t, bias=r(31)), ValueError, "bias"),
+    ("lin row_add dtype", lambda t: _lin(t, row_add=r(8, 32).double()), TypeError, "row_add"),
+    ("lin row_add shape", lambda t: _lin(t, row_add=r(1, 32)), ValueError, "row_add"),
+    ("lin row_add strided", lambda t: _lin(t, row_add=r(32, 8).t()), ValueError, "row_add"),
+    ("lin rows", lambda t: _lin(t, x=t["x"][:4], out=t["out32"][:4]), ValueError, "5 to 16 rows"),
+    ("lin x strided", lambda t: _lin(t, x=_transposed(t["x"])), ValueError, "contiguous"),
+    ("lin K stride", lambda t: _lin(t, weight=_strided_k(t["W"])), ValueError, "unit stride"),
+    ("lin out shape", lambda t: _lin(t, out=t["out32"][:, :16]), ValueError, "out"),
+    ("lin out dtype", lambda t: _lin(t, out=t["out32"].bfloat16()), TypeError, "out"),
+    ("lin out device", lambda t: _lin(t, out=t["out32"].cpu()), ValueError, "out"),
+    ("lin ss_out size", lambda t: _lin(t, ss_out=t["ssh"]), ValueError, "ss_out"),
+    ("lin ss_out dtype", lambda t: _lin(t, ss_out=t["ss32"].half()), ValueError, "ss_out"),
+    ("lin ss_out missing", lambda t: _lin(t, ss_out=None), ValueError, "ss_out"),
+    # post_attn_mlp_sumsq
+    ("mlp hidden dtype", lambda t: _mlp(t, hidden=t["hidden"].float()), TypeError, "float16"),
+    ("mlp widths", lambda t: _mlp(t, w_gate_up=t["wgu"][:200]), ValueError, "w_gate_up"),
+    ("mlp weight dtype", lambda t: _mlp(t, w_down=t["wd"].bfloat16()), TypeError, "MLP weights"),
+    ("mlp norm weight", lambda t: _mlp(t, norm_weight=t["nw"][:8]), ValueError, "weight"),
+    ("mlp eps", lambda t: _mlp(t, eps=float("inf")), ValueError, "eps"),
+    ("mlp kind simt", lambda t: _mlp(t, kind="simt"), ValueError, "'dot'"),
+    ("mlp rows", lambda t: _mlp(t, hidden=t["hidden"][:4], out=t["outh"][:4]), ValueError, "5 to 16 rows"),
+    ("mlp w_gate_up strided", lambda t: _mlp(t, w_gate_up=_transposed(t["wgu"])), ValueError, "w_gate_up"),
+    ("mlp w_down strided", lambda t: _mlp(t, w_down=_transposed(t["wd"])), ValueError, "w_down"),
+    ("mlp out shape", lambda t: _mlp(t, out=t["out32"]), ValueError, "out"),
+    ("mlp mid shape", lambda t: _mlp(t, mid=t["out32"]), ValueError, "mid"),
+    ("mlp ss_in size", lambda t: _mlp(t, ss_in=t["ss32"]), ValueError, "ss_in"),
+    ("mlp ss_out device", lambda t: _mlp(t, ss_out=t["ssh2"].cpu()), ValueError, "ss_out"),
+    # pre_attn_qkv_sumsq
+    ("qkv K", lambda t: _qkv(t, w_qkv=t["wqkv"][:, :32].contiguous()), ValueError, "K"),
+    ("qkv weight dtype", lambda t: _qkv(t, w_qkv=t["wqkv"].bfloat16()), TypeError, "w_qkv"),
+    ("qkv bias dtype", lambda t: _qkv(t, bias=r(48, dtype=torch.bfloat16)), TypeError, "bias"),
+    ("qkv kind simt", lambda t: _qkv(t, kind="simt"), ValueError, "'dot'"),
+    ("qkv w strided", lambda t: _qkv(t, w_qkv=_transposed(t["wqkv"])), ValueError, "w_qkv"),
+    ("qkv ss_in missing", lambda t: _qkv(t, ss_in=None), ValueError, "ss_in"),
+    ("qkv ss_in size", lambda t: _qkv(t, ss_in=t["ss32"]), ValueError, "ss_in"),
+    ("qkv out shape", lambda t: _qkv(t, out=t["out32"]), ValueError, "out"),
+    ("qkv rope_cols", lambda t: _qkv(t, rope_cols=40), ValueError, "rope_cols"),
+    # linear_fp8_sumsq
+    ("lin8 codes", lambda t: _lin8(t, weight=t["W"]), TypeError, "float8_e4m3fn"),
+    ("lin8 scale", lambda t: _lin8(t, scale=t["s8"][:3]), ValueError, "scale"),
+    ("lin8 K", lambda t: _lin8(t, x=t["x"][:, :32].contiguous()), ValueError, "K"),
+    ("lin8 rows", lambda t: _lin8(t, x=t["x"][:4], out=t["out32"][:4]), ValueError, "5 to 16 rows"),
+    ("lin8 out shape", lambda t: _lin8(t, out=t["outh"]), ValueError, "out"),
+    ("lin8 ss_out size", lambda t: _lin8(t, ss_out=t["ssh"]), ValueError, "ss_out"),
+    # post_attn_mlp_fp8_sumsq
+    ("mlp8 codes", lambda t: _mlp8(t, w_gate_up=t["wgu"]), TypeError, "float8_e4m3fn"),
+    ("mlp8 gate_up scale", lambda t: _mlp8(t, gate_up_scale=t["s8gu"][:5]), ValueError, "scale"),
+    ("mlp8 down scale", lambda t: _mlp8(t, down_scale=t["s8d"].half()), ValueError, "scale"),
+    ("mlp8 out shape", lambda t: _mlp8(t, out=t["out32"]), ValueError, "out"),
+    ("mlp8 mid dtype", lambda t: _mlp8(t, mid=torch.empty(8, 128, device=DEV, dtype=torch.bfloat16)),
+     TypeError, "mid"),
+    ("mlp8 ss_in dtype", lambda t: _mlp8(t, ss_in=t["ssh"].half()), ValueError, "ss_in"),
+    # pre_attn_qkv_fp8_sumsq
+    ("qkv8 scale", lambda t: _qkv8(t, scale=t["s8qkv"][:7]), ValueError, "scale"),
+    ("qkv8 K", lambda t: _qkv8(t, hidden=r(8, 32, seed=3)), ValueError, "K"),
+    ("qkv8 ss_in missing", lambda t: _qkv8(t, ss_in=None), ValueError, "ss_in"),
+    ("qkv8 out shape", lambda t: _qkv8(t, out=t["outh"]), ValueError, "out"),
+]
+
+
+@pytest.fixture(scope="module")
+def sumsq_tensors():
+    return _sumsq_tensors()
+
+
+@pytest.mark.parametrize("case", [c[0] for c in BAD_SUMSQ])
+def test_every_row_sum_rule_rejects_before_launch(case, sumsq_tensors):
+    _, call, exc, word = next(c for c in BAD_SUMSQ if c[0] == case)
+    t = sumsq_tensors
+    before = {k: v.clone() for k, v in t.items() if k.startswith(("out", "ss"))}
+    with pytest.raises(exc, match=word):
+        call(t)
+    torch.cuda.synchronize()
+    for k, v in before.items():  # nothing was launched: outputs and sums untouched
+        assert torch.equal(t[k], v), k
+
+
+def test_row_sum_forms_accept_the_valid_arguments(sumsq_tensors):
+    """The same tensors with nothing broken pass every rule and run."""
+    t = sumsq_tensors
+    for call in (_lin, _mlp, _qkv, _lin8, _mlp8, _qkv8):
+        call(t)
+    torch.cuda.synchronize()
 
 
 def test_cached_plans_follow_new_values_and_strides():

@@ -3,9 +3,15 @@
 with a caller-owned `mid`: the same kernels, so the outputs must be identical,
 and both within the GEMV tolerance of the oracle (fp16 rtol=atol=2e-2, the
 reference's tests/test_ops.py:27-35). Two calls in a row, the second smaller,
-since every call on a GPU reuses that GPU's array; then a graph capture."""
+since every call on a GPU reuses that GPU's array; then a graph capture, and a
+fresh process whose very first call is made under capture."""
 
 from __future__ import annotations
+
+import subprocess
+import sys
+import textwrap
+from pathlib import Path
 
 import pytest
 import torch
@@ -99,6 +105,55 @@ def test_noalloc_llama3_8b_widths_and_graph_capture(L):
         torch.cuda.synchronize()
         torch.testing.assert_close(out, y_ref, rtol=0, atol=0)
         _ = (hd.float() * 2).sum().item()  # unrelated eager work between replays
+
+
+# A fresh process whose first fd_post_attn_mlp_noalloc call is inside a graph
+# capture: the library's set-up (fd_init, run by the loader) has resolved the
+# array's address before the capture, so the captured call performs no lookup.
+_FIRST_CALL_CAPTURED = textwrap.dedent("""
+    import sys
+    sys.path[:0] = [{root!r}, {pkg!r}]
+    import torch
+    import fused_decode._lib as L
+
+    L.lib()  # loads the library; its set-up runs here, outside any capture
+    m, h, i = 8, 512, 2048
+    g = torch.Generator().manual_seed(7)
+    r = lambda *s, scale=1.0, mean=0.0: (torch.randn(*s, generator=g) * scale + mean).half().cuda()
+    hid, nw, wgu, wd = r(m, h), r(h, scale=0.1, mean=1.0), r(2 * i, h, scale=h ** -0.5), r(h, i, scale=i ** -0.5)
+    out = torch.zeros(m, h, device="cuda", dtype=torch.float16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    print("[noalloc subprocess] capturing the first call", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        L.check("fd_post_attn_mlp_noalloc", L.lib().fd_post_attn_mlp_noalloc(
+            out.data_ptr(), hid.data_ptr(), nw.data_ptr(), L.FD_F16, wgu.data_ptr(), wd.data_ptr(),
+            m, h, i, 1e-5, L.FD_KIND_DOT, L.FD_F16, side.cuda_stream))
+    y_ref = torch.empty(m, h, device="cuda", dtype=torch.float16)
+    mid = torch.empty(m, i, device="cuda", dtype=torch.float16)
+    L.check("fd_post_attn_mlp", L.lib().fd_post_attn_mlp(
+        y_ref.data_ptr(), mid.data_ptr(), hid.data_ptr(), nw.data_ptr(), L.FD_F16, wgu.data_ptr(),
+        wd.data_ptr(), m, h, i, 1e-5, L.FD_KIND_DOT, L.FD_F16, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, y_ref), f"replay {{rep}} differs from fd_post_attn_mlp"
+        _ = (hid.float() * 2).sum().item()  # unrelated eager work between replays
+    print("[noalloc subprocess] ok", flush=True)
+""")
+
+
+def test_noalloc_first_call_under_capture_in_a_fresh_process():
+    root = Path(__file__).resolve().parents[1]
+    code = _FIRST_CALL_CAPTURED.format(root=str(root), pkg=str(root / "fused-decode_amd"))
+    print("[noalloc] fresh process, first call captured, m=8 h=512 i=2048", flush=True)
+    proc = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    print(proc.stdout[-2000:], proc.stderr[-2000:], flush=True)
+    assert proc.returncode == 0 and "[noalloc subprocess] ok" in proc.stdout
 
 
 def test_noalloc_rejects_sizes_beyond_the_scratch(L):
