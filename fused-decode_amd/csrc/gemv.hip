@@ -48,6 +48,11 @@ namespace fd {
 // Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
 // are R*M floats).
 template <int M> struct SimtRows { static constexpr int R = 4; };
+// The persistent SIMT GEMV: four rows up to M = 4, two from 5, where the 8*M-float
+// sums and their butterfly per tile cost the most (Llama-3-8B shapes, M = 8 / 16:
+// N = K = 4096 9.18 / 12.97 us with two rows against 9.18 / 14.78 with four;
+// N = 6144 11.89 / 17.40 against 12.30 / 19.79).
+template <int M> struct SimtPxRows { static constexpr int R = M <= 4 ? 4 : 2; };
 // Fused gate/up: R gate rows + R up rows.
 template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
 // Fused QKV: R rows per tile (R/2 rotate-half pairs in a rotated tile); eight
@@ -133,6 +138,84 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
       float s = 0.f;
       for (int i = 0; i < nw; ++i) s += part[i * V + t];
       y[m * sym + n * syn] = from_f32<T>(epilogue(e, s, m, n));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Persistent SIMT GEMV with the activations held in registers (exact M from 2
+// rows, K up to one 512-element chunk per wave)
+//
+// gemv_simt_kernel re-reads a wave's M activation vectors for every tile it
+// works on and, with one K chunk per wave at K = 4096, waits out one memory
+// latency per tile before a workgroup barrier. Here each wave owns one K chunk
+// for the whole launch: it loads its M activation vectors once, then walks the
+// workgroup's weight tiles (blockIdx.x, + gridDim.x, ...; R rows each) with the
+// next tile's rows in flight during this tile's math (stream_steps). After each
+// tile the wave folds its R*M sums across its lanes (butterfly_sum) and parks
+// them in LDS; one barrier after the last tile, then the workgroup adds the
+// waves' sums of every tile it owns and writes the outputs. No barrier stands
+// between tiles, so a wave whose loads arrive late delays no other.
+__host__ __device__ constexpr size_t simt_px_lds(int tiles_per_wg, int nw, int V) {
+  return sizeof(float) * (size_t)tiles_per_wg * nw * V;
+}
+
+template <typename T, int M, int R, bool NTW>
+__global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
+    T* y, const T* x, const T* w, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
+    int64_t syn, Epi e, int tiles) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(R * M);
+  extern __shared__ __align__(16) float parts[];  // [my tile][wave][V]
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int nt = block_threads(), nw = nt / kWave;
+  const int g = (int)gridDim.x;
+  const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
+  const int k = (wave * kWave + lane) * 8;  // this lane's K chunk (past K: loads a dummy, never used)
+  const bool kin = k < K;
+  const int kc = kin ? k : 0;
+
+  struct Regs {
+    V8 v[R];
+  };
+  // tile i of this workgroup: its R rows at this lane's chunk (rows past N load
+  // the matrix's first 16 bytes, never used)
+  auto issue = [&](Regs& q, int i) {
+    const int64_t n0 = (int64_t)((int)blockIdx.x + i * g) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = n0 + r;
+      q.v[r] = load8w<NTW, T>(n < N ? w + n * swn + kc : w);
+    }
+  };
+  Regs a, b;
+  if (mine > 0) issue(a, 0);
+  V8 xv[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) xv[m] = load8<T>(x + m * sxm + kc);
+  auto consume = [&](const Regs& q, int i) {
+    float acc[V];
+#pragma unroll
+    for (int j = 0; j < V; ++j) acc[j] = 0.f;
+    if (kin) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[r], xv[m], acc[r * M + m]);
+    }
+    butterfly_sum<V>(acc, lane);
+    if (butterfly_writer<V>(lane)) parts[(i * nw + wave) * V + butterfly_index<V>(lane)] = acc[0];
+  };
+  stream_steps(mine, a, b, issue, consume);
+  __syncthreads();
+  for (int t = tid; t < mine * R * M; t += nt) {
+    const int i = t / (R * M), rm = t % (R * M);
+    const int r = rm / M, m = rm % M;
+    const int64_t n = (int64_t)((int)blockIdx.x + i * g) * R + r;
+    if (n < N) {
+      float sum = 0.f;
+      for (int j = 0; j < nw; ++j) sum += parts[(i * nw + j) * V + rm];
+      y[m * sym + n * syn] = from_f32<T>(epilogue(e, sum, m, n));
     }
   }
 }
@@ -571,33 +654,78 @@ void launch_simt_r(void* y, const void* x, const void* w, int N, int K, int64_t 
                      K, sxm, swn, sym, syn, e);
 }
 
-// Default: 4 rows, waves = the largest divisor of the K chunks up to 8. Rows 8
-// exist up to M = 8 (R*M accumulators per lane).
+// The persistent SIMT GEMV: one wave per 512-element K chunk (K <= 8 chunks),
+// a grid of two workgroups per CU (fewer when the tiles are fewer), each owning
+// every gridDim-th tile; LDS holds its tiles' per-wave sums.
+template <typename T, int M, int R>
+int launch_simt_px_r(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                     int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+  constexpr int V = pow2_ceil(R * M);
+  const int nw = (K + kChunk - 1) / kChunk;
+  if (nw < 1 || nw > kMaxWaves)
+    return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV takes K up to %d", kMaxWaves * kChunk);
+  const int tiles = (N + R - 1) / R;
+  int grid = 2 * device_cus();
+  if (grid > tiles) grid = tiles;
+  const int per = (tiles + grid - 1) / grid;
+  const size_t lds = simt_px_lds(per, nw, V);
+  if (lds > kMaxLds / 2) return set_error(FD_EUNSUPPORTED, "too many tiles per workgroup for the LDS sums");
+  auto kernel = gemv_simt_px_kernel<T, M, R, kNtWeights>;
+  if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(nw * kWave), lds, st, static_cast<T*>(y),
+                     static_cast<const T*>(x), static_cast<const T*>(w), N, K, sxm, swn, sym, syn, e, tiles);
+  return FD_OK;
+}
+
+// Can the persistent SIMT GEMV take this launch (R rows per tile)?
+inline bool simt_px_fits(int N, int K, int R, int M) {
+  if (K <= 0 || K > kMaxWaves * kChunk) return false;
+  const int tiles = (N + R - 1) / R;
+  const int grid = 2 * device_cus() < tiles ? 2 * device_cus() : tiles;
+  const int per = (tiles + grid - 1) / grid;
+  return simt_px_lds(per, (K + kChunk - 1) / kChunk, pow2_ceil(R * M)) <= kMaxLds / 2;
+}
+
+// Default: 4 rows, waves = one per 512-element K chunk up to 8; from 2 rows the
+// persistent kernel where K is at most eight chunks (stages 0 or 2; it runs one
+// wave per chunk whatever the tile's waves), else (or with stages 1) the
+// per-tile kernel. Rows 8 exist up to M = 8 (R*M accumulators per lane).
 template <typename T, int M>
-void launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
-                 int64_t sym, int64_t syn, const Epi& e, const Tile& t, hipStream_t st) {
+int launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                int64_t sym, int64_t syn, const Epi& e, const Tile& t, hipStream_t st) {
   const int nw = t.waves ? t.waves : pick_waves((K + kChunk - 1) / kChunk);
-  const int rows = t.rows ? t.rows : SimtRows<M>::R;
-  if (rows == 2)
+  // (K = 0 has no chunk: the per-tile kernel writes the bias/row_add-only outputs)
+  const bool px = t.stages == 2 ||
+                  (t.stages == 0 && M >= 2 && simt_px_fits(N, K, t.rows ? t.rows : SimtPxRows<M>::R, M));
+  const int rows = t.rows ? t.rows : px ? SimtPxRows<M>::R : SimtRows<M>::R;
+  const int r = rows == 2 ? 2 : rows == 8 && M <= 8 ? 8 : 4;
+  constexpr int R8 = M <= 8 ? 8 : 4;
+  if (px) {
+    if (r == 2) return launch_simt_px_r<T, M, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+    if (r == 8) return launch_simt_px_r<T, M, R8>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+    return launch_simt_px_r<T, M, 4>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+  }
+  if (r == 2)
     launch_simt_r<T, M, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
-  else if (rows == 8 && M <= 8)
-    launch_simt_r<T, M, (M <= 8 ? 8 : 4)>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
+  else if (r == 8)
+    launch_simt_r<T, M, R8>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
   else
     launch_simt_r<T, M, 4>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);
+  return FD_OK;
 }
 
 template <typename T>
-void launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
-                   int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Tile& t,
-                   hipStream_t st) {
+int launch_simt_m(int M, void* y, const void* x, const void* w, int N, int K, int64_t sxm,
+                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, const Tile& t,
+                  hipStream_t st) {
   switch (M) {
 #define FD_CASE(MM) \
-  case MM: launch_simt<T, MM>(y, x, w, N, K, sxm, swn, sym, syn, e, t, st); break;
+  case MM: return launch_simt<T, MM>(y, x, w, N, K, sxm, swn, sym, syn, e, t, st);
     FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
     FD_CASE(9) FD_CASE(10) FD_CASE(11) FD_CASE(12) FD_CASE(13) FD_CASE(14) FD_CASE(15)
     FD_CASE(16)
 #undef FD_CASE
-    default: break;
+    default: return set_error(FD_EINVAL, "M must be in [1, 16]");
   }
 }
 
@@ -796,7 +924,8 @@ int check_tile(const Tile& t, int64_t M, int kind) {
     if (t.rows != 0 && t.rows != 2 && t.rows != 4 && t.rows != 8)
       return set_error(FD_EINVAL, "rows per workgroup must be 2, 4 or 8 (SIMT) or 16 (MFMA)");
     if (t.rows == 8 && M > 8) return set_error(FD_EINVAL, "8 SIMT rows per workgroup need M <= 8");
-    if (t.stages < 0 || t.stages > 1) return set_error(FD_EINVAL, "SIMT stages must be 0 or 1");
+    if (t.stages < 0 || t.stages > 2)
+      return set_error(FD_EINVAL, "SIMT stages must be 0 (default), 1 (per-tile) or 2 (persistent)");
   }
   return FD_OK;
 }
@@ -828,13 +957,12 @@ int linear_dispatch(void* y, const void* x, const void* w, const Epi& e, int64_t
   if (act_dtype == FD_F16) {
     if (mfma)
       return launch_mfma<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
-    launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
+    return launch_simt_m<f16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   } else {
     if (mfma)
       return launch_mfma<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, st, nullptr, &t);
-    launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
+    return launch_simt_m<bf16>((int)M, y, x, w, (int)N, (int)K, sxm, swn, sym, syn, e, t, st);
   }
-  return FD_OK;
 }
 
 }  // namespace

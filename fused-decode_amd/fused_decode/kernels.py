@@ -197,10 +197,13 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
 def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
     """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot"):
     the MFMA GEMV runs four waves (two below four K units) with two units in
-    flight each; the SIMT GEMV one wave per 512-element K chunk, up to eight."""
+    flight each; for the SIMT GEMV (0, waves, 0) leaves rows and form to the
+    library: the persistent kernel (stages 2) from 2 rows where K is at most
+    eight 512-element chunks, else the per-tile one (stages 1), with one wave
+    per chunk up to eight."""
     if kern == "dot":
         return 16, (4 if -(-k // 128) >= 4 else 2), 2
-    return 4, _waves(-(-k // 512)), 1
+    return 0, _waves(-(-k // 512)), 0
 
 
 def _waves(items: int) -> int:

@@ -150,7 +150,7 @@ def test_tiled_linear_rejects_tiles_the_kernel_cannot_run(L):
 
     assert call(1, 1, rows=3) == L.FD_EINVAL          # SIMT rows are 2, 4 or 8
     assert call(9, 1, rows=8) == L.FD_EINVAL          # 8 rows only up to M = 8
-    assert call(1, 1, stages=2) == L.FD_EINVAL        # SIMT has one stage
+    assert call(1, 1, stages=3) == L.FD_EINVAL        # SIMT forms: 1 per-tile, 2 persistent
     assert call(1, 1, rows=16) == L.FD_EINVAL         # 16 rows = the MFMA kernel, kind dot only
     assert call(8, 0, rows=5) == L.FD_EINVAL
     assert call(8, 0, stages=4) == L.FD_EINVAL        # MFMA: 1-3 units in flight

@@ -88,16 +88,17 @@ def test_linear_config_tiling(monkeypatch):
     assert kernels.linear_config("dot", 4096, 4096) == (16, 128, 4, 2)        # MFMA kernel, 2 units in flight
     assert kernels.linear_config("dot", 28672, 4096, 8) == (16, 128, 4, 2)
     assert kernels.linear_config("dot", 64, 256, 8) == (16, 128, 2, 2)        # two K units: two waves
-    assert kernels.linear_config("dot", 4096, 4096, 1) == (4, 512, 8, 1)      # dot below 8 rows: SIMT
+    # dot below 5 rows: SIMT, rows and form left to the library (0 rows, stages 0)
+    assert kernels.linear_config("dot", 4096, 4096, 1) == (0, 512, 8, 0)
     monkeypatch.setattr(kernels, "_TILE_TABLE", {"dot:4096x4096:m4": [16, 8, 1]})
     assert kernels.linear_config("dot", 4096, 4096, 4) == (16, 128, 8, 1)     # the table picks MFMA
     monkeypatch.setattr(kernels, "_TILE_TABLE", {})
-    assert kernels.linear_config("simt", 4096, 14336) == (4, 512, 8, 1)
-    assert kernels.linear_config("simt", 64, 100) == (4, 512, 1, 1)
+    assert kernels.linear_config("simt", 4096, 14336) == (0, 512, 8, 0)
+    assert kernels.linear_config("simt", 64, 100) == (0, 512, 1, 0)
     # a measured table entry wins for its exact shape and row count
     monkeypatch.setattr(kernels, "_TILE_TABLE", {"simt:4096x4096:m1": [2, 8, 1]})
     assert kernels.linear_config("simt", 4096, 4096, 1) == (2, 512, 8, 1)
-    assert kernels.linear_config("simt", 4096, 4096, 2) == (4, 512, 8, 1)
+    assert kernels.linear_config("simt", 4096, 4096, 2) == (0, 512, 8, 0)
     # the reference's override variable, with this build's meaning of the fields
     monkeypatch.setenv("FUSED_DECODE_LINEAR", "8,512,4,1")
     assert kernels.linear_config("simt", 4096, 4096, 1) == (8, 512, 4, 1)

@@ -19,10 +19,11 @@ def rnd(*shape, seed, scale=1.0):
     return (torch.randn(*shape, generator=g) * scale).to(torch.float16)
 
 
-# (rows, waves, stages): SIMT rows 2/4/8 with 1-8 waves; MFMA (16 rows) with 2, 4 or
-# 8 waves and 1-3 K units in flight per wave
-TILES = [(2, 4, 1), (2, 8, 1), (4, 3, 1), (8, 8, 1), (16, 8, 1), (16, 4, 2), (16, 2, 3), (16, 4, 3),
-         (16, 8, 2), (0, 0, 0)]
+# (rows, waves, stages): SIMT rows 2/4/8, the per-tile kernel (stages 1) with 1-8
+# waves and the persistent one (stages 2, one wave per K chunk); MFMA (16 rows)
+# with 2, 4 or 8 waves and 1-3 K units in flight per wave
+TILES = [(2, 4, 1), (2, 8, 1), (4, 3, 1), (8, 8, 1), (2, 0, 2), (4, 0, 2), (8, 0, 2), (16, 8, 1), (16, 4, 2),
+         (16, 2, 3), (16, 4, 3), (16, 8, 2), (0, 0, 0)]
 
 
 # 8 SIMT rows per workgroup take M <= 8 (the library rejects more)
