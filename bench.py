@@ -403,21 +403,25 @@ def main() -> None:
 
     decode = None
     if not args.no_decode_step:
-        from fused_decode.decode_step import DecodeStep, time_step
+        from fused_decode.decode_step import DecodeStep, time_replays, two_states
 
-        decode = {"workload": "32-layer Llama-3-8B decode step minus attention, hipGraph, fp16; fused = "
-                              "pre_attn_qkv + O-proj + post_attn_mlp, unfused = the reference's operators, "
-                              "fp8 = fused with E4M3 weights; gbs over each form's weight bytes"}
+        decode = {"workload": "32-layer Llama-3-8B decode step minus attention, hipGraph, fp16 (fp8: E4M3 "
+                              "weights; unfused: the reference's operators); us: median of 30 replays; states: "
+                              "[fast us, n, slow us, n] when replays split into two rates"}
         for m in (1, 8):
             for form in ("fused", "unfused", "fp8"):
                 ds = DecodeStep(m=m, layers=32, dtype=torch.float16, fused=form != "unfused",
                                 weights="fp8" if form == "fp8" else "fp16")
-                g_us = time_step(ds, 10, 2, graph=True)
+                summ = two_states([r["us"] for r in time_replays(ds, 30, 2)])
+                g_us = summ["all"]["median_us"]
                 key = f"m{m}" if form == "fused" else f"m{m}_{form}"
                 decode[f"{key}_us"] = round(g_us, 1)
                 decode[f"{key}_gbs"] = round(ds.weight_bytes / (g_us * 1e-6) / 1e9, 1)
                 decode[f"{key}_launches"] = ds.launches_per_layer
-                progress(f"decode step {key}: {g_us:.1f} us")
+                if "fast" in summ:
+                    decode[f"{key}_states"] = [summ["fast"]["median_us"], summ["fast"]["n"],
+                                               summ["slow"]["median_us"], summ["slow"]["n"]]
+                progress(f"decode step {key}: {g_us:.1f} us {summ}")
                 del ds
                 torch.cuda.empty_cache()
     ops_rows = None

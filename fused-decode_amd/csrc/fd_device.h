@@ -189,6 +189,18 @@ __device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float acc) {
   return acc;
 }
 
+// acc + the squares of the two T values packed in `pair`, in float32.
+template <typename T>
+__device__ __forceinline__ float sq_dot2(uint32_t pair, float acc) {
+  if constexpr (std::is_same<T, f16>::value) {
+    const f16x2 v = __builtin_bit_cast(f16x2, pair);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  } else {
+    const bf16x2 v = __builtin_bit_cast(bf16x2, pair);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  }
+}
+
 // 16x16x32 MFMA: D[16x16] += A[16x32] * B[32x16], float32 accumulate.
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

@@ -113,18 +113,6 @@ __device__ __forceinline__ void load8_norm_w(const void* p, int dtype, int64_t k
     load8_f32<f16>(static_cast<const f16*>(p) + k, f);
 }
 
-// acc + the squares of the two T values packed in `pair`, in float32.
-template <typename T>
-__device__ __forceinline__ float sq_dot2(uint32_t pair, float acc) {
-  if constexpr (std::is_same<T, f16>::value) {
-    const f16x2 v = __builtin_bit_cast(f16x2, pair);
-    return __builtin_amdgcn_fdot2(v, v, acc, false);
-  } else {
-    const bf16x2 v = __builtin_bit_cast(bf16x2, pair);
-    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
-  }
-}
-
 __device__ __forceinline__ void store_norm_chunk(float* wl, const u32x4& v, int c, int dtype) {
   if (dtype == FD_F32) {
     reinterpret_cast<f32x4*>(wl)[c] = __builtin_bit_cast(f32x4, v);

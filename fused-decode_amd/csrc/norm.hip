@@ -90,72 +90,101 @@ __global__ __launch_bounds__(NT) void rms_vec_kernel(T* y, T* ro, const T* x, co
   }
 }
 
-// One wave per row, several rows per workgroup: the reduction is wave shuffles
-// only (no LDS, no workgroup barrier), and each lane keeps VPL vectors of its
-// row in registers. Activations stream through nontemporal loads and stores
-// (read and written exactly once).
+// One wave per row, four rows per workgroup: the reduction is wave shuffles
+// only, and each lane keeps VPL vectors of its row in registers. Activations
+// stream through nontemporal loads and stores (read and written exactly once).
+// The norm weight (n * sizeof(W) bytes, L2-resident, shared by every row) is
+// staged once per workgroup in LDS: its loads go out before the row's, and the
+// output pass reads it from LDS, so it holds no registers while the row loads
+// are in flight. Without the residual the kernel is held to 64 VGPRs up to n =
+// 4096 (the row packed, widened again in the output pass), so eight waves per
+// SIMD keep every row of an 8192 x 4096 norm resident at once.
+template <typename W>
+__host__ __device__ constexpr int norm_w_chunks_per_thread(int vpl) {
+  return vpl * (int)sizeof(W) / 8 > 0 ? vpl * (int)sizeof(W) / 8 : 1;  // n <= vpl * 512
+}
+
 template <typename T, typename W, int VPL, bool ADD>
-__global__ __launch_bounds__(256) void rms_wave_kernel(T* y, T* ro, const T* x, const T* r,
+__global__ __launch_bounds__(256, !ADD && VPL <= 8 ? 8 : 1) void rms_wave_kernel(T* y, T* ro, const T* x, const T* r,
                                                       const W* __restrict__ w, RowGrid grid,
                                                       RowStrides lx, RowStrides lr,
                                                       RowStrides ly, RowStrides lro, int n,
                                                       uint32_t rows, float eps) {
   typedef typename Vec8<T>::type V8;
+  constexpr int WPT = norm_w_chunks_per_thread<W>(VPL);
+  extern __shared__ __align__(16) u32x4 wsm[];  // the norm weight, n * sizeof(W) bytes
+  const int wchunks = n * (int)sizeof(W) / 16;
+  const u32x4* wsrc = reinterpret_cast<const u32x4*>(w);
+  u32x4 wr[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int c = threadIdx.x + i * 256;
+    wr[i] = wsrc[c < wchunks ? c : 0];
+  }
   const uint32_t row = blockIdx.x * 4 + threadIdx.x / kWave;
-  if (row >= rows) return;
+  const bool live = row < rows;  // the last workgroup's waves past the rows only stage the weight
   const int lane = threadIdx.x & (kWave - 1);
-  const RowPos p = row_pos(grid, row);
+  const RowPos p = row_pos(grid, live ? row : 0);
   const T* xr = x + row_off(lx, p);
   const T* rr = ADD ? r + row_off(lr, p) : nullptr;
   V8 a[VPL], b[VPL];
-  Raw8<W> wv[VPL];
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
-    if (k < n) {
+    if (live && k < n) {
       a[j] = load8_nt<T>(xr + k);
       if (ADD) b[j] = load8_nt<T>(rr + k);
     }
   }
-  // the weight (L2-resident, shared by every row) is fetched before the
-  // reduction so its latency overlaps the activation loads
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int k = (j * kWave + lane) * 8;
-    if (k < n) wv[j].load(w + k);
+  for (int i = 0; i < WPT; ++i) {
+    const int c = threadIdx.x + i * 256;
+    if (c < wchunks) wsm[c] = wr[i];
   }
-  // rms: the row stays packed and is widened again in the output pass;
-  // add_rms: the float32 sums are kept (recomputing them costs more registers)
+  __syncthreads();
+  if (!live) return;
+  // rms: the row stays packed in registers and its packed pairs are squared
+  // with v_dot2, so nothing is widened before the output pass; add_rms keeps
+  // the float32 sums x + r and writes residual_out = round(sum) in the first
+  // pass (it does not depend on the norm), so those stores overlap the reduction.
   float v[ADD ? VPL : 1][8];
-  auto val = [&](int j, int i) { return ADD ? v[ADD ? j : 0][i] : to_f32(a[j][i]); };
   float ss = 0.f;
+  T* ror = ADD ? ro + row_off(lro, p) : nullptr;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
+    if (k >= n) continue;
+    if constexpr (ADD) {
+      V8 s;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      if constexpr (ADD) v[j][i] = k < n ? to_f32(a[j][i]) + to_f32(b[j][i]) : 0.f;
-      const float t = k < n ? val(j, i) : 0.f;
-      ss += t * t;
+      for (int i = 0; i < 8; ++i) {
+        v[j][i] = to_f32(a[j][i]) + to_f32(b[j][i]);
+        ss += v[j][i] * v[j][i];
+        s[i] = from_f32<T>(v[j][i]);
+      }
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s), reinterpret_cast<u32x4*>(ror + k));
+    } else {
+      const u32x4 pk = __builtin_bit_cast(u32x4, a[j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss = sq_dot2<T>(pk[i], ss);
     }
   }
   ss = wave_sum(ss);
   const float inv = rsqrtf(ss / (float)n + eps);
   T* yr = y + row_off(ly, p);
-  T* ror = ADD ? ro + row_off(lro, p) : nullptr;
+  const W* wl = reinterpret_cast<const W*>(wsm);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int k = (j * kWave + lane) * 8;
     if (k < n) {
+      Raw8<W> wv;
+      wv.load(wl + k);
       V8 o;
-      if (ADD) {
-        V8 s;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s[i] = from_f32<T>(val(j, i));
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, s), reinterpret_cast<u32x4*>(ror + k));
+      for (int i = 0; i < 8; ++i) {
+        const float x = ADD ? v[ADD ? j : 0][i] : to_f32(a[j][i]);
+        o[i] = from_f32<T>(x * inv * wv[i]);
       }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = from_f32<T>(val(j, i) * inv * wv[j][i]);
       __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), reinterpret_cast<u32x4*>(yr + k));
     }
   }
@@ -210,8 +239,9 @@ template <typename T, typename W, int VPL, bool ADD>
 void launch_wave(void* y, void* ro, const void* x, const void* r, const void* w,
                  const fd_rows& lx, const fd_rows& lr, const fd_rows& ly, const fd_rows& lro,
                  int64_t rows, float eps, hipStream_t st) {
+  const size_t lds = (size_t)(lx.n * (int64_t)sizeof(W) + 15) / 16 * 16;  // the staged norm weight
   hipLaunchKernelGGL((rms_wave_kernel<T, W, VPL, ADD>), dim3((unsigned)((rows + 3) / 4)),
-                     dim3(256), 0, st, static_cast<T*>(y), static_cast<T*>(ro),
+                     dim3(256), lds, st, static_cast<T*>(y), static_cast<T*>(ro),
                      static_cast<const T*>(x), static_cast<const T*>(r),
                      static_cast<const W*>(w), row_grid(lx), row_strides(lx), row_strides(lr),
                      row_strides(ly), row_strides(lro), (int)lx.n, (uint32_t)rows, eps);

@@ -31,6 +31,30 @@ __global__ __launch_bounds__(kRoofThreads) void copy_vec_kernel(u32x4* dst, cons
   }
 }
 
+// The copy's persistent form: a fixed grid walks the vectors grid-stride, each
+// thread moving kRoofUnroll of them per pass (loads, then stores). Measured
+// faster than copy_vec_kernel's one-pass grid on copies of 30-120 MB (33.6 MB:
+// 6.0 against 7.1 us with 8 workgroups per CU), slower at 1 GiB, so it is a
+// second candidate for a kernel's same-size copy ceiling, not the roof.
+__global__ __launch_bounds__(kRoofThreads) void copy_persist_kernel(u32x4* dst, const u32x4* src,
+                                                                    int64_t nvec) {
+  const int64_t stride = (int64_t)gridDim.x * (kRoofThreads * kRoofUnroll);
+  for (int64_t base = (int64_t)blockIdx.x * (kRoofThreads * kRoofUnroll) + threadIdx.x; base < nvec;
+       base += stride) {
+    u32x4 v[kRoofUnroll];
+#pragma unroll
+    for (int i = 0; i < kRoofUnroll; ++i) {
+      const int64_t e = base + i * kRoofThreads;
+      if (e < nvec) v[i] = __builtin_nontemporal_load(src + e);
+    }
+#pragma unroll
+    for (int i = 0; i < kRoofUnroll; ++i) {
+      const int64_t e = base + i * kRoofThreads;
+      if (e < nvec) __builtin_nontemporal_store(v[i], dst + e);
+    }
+  }
+}
+
 // The copy's loads alone: each thread xors its kRoofUnroll vectors, a wave
 // combines its lanes, and the flag is set where a wave's result equals `key`,
 // so no load can be dropped and the stores are one per 64 KiB at most.
@@ -49,6 +73,26 @@ __global__ __launch_bounds__(kRoofThreads) void read_vec_kernel(const u32x4* src
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) acc ^= (uint32_t)__shfl_xor((int)acc, off);
   if ((threadIdx.x & (kWave - 1)) == 0 && acc == key) atomicOr(hit, 1u);
+}
+
+// Clock probe: lane 0 of each workgroup records where it ran -- its XCD's id
+// and its CU's position in it (the SE, SH and CU fields of HW_ID) in one word --
+// the shader clock counter (s_memtime) and the constant-rate wall clock
+// (s_memrealtime). The shader counters of different CUs are not synchronised,
+// so two probes on one stream around a piece of work are compared CU by CU:
+// a CU's counter advance over the wall clock's is proportional to its gfx
+// clock during the work.
+__global__ __launch_bounds__(64) void clock_probe_kernel(unsigned long long* out) {
+  if (threadIdx.x == 0) {
+    unsigned xcc, hw;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+    const unsigned long long t = __builtin_amdgcn_s_memtime();
+    const unsigned long long w = __builtin_amdgcn_s_memrealtime();
+    out[3 * blockIdx.x] = ((unsigned long long)(xcc & 0xfu) << 8) | ((hw >> 8) & 0xffu);
+    out[3 * blockIdx.x + 1] = t;
+    out[3 * blockIdx.x + 2] = w;
+  }
 }
 
 __global__ __launch_bounds__(kRoofThreads) void copy_byte_kernel(uint8_t* dst, const uint8_t* src,
@@ -125,6 +169,18 @@ extern "C" int fd_copy(void* dst, const void* src, int64_t bytes, void* stream) 
   return check_launch();
 }
 
+extern "C" int fd_copy_persistent(void* dst, const void* src, int64_t bytes, int workgroups, void* stream) {
+  if (bytes < 0) return set_error(FD_EINVAL, "bytes must be >= 0");
+  if (workgroups < 1) return set_error(FD_EINVAL, "workgroups must be >= 1");
+  if (bytes == 0) return FD_OK;
+  if (!dst || !src) return set_error(FD_EINVAL, "null pointer argument");
+  if (!aligned16(dst) || !aligned16(src) || bytes % 16 != 0)
+    return set_error(FD_EUNSUPPORTED, "the persistent copy needs 16-byte aligned pointers and bytes %% 16 == 0");
+  hipLaunchKernelGGL(copy_persist_kernel, dim3((unsigned)workgroups), dim3(kRoofThreads), 0,
+                     static_cast<hipStream_t>(stream), (u32x4*)dst, (const u32x4*)src, bytes / 16);
+  return check_launch();
+}
+
 extern "C" int fd_read(const void* src, int64_t bytes, int key, void* hit, void* stream) {
   if (bytes < 0) return set_error(FD_EINVAL, "bytes must be >= 0");
   if (bytes == 0) return FD_OK;
@@ -138,6 +194,19 @@ extern "C" int fd_read(const void* src, int64_t bytes, int key, void* hit, void*
   hipLaunchKernelGGL(read_vec_kernel, dim3((unsigned)blocks), dim3(kRoofThreads), 0,
                      static_cast<hipStream_t>(stream), (const u32x4*)src, nvec, (uint32_t)key,
                      static_cast<uint32_t*>(hit));
+  return check_launch();
+}
+
+extern "C" int fd_clock_probe(unsigned long long* out, int workgroups, int* wall_khz, void* stream) {
+  if (!out || !wall_khz) return set_error(FD_EINVAL, "null pointer argument");
+  if (workgroups < 1 || workgroups > 4096) return set_error(FD_EINVAL, "workgroups must be in [1, 4096]");
+  if ((uintptr_t)out % 8 != 0) return set_error(FD_EINVAL, "out must be 8-byte aligned");
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(wall_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return set_error(FD_ELAUNCH, "cannot read the wall clock rate");
+  hipLaunchKernelGGL(clock_probe_kernel, dim3((unsigned)workgroups), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     out);
   return check_launch();
 }
 

@@ -88,6 +88,8 @@ SIGNATURES: dict[str, list] = {
     "fd_pre_attn_qkv_fp8_sumsq": [_p, _p, _p, _i, _p, _p, _p, _i, _p, _p, _i, _l, _l, _l, _l, _l, _l, _f, _i,
                                   _p, _l, _p],
     "fd_copy": [_p, _p, _l, _p],
+    "fd_copy_persistent": [_p, _p, _l, _i, _p],
+    "fd_clock_probe": [_p, _i, ctypes.POINTER(ctypes.c_int), _p],
     "fd_triad": [_p, _p, _p, _f, _l, _i, _p],
     "fd_read": [_p, _l, _i, _p, _p],
 }

@@ -31,7 +31,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib, kernels
-from .kernels import launch_copy, launch_read, launch_triad
+from .kernels import launch_copy, launch_copy_persistent, launch_read, launch_triad
 from .ops import add_rms_norm, linear_decode, post_attn_mlp, pre_attn_qkv, rms_norm, rope, swiglu
 
 LLAMA_H = 4096
@@ -43,6 +43,10 @@ ROTATE_TARGET = 2 * MALL_BYTES + 64 * 1024 * 1024
 
 def _sync() -> None:
     torch.cuda.synchronize()
+
+
+def _cus() -> int:
+    return torch.cuda.get_device_properties(0).multi_processor_count
 
 
 def time_us(fn, iters: int, warmup: int = 10, rounds: int = 5) -> float:
@@ -514,9 +518,8 @@ def _g3(v: float) -> float:
     return float(f"{v:.3g}")
 
 
-OPS_SUMMARY_COLS = ("[dev_us, pct_copy_roof, pct_same_size, max_abs_vs_fp32] per op; GEMV groups "
-                    "[dev_us per M, pct_copy_roof per M, pct_same_size per M, max max_abs] for M=1,2,4,8,16; "
-                    "F.linear: hipBLASLt dev_us per M")
+OPS_SUMMARY_COLS = ("[dev_us, pct_copy_roof, pct_same_size, max_abs]; gemv: those per M=1,2,4,8,16, "
+                    "one max_abs; F.linear: hipBLASLt dev_us per M")
 
 
 def summarize_ops(rows: list[dict]) -> dict:
@@ -575,8 +578,9 @@ def ops_block(roof: float, log=print) -> list[dict]:
     def same_size(kind: str, nbytes: int) -> dict:
         """The roof kernel moving an op's bytes the same way, timed like its
         dev_us (a HIP graph over rotated buffers): a copy of half each way for
-        ops that read and write as much, a triad for two reads and a write, a
-        read of all of them for the GEMVs."""
+        ops that read and write as much (the faster of fd_copy's one-pass grid
+        and its persistent form at 4 and 8 workgroups per CU), a triad for two
+        reads and a write, a read of all of them for the GEMVs."""
         key = (kind, nbytes)
         if key not in roofs:
             if kind == "triad":  # two reads and one write, fp16
@@ -585,12 +589,16 @@ def ops_block(roof: float, log=print) -> list[dict]:
                 src = [torch.zeros(n, dtype=torch.float16, device="cuda") for _ in range(3 * k)]
                 roofs[key] = graph_us(lambda i: launch_triad(src[3 * (i % k)], src[3 * (i % k) + 1],
                                                              src[3 * (i % k) + 2], 1.0), k)
-            elif kind == "copy":
+            elif kind == "copy":  # the faster of fd_copy and its persistent form
                 half = max(16, nbytes // 2 // 16 * 16)
                 k = copies_for(2 * half)
                 src = [torch.zeros(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
                 dst = [torch.empty(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
-                roofs[key] = graph_us(lambda i: launch_copy(dst[i % k], src[i % k]), k)
+                times = [graph_us(lambda i: launch_copy(dst[i % k], src[i % k]), k)]
+                for per_cu in (4, 8):
+                    wg = per_cu * _cus()
+                    times.append(graph_us(lambda i: launch_copy_persistent(dst[i % k], src[i % k], wg), k))
+                roofs[key] = min(t for t in times if t is not None)
             else:
                 n = max(16, nbytes // 16 * 16)
                 k = copies_for(n)
@@ -748,6 +756,46 @@ def trace_gaps(csv_path: str) -> None:
               f"all gaps mean {statistics.mean(gaps) if gaps else 0.0:5.2f} us")
 
 
+# Byte counts of the benchmark configurations whose same-size ceilings matter:
+# the 4096^2 and 6144x4096 GEMVs at M=1, RoPE over 2048 tokens, the K=14336 GEMV,
+# rms_norm 8192x4096, SwiGLU 2048x14336, the N=28672 GEMV, add_rms_norm, 1 GiB.
+CEILING_SIZES = (33_570_816, 34_603_008, 50_352_128, 117_477_376, 134_225_920, 176_160_768, 234_946_560,
+                 268_443_648, 1 << 30)
+
+
+def ceilings() -> list[dict]:
+    """Device time (one HIP graph over rotated buffers, as every dev_us) of the
+    read roof (fd_read), the copy roof (fd_copy, half the bytes each way) and
+    the copy's persistent form at 2, 4 and 8 workgroups per CU, at each size of
+    CEILING_SIZES; prints a markdown table (GB/s over the bytes moved)."""
+    cus = _cus()
+    rows = []
+    print("| Bytes | fd_read us | GB/s | fd_copy us | GB/s | persistent 2/CU | 4/CU | 8/CU | best copy GB/s |")
+    print("|---|---|---|---|---|---|---|---|---|")
+    for nbytes in CEILING_SIZES:
+        n = nbytes // 16 * 16
+        k = copies_for(n)
+        src = [torch.zeros(n, dtype=torch.uint8, device="cuda") for _ in range(k)]
+        hit = torch.zeros(1, dtype=torch.int32, device="cuda")
+        read = graph_us(lambda i: launch_read(src[i % k], hit), k)
+        del src
+        torch.cuda.empty_cache()
+        half = n // 2 // 16 * 16
+        k = copies_for(2 * half)
+        a = [torch.zeros(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
+        b = [torch.empty(half, dtype=torch.uint8, device="cuda") for _ in range(k)]
+        copy = graph_us(lambda i: launch_copy(b[i % k], a[i % k]), k)
+        pers = {p: graph_us(lambda i, p=p: launch_copy_persistent(b[i % k], a[i % k], p * cus), k) for p in (2, 4, 8)}
+        del a, b
+        torch.cuda.empty_cache()
+        best = min([copy, *pers.values()])
+        row = {"bytes": n, "read_us": read, "copy_us": copy, **{f"persistent_{p}_us": v for p, v in pers.items()}}
+        rows.append(row)
+        print(f"| {n:,} | {read:.2f} | {n / read / 1e3:.0f} | {copy:.2f} | {2 * half / copy / 1e3:.0f} | "
+              f"{pers[2]:.2f} | {pers[4]:.2f} | {pers[8]:.2f} | {2 * half / best / 1e3:.0f} |", flush=True)
+    return rows
+
+
 TIE_BAND = 1.05  # per-shape slack of the cutoff rule
 
 
@@ -830,11 +878,18 @@ def main() -> None:
     ap.add_argument("--only", choices=["pointwise", "linear", "mlp", "qkv", "fp8", "graph"], default=None)
     ap.add_argument("--tune", action="store_true", help="GEMV tile search (writes --tune-out if given)")
     ap.add_argument("--tune-out", default=None)
+    ap.add_argument("--ceilings", action="store_true",
+                    help="time the read and copy roof patterns at the decode ops' sizes and exit")
     ap.add_argument("--trace-gaps", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel trace of --only graph and exit")
     args = ap.parse_args()
     if args.trace_gaps:
         trace_gaps(args.trace_gaps)
+        return
+    if args.ceilings:
+        _lib.lib()
+        torch.cuda.set_device(0)
+        ceilings()
         return
     _lib.lib()
     torch.cuda.set_device(0)

@@ -247,6 +247,141 @@ def time_step(ds: DecodeStep, steps: int, warmup: int, graph: bool) -> float:
     return start.elapsed_time(end) * 1000.0 / steps
 
 
+# A child process (no torch, no GPU work) that samples the current clock of the
+# gfx, memory, data-fabric and SoC domains with amdsmi every PERIOD seconds and
+# appends one JSON line per sample (time.monotonic stamps, shared with the parent)
+# to PATH, until the parent removes the STOP file.
+_CLOCK_SAMPLER = """
+import json, os, sys, time
+import amdsmi
+path, stop, period, index = sys.argv[1], sys.argv[2], float(sys.argv[3]), int(sys.argv[4])
+amdsmi.amdsmi_init()
+dev = amdsmi.amdsmi_get_processor_handles()[index]
+kinds = {"gfx": amdsmi.AmdSmiClkType.GFX, "mem": amdsmi.AmdSmiClkType.MEM, "df": amdsmi.AmdSmiClkType.DF,
+         "soc": amdsmi.AmdSmiClkType.SOC}
+with open(path, "w") as out:
+    while os.path.exists(stop):
+        t0 = time.monotonic()
+        row = {}
+        for name, kind in kinds.items():
+            try:
+                row[name] = amdsmi.amdsmi_get_clock_info(dev, kind).get("clk")
+            except Exception as exc:
+                row[name] = None
+        row["t0"], row["t1"] = t0, time.monotonic()
+        out.write(json.dumps(row) + "\\n")
+        out.flush()
+        time.sleep(period)
+amdsmi.amdsmi_shut_down()
+"""
+
+
+class ClockSampler:
+    """Runs _CLOCK_SAMPLER in a child process for the duration of a with block;
+    ``samples`` then holds its rows (clock MHz per domain, monotonic t0/t1)."""
+
+    def __init__(self, path: str, period: float = 0.005):
+        self.path, self.period, self.samples = path, period, []
+
+    def __enter__(self):
+        import subprocess
+        import sys
+        import time
+
+        self.stop = self.path + ".run"
+        open(self.stop, "w").close()
+        self.proc = subprocess.Popen([sys.executable, "-c", _CLOCK_SAMPLER, self.path, self.stop, str(self.period),
+                                      str(torch.cuda.current_device())])
+        time.sleep(1.0)  # the child's amdsmi_init
+        return self
+
+    def __exit__(self, *exc):
+        import os
+
+        os.remove(self.stop)
+        self.proc.wait(timeout=30)
+        with open(self.path) as f:
+            self.samples = [json.loads(line) for line in f if line.strip()]
+        return False
+
+    def between(self, t0: float, t1: float) -> list[dict]:
+        """Samples whose reading overlapped the window [t0, t1]."""
+        return [s for s in self.samples if s["t0"] <= t1 and s["t1"] >= t0]
+
+
+def counter_rates(pa: list, pb: list) -> dict:
+    """Per XCD, the median over its CUs of each CU's shader-counter advance over
+    the wall clock's between two clock-probe results (kernels.clock_probe rows:
+    [XCD << 8 | CU position, counter, wall]); a CU seen by only one probe is
+    skipped."""
+    import statistics
+
+    first_a, first_b = {}, {}
+    for key, t, w in pa:
+        first_a.setdefault(key, (t, w))
+    for key, t, w in pb:
+        first_b.setdefault(key, (t, w))
+    per_xcd: dict = {}
+    for key in first_a.keys() & first_b.keys():
+        dt, dw = first_b[key][0] - first_a[key][0], first_b[key][1] - first_a[key][1]
+        if dw > 0 and dt > 0:
+            per_xcd.setdefault(key >> 8, []).append(dt / dw)
+    return {x: round(statistics.median(v), 2) for x, v in sorted(per_xcd.items())}
+
+
+def time_replays(ds: DecodeStep, replays: int, warmup: int, probe_wgs: int = 4096) -> list[dict]:
+    """Each graph replay timed on its own (HIP events around it, synchronised
+    after it) between two clock probes on the same stream (kernels.clock_probe,
+    enough workgroups to land on every CU): per XCD, the median over its CUs of
+    the shader counter's advance over the wall clock's across the replay
+    (``counter_rate``, counter ticks per wall-clock tick), which is
+    proportional to the XCD's average gfx clock during the replay."""
+    from .kernels import clock_probe
+
+    if ds.graph is None:
+        ds.capture()
+    for _ in range(warmup):
+        ds.replay()
+    torch.cuda.synchronize()
+    pa = torch.zeros(probe_wgs, 3, dtype=torch.int64, device="cuda")
+    pb = torch.zeros_like(pa)
+    out = []
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    import time
+
+    for i in range(replays):
+        t0 = time.monotonic()
+        khz = clock_probe(pa)
+        start.record()
+        ds.replay()
+        end.record()
+        clock_probe(pb)
+        torch.cuda.synchronize()
+        out.append({"replay": i, "us": round(start.elapsed_time(end) * 1000.0, 1),
+                    "counter_rate_per_xcd": counter_rates(pa.cpu().tolist(), pb.cpu().tolist()), "wall_khz": khz,
+                    "t0": t0, "t1": time.monotonic()})
+    return out
+
+
+def two_states(times: list[float]) -> dict:
+    """Split replay times at the widest gap in their sorted order (the boundary
+    between two steady rates, when there are two) and summarise each side and
+    the whole: count, median, spread."""
+    import statistics
+
+    st = sorted(times)
+    gaps = [(b - a, i) for i, (a, b) in enumerate(zip(st, st[1:]))]
+    widest, at = max(gaps) if gaps else (0.0, 0)
+    summary = {"all": {"n": len(st), "median_us": round(statistics.median(st), 1),
+                       "min_us": st[0], "max_us": st[-1]}}
+    # two states only when the widest gap exceeds 1% of the median and both sides hold >= 3 replays
+    if widest > 0.01 * statistics.median(st) and 3 <= at + 1 <= len(st) - 3:
+        lo, hi = st[:at + 1], st[at + 1:]
+        summary["fast"] = {"n": len(lo), "median_us": round(statistics.median(lo), 1), "max_us": lo[-1]}
+        summary["slow"] = {"n": len(hi), "median_us": round(statistics.median(hi), 1), "min_us": hi[0]}
+    return summary
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--m", type=int, nargs="+", default=[1, 8])
@@ -257,8 +392,21 @@ def main() -> None:
     ap.add_argument("--unfused", action="store_true", help="compose the reference's operators (6 launches/layer at M < 5)")
     ap.add_argument("--weights", choices=["fp16", "fp8"], default="fp16", help="projection weights (fp8: E4M3 + row scales)")
     ap.add_argument("--no-rowsq", action="store_true", help="no row-sum handoff (each RMSNorm derives its sums from its own input)")
+    ap.add_argument("--replays", type=int, default=0,
+                    help="time this many graph replays one by one, each between two clock probes")
+    ap.add_argument("--fresh", type=int, default=1, help="with --replays: step objects built and timed in turn")
+    ap.add_argument("--churn", type=float, default=0.0,
+                    help="with --replays: allocate, touch and free this many GB before building each step object")
+    ap.add_argument("--smi", default=None, metavar="JSONL",
+                    help="with --replays: sample the gfx, memory, fabric and SoC clocks (amdsmi, a child process) "
+                         "into this file and report each replay's")
+    ap.add_argument("--keep", action="store_true",
+                    help="with --replays: keep every step object alive (each takes new memory) instead of freeing it")
     args = ap.parse_args()
     dtype = torch.float16 if args.dtype == "fp16" else torch.bfloat16
+    if args.replays:
+        replay_report(args, dtype)
+        return
     for m in args.m:
         ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused, weights=args.weights,
                         rowsq=not args.no_rowsq)
@@ -277,6 +425,73 @@ def main() -> None:
         }), flush=True)
         del ds
         torch.cuda.empty_cache()
+
+
+def replay_report(args, dtype) -> None:
+    """--replays: per M and fresh step object, one JSON line per replay (its time
+    and each XCD's shader-counter rate during it; with --smi the clock levels
+    the sampler saw inside it), and a summary line: the replay times split into
+    their steady states, each with its median rate."""
+    import contextlib
+    import statistics
+
+    kept = []
+    sampler = ClockSampler(args.smi) if args.smi else None
+    with sampler if sampler else contextlib.nullcontext():
+        runs = _replay_runs(args, dtype, kept, sampler)
+    if not sampler:
+        return
+    for m, f, rows in runs:
+        for r in rows:
+            smp = sampler.between(r["t0"], r["t1"])
+            for dom in ("gfx", "mem", "df", "soc"):
+                vals = [s[dom] for s in smp if isinstance(s.get(dom), (int, float))]
+                r[f"{dom}_mhz"] = sorted(set(vals)) if vals else None
+            r["smi_samples"] = len(smp)
+            print(json.dumps(r), flush=True)
+    print(json.dumps({"smi_samples_total": len(sampler.samples),
+                      "smi_call_ms_median": round(1e3 * statistics.median(s["t1"] - s["t0"] for s in sampler.samples), 2)
+                      if sampler.samples else None}), flush=True)
+
+
+def _replay_runs(args, dtype, kept, sampler) -> list:
+    """The replays of replay_report: (m, fresh, rows) per step object; rows are
+    printed here unless a sampler's samples are to be attached first."""
+    import statistics
+
+    runs = []
+    for m in args.m:
+        for f in range(args.fresh):
+            if args.churn > 0:  # memory the step's weights may then be placed in after it was freed
+                blocks = [torch.ones(1 << 30, dtype=torch.uint8, device="cuda") for _ in range(int(args.churn))]
+                torch.cuda.synchronize()
+                del blocks
+                torch.cuda.empty_cache()
+            ds = DecodeStep(m=m, layers=args.layers, dtype=dtype, fused=not args.unfused, weights=args.weights,
+                            rowsq=not args.no_rowsq)
+            rows = time_replays(ds, args.replays, args.warmup)
+            for r in rows:
+                clk = list(r["counter_rate_per_xcd"].values())
+                r.update(m=m, fresh=f, counter_rate_median=round(statistics.median(clk), 2) if clk else None)
+            runs.append((m, f, rows))
+            if not sampler:
+                for r in rows:
+                    print(json.dumps(r), flush=True)
+            summ = two_states([r["us"] for r in rows])
+            for state in ("fast", "slow"):
+                if state in summ:
+                    sel = [r["counter_rate_median"] for r in rows if r["counter_rate_median"] is not None
+                           and (r["us"] <= summ["fast"]["max_us"]) == (state == "fast")]
+                    summ[state]["counter_rate_median"] = round(statistics.median(sel), 2) if sel else None
+            clk_all = [r["counter_rate_median"] for r in rows if r["counter_rate_median"] is not None]
+            summ["all"]["counter_rate_median"] = round(statistics.median(clk_all), 2) if clk_all else None
+            print(json.dumps({"summary": True, "m": m, "fresh": f, "weights": args.weights, "churn_gb": args.churn,
+                              "kept": args.keep, **summ}), flush=True)
+            if args.keep:
+                kept.append(ds)
+            del ds
+            torch.cuda.empty_cache()
+    return runs
 
 
 if __name__ == "__main__":

@@ -337,6 +337,31 @@ def launch_copy(dst: torch.Tensor, src: torch.Tensor) -> None:
         fail("fd_copy", status)
 
 
+def launch_copy_persistent(dst: torch.Tensor, src: torch.Tensor, workgroups: int) -> None:
+    """The copy roof's persistent form (``fd_copy_persistent``): ``workgroups``
+    workgroups walk the 16-byte vectors grid-stride; same contract as
+    ``launch_copy`` plus 16-byte aligned tensors of a 16-byte multiple."""
+    nbytes = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() != nbytes:
+        raise ValueError("copy needs equal byte sizes")
+    _lib.check("fd_copy_persistent", _lib.lib().fd_copy_persistent(
+        dst.data_ptr(), src.data_ptr(), nbytes, int(workgroups), stream_of(src)))
+
+
+def clock_probe(out: torch.Tensor) -> int:
+    """``fd_clock_probe`` into ``out`` (int64 ``[W, 3]`` on the GPU, W workgroups:
+    XCD id, shader clock counter, wall clock counter per row) on the current
+    stream; returns the wall clock's rate in kHz."""
+    import ctypes
+
+    if out.dtype != torch.int64 or out.ndim != 2 or out.shape[1] != 3 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous int64 [W, 3] tensor")
+    khz = ctypes.c_int(0)
+    _lib.check("fd_clock_probe", _lib.lib().fd_clock_probe(out.data_ptr(), int(out.shape[0]), ctypes.byref(khz),
+                                                           stream_of(out)))
+    return khz.value
+
+
 def launch_read(src: torch.Tensor, hit: torch.Tensor, key: int = 0x2545F491) -> None:
     """Read roof: stream ``src`` (contiguous, 16-byte multiple) and set bit 0 of
     the int32 ``hit`` where the xor of a wave's words equals ``key``."""

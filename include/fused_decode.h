@@ -365,6 +365,28 @@ int fd_triad(void* c, const void* a, const void* b, float scale, int64_t n, int 
  */
 int fd_read(const void* src, int64_t bytes, int key, void* hit, void* stream);
 
+/*
+ * The copy roof's persistent form: dst = src over `bytes` bytes with a fixed
+ * grid of `workgroups` 256-thread workgroups walking the 16-byte vectors
+ * grid-stride, four per thread per pass (16-byte aligned pointers and bytes %
+ * 16 == 0, else FD_EUNSUPPORTED). On copies of tens of MB it can beat fd_copy's
+ * one-pass grid, so the bench times both and takes the faster as a kernel's
+ * same-size copy ceiling. No reference counterpart.
+ */
+int fd_copy_persistent(void* dst, const void* src, int64_t bytes, int workgroups, void* stream);
+
+/*
+ * Clock probe, a measurement aid: `workgroups` (1..4096) one-wave workgroups
+ * each write three uint64 to out[3*i..3*i+2] (8-byte aligned): where it ran
+ * (XCD id << 8 | the SE, SH and CU fields of HW_ID), that CU's shader clock
+ * counter (s_memtime) and the constant-rate wall clock (s_memrealtime), whose
+ * rate in kHz goes to *wall_khz. The shader counters of different CUs are not
+ * synchronised: probes before and after a piece of work on one stream are
+ * compared CU by CU, each CU's counter advance over the wall clock's being
+ * proportional to its gfx clock during the work. No reference counterpart.
+ */
+int fd_clock_probe(unsigned long long* out, int workgroups, int* wall_khz, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

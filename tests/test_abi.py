@@ -47,11 +47,21 @@ def test_version_and_error_string(L):
     assert lib.fd_copy(None, None, -1, None) == L.FD_EINVAL
     assert b"bytes" in lib.fd_last_error()
     assert lib.fd_copy(None, None, 0, None) == L.FD_OK  # empty copy: nothing to do
+    assert lib.fd_copy_persistent(None, None, -16, 8, None) == L.FD_EINVAL
+    assert lib.fd_copy_persistent(None, None, 16, 0, None) == L.FD_EINVAL and b"workgroups" in lib.fd_last_error()
+    assert lib.fd_copy_persistent(None, None, 0, 8, None) == L.FD_OK
+    khz = ctypes.c_int(0)
+    assert lib.fd_clock_probe(None, 8, ctypes.byref(khz), None) == L.FD_EINVAL
+    assert lib.fd_clock_probe(FAKE, 0, ctypes.byref(khz), None) == L.FD_EINVAL and b"workgroups" in lib.fd_last_error()
+    assert lib.fd_clock_probe(FAKE + 4, 8, ctypes.byref(khz), None) == L.FD_EINVAL
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="host-only argument checks")
 def test_read_rejects(L):
     lib = L.lib()
+    assert lib.fd_copy_persistent(0x1008, 0x2000, 16, 8, None) == L.FD_EUNSUPPORTED  # misaligned destination
+    assert lib.fd_copy_persistent(0x1000, 0x2000, 24, 8, None) == L.FD_EUNSUPPORTED  # not whole vectors
+    assert lib.fd_copy_persistent(None, 0x2000, 16, 8, None) == L.FD_EINVAL
     assert lib.fd_read(0x1000, -16, 0, 0x2000, None) == L.FD_EINVAL
     assert lib.fd_read(None, 0, 0, None, None) == L.FD_OK        # nothing to read
     assert lib.fd_read(None, 16, 0, 0x2000, None) == L.FD_EINVAL

@@ -69,10 +69,11 @@ def test_headline_line_fits_and_parses():
     rows = _synthetic_rows()
     mlp = {dt: {m: {"eager_us": 12345.678, "graph_us": 12345.678, "graph_per_call_us": 12345.678}
                 for m in (1, 8)} for dt in ("f16", "bf16")}
-    decode = {"workload": "x" * 250}
+    decode = {"workload": "x" * 260}
     for m in (1, 8):
         for key in (f"m{m}", f"m{m}_unfused", f"m{m}_fp8"):
-            decode.update({f"{key}_us": 12345.6, f"{key}_gbs": 12345.6, f"{key}_launches": 7})
+            decode.update({f"{key}_us": 12345.6, f"{key}_gbs": 12345.6, f"{key}_launches": 7,
+                           f"{key}_states": [12345.6, 30, 12345.6, 30]})
     cpu = {"value": 12345.6, "unit": "us", "cores": 128, "kind": "port", "sample": "s" * 200,
            "cpu_model": "m" * 60, "cpus_visible": 256, "torch_threads": 128}
     line = mod.headline(steps=200, warmup=20, kind="dot", mlp=mlp, gate_us=35.123456, roof=6543.21,

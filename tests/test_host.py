@@ -146,11 +146,13 @@ def test_tile_table_matches_the_dispatch_constants():
     for key, (rows, waves, stages) in table["entries"].items():
         kind, shape, m = key.split(":")
         m = int(m[1:])
-        assert kind in ("dot", "simt") and 1 <= waves <= 8
+        assert kind in ("dot", "simt") and 0 <= waves <= 8
         if rows == 16:
             assert kind == "dot" and stages in (1, 2, 3) and waves in (2, 4, 8)
-        else:
-            assert rows in (2, 4, 8) and rows * m <= 64 and stages == 1
+        else:  # SIMT: the per-tile kernel (stages 1, 1-8 waves) or the persistent one
+            # (stages 2, one wave per K chunk of at most eight)
+            assert rows in (2, 4, 8) and rows * m <= 64 and stages in (1, 2)
+            assert (stages == 1 and waves >= 1) or (stages == 2 and int(shape.split("x")[1]) <= 8 * 512)
 
 
 def test_quantize_fp8_on_cpu_matches_the_oracle():

@@ -41,6 +41,22 @@ def test_copy_is_exact_and_stays_in_bounds(L, nbytes, src_off):
     assert bool((dst[nbytes:] == 0xA5).all())  # nothing written past the copy
 
 
+@pytest.mark.parametrize("nbytes", [16, 4096 + 48, (1 << 20) + 32, 64 << 20])
+@pytest.mark.parametrize("workgroups", [1, 7, 2048])
+def test_persistent_copy_is_exact_and_stays_in_bounds(L, nbytes, workgroups):
+    """fd_copy_persistent: grids smaller than the data (several grid-stride
+    passes) and larger (idle workgroups), guard bytes past the end untouched."""
+    print(f"[roof] persistent copy {nbytes} bytes, {workgroups} workgroups", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(nbytes + workgroups)
+    src = torch.randint(0, 256, (nbytes + 64,), generator=g, device=DEV, dtype=torch.uint8)
+    dst = torch.full((nbytes + 64,), 0xA5, device=DEV, dtype=torch.uint8)
+    L.check("fd_copy_persistent", L.lib().fd_copy_persistent(dst.data_ptr(), src.data_ptr(), nbytes, workgroups,
+                                                             _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src[:nbytes])
+    assert bool((dst[nbytes:] == 0xA5).all())
+
+
 def test_launch_copy_wrapper(L):
     from fused_decode.kernels import launch_copy
 
@@ -142,3 +158,38 @@ def test_read_launcher(L):
     launch_read(src, hit, key=0)
     torch.cuda.synchronize()
     assert int(hit.item()) == 1
+
+
+def test_clock_probe_brackets_work(L):
+    """Two clock probes (4096 workgroups, so every CU is seen by both) around a
+    1 GiB copy: the wall span of every CU is no shorter than the copy the events
+    timed, and each XCD's median counter rate (its CUs' shader-counter advance
+    per wall-clock tick) is positive and within 30% of every other XCD's."""
+    from fused_decode.decode_step import counter_rates
+    from fused_decode.kernels import clock_probe, launch_copy
+
+    print("[roof] clock probe around a 1 GiB copy", flush=True)
+    src = torch.ones(1 << 30, dtype=torch.uint8, device=DEV)
+    dst = torch.empty_like(src)
+    pa = torch.zeros(4096, 3, dtype=torch.int64, device=DEV)
+    pb = torch.zeros_like(pa)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    khz = clock_probe(pa)
+    start.record()
+    launch_copy(dst, src)
+    end.record()
+    clock_probe(pb)
+    torch.cuda.synchronize()
+    copy_us = start.elapsed_time(end) * 1000.0
+    assert khz > 0
+    a, b = pa.cpu().tolist(), pb.cpu().tolist()
+    wall_first = {}
+    for key, _, w in a:
+        wall_first.setdefault(key, w)
+    for key, _, w in b:
+        if key in wall_first:
+            assert (w - wall_first[key]) / khz * 1000.0 >= 0.9 * copy_us
+    rates = counter_rates(a, b)
+    print(f"[roof] counter rate per XCD {rates}, wall {khz} kHz, copy {copy_us:.1f} us", flush=True)
+    assert len(rates) >= 1
+    assert min(rates.values()) > 0 and max(rates.values()) <= 1.3 * min(rates.values())
