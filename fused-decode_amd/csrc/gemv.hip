@@ -48,10 +48,11 @@ namespace fd {
 // Rows of the weight tile per SIMT workgroup for exact M (per-lane accumulators
 // are R*M floats).
 template <int M> struct SimtRows { static constexpr int R = 4; };
-// The persistent SIMT GEMV: four rows up to M = 4, two from 5, where the 8*M-float
-// sums and their butterfly per tile cost the most (Llama-3-8B shapes, M = 8 / 16:
-// N = K = 4096 9.18 / 12.97 us with two rows against 9.18 / 14.78 with four;
-// N = 6144 11.89 / 17.40 against 12.30 / 19.79).
+// The persistent SIMT GEMV with one K chunk per lane: four rows up to M = 4, two
+// from 5, where the 8*M-float sums and their butterfly per tile cost the most
+// (Llama-3-8B shapes, M = 8 / 16: N = K = 4096 9.18 / 12.97 us with two rows
+// against 9.18 / 14.78 with four; N = 6144 11.89 / 17.40 against 12.30 / 19.79);
+// with more chunks per lane, two rows at every M.
 template <int M> struct SimtPxRows { static constexpr int R = M <= 4 ? 4 : 2; };
 // Fused gate/up: R gate rows + R up rows.
 template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
@@ -144,23 +145,26 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 
 // ---------------------------------------------------------------------------
 // Persistent SIMT GEMV with the activations held in registers (exact M from 2
-// rows, K up to one 512-element chunk per wave)
+// rows, K up to CPL 512-element chunks per lane and eight waves)
 //
 // gemv_simt_kernel re-reads a wave's M activation vectors for every tile it
 // works on and, with one K chunk per wave at K = 4096, waits out one memory
-// latency per tile before a workgroup barrier. Here each wave owns one K chunk
-// for the whole launch: it loads its M activation vectors once, then walks the
+// latency per tile before a workgroup barrier. Here each wave owns CPL K chunks
+// (1, 2 or 4: chunks wave, wave + nw, ...) for the whole launch: it loads its
+// CPL * M activation vectors once, then walks the
 // workgroup's weight tiles (blockIdx.x, + gridDim.x, ...; R rows each) with the
 // next tile's rows in flight during this tile's math (stream_steps). After each
 // tile the wave folds its R*M sums across its lanes (butterfly_sum) and parks
 // them in LDS; one barrier after the last tile, then the workgroup adds the
 // waves' sums of every tile it owns and writes the outputs. No barrier stands
-// between tiles, so a wave whose loads arrive late delays no other.
+// between tiles, so a wave whose loads arrive late delays no other. More chunks
+// per lane spread the per-tile butterfly over more products (the activations'
+// registers grow by M * 4 per chunk) and let K = 14336 run on seven waves.
 __host__ __device__ constexpr size_t simt_px_lds(int tiles_per_wg, int nw, int V) {
   return sizeof(float) * (size_t)tiles_per_wg * nw * V;
 }
 
-template <typename T, int M, int R, bool NTW>
+template <typename T, int M, int R, int CPL, bool NTW>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
     T* y, const T* x, const T* w, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
     int64_t syn, Epi e, int tiles) {
@@ -171,37 +175,51 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
   const int nt = block_threads(), nw = nt / kWave;
   const int g = (int)gridDim.x;
   const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
-  const int k = (wave * kWave + lane) * 8;  // this lane's K chunk (past K: loads a dummy, never used)
-  const bool kin = k < K;
-  const int kc = kin ? k : 0;
+  // this lane's CPL K chunks: chunk wave + c * nw of the row (past K: a dummy
+  // address, never used)
+  int kc[CPL];
+  bool kin[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int k = ((wave + c * nw) * kWave + lane) * 8;
+    kin[c] = k < K;
+    kc[c] = kin[c] ? k : 0;
+  }
 
   struct Regs {
-    V8 v[R];
+    V8 v[CPL][R];
   };
-  // tile i of this workgroup: its R rows at this lane's chunk (rows past N load
-  // the matrix's first 16 bytes, never used)
+  // tile i of this workgroup: its R rows at this lane's chunks (rows past N
+  // load the matrix's first 16 bytes, never used)
   auto issue = [&](Regs& q, int i) {
     const int64_t n0 = (int64_t)((int)blockIdx.x + i * g) * R;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t n = n0 + r;
-      q.v[r] = load8w<NTW, T>(n < N ? w + n * swn + kc : w);
-    }
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int64_t n = n0 + r;
+        q.v[c][r] = load8w<NTW, T>(n < N ? w + n * swn + kc[c] : w);
+      }
   };
   Regs a, b;
   if (mine > 0) issue(a, 0);
-  V8 xv[M];
+  V8 xv[CPL][M];
 #pragma unroll
-  for (int m = 0; m < M; ++m) xv[m] = load8<T>(x + m * sxm + kc);
+  for (int c = 0; c < CPL; ++c)
+#pragma unroll
+    for (int m = 0; m < M; ++m) xv[c][m] = load8<T>(x + m * sxm + kc[c]);
   auto consume = [&](const Regs& q, int i) {
     float acc[V];
 #pragma unroll
     for (int j = 0; j < V; ++j) acc[j] = 0.f;
-    if (kin) {
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+    for (int c = 0; c < CPL; ++c) {
+      if (kin[c]) {
 #pragma unroll
-        for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[r], xv[m], acc[r * M + m]);
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[c][r], xv[c][m], acc[r * M + m]);
+      }
     }
     butterfly_sum<V>(acc, lane);
     if (butterfly_writer<V>(lane)) parts[(i * nw + wave) * V + butterfly_index<V>(lane)] = acc[0];
@@ -654,56 +672,103 @@ void launch_simt_r(void* y, const void* x, const void* w, int N, int K, int64_t 
                      K, sxm, swn, sym, syn, e);
 }
 
-// The persistent SIMT GEMV: one wave per 512-element K chunk (K <= 8 chunks),
-// a grid of two workgroups per CU (fewer when the tiles are fewer), each owning
-// every gridDim-th tile; LDS holds its tiles' per-wave sums.
-template <typename T, int M, int R>
+// The persistent SIMT GEMV: `cpl` 512-element K chunks per lane (1, 2 or 4),
+// ceil(chunks / cpl) waves of at most eight, a grid of two workgroups per CU
+// (fewer when the tiles are fewer), each owning every gridDim-th tile; LDS
+// holds its tiles' per-wave sums.
+inline int simt_px_waves(int K, int cpl) {
+  const int chunks = (K + kChunk - 1) / kChunk;
+  return (chunks + cpl - 1) / cpl;
+}
+
+template <typename T, int M, int R, int CPL>
 int launch_simt_px_r(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
                      int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
   constexpr int V = pow2_ceil(R * M);
-  const int nw = (K + kChunk - 1) / kChunk;
-  if (nw < 1 || nw > kMaxWaves)
-    return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV takes K up to %d", kMaxWaves * kChunk);
+  const int nw = simt_px_waves(K, CPL);
+  if (K <= 0 || nw > kMaxWaves)
+    return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV takes K up to %d with %d chunks per lane",
+                     kMaxWaves * kChunk * CPL, CPL);
   const int tiles = (N + R - 1) / R;
   int grid = 2 * device_cus();
   if (grid > tiles) grid = tiles;
   const int per = (tiles + grid - 1) / grid;
   const size_t lds = simt_px_lds(per, nw, V);
   if (lds > kMaxLds / 2) return set_error(FD_EUNSUPPORTED, "too many tiles per workgroup for the LDS sums");
-  auto kernel = gemv_simt_px_kernel<T, M, R, kNtWeights>;
+  auto kernel = gemv_simt_px_kernel<T, M, R, CPL, kNtWeights>;
   if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(nw * kWave), lds, st, static_cast<T*>(y),
                      static_cast<const T*>(x), static_cast<const T*>(w), N, K, sxm, swn, sym, syn, e, tiles);
   return FD_OK;
 }
 
-// Can the persistent SIMT GEMV take this launch (R rows per tile)?
-inline bool simt_px_fits(int N, int K, int R, int M) {
-  if (K <= 0 || K > kMaxWaves * kChunk) return false;
+// K chunks per lane of the persistent SIMT GEMV: what `waves` asks for (the
+// chunks spread over that many waves, rounded up to 1, 2 or 4), else the
+// fewest that keep K within eight waves, and two from 5 rows: the butterfly per
+// tile then covers twice the products (K = 4096, M = 8: N = 4096 9.30 against
+// 9.92 us, N = 28672 39.47 against 42.09; M = 16: 12.30 against 12.93, 55.89
+// against 65.96).
+inline int simt_px_cpl(int M, int K, int waves) {
+  const int chunks = (K + kChunk - 1) / kChunk;
+  int cpl = waves > 0 ? (chunks + waves - 1) / waves : (chunks + kMaxWaves - 1) / kMaxWaves;
+  if (waves <= 0 && M >= 5 && cpl < 2) cpl = 2;
+  return cpl <= 1 ? 1 : cpl <= 2 ? 2 : 4;
+}
+
+// Register budget of the persistent SIMT GEMV (VGPRs per lane): the CPL*M
+// activation vectors, two buffers of R*CPL weight vectors and the padded sums,
+// at most 224 (beyond that the compiler spills: M = 16, 4 rows, 2 chunks).
+__host__ __device__ constexpr bool simt_px_regs_ok(int M, int R, int cpl) {
+  return cpl * M * 4 + 8 * R * cpl + pow2_ceil(R * M) <= 224;
+}
+
+// Can the persistent SIMT GEMV take this launch (R rows per tile, cpl chunks per lane)?
+inline bool simt_px_fits(int N, int K, int R, int M, int cpl) {
+  if (K <= 0 || simt_px_waves(K, cpl) > kMaxWaves || !simt_px_regs_ok(M, R, cpl)) return false;
   const int tiles = (N + R - 1) / R;
   const int grid = 2 * device_cus() < tiles ? 2 * device_cus() : tiles;
   const int per = (tiles + grid - 1) / grid;
-  return simt_px_lds(per, (K + kChunk - 1) / kChunk, pow2_ceil(R * M)) <= kMaxLds / 2;
+  return simt_px_lds(per, simt_px_waves(K, cpl), pow2_ceil(R * M)) <= kMaxLds / 2;
+}
+
+template <typename T, int M, int R>
+int launch_simt_px_c(int cpl, void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
+                     int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
+  if (cpl == 1) return launch_simt_px_r<T, M, R, 1>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+  if constexpr (simt_px_regs_ok(M, R, 2))
+    if (cpl == 2) return launch_simt_px_r<T, M, R, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+  if constexpr (simt_px_regs_ok(M, R, 4))
+    if (cpl == 4) return launch_simt_px_r<T, M, R, 4>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+  return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV's registers do not hold M = %d with %d rows and "
+                   "%d chunks per lane", M, R, cpl);
 }
 
 // Default: 4 rows, waves = one per 512-element K chunk up to 8; from 2 rows the
-// persistent kernel where K is at most eight chunks (stages 0 or 2; it runs one
-// wave per chunk whatever the tile's waves), else (or with stages 1) the
-// per-tile kernel. Rows 8 exist up to M = 8 (R*M accumulators per lane).
+// persistent kernel where K fits eight waves of up to four chunks per lane
+// (stages 0 or 2; with stages 2 the tile's waves set the chunks per lane), else
+// (or with stages 1) the per-tile kernel. Rows 8 exist up to M = 8 (R*M
+// accumulators per lane).
 template <typename T, int M>
 int launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
                 int64_t sym, int64_t syn, const Epi& e, const Tile& t, hipStream_t st) {
   const int nw = t.waves ? t.waves : pick_waves((K + kChunk - 1) / kChunk);
   // (K = 0 has no chunk: the per-tile kernel writes the bias/row_add-only outputs)
-  const bool px = t.stages == 2 ||
-                  (t.stages == 0 && M >= 2 && simt_px_fits(N, K, t.rows ? t.rows : SimtPxRows<M>::R, M));
-  const int rows = t.rows ? t.rows : px ? SimtPxRows<M>::R : SimtRows<M>::R;
+  const bool waves_set = t.stages == 2 && t.waves > 0;
+  int cpl = simt_px_cpl(M, K, waves_set ? t.waves : 0);
+  const int px_rows = t.rows ? t.rows : cpl > 1 ? 2 : SimtPxRows<M>::R;
+  // defaulted chunks per lane step down until the registers hold them (never
+  // below what keeps K within eight waves)
+  while (!waves_set && cpl > 1 && !simt_px_regs_ok(M, px_rows, cpl) &&
+         simt_px_waves(K, cpl / 2) <= kMaxWaves)
+    cpl /= 2;
+  const bool px = t.stages == 2 || (t.stages == 0 && M >= 2 && simt_px_fits(N, K, px_rows, M, cpl));
+  const int rows = t.rows ? t.rows : px ? px_rows : SimtRows<M>::R;
   const int r = rows == 2 ? 2 : rows == 8 && M <= 8 ? 8 : 4;
   constexpr int R8 = M <= 8 ? 8 : 4;
   if (px) {
-    if (r == 2) return launch_simt_px_r<T, M, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
-    if (r == 8) return launch_simt_px_r<T, M, R8>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
-    return launch_simt_px_r<T, M, 4>(y, x, w, N, K, sxm, swn, sym, syn, e, st);
+    if (r == 2) return launch_simt_px_c<T, M, 2>(cpl, y, x, w, N, K, sxm, swn, sym, syn, e, st);
+    if (r == 8) return launch_simt_px_c<T, M, R8>(cpl, y, x, w, N, K, sxm, swn, sym, syn, e, st);
+    return launch_simt_px_c<T, M, 4>(cpl, y, x, w, N, K, sxm, swn, sym, syn, e, st);
   }
   if (r == 2)
     launch_simt_r<T, M, 2>(y, x, w, N, K, sxm, swn, sym, syn, e, nw, st);

@@ -824,11 +824,14 @@ def tune(dtype, out_path: str | None = None) -> dict:
             hip_us[f"{n}x{kk}:m{m}"] = graph_us(lambda i: F.linear(x, ws[i % k]), k)
             for kind in ("simt", "dot"):
                 dflt = kernels.default_tile(kernels._kernel_of(kind, m), n, kk)
-                # SIMT: the per-tile kernel over rows and waves, the persistent one
-                # (one wave per K chunk) over rows where K is at most eight chunks
+                # SIMT: the per-tile kernel over rows and waves, the persistent one over
+                # rows and waves (its waves set 1, 2 or 4 K chunks per lane)
                 cands = {(r, w, 1) for r in (2, 4, 8) if r * m <= 64 for w in (4, 8, dflt[1])}
-                if kk <= 8 * 512:
-                    cands |= {(r, 0, 2) for r in (2, 4, 8) if r * m <= 64}
+                chunks = -(-kk // 512)
+                for cpl in (1, 2, 4):
+                    w = -(-chunks // cpl)
+                    if w <= 8:
+                        cands |= {(r, w, 2) for r in (2, 4, 8) if r * m <= 64 and r * cpl <= 8}
                 if kind == "dot":  # the DMA MFMA GEMV: waves x units in flight within a CU's LDS
                     br = 4 if m <= 4 else 8 if m <= 8 else 16
                     cands |= {(16, w, st) for w in (2, 4, 8) for st in (1, 2, 3)

@@ -198,9 +198,9 @@ def default_tile(kern: str, n: int, k: int) -> tuple[int, int, int]:
     """The library's own choice (rows, waves, stages) for a kernel ("simt" or "dot"):
     the MFMA GEMV runs four waves (two below four K units) with two units in
     flight each; for the SIMT GEMV (0, waves, 0) leaves rows and form to the
-    library: the persistent kernel (stages 2) from 2 rows where K is at most
-    eight 512-element chunks, else the per-tile one (stages 1), with one wave
-    per chunk up to eight."""
+    library: the persistent kernel (stages 2; its waves set 1, 2 or 4 K chunks
+    per lane) from 2 rows where its registers hold them, else the per-tile one
+    (stages 1), with one wave per chunk up to eight."""
     if kern == "dot":
         return 16, (4 if -(-k // 128) >= 4 else 2), 2
     return 0, _waves(-(-k // 512)), 0
