@@ -654,13 +654,18 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
 
 namespace {
 
-constexpr int kMfmaMinM = 5;   // kind=dot uses MFMA from this M on (tile search: MFMA wins from 5 rows on every decode shape)
+// kind=dot runs the MFMA GEMV from this M on unless a tile names the other kernel:
+// the tile table does so per shape where the tile search measured it faster
+// (MFMA already at M = 3-4 on N = 28672, the persistent SIMT kernel still at M = 5
+// on N = 6144). The fused MLP and QKV take their MFMA routes, and the row-sum
+// handoff runs, from this M on.
+constexpr int kMfmaMinM = 5;
 
 // Tiling of one GEMV launch; 0 = the default for the kernel that runs.
 struct Tile {
   int rows;    // weight rows per workgroup (SIMT 2, 4, 8; MFMA 16)
   int waves;   // waves per workgroup, 1..8
-  int stages;  // MFMA K units in flight per wave (1, 2); SIMT 1
+  int stages;  // MFMA: K units in flight per wave (1-3); SIMT: 1 per-tile, 2 persistent kernel
 };
 
 template <typename T, int M, int R>

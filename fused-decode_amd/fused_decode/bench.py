@@ -288,6 +288,31 @@ def bench_linear(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
+def one_gemv(m: int, n: int, kk: int, kind: str, dtype, replays: int = 20) -> dict:
+    """One decode GEMV alone: device time per call from a HIP graph over rotated
+    weights (the ops block's `dev_us`), beside a read of the same bytes timed the
+    same way. A profiler run over it sees only this kernel and the read."""
+    e = torch.empty((), dtype=dtype).element_size()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    k = copies_for(n * kk * e)
+    ws = [_gen((n, kk), dtype, g, kk ** -0.5) for _ in range(k)]
+    x = _gen((m, kk), dtype, g)
+    out = torch.empty(m, n, device="cuda", dtype=dtype)
+    dev = graph_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), k, replays)
+    del ws
+    torch.cuda.empty_cache()
+    nbytes = (m * kk + n * kk + m * n) * e
+    kr = copies_for(nbytes)
+    srcs = [torch.zeros(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(kr)]
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    read = graph_us(lambda i: launch_read(srcs[i % kr], flag), kr, replays)
+    row = {"op": "linear_decode", "shape": [m, n, kk], "dtype": str(dtype).replace("torch.", ""), "kind": kind,
+           "bytes": nbytes, "dev_us": round(dev, 3), "gbs": round(nbytes / dev / 1e3, 1),
+           "same_size_read_us": round(read, 3), "pct_same_size": round(100 * read / dev, 1)}
+    print(json.dumps(row), flush=True)
+    return row
+
+
 def bench_mlp(dtype, roof, quick, cpu) -> list[dict]:
     rows = []
     e = torch.empty((), dtype=dtype).element_size()
@@ -883,6 +908,10 @@ def main() -> None:
     ap.add_argument("--tune-out", default=None)
     ap.add_argument("--ceilings", action="store_true",
                     help="time the read and copy roof patterns at the decode ops' sizes and exit")
+    ap.add_argument("--gemv", default=None, metavar="M,N,K",
+                    help="time one GEMV (with --kind, --dtype, --replays) beside a same-size read and exit")
+    ap.add_argument("--kind", choices=["dot", "simt"], default="dot")
+    ap.add_argument("--replays", type=int, default=20)
     ap.add_argument("--trace-gaps", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel trace of --only graph and exit")
     args = ap.parse_args()
@@ -896,6 +925,10 @@ def main() -> None:
         return
     _lib.lib()
     torch.cuda.set_device(0)
+    if args.gemv:
+        m, n, kk = (int(v) for v in args.gemv.split(","))
+        one_gemv(m, n, kk, args.kind, torch.bfloat16 if args.dtype == "bf16" else torch.float16, args.replays)
+        return
     if args.tune:
         tune(torch.float16 if args.dtype != "bf16" else torch.bfloat16, args.tune_out)
         return

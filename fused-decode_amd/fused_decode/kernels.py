@@ -169,7 +169,9 @@ def linear_config(kind: str, n: int, k: int, m: int | None = None) -> tuple[int,
     ``FUSED_DECODE_LINEAR=block_n,block_k,warps,stages`` overrides it as in the
     reference (kernels.py:589-603): block_n = rows per workgroup, block_k the
     kernel's step (SIMT 512, MFMA 128), warps = waves (SIMT 1-8, MFMA 2, 4 or
-    8), stages = MFMA K units in flight per wave (1-3; SIMT 1). Otherwise the measured table
+    8), stages = MFMA K units in flight per wave (1-3) or the SIMT form (0 the
+    library's choice, 1 per-tile, 2 persistent, whose waves then set the K chunks
+    each lane keeps). Otherwise the measured table
     (``tiles_gfx950.json``, per kind, N, K and M) decides for its shapes, and
     the library's defaults (MFMA for "dot" from 5 rows) for the rest."""
     forced = os.environ.get("FUSED_DECODE_LINEAR")
