@@ -189,6 +189,35 @@ __device__ __forceinline__ float dot8(bf16x8 a, bf16x8 b, float acc) {
   return acc;
 }
 
+// dot8(a, b, 0.f) with the first pair's product taken by the VOP3P form of
+// v_dot2 and an inline-constant zero addend, so no register is zeroed first
+// (the compiler otherwise zeroes one and uses v_dot2c). The same sums in the
+// same order as dot8.
+__device__ __forceinline__ float dot8_first(f16x8 a, f16x8 b) {
+  const u32x4 ua = __builtin_bit_cast(u32x4, a), ub = __builtin_bit_cast(u32x4, b);
+  float acc;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(acc) : "v"(ua[0]), "v"(ub[0]));
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 2, 3),
+                               __builtin_shufflevector(b, b, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 4, 5),
+                               __builtin_shufflevector(b, b, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2(__builtin_shufflevector(a, a, 6, 7),
+                               __builtin_shufflevector(b, b, 6, 7), acc, false);
+  return acc;
+}
+__device__ __forceinline__ float dot8_first(bf16x8 a, bf16x8 b) {
+  const u32x4 ua = __builtin_bit_cast(u32x4, a), ub = __builtin_bit_cast(u32x4, b);
+  float acc;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(acc) : "v"(ua[0]), "v"(ub[0]));
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 2, 3),
+                                        __builtin_shufflevector(b, b, 2, 3), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 4, 5),
+                                        __builtin_shufflevector(b, b, 4, 5), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(a, a, 6, 7),
+                                        __builtin_shufflevector(b, b, 6, 7), acc, false);
+  return acc;
+}
+
 // acc + the squares of the two T values packed in `pair`, in float32.
 template <typename T>
 __device__ __forceinline__ float sq_dot2(uint32_t pair, float acc) {

@@ -52,7 +52,7 @@ template <int M> struct SimtRows { static constexpr int R = 4; };
 // from 5, where the 8*M-float sums and their butterfly per tile cost the most
 // (Llama-3-8B shapes, M = 8 / 16: N = K = 4096 9.18 / 12.97 us with two rows
 // against 9.18 / 14.78 with four; N = 6144 11.89 / 17.40 against 12.30 / 19.79);
-// with more chunks per lane, two rows at every M.
+// with more chunks per lane simt_px_rows decides.
 template <int M> struct SimtPxRows { static constexpr int R = M <= 4 ? 4 : 2; };
 // Fused gate/up: R gate rows + R up rows.
 template <int M> struct MlpRows { static constexpr int R = M <= 4 ? 4 : 2; };
@@ -171,7 +171,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
   typedef typename Vec8<T>::type V8;
   constexpr int V = pow2_ceil(R * M);
   extern __shared__ __align__(16) float parts[];  // [my tile][wave][V]
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // scalar: the tests below branch once
   const int nt = block_threads(), nw = nt / kWave;
   const int g = (int)gridDim.x;
   const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
@@ -185,6 +186,10 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
     kin[c] = k < K;
     kc[c] = kin[c] ? k : 0;
   }
+  // every chunk of this wave inside K (every wave when the chunks fill the
+  // waves evenly): its sums start from the first chunk's products, with no
+  // masking and no separate zeroing
+  const bool whole = ((wave + (CPL - 1) * nw) * kWave + kWave - 1) * 8 < K;
 
   struct Regs {
     V8 v[CPL][R];
@@ -194,12 +199,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
   auto issue = [&](Regs& q, int i) {
     const int64_t n0 = (int64_t)((int)blockIdx.x + i * g) * R;
 #pragma unroll
-    for (int c = 0; c < CPL; ++c)
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = n0 + r;
+      const T* wr = n < N ? w + n * swn : w;  // a wave-uniform row base
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int64_t n = n0 + r;
-        q.v[c][r] = load8w<NTW, T>(n < N ? w + n * swn + kc[c] : w);
-      }
+      for (int c = 0; c < CPL; ++c) q.v[c][r] = load8w<NTW, T>(wr + kc[c]);
+    }
   };
   Regs a, b;
   if (mine > 0) issue(a, 0);
@@ -210,15 +215,30 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
     for (int m = 0; m < M; ++m) xv[c][m] = load8<T>(x + m * sxm + kc[c]);
   auto consume = [&](const Regs& q, int i) {
     float acc[V];
+    if (whole) {
 #pragma unroll
-    for (int j = 0; j < V; ++j) acc[j] = 0.f;
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      if (kin[c]) {
+        for (int m = 0; m < M; ++m) acc[r * M + m] = dot8_first(q.v[0][r], xv[0][m]);
+#pragma unroll
+      for (int c = 1; c < CPL; ++c)
 #pragma unroll
         for (int r = 0; r < R; ++r)
 #pragma unroll
           for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[c][r], xv[c][m], acc[r * M + m]);
+#pragma unroll
+      for (int j = R * M; j < V; ++j) acc[j] = 0.f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        if (kin[c]) {
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[c][r], xv[c][m], acc[r * M + m]);
+        }
       }
     }
     butterfly_sum<V>(acc, lane);
@@ -656,8 +676,8 @@ namespace {
 
 // kind=dot runs the MFMA GEMV from this M on unless a tile names the other kernel:
 // the tile table does so per shape where the tile search measured it faster
-// (MFMA already at M = 3-4 on N = 28672, the persistent SIMT kernel still at M = 5
-// on N = 6144). The fused MLP and QKV take their MFMA routes, and the row-sum
+// (MFMA already at M = 3-4 on N = 28672 and K = 14336, the persistent SIMT kernel
+// still at M = 5-9 on N = 6144). The fused MLP and QKV take their MFMA routes, and the row-sum
 // handoff runs, from this M on.
 constexpr int kMfmaMinM = 5;
 
@@ -678,12 +698,24 @@ void launch_simt_r(void* y, const void* x, const void* w, int N, int K, int64_t 
 }
 
 // The persistent SIMT GEMV: `cpl` 512-element K chunks per lane (1, 2 or 4),
-// ceil(chunks / cpl) waves of at most eight, a grid of two workgroups per CU
-// (fewer when the tiles are fewer), each owning every gridDim-th tile; LDS
-// holds its tiles' per-wave sums.
+// ceil(chunks / cpl) waves of at most eight, a grid of one or two workgroups
+// per CU (simt_px_grid; fewer when the tiles are fewer), each owning every
+// gridDim-th tile; LDS holds its tiles' per-wave sums.
 inline int simt_px_waves(int K, int cpl) {
   const int chunks = (K + kChunk - 1) / kChunk;
   return (chunks + cpl - 1) / cpl;
+}
+
+// Workgroups of the persistent SIMT GEMV. Each one reads all M activation rows
+// into registers (M*K elements from L2) before its first tile, so a second
+// workgroup per CU pays off only while the weight rows each one streams still
+// outweigh that: two per CU where N >= 4*M*CUs, else one (M = 8, K = 4096:
+// N = 4096 9.05 -> 8.67 us and N = 6144 11.86 -> 11.78 with one per CU,
+// N = 4096 K = 14336 26.2 -> 24.9, but N = 28672 40.9 -> 42.9).
+inline bool simt_px_one_per_cu(int N, int M) { return N < 4 * M * device_cus(); }
+inline int simt_px_grid(int N, int M, int tiles) {
+  const int grid = (simt_px_one_per_cu(N, M) ? 1 : 2) * device_cus();
+  return grid < tiles ? grid : tiles;
 }
 
 template <typename T, int M, int R, int CPL>
@@ -695,8 +727,7 @@ int launch_simt_px_r(void* y, const void* x, const void* w, int N, int K, int64_
     return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV takes K up to %d with %d chunks per lane",
                      kMaxWaves * kChunk * CPL, CPL);
   const int tiles = (N + R - 1) / R;
-  int grid = 2 * device_cus();
-  if (grid > tiles) grid = tiles;
+  const int grid = simt_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
   const size_t lds = simt_px_lds(per, nw, V);
   if (lds > kMaxLds / 2) return set_error(FD_EUNSUPPORTED, "too many tiles per workgroup for the LDS sums");
@@ -731,9 +762,19 @@ __host__ __device__ constexpr bool simt_px_regs_ok(int M, int R, int cpl) {
 inline bool simt_px_fits(int N, int K, int R, int M, int cpl) {
   if (K <= 0 || simt_px_waves(K, cpl) > kMaxWaves || !simt_px_regs_ok(M, R, cpl)) return false;
   const int tiles = (N + R - 1) / R;
-  const int grid = 2 * device_cus() < tiles ? 2 * device_cus() : tiles;
+  const int grid = simt_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
   return simt_px_lds(per, simt_px_waves(K, cpl), pow2_ceil(R * M)) <= kMaxLds / 2;
+}
+
+// Default rows per tile of the persistent SIMT GEMV: up to 4 rows, 4; with
+// more than one K chunk per lane, 4 where one workgroup per CU runs and the
+// registers hold them (M = 8, K = 4096, one per CU: N = 4096 8.67 -> 8.54 us,
+// N = 6144 11.78 -> 11.29), else 2.
+template <int M>
+inline int simt_px_rows(int N, int cpl) {
+  if (cpl <= 1) return SimtPxRows<M>::R;
+  return M <= 8 && simt_px_one_per_cu(N, M) && simt_px_regs_ok(M, 4, cpl) ? 4 : 2;
 }
 
 template <typename T, int M, int R>
@@ -760,7 +801,7 @@ int launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm
   // (K = 0 has no chunk: the per-tile kernel writes the bias/row_add-only outputs)
   const bool waves_set = t.stages == 2 && t.waves > 0;
   int cpl = simt_px_cpl(M, K, waves_set ? t.waves : 0);
-  const int px_rows = t.rows ? t.rows : cpl > 1 ? 2 : SimtPxRows<M>::R;
+  const int px_rows = t.rows ? t.rows : simt_px_rows<M>(N, cpl);
   // defaulted chunks per lane step down until the registers hold them (never
   // below what keeps K within eight waves)
   while (!waves_set && cpl > 1 && !simt_px_regs_ok(M, px_rows, cpl) &&

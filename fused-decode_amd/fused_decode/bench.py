@@ -835,7 +835,8 @@ def tune(dtype, out_path: str | None = None) -> dict:
     the value for DECODE_LINEAR_MAX_M: the largest M up to which, at every row
     count, the default kind's best tiles run a decode layer's four GEMVs faster
     in sum than F.linear with no shape more than 5% slower (``strict_max_m``:
-    every shape faster)."""
+    every shape faster), and the same cutoff for kind "simt"
+    (``simt_decode_linear_max_m``, SIMT_DECODE_LINEAR_MAX_M)."""
     g = torch.Generator(device="cuda").manual_seed(4)
     e = torch.empty((), dtype=dtype).element_size()
     shapes = [(4096, 4096), (4096, 14336), (28672, 4096), (6144, 4096)]
@@ -876,20 +877,27 @@ def tune(dtype, out_path: str | None = None) -> dict:
                       f"F.linear {hip_us[f'{n}x{kk}:m{m}']:8.2f} us", flush=True)
         del ws
         torch.cuda.empty_cache()
-    max_m = strict_m = 0
-    for m in range(1, 17):
-        ours = [best_us[kernels.tile_key("dot", n, kk, m)] for n, kk in shapes]
-        theirs = [hip_us[f"{n}x{kk}:m{m}"] for n, kk in shapes]
-        if strict_m == m - 1 and all(a <= b for a, b in zip(ours, theirs)):
-            strict_m = m
-        if max_m == m - 1 and sum(ours) < sum(theirs) and all(a <= TIE_BAND * b for a, b in zip(ours, theirs)):
-            max_m = m
+    def cutoffs(kind: str) -> tuple[int, int]:
+        max_m = strict_m = 0
+        for m in range(1, 17):
+            ours = [best_us[kernels.tile_key(kind, n, kk, m)] for n, kk in shapes]
+            theirs = [hip_us[f"{n}x{kk}:m{m}"] for n, kk in shapes]
+            if strict_m == m - 1 and all(a <= b for a, b in zip(ours, theirs)):
+                strict_m = m
+            if max_m == m - 1 and sum(ours) < sum(theirs) and all(a <= TIE_BAND * b for a, b in zip(ours, theirs)):
+                max_m = m
+        return max_m, strict_m
+
+    max_m, strict_m = cutoffs("dot")
+    simt_max_m, simt_strict_m = cutoffs("simt")
     table = {"arch": torch.cuda.get_device_properties(0).gcnArchName.split(":")[0],
              "dtype": str(dtype).replace("torch.", ""), "entries": entries,
              "best_us": best_us, "default_us": default_us, "hipblas_us": hip_us,
-             "decode_linear_max_m": max_m, "strict_max_m": strict_m}
+             "decode_linear_max_m": max_m, "strict_max_m": strict_m,
+             "simt_decode_linear_max_m": simt_max_m, "simt_strict_max_m": simt_strict_m}
     print(f"DECODE_LINEAR_MAX_M: {max_m} (a layer's four GEMVs faster in sum, none more than "
           f"{100 * (TIE_BAND - 1):.0f}% slower than F.linear); every shape faster up to M={strict_m}; "
+          f"kind simt: {simt_max_m} (every shape faster up to M={simt_strict_m}); "
           f"{len(entries)} tiles beat the default by >= 3%", flush=True)
     if out_path:
         with open(out_path, "w") as f:

@@ -20,7 +20,8 @@ pointers (the library checks alignment and picks its vector or generic kernels
 itself on every call).
 
 ``linear_decode`` uses the hand-written GEMV up to ``DECODE_LINEAR_MAX_M`` rows
-by default and ``F.linear`` (hipBLASLt) above it; passing ``kind`` forces the
+by default (``SIMT_DECODE_LINEAR_MAX_M`` for kind "simt" chosen through the
+environment) and ``F.linear`` (hipBLASLt) above it; passing ``kind`` forces the
 GEMV up to 16 rows, as in the reference.
 """
 
@@ -56,11 +57,19 @@ from .kernels import (
 # hipBLASLt's F.linear, none of them more than 5% slower (each strictly faster
 # up to 14 rows), so the HIP GEMV is the default over the whole hand range.
 DECODE_LINEAR_MAX_M = 16
+# The same cutoff for the SIMT kernel, which the default dispatcher runs when
+# FUSED_DECODE_LINEAR_KIND selects kind "simt": from 9 rows its v_dot2 work on
+# the down projection (K = 14336, whose activations no longer fit the persistent
+# kernel's registers) makes it slower than F.linear (31.7 against 26.1 us at
+# M = 9), so the default stops at 8 there. A caller that names the kind still
+# gets the SIMT kernel up to 16 rows, as in the reference.
+SIMT_DECODE_LINEAR_MAX_M = 8
 _FORCED_LIMIT = 16  # rows the GEMV takes when the caller names a kind
 _FP8_ROWS = 16  # rows the E4M3 kernels take
 
 __all__ = [
     "DECODE_LINEAR_MAX_M",
+    "SIMT_DECODE_LINEAR_MAX_M",
     "add_rms_norm",
     "linear_decode",
     "post_attn_mlp",
@@ -392,6 +401,11 @@ def _check_out(out, expected: tuple, like: torch.Tensor) -> None:
         raise ValueError("out must be contiguous")
 
 
+def _default_limit(kind: str) -> int:
+    """Rows up to which the default dispatcher runs the HIP GEMV of `kind`."""
+    return DECODE_LINEAR_MAX_M if kind == "dot" else SIMT_DECODE_LINEAR_MAX_M
+
+
 def linear_decode(
     x: torch.Tensor,
     weight: torch.Tensor,
@@ -403,7 +417,8 @@ def linear_decode(
 ) -> torch.Tensor:
     """``y = x @ weight.T + bias (+ row_add)``, weight ``[N, K]`` like ``F.linear``.
 
-    The HIP GEMV runs for a flattened batch up to ``DECODE_LINEAR_MAX_M`` rows,
+    The HIP GEMV runs for a flattened batch up to ``DECODE_LINEAR_MAX_M`` rows
+    (``SIMT_DECODE_LINEAR_MAX_M`` when FUSED_DECODE_LINEAR_KIND selects "simt"),
     or up to 16 when ``kind`` ("dot" or "simt") is given; wider batches call
     ``F.linear`` (bit-identical to it), with row_add added in float32.
     Reference: ops.py:212-280.
@@ -422,8 +437,8 @@ def linear_decode(
 
 def _plan_linear(x, weight, bias, row_add, out, kind) -> Plan:
     check("linear_decode", x=x, weight=weight, bias=bias, row_add=row_add, kind=kind)
-    limit = _FORCED_LIMIT if kind is not None else DECODE_LINEAR_MAX_M
     kind_r = resolve_kind(kind)
+    limit = _FORCED_LIMIT if kind is not None else _default_limit(kind_r)
     n, k = (int(d) for d in weight.shape)
     m = 1 if x.ndim == 1 else math.prod(x.shape[:-1])
     expected = (n,) if x.ndim == 1 else (*x.shape[:-1], n)

@@ -336,6 +336,32 @@ def test_environment_changes_reach_cached_signatures(monkeypatch):
         f.rms_norm(xs, w)
 
 
+def test_simt_kind_from_the_environment_stops_at_its_own_cutoff(monkeypatch):
+    """With kind "simt" chosen through FUSED_DECODE_LINEAR_KIND the default
+    dispatcher runs the HIP GEMV up to SIMT_DECODE_LINEAR_MAX_M rows and F.linear
+    (bit-identical) above; naming the kind still runs the HIP GEMV up to 16 rows
+    (reference ops.py:247-249)."""
+    import torch.nn.functional as F
+
+    f = fd()
+    from fused_decode import ops
+
+    monkeypatch.delenv("FUSED_DECODE_LINEAR", raising=False)
+    monkeypatch.setenv("FUSED_DECODE_LINEAR_KIND", "simt")
+    W = r(96, 512, seed=5, scale=0.05)
+    for m in (ops.SIMT_DECODE_LINEAR_MAX_M, ops.SIMT_DECODE_LINEAR_MAX_M + 1, 16):
+        x = r(m, 512, seed=m)
+        ref = O.linear(npf(x), npf(W), dtype="f16")
+        y = f.linear_decode(x, W)
+        close(y, ref, "linear")
+        if m > ops.SIMT_DECODE_LINEAR_MAX_M:
+            assert torch.equal(y, F.linear(x, W))
+        close(f.linear_decode(x, W, kind="simt"), ref, "linear")
+    monkeypatch.setenv("FUSED_DECODE_LINEAR_KIND", "dot")
+    x = r(16, 512, seed=16)
+    close(f.linear_decode(x, W), O.linear(npf(x), npf(W), dtype="f16"), "linear")
+
+
 @pytest.mark.parametrize("form", ["vector", "row", "column", "full", "full_strided", "scalar", "lead3",
                                   "flat_mn", "permuted"])
 def test_linear_row_add_and_flattening_forms(form):

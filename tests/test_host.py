@@ -134,8 +134,9 @@ def test_exports_match_reference_surface():
 
 
 def test_tile_table_matches_the_dispatch_constants():
-    """The committed gfx950 tile table: its cutoff is DECODE_LINEAR_MAX_M, and every
-    entry is a tile the library accepts for its kernel and row count."""
+    """The committed gfx950 tile table: its cutoffs are DECODE_LINEAR_MAX_M and
+    SIMT_DECODE_LINEAR_MAX_M, and every entry is a tile the library accepts for
+    its kernel and row count."""
     import json
 
     with open(kernels.TILE_TABLE_FILE) as f:
@@ -143,6 +144,8 @@ def test_tile_table_matches_the_dispatch_constants():
     assert table["arch"] == "gfx950"
     assert table["decode_linear_max_m"] == ops.DECODE_LINEAR_MAX_M
     assert 1 <= table["strict_max_m"] <= table["decode_linear_max_m"]
+    assert table["simt_decode_linear_max_m"] == ops.SIMT_DECODE_LINEAR_MAX_M
+    assert 1 <= table["simt_strict_max_m"] <= table["simt_decode_linear_max_m"]
     for key, (rows, waves, stages) in table["entries"].items():
         kind, shape, m = key.split(":")
         m = int(m[1:])
