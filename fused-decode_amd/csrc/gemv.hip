@@ -38,6 +38,7 @@
 // and weight stream with tiles placed so that both halves of every rotate-half
 // pair land in one workgroup, which applies RoPE in the epilogue.
 #include <mutex>
+#include <type_traits>
 
 #include "fd_dma.h"
 #include "fd_gemv.h"
@@ -542,6 +543,164 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_simt_kernel(
   stream_steps(p.total, a, b, issue, consume);
 }
 
+// Fused QKV on the persistent SIMT GEMV (gemv_simt_px_kernel). Every wave loads
+// its CPL K chunks of the M hidden rows into registers once; the workgroup adds
+// their sums of squares (one barrier) and each wave normalises its chunks in
+// place, round(x * inv * w) as stage_normed does. The tiles of R weight rows,
+// placed by TileRows<R> (R/2 rotate-half pairs of one head, or R consecutive
+// rows past rope_cols), then stream as in the GEMV with the normalised rows
+// in registers, and after the last tile the workgroup adds the waves' sums,
+// applies the bias, rounds, and rotates the pairs of rotated tiles.
+template <typename T, int M, int R, int CPL, bool NTW>
+__global__ __launch_bounds__(kMaxWaves * kWave) void qkv_px_kernel(
+    T* y, const T* x, const void* nwp, int nw_dtype, const T* w, int H, int N, float eps,
+    int tiles, Epi e, Rope rp) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int V = pow2_ceil(R * M);
+  constexpr int MP = pow2_ceil(M);
+  constexpr int P = R / 2;
+  extern __shared__ __align__(16) float pxs[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int nt = block_threads(), nw = nt / kWave;
+  const int g = (int)gridDim.x;
+  const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
+  float* parts = pxs;                                 // [my tile][wave][V]
+  float* ssq = pxs + (size_t)mine * nw * V;           // [wave][MP]
+  float* inv = ssq + kMaxWaves * MP;                  // [MP]
+  int kc[CPL];
+  bool kin[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int k = ((wave + c * nw) * kWave + lane) * 8;
+    kin[c] = k < H;
+    kc[c] = kin[c] ? k : 0;
+  }
+  const bool whole = ((wave + (CPL - 1) * nw) * kWave + kWave - 1) * 8 < H;
+
+  struct Regs {
+    V8 v[CPL][R];
+  };
+  auto issue = [&](Regs& q, int i) {
+    const TileRows<R> tr(rp, (int)blockIdx.x + i * g);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = tr.row(r);
+      const T* wr = n < N ? w + n * H : w;  // a wave-uniform row base
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) q.v[c][r] = load8w<NTW, T>(wr + kc[c]);
+    }
+  };
+  // the rows and the norm weight first, then the first tile's weights: the norm
+  // waits only for its own loads (they complete in issue order) while the tile
+  // streams (Llama-3-8B QKV, M = 5 / 8: 12.4 / 13.7 us, against 13.3 / 13.9
+  // with the tile issued first and 12.7 / 14.4 with two tiles issued here)
+  V8 xv[CPL][M];
+  float wf[CPL][8];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) xv[c][m] = load8<T>(x + (int64_t)m * H + kc[c]);
+    load8_norm_w(nwp, nw_dtype, kc[c], wf[c]);
+  }
+  Regs a, b;
+  if (mine > 0) issue(a, 0);
+  // RMSNorm: the rows' sums of squares over this lane's chunks (v_dot2 of each
+  // pair with itself), the waves', then the workgroup's; every wave normalises
+  // its own chunks (norm_frag: x * inv as one v_fma_mix for fp16)
+  float ss[MP];
+#pragma unroll
+  for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPL; ++c)
+    if (kin[c]) {
+#pragma unroll
+      for (int m = 0; m < M; ++m) {
+        const u32x4 u = __builtin_bit_cast(u32x4, xv[c][m]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ss[m] = sq_dot2<T>(u[j], ss[m]);
+      }
+    }
+  butterfly_sum<MP>(ss, lane);
+  if (butterfly_writer<MP>(lane)) ssq[wave * MP + butterfly_index<MP>(lane)] = ss[0];
+  __syncthreads();
+  if (tid < M) {
+    float s = 0.f;
+    for (int i = 0; i < nw; ++i) s += ssq[i * MP + tid];
+    inv[tid] = rsqrtf(s / (float)H + eps);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const u32x4 w0 = __builtin_bit_cast(u32x4, f32x4{wf[c][0], wf[c][1], wf[c][2], wf[c][3]});
+    const u32x4 w1 = __builtin_bit_cast(u32x4, f32x4{wf[c][4], wf[c][5], wf[c][6], wf[c][7]});
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      xv[c][m] = __builtin_bit_cast(V8, norm_frag<T>(__builtin_bit_cast(u32x4, xv[c][m]), inv[m], w0, w1));
+  }
+  auto consume = [&](const Regs& q, int i) {
+    float acc[V];
+    if (whole) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < M; ++m) acc[r * M + m] = dot8_first(q.v[0][r], xv[0][m]);
+#pragma unroll
+      for (int c = 1; c < CPL; ++c)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[c][r], xv[c][m], acc[r * M + m]);
+#pragma unroll
+      for (int j = R * M; j < V; ++j) acc[j] = 0.f;
+    } else {
+#pragma unroll
+      for (int j = 0; j < V; ++j) acc[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        if (kin[c]) {
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < M; ++m) acc[r * M + m] = dot8(q.v[c][r], xv[c][m], acc[r * M + m]);
+        }
+      }
+    }
+    butterfly_sum<V>(acc, lane);
+    if (butterfly_writer<V>(lane)) parts[(i * nw + wave) * V + butterfly_index<V>(lane)] = acc[0];
+  };
+  stream_steps(mine, a, b, issue, consume);
+  __syncthreads();
+  for (int t = tid; t < mine * R * M; t += nt) {
+    const int i = t / (R * M), rm = t % (R * M);
+    const TileRows<R> tr(rp, (int)blockIdx.x + i * g);
+    const float* pt = parts + (size_t)i * nw * V;
+    if (tr.rotated()) {
+      if (rm >= P * M) continue;  // one item per rotate-half pair
+      const int p = rm / M, m = rm % M;
+      float s1 = 0.f, s2 = 0.f;
+      for (int j = 0; j < nw; ++j) {
+        s1 += pt[j * V + p * M + m];
+        s2 += pt[j * V + (p + P) * M + m];
+      }
+      const int64_t n1 = tr.row(p), n2 = tr.row(p + P);
+      float o1, o2;
+      rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, s1, m, n1)), round_as<T>(epilogue(e, s2, m, n2)), o1,
+                o2);
+      y[m * (int64_t)N + n1] = from_f32<T>(o1);
+      y[m * (int64_t)N + n2] = from_f32<T>(o2);
+    } else {
+      const int r = rm / M, m = rm % M;
+      const int64_t n = tr.row(r);
+      if (n < N) {
+        float s = 0.f;
+        for (int j = 0; j < nw; ++j) s += pt[j * V + rm];
+        y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, s, m, n));
+      }
+    }
+  }
+}
+
 // MFMA form of the gate/up launch for M >= kMfmaMinM (M padded to 16): a tile of
 // 16 gate rows and the matching 16 up rows per workgroup, streamed with the
 // row-contiguous load + LDS relayout of gemv_mfma_relayout_kernel. B operand:
@@ -955,6 +1114,89 @@ int launch_qkv_simt(void* y, const void* hidden, const void* nw, int nw_dtype, c
     if (norm_in_regs(M, H, nwv * kWave)) return launch(qkv_simt_kernel<T, M, R, kNtWeights, true>);
   }
   return launch(qkv_simt_kernel<T, M, R, kNtWeights, false>);
+}
+
+// The persistent SIMT form of the fused QKV: the GEMV's launch shape (K chunks
+// per lane from simt_px_cpl, workgroups from simt_px_grid, rows per tile from
+// simt_px_rows, all even so rotated tiles hold whole pairs). Its LDS holds the
+// tiles' per-wave sums and the norm's per-wave sums of squares.
+template <typename T, int M, int R, int CPL>
+int launch_qkv_px_r(void* y, const void* hidden, const void* nw, int nw_dtype, const void* w, int H, int N,
+                    float eps, const Epi& e, Rope rp, hipStream_t st) {
+  constexpr int V = pow2_ceil(R * M), MP = pow2_ceil(M);
+  const int nwv = simt_px_waves(H, CPL);
+  rp.tiles = rp.cols / R;
+  const int tiles = rp.tiles + (N - rp.cols + R - 1) / R;
+  const int grid = simt_px_grid(N, M, tiles);
+  const int per = (tiles + grid - 1) / grid;
+  const size_t lds = sizeof(float) * ((size_t)per * nwv * V + kMaxWaves * MP + MP);
+  auto kernel = qkv_px_kernel<T, M, R, CPL, kNtWeights>;
+  if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(y),
+                     static_cast<const T*>(hidden), nw, nw_dtype, static_cast<const T*>(w), H, N, eps, tiles, e, rp);
+  return FD_OK;
+}
+
+// Chunks per lane and rows per tile of the persistent SIMT QKV, as the GEMV
+// would choose them for [N, H] weights; false where that kernel cannot take H
+// (more than 8 waves of 4 chunks) or its LDS sums.
+template <int M>
+bool qkv_px_shape(int N, int H, int& rows, int& cpl) {
+  cpl = simt_px_cpl(M, H, 0);
+  rows = simt_px_rows<M>(N, cpl);
+  while (cpl > 1 && !simt_px_regs_ok(M, rows, cpl) && simt_px_waves(H, cpl / 2) <= kMaxWaves) cpl /= 2;
+  return simt_px_fits(N, H, rows, M, cpl);
+}
+
+template <typename T, int M>
+int launch_qkv_px(void* y, const void* hidden, const void* nw, int nw_dtype, const void* w, int H, int N,
+                  float eps, const Epi& e, const Rope& rp, hipStream_t st) {
+  int rows = 0, cpl = 0;
+  if (!qkv_px_shape<M>(N, H, rows, cpl))
+    return set_error(FD_EUNSUPPORTED, "the persistent SIMT QKV does not take H = %d", H);
+  auto go = [&](auto rtag, auto ctag) -> int {
+    constexpr int RR = decltype(rtag)::value, CC = decltype(ctag)::value;
+    if constexpr (simt_px_regs_ok(M, RR, CC))
+      return launch_qkv_px_r<T, M, RR, CC>(y, hidden, nw, nw_dtype, w, H, N, eps, e, rp, st);
+    return set_error(FD_EUNSUPPORTED, "the persistent SIMT QKV's registers do not hold M = %d", M);
+  };
+  using R2 = std::integral_constant<int, 2>;
+  using R4 = std::integral_constant<int, 4>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C4 = std::integral_constant<int, 4>;
+  if (rows == 4) return cpl == 1 ? go(R4{}, C1{}) : cpl == 2 ? go(R4{}, C2{}) : go(R4{}, C4{});
+  return cpl == 1 ? go(R2{}, C1{}) : cpl == 2 ? go(R2{}, C2{}) : go(R2{}, C4{});
+}
+
+// Whether the persistent SIMT QKV takes this launch: kind simt up to
+// kQkvPxMaxM rows, kind dot up to kQkvPxDotMaxM (Llama-3-8B QKV, fp16: M = 1 /
+// 2 / 4 10.8 / 10.9 / 11.2 us against 11.0 / 11.7 / 14.5 for the per-tile SIMT
+// kernel; M = 5 / 6 12.4 / 12.5 against 13.4 / 13.5 for the MFMA kernel, which
+// ties it at M = 8: 13.8).
+constexpr int kQkvPxMaxM = 8;
+constexpr int kQkvPxDotMaxM = 6;
+inline bool qkv_px_takes(int M, int N, int H) {
+  int rows = 0, cpl = 0;
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return qkv_px_shape<MM>(N, H, rows, cpl);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+#undef FD_CASE
+    default: return false;
+  }
+}
+
+template <typename T>
+int launch_qkv_px_m(int M, void* y, const void* hidden, const void* nw, int nw_dtype, const void* w, int H,
+                    int N, float eps, const Epi& e, const Rope& rp, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return launch_qkv_px<T, MM>(y, hidden, nw, nw_dtype, w, H, N, eps, e, rp, st);
+    FD_CASE(1) FD_CASE(2) FD_CASE(3) FD_CASE(4) FD_CASE(5) FD_CASE(6) FD_CASE(7) FD_CASE(8)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "the persistent SIMT QKV takes M in [1, %d]", kQkvPxMaxM);
+  }
 }
 
 template <typename T>
@@ -1408,7 +1650,12 @@ int pre_attn_qkv_entry(void* y, void* normed, const void* hidden, const void* no
   if (H % 8 != 0) return set_error(FD_EUNSUPPORTED, "H must be a multiple of 8");
   hipStream_t st = static_cast<hipStream_t>(stream);
   int rc;
-  if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
+  if (M <= (kind == FD_KIND_SIMT ? kQkvPxMaxM : kQkvPxDotMaxM) && qkv_px_takes((int)M, (int)N, (int)H)) {
+    rc = act_dtype == FD_F16
+             ? launch_qkv_px_m<f16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H, (int)N, eps, e, rp, st)
+             : launch_qkv_px_m<bf16>((int)M, y, hidden, norm_w, norm_w_dtype, w_qkv, (int)H, (int)N, eps, e, rp, st);
+    if (rc != FD_OK) return rc;
+  } else if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
     FoldNorm fn{norm_w, norm_w_dtype, eps};
     if (rq) fn.sq = *rq;
