@@ -19,6 +19,8 @@
 // GEMV of fd_dma.h (codes decoded after their LDS read), the MLP's gate/up in a
 // relayout kernel that decodes the codes into an LDS tile.
 
+#include <type_traits>
+
 #include "fd_dma.h"
 #include "fd_gemv.h"
 #include "fd_internal.h"
@@ -132,6 +134,216 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_fp8_kernel(
       float s = 0.f;
       for (int i = 0; i < nw; ++i) s += part[i * V + t];
       y[m * sym + n * syn] = from_f32<T>(epilogue(e, s * wscale[n], m, n));
+    }
+  }
+}
+
+// v_dot2 of a pair with a pair and an inline-constant zero addend (the first
+// product of a sum: no register is zeroed first).
+__device__ __forceinline__ float dot2_first(uint32_t a, uint32_t b, f16) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float dot2_first(uint32_t a, uint32_t b, bf16) {
+  float r;
+  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// Persistent SIMT GEMV with E4M3 weights, the layout of gemv_simt_px_kernel
+// with one 16-byte load of 16 codes per lane, row and chunk: each wave keeps
+// its CPL 1024-element K chunks of the M activation rows in registers (8 pairs
+// per row and chunk), and the workgroup walks every gridDim-th tile of R rows,
+// decoding each lane's codes exactly to T pairs once per row before the M
+// rows' v_dot2s. After the last tile it adds the waves' sums and applies the
+// channel scale and the epilogue. QKV: the RMSNorm is applied to the
+// registers first (as qkv_px_kernel), the rows are placed by TileRows<R>, and
+// the epilogue scales, adds the bias, rounds and rotates (y is [M, N]).
+template <typename T, int M, int R, int CPL, bool QKV>
+__global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
+    T* y, const T* x, const uint8_t* w, const float* wscale, int N, int K, int64_t sxm, int64_t swn,
+    int64_t sym, int64_t syn, Epi e, int tiles, const void* nwp, int nw_dtype, float eps, Rope rp) {
+  constexpr int V = pow2_ceil(R * M);
+  constexpr int MP = pow2_ceil(M);
+  constexpr int P = R / 2;
+  extern __shared__ __align__(16) float pxs8[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int nt = block_threads(), nw = nt / kWave;
+  const int g = (int)gridDim.x;
+  const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
+  float* parts = pxs8;                        // [my tile][wave][V]
+  float* ssq = pxs8 + (size_t)mine * nw * V;  // QKV: [wave][MP], then inv[MP]
+  float* inv = ssq + kMaxWaves * MP;
+  int kc[CPL];
+  bool kin[CPL];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+    const int k = ((wave + c * nw) * kWave + lane) * 16;
+    kin[c] = k < K;
+    kc[c] = kin[c] ? k : 0;
+  }
+  const bool whole = ((wave + (CPL - 1) * nw) * kWave + kWave - 1) * 16 < K;
+  auto row_of = [&](int i, int r) -> int64_t {
+    const int tile = (int)blockIdx.x + i * g;
+    if constexpr (QKV)
+      return TileRows<R>(rp, tile).row(r);
+    else
+      return (int64_t)tile * R + r;
+  };
+  struct Regs {
+    u32x4 v[CPL][R];
+  };
+  auto issue = [&](Regs& q, int i) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t n = row_of(i, r);
+      const uint8_t* wr = n < N ? w + n * swn : w;  // a wave-uniform row base
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) q.v[c][r] = load16_nt(wr + kc[c]);
+    }
+  };
+  // the activation rows (and the norm weight) first, then the first tile
+  uint32_t xp[CPL][M][8];
+  float wf[QKV ? CPL : 1][16];
+#pragma unroll
+  for (int c = 0; c < CPL; ++c) {
+#pragma unroll
+    for (int m = 0; m < M; ++m) {
+      const u32x4 a = __builtin_bit_cast(u32x4, load8<T>(x + m * sxm + kc[c]));
+      const u32x4 b = __builtin_bit_cast(u32x4, load8<T>(x + m * sxm + kc[c] + 8));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xp[c][m][j] = a[j];
+        xp[c][m][j + 4] = b[j];
+      }
+    }
+    if constexpr (QKV) {
+      float lo[8], hi[8];
+      load8_norm_w(nwp, nw_dtype, kc[c], lo);
+      load8_norm_w(nwp, nw_dtype, kc[c] + 8, hi);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        wf[c][j] = lo[j];
+        wf[c][j + 8] = hi[j];
+      }
+    }
+  }
+  Regs a, b;
+  if (mine > 0) issue(a, 0);
+  if constexpr (QKV) {
+    float ss[MP];
+#pragma unroll
+    for (int m = 0; m < MP; ++m) ss[m] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+      if (kin[c]) {
+#pragma unroll
+        for (int m = 0; m < M; ++m)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss[m] = sq_dot2<T>(xp[c][m][j], ss[m]);
+      }
+    butterfly_sum<MP>(ss, lane);
+    if (butterfly_writer<MP>(lane)) ssq[wave * MP + butterfly_index<MP>(lane)] = ss[0];
+    __syncthreads();
+    if (tid < M) {
+      float sum = 0.f;
+      for (int i = 0; i < nw; ++i) sum += ssq[i * MP + tid];
+      inv[tid] = rsqrtf(sum / (float)K + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4 w0 = __builtin_bit_cast(u32x4, f32x4{wf[c][8 * h], wf[c][8 * h + 1], wf[c][8 * h + 2],
+                                                         wf[c][8 * h + 3]});
+        const u32x4 w1 = __builtin_bit_cast(u32x4, f32x4{wf[c][8 * h + 4], wf[c][8 * h + 5],
+                                                         wf[c][8 * h + 6], wf[c][8 * h + 7]});
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+          const u32x4 raw{xp[c][m][4 * h], xp[c][m][4 * h + 1], xp[c][m][4 * h + 2], xp[c][m][4 * h + 3]};
+          const u32x4 o = norm_frag<T>(raw, inv[m], w0, w1);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) xp[c][m][4 * h + j] = o[j];
+        }
+      }
+  }
+  auto consume = [&](const Regs& q, int i) {
+    float acc[V];
+#pragma unroll
+    for (int j = R * M; j < V; ++j) acc[j] = 0.f;
+    if (whole) {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          uint32_t pw[8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) fp8x4_to_pairs<T>(q.v[c][r][j], pw[2 * j], pw[2 * j + 1]);
+#pragma unroll
+          for (int m = 0; m < M; ++m) {
+            float s = c == 0 ? dot2_first(pw[0], xp[c][m][0], T{}) : dot2(pw[0], xp[c][m][0], acc[r * M + m], T{});
+#pragma unroll
+            for (int j = 1; j < 8; ++j) s = dot2(pw[j], xp[c][m][j], s, T{});
+            acc[r * M + m] = s;
+          }
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < R * M; ++j) acc[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+        if (kin[c]) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            uint32_t pw[8];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fp8x4_to_pairs<T>(q.v[c][r][j], pw[2 * j], pw[2 * j + 1]);
+#pragma unroll
+            for (int m = 0; m < M; ++m)
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc[r * M + m] = dot2(pw[j], xp[c][m][j], acc[r * M + m], T{});
+          }
+        }
+    }
+    butterfly_sum<V>(acc, lane);
+    if (butterfly_writer<V>(lane)) parts[(i * nw + wave) * V + butterfly_index<V>(lane)] = acc[0];
+  };
+  stream_steps(mine, a, b, issue, consume);
+  __syncthreads();
+  for (int t = tid; t < mine * R * M; t += nt) {
+    const int i = t / (R * M), rm = t % (R * M);
+    const float* pt = parts + (size_t)i * nw * V;
+    if constexpr (QKV) {
+      const TileRows<R> tr(rp, (int)blockIdx.x + i * g);
+      if (tr.rotated()) {
+        if (rm >= P * M) continue;  // one item per rotate-half pair
+        const int p = rm / M, m = rm % M;
+        float s1 = 0.f, s2 = 0.f;
+        for (int j = 0; j < nw; ++j) {
+          s1 += pt[j * V + p * M + m];
+          s2 += pt[j * V + (p + P) * M + m];
+        }
+        const int64_t n1 = tr.row(p), n2 = tr.row(p + P);
+        float o1, o2;
+        rope_pair(rp, m, tr.col(p), round_as<T>(epilogue(e, s1 * wscale[n1], m, n1)),
+                  round_as<T>(epilogue(e, s2 * wscale[n2], m, n2)), o1, o2);
+        y[m * (int64_t)N + n1] = from_f32<T>(o1);
+        y[m * (int64_t)N + n2] = from_f32<T>(o2);
+        continue;
+      }
+    }
+    const int r = rm / M, m = rm % M;
+    const int64_t n = row_of(i, r);
+    if (n < N) {
+      float sum = 0.f;
+      for (int j = 0; j < nw; ++j) sum += pt[j * V + rm];
+      if constexpr (QKV)
+        y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, sum * wscale[n], m, n));
+      else
+        y[m * sym + n * syn] = from_f32<T>(epilogue(e, sum * wscale[n], m, n));
     }
   }
 }
@@ -530,6 +742,119 @@ template <int M> struct Fp8QkvRows { static constexpr int R = M <= 2 ? 8 : 4; };
 constexpr int kFp8MfmaMinM = 5;
 
 
+// The persistent fp8 SIMT kernel (fp8_px_kernel): the fewest 1024-element
+// chunks per lane (1, 2 or 4) that keep K within eight waves, four rows per
+// tile where the registers hold them, else two; one workgroup per CU unless
+// N >= 8*M*CUs (each workgroup first reads M*K activations, as many bytes as
+// 2*M rows of codes). Used for M in [kFp8PxMinM, kFp8PxMaxM], where it beats
+// the per-tile SIMT kernels (Llama-3-8B shapes, M = 2 / 4: N = K = 4096 5.44 /
+// 5.86 us against 5.56 / 6.51; N = 6144 6.56 / 7.19 against 7.11 / 8.36;
+// K = 14336 12.8 / 12.9 against 13.4 / 16.1; N = 28672 20.6 / 22.2 against
+// 21.7 / 28.2; the fused QKV at M = 4 10.7 against 12.3). From 5 rows its
+// decode and v_dot2 work make it slower than the MFMA kernel (M = 8, N = 6144:
+// 9.1 against 8.6 us); at one row the two SIMT forms tie.
+constexpr int kFp8PxMinM = 2;
+constexpr int kFp8PxMaxM = 4;
+__host__ __device__ constexpr bool fp8_px_regs_ok(int M, int R, int cpl) {
+  return cpl * M * 8 + 8 * R * cpl + pow2_ceil(R * M) <= 224;
+}
+inline int fp8_px_waves(int K, int cpl) {
+  const int chunks = (K + kChunk8 - 1) / kChunk8;
+  return (chunks + cpl - 1) / cpl;
+}
+inline int fp8_px_grid(int N, int M, int tiles) {
+  const int cus = device_cus();
+  const int grid = (N < 8 * M * cus ? 1 : 2) * cus;
+  return grid < tiles ? grid : tiles;
+}
+template <int M>
+bool fp8_px_shape(int N, int K, bool qkv_cols, int& rows, int& cpl) {
+  if (K <= 0) return false;
+  const int chunks = (K + kChunk8 - 1) / kChunk8;
+  cpl = chunks <= kMaxWaves ? 1 : chunks <= 2 * kMaxWaves ? 2 : 4;
+  if (fp8_px_waves(K, cpl) > kMaxWaves) return false;
+  rows = fp8_px_regs_ok(M, 4, cpl) ? 4 : 2;
+  if (!fp8_px_regs_ok(M, rows, cpl)) return false;
+  (void)qkv_cols;
+  const int tiles = (N + rows - 1) / rows + 1;  // a QKV may split its rows into one more tile
+  const int grid = fp8_px_grid(N, M, tiles);
+  const int per = (tiles + grid - 1) / grid;
+  const size_t lds = sizeof(float) * ((size_t)per * fp8_px_waves(K, cpl) * pow2_ceil(rows * M) +
+                                      kMaxWaves * pow2_ceil(M) + pow2_ceil(M));
+  return lds <= kMaxLds / 2;
+}
+
+template <typename T, int M, int R, int CPL, bool QKV>
+int launch_fp8_px_r(void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
+                    int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype,
+                    float eps, Rope rp, hipStream_t st) {
+  constexpr int V = pow2_ceil(R * M), MP = pow2_ceil(M);
+  const int nwv = fp8_px_waves(K, CPL);
+  int tiles = (N + R - 1) / R;
+  if constexpr (QKV) {
+    rp.tiles = rp.cols / R;
+    tiles = rp.tiles + (N - rp.cols + R - 1) / R;
+  }
+  const int grid = fp8_px_grid(N, M, tiles);
+  const int per = (tiles + grid - 1) / grid;
+  const size_t lds = sizeof(float) * ((size_t)per * nwv * V + kMaxWaves * MP + MP);
+  auto kernel = fp8_px_kernel<T, M, R, CPL, QKV>;
+  if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(y), static_cast<const T*>(x),
+                     w, s, N, K, sxm, swn, sym, syn, e, tiles, nwp, nw_dtype, eps, rp);
+  return FD_OK;
+}
+
+template <typename T, int M, bool QKV>
+int launch_fp8_px(void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
+                  int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype, float eps,
+                  const Rope& rp, hipStream_t st) {
+  int rows = 0, cpl = 0;
+  if (!fp8_px_shape<M>(N, K, QKV, rows, cpl))
+    return set_error(FD_EUNSUPPORTED, "the persistent fp8 SIMT kernel does not take K = %d", K);
+  auto go = [&](auto rtag, auto ctag) -> int {
+    constexpr int RR = decltype(rtag)::value, CC = decltype(ctag)::value;
+    if constexpr (fp8_px_regs_ok(M, RR, CC))
+      return launch_fp8_px_r<T, M, RR, CC, QKV>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp,
+                                                st);
+    return set_error(FD_EUNSUPPORTED, "the persistent fp8 SIMT kernel's registers do not hold M = %d", M);
+  };
+  using R2 = std::integral_constant<int, 2>;
+  using R4 = std::integral_constant<int, 4>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C4 = std::integral_constant<int, 4>;
+  if (rows == 4) return cpl == 1 ? go(R4{}, C1{}) : cpl == 2 ? go(R4{}, C2{}) : go(R4{}, C4{});
+  return cpl == 1 ? go(R2{}, C1{}) : cpl == 2 ? go(R2{}, C2{}) : go(R2{}, C4{});
+}
+
+inline bool fp8_px_takes(int M, int N, int K, bool qkv) {
+  if (M < kFp8PxMinM || M > kFp8PxMaxM) return false;
+  int rows = 0, cpl = 0;
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM: return fp8_px_shape<MM>(N, K, qkv, rows, cpl);
+    FD_CASE(2) FD_CASE(3) FD_CASE(4)
+#undef FD_CASE
+    default: return false;
+  }
+}
+
+template <typename T, bool QKV>
+int launch_fp8_px_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
+                    int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype, float eps,
+                    const Rope& rp, hipStream_t st) {
+  switch (M) {
+#define FD_CASE(MM) \
+  case MM:                                                                                                     \
+    return launch_fp8_px<T, MM, QKV>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp, st);
+    FD_CASE(2) FD_CASE(3) FD_CASE(4)
+#undef FD_CASE
+    default: return set_error(FD_EINVAL, "the persistent fp8 SIMT kernel takes M in [%d, %d]", kFp8PxMinM,
+                              kFp8PxMaxM);
+  }
+}
+
 // The MFMA form (kFp8MfmaMinM rows and up): the DMA GEMV of fd_dma.h. `rp`
 // (fused QKV): tiles placed by TileRows<16> with RoPE in the epilogue; `fold`:
 // the RMSNorm of x folded in (x = raw activations).
@@ -710,9 +1035,19 @@ int linear_fp8_entry(void* y, const void* x, const void* w8, const float* w_scal
   e.ss = ss_out;  // the MFMA form writes it (the caller checked M)
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w8);
-  const int rc = act_dtype == FD_F16
-                     ? launch_gemv_fp8_m<f16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st)
-                     : launch_gemv_fp8_m<bf16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  int rc;
+  if (!ss_out && fp8_px_takes((int)M, (int)N, (int)K, false)) {
+    const Rope none{};
+    rc = act_dtype == FD_F16
+             ? launch_fp8_px_m<f16, false>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, nullptr,
+                                          FD_F32, 0.f, none, st)
+             : launch_fp8_px_m<bf16, false>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e,
+                                           nullptr, FD_F32, 0.f, none, st);
+  } else {
+    rc = act_dtype == FD_F16
+             ? launch_gemv_fp8_m<f16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st)
+             : launch_gemv_fp8_m<bf16>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, st);
+  }
   if (rc != FD_OK) return rc;
   return check_launch();
 }
@@ -867,7 +1202,14 @@ int pre_attn_qkv_fp8_entry(void* y, void* normed, const void* hidden, const void
   if (H % 16 != 0) return set_error(FD_EUNSUPPORTED, "the fp8 QKV needs H %% 16 == 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w_qkv8);
-  if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
+  if (fp8_px_takes((int)M, (int)N, (int)H, true)) {
+    const int rc = act_dtype == FD_F16
+                       ? launch_fp8_px_m<f16, true>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
+                                                    norm_w, norm_w_dtype, eps, rp, st)
+                       : launch_fp8_px_m<bf16, true>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
+                                                     norm_w, norm_w_dtype, eps, rp, st);
+    if (rc != FD_OK) return rc;
+  } else if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
     rp.tiles = (int)(rope_cols / 16);
     FoldNorm fn{norm_w, norm_w_dtype, eps};
     if (rq) fn.sq = *rq;

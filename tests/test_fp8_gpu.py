@@ -57,7 +57,7 @@ def test_quantizer_matches_oracle():
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("m", [1, 2, 5, 8, 13, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 13, 16])
 def test_linear_fp8_matches_oracle(dtype, m):
     import fused_decode as fd
 
@@ -84,6 +84,8 @@ def test_linear_fp8_llama_shapes(dtype, nk):
     torch.testing.assert_close(y[:2].float().cpu(), torch.from_numpy(ref), **tol(dtype))
     y1 = fd.linear_decode_fp8(x[:1].to(DEV), q, s)  # the M = 1 kernel gives the same row
     torch.testing.assert_close(y1.float().cpu(), torch.from_numpy(ref[:1]), **tol(dtype))
+    y4 = fd.linear_decode_fp8(x[:4].to(DEV), q, s)  # and the persistent SIMT kernel (2-4 rows)
+    torch.testing.assert_close(y4[:2].float().cpu(), torch.from_numpy(ref), **tol(dtype))
 
 
 def test_linear_fp8_fallback_shapes():
@@ -374,7 +376,7 @@ def test_pre_attn_qkv_fp8_matches_oracle(dtype, m):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("m", [1, 5, 8, 16])
+@pytest.mark.parametrize("m", [1, 3, 5, 8, 16])
 def test_pre_attn_qkv_fp8_norm_weight_in_other_dtypes(dtype, m):
     """A float32 or other-half-type norm weight: the folded MFMA path (5+ rows)
     converts it while staging each K chunk, the SIMT path per element."""
@@ -400,7 +402,7 @@ def test_pre_attn_qkv_fp8_several_tiles_per_workgroup(m):
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
 
 
-@pytest.mark.parametrize("m", [1, 8])
+@pytest.mark.parametrize("m", [1, 4, 8])
 def test_pre_attn_qkv_fp8_shared_angles_and_rope_cols_edges(m):
     """One cos/sin row for every token in each angle dtype; rope_cols 0 (norm +
     GEMV only) and N (every column rotated)."""

@@ -77,7 +77,7 @@ def oracle(hidden, norm_w, w, b, cos, sin, rope_cols, dtype, eps=1e-5):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("kind", ["dot", "simt"])
-@pytest.mark.parametrize("m", [1, 2, 5, 8, 11, 16])
+@pytest.mark.parametrize("m", [1, 2, 4, 5, 6, 7, 8, 11, 16])
 def test_pre_attn_qkv_matches_oracle(dtype, kind, m):
     hidden, nw, w, b, cos, sin, rc = case(m, 512, 4, 2, 64, dtype, seed=m)
     y = run(hidden, nw, w, b, cos, sin, rc, kind)
