@@ -157,16 +157,21 @@ __device__ __forceinline__ float dot2_first(uint32_t a, uint32_t b, bf16) {
 // per row and chunk), and the workgroup walks every gridDim-th tile of R rows,
 // decoding each lane's codes exactly to T pairs once per row before the M
 // rows' v_dot2s. After the last tile it adds the waves' sums and applies the
-// channel scale and the epilogue. QKV: the RMSNorm is applied to the
+// channel scale and the epilogue. kPxQkv: the RMSNorm is applied to the
 // registers first (as qkv_px_kernel), the rows are placed by TileRows<R>, and
 // the epilogue scales, adds the bias, rounds and rotates (y is [M, N]).
-template <typename T, int M, int R, int CPL, bool QKV>
+// kPxGateUp: the same RMSNorm; a tile is R/2 gate rows j.. and the matching up
+// rows I + j.. of w [2I, K] (N = 2I), and the epilogue writes
+// y[m, j] = round(silu(round(g * s_g)) * round(u * s_u)) into y [M, I].
+enum Fp8PxMode { kPxGemv = 0, kPxQkv = 1, kPxGateUp = 2 };
+template <typename T, int M, int R, int CPL, int MODE>
 __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
     T* y, const T* x, const uint8_t* w, const float* wscale, int N, int K, int64_t sxm, int64_t swn,
     int64_t sym, int64_t syn, Epi e, int tiles, const void* nwp, int nw_dtype, float eps, Rope rp) {
   constexpr int V = pow2_ceil(R * M);
   constexpr int MP = pow2_ceil(M);
-  constexpr int P = R / 2;
+  constexpr int P = R / 2;  // kPxQkv: pairs per rotated tile; kPxGateUp: gate rows per tile
+  const int I = N / 2;       // kPxGateUp: the gate (and up) rows
   extern __shared__ __align__(16) float pxs8[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -174,7 +179,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
   const int g = (int)gridDim.x;
   const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
   float* parts = pxs8;                        // [my tile][wave][V]
-  float* ssq = pxs8 + (size_t)mine * nw * V;  // QKV: [wave][MP], then inv[MP]
+  float* ssq = pxs8 + (size_t)mine * nw * V;  // norm: [wave][MP], then inv[MP]
   float* inv = ssq + kMaxWaves * MP;
   int kc[CPL];
   bool kin[CPL];
@@ -187,10 +192,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
   const bool whole = ((wave + (CPL - 1) * nw) * kWave + kWave - 1) * 16 < K;
   auto row_of = [&](int i, int r) -> int64_t {
     const int tile = (int)blockIdx.x + i * g;
-    if constexpr (QKV)
+    if constexpr (MODE == kPxQkv) {
       return TileRows<R>(rp, tile).row(r);
-    else
+    } else if constexpr (MODE == kPxGateUp) {
+      const int64_t j = (int64_t)tile * P + (r % P);
+      return r < P ? j : I + j;  // rows past I: loaded, never stored
+    } else {
       return (int64_t)tile * R + r;
+    }
   };
   struct Regs {
     u32x4 v[CPL][R];
@@ -206,7 +215,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
   };
   // the activation rows (and the norm weight) first, then the first tile
   uint32_t xp[CPL][M][8];
-  float wf[QKV ? CPL : 1][16];
+  float wf[MODE != kPxGemv ? CPL : 1][16];
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
 #pragma unroll
@@ -219,7 +228,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
         xp[c][m][j + 4] = b[j];
       }
     }
-    if constexpr (QKV) {
+    if constexpr (MODE != kPxGemv) {
       float lo[8], hi[8];
       load8_norm_w(nwp, nw_dtype, kc[c], lo);
       load8_norm_w(nwp, nw_dtype, kc[c] + 8, hi);
@@ -232,7 +241,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
   }
   Regs a, b;
   if (mine > 0) issue(a, 0);
-  if constexpr (QKV) {
+  if constexpr (MODE != kPxGemv) {
     float ss[MP];
 #pragma unroll
     for (int m = 0; m < MP; ++m) ss[m] = 0.f;
@@ -313,10 +322,27 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
   };
   stream_steps(mine, a, b, issue, consume);
   __syncthreads();
+  if constexpr (MODE == kPxGateUp) {
+    for (int t = tid; t < mine * P * M; t += nt) {
+      const int i = t / (P * M), rm = t % (P * M);
+      const float* pt = parts + (size_t)i * nw * V;
+      const int r = rm / M, m = rm % M;
+      const int64_t j = (int64_t)((int)blockIdx.x + i * g) * P + r;
+      if (j < I) {
+        float gs = 0.f, us = 0.f;
+        for (int q = 0; q < nw; ++q) {
+          gs += pt[q * V + rm];
+          us += pt[q * V + P * M + rm];
+        }
+        y[m * (int64_t)I + j] = swiglu_out<T>(gs * wscale[j], us * wscale[I + j]);
+      }
+    }
+    return;
+  }
   for (int t = tid; t < mine * R * M; t += nt) {
     const int i = t / (R * M), rm = t % (R * M);
     const float* pt = parts + (size_t)i * nw * V;
-    if constexpr (QKV) {
+    if constexpr (MODE == kPxQkv) {
       const TileRows<R> tr(rp, (int)blockIdx.x + i * g);
       if (tr.rotated()) {
         if (rm >= P * M) continue;  // one item per rotate-half pair
@@ -340,7 +366,7 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void fp8_px_kernel(
     if (n < N) {
       float sum = 0.f;
       for (int j = 0; j < nw; ++j) sum += pt[j * V + rm];
-      if constexpr (QKV)
+      if constexpr (MODE == kPxQkv)
         y[m * (int64_t)N + n] = from_f32<T>(epilogue(e, sum * wscale[n], m, n));
       else
         y[m * sym + n * syn] = from_f32<T>(epilogue(e, sum * wscale[n], m, n));
@@ -768,14 +794,13 @@ inline int fp8_px_grid(int N, int M, int tiles) {
   return grid < tiles ? grid : tiles;
 }
 template <int M>
-bool fp8_px_shape(int N, int K, bool qkv_cols, int& rows, int& cpl) {
+bool fp8_px_shape(int N, int K, int& rows, int& cpl) {
   if (K <= 0) return false;
   const int chunks = (K + kChunk8 - 1) / kChunk8;
   cpl = chunks <= kMaxWaves ? 1 : chunks <= 2 * kMaxWaves ? 2 : 4;
   if (fp8_px_waves(K, cpl) > kMaxWaves) return false;
   rows = fp8_px_regs_ok(M, 4, cpl) ? 4 : 2;
   if (!fp8_px_regs_ok(M, rows, cpl)) return false;
-  (void)qkv_cols;
   const int tiles = (N + rows - 1) / rows + 1;  // a QKV may split its rows into one more tile
   const int grid = fp8_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
@@ -784,38 +809,40 @@ bool fp8_px_shape(int N, int K, bool qkv_cols, int& rows, int& cpl) {
   return lds <= kMaxLds / 2;
 }
 
-template <typename T, int M, int R, int CPL, bool QKV>
+template <typename T, int M, int R, int CPL, int MODE>
 int launch_fp8_px_r(void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
                     int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype,
                     float eps, Rope rp, hipStream_t st) {
   constexpr int V = pow2_ceil(R * M), MP = pow2_ceil(M);
   const int nwv = fp8_px_waves(K, CPL);
   int tiles = (N + R - 1) / R;
-  if constexpr (QKV) {
+  if constexpr (MODE == kPxQkv) {
     rp.tiles = rp.cols / R;
     tiles = rp.tiles + (N - rp.cols + R - 1) / R;
+  } else if constexpr (MODE == kPxGateUp) {
+    tiles = (N / 2 + R / 2 - 1) / (R / 2);
   }
   const int grid = fp8_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
   const size_t lds = sizeof(float) * ((size_t)per * nwv * V + kMaxWaves * MP + MP);
-  auto kernel = fp8_px_kernel<T, M, R, CPL, QKV>;
+  auto kernel = fp8_px_kernel<T, M, R, CPL, MODE>;
   if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(nwv * kWave), lds, st, static_cast<T*>(y), static_cast<const T*>(x),
                      w, s, N, K, sxm, swn, sym, syn, e, tiles, nwp, nw_dtype, eps, rp);
   return FD_OK;
 }
 
-template <typename T, int M, bool QKV>
+template <typename T, int M, int MODE>
 int launch_fp8_px(void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
                   int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype, float eps,
                   const Rope& rp, hipStream_t st) {
   int rows = 0, cpl = 0;
-  if (!fp8_px_shape<M>(N, K, QKV, rows, cpl))
+  if (!fp8_px_shape<M>(N, K, rows, cpl))
     return set_error(FD_EUNSUPPORTED, "the persistent fp8 SIMT kernel does not take K = %d", K);
   auto go = [&](auto rtag, auto ctag) -> int {
     constexpr int RR = decltype(rtag)::value, CC = decltype(ctag)::value;
     if constexpr (fp8_px_regs_ok(M, RR, CC))
-      return launch_fp8_px_r<T, M, RR, CC, QKV>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp,
+      return launch_fp8_px_r<T, M, RR, CC, MODE>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp,
                                                 st);
     return set_error(FD_EUNSUPPORTED, "the persistent fp8 SIMT kernel's registers do not hold M = %d", M);
   };
@@ -828,26 +855,26 @@ int launch_fp8_px(void* y, const void* x, const uint8_t* w, const float* s, int 
   return cpl == 1 ? go(R2{}, C1{}) : cpl == 2 ? go(R2{}, C2{}) : go(R2{}, C4{});
 }
 
-inline bool fp8_px_takes(int M, int N, int K, bool qkv) {
+inline bool fp8_px_takes(int M, int N, int K) {
   if (M < kFp8PxMinM || M > kFp8PxMaxM) return false;
   int rows = 0, cpl = 0;
   switch (M) {
 #define FD_CASE(MM) \
-  case MM: return fp8_px_shape<MM>(N, K, qkv, rows, cpl);
+  case MM: return fp8_px_shape<MM>(N, K, rows, cpl);
     FD_CASE(2) FD_CASE(3) FD_CASE(4)
 #undef FD_CASE
     default: return false;
   }
 }
 
-template <typename T, bool QKV>
+template <typename T, int MODE>
 int launch_fp8_px_m(int M, void* y, const void* x, const uint8_t* w, const float* s, int N, int K, int64_t sxm,
                     int64_t swn, int64_t sym, int64_t syn, const Epi& e, const void* nwp, int nw_dtype, float eps,
                     const Rope& rp, hipStream_t st) {
   switch (M) {
 #define FD_CASE(MM) \
   case MM:                                                                                                     \
-    return launch_fp8_px<T, MM, QKV>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp, st);
+    return launch_fp8_px<T, MM, MODE>(y, x, w, s, N, K, sxm, swn, sym, syn, e, nwp, nw_dtype, eps, rp, st);
     FD_CASE(2) FD_CASE(3) FD_CASE(4)
 #undef FD_CASE
     default: return set_error(FD_EINVAL, "the persistent fp8 SIMT kernel takes M in [%d, %d]", kFp8PxMinM,
@@ -1036,12 +1063,12 @@ int linear_fp8_entry(void* y, const void* x, const void* w8, const float* w_scal
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w8);
   int rc;
-  if (!ss_out && fp8_px_takes((int)M, (int)N, (int)K, false)) {
+  if (!ss_out && fp8_px_takes((int)M, (int)N, (int)K)) {
     const Rope none{};
     rc = act_dtype == FD_F16
-             ? launch_fp8_px_m<f16, false>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, nullptr,
+             ? launch_fp8_px_m<f16, kPxGemv>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e, nullptr,
                                           FD_F32, 0.f, none, st)
-             : launch_fp8_px_m<bf16, false>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e,
+             : launch_fp8_px_m<bf16, kPxGemv>((int)M, y, x, w, w_scale, (int)N, (int)K, sxm, swn, sym, syn, e,
                                            nullptr, FD_F32, 0.f, none, st);
   } else {
     rc = act_dtype == FD_F16
@@ -1132,6 +1159,15 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
                   : run(mlp_gate_up_fp8_relayout_kernel<f16, false, true>,
                         mlp_gate_up_fp8_relayout_kernel<bf16, false, true>);
     if (rc != FD_OK) return rc;
+  } else if (fp8_px_takes((int)M, (int)(2 * I), (int)H)) {
+    const Epi none_e{};
+    const Rope none{};
+    rc = act_dtype == FD_F16
+             ? launch_fp8_px_m<f16, kPxGateUp>((int)M, mid, hidden, wgu, gate_up_scale, (int)(2 * I), (int)H, H, H,
+                                               I, 1, none_e, norm_w, norm_w_dtype, eps, none, st)
+             : launch_fp8_px_m<bf16, kPxGateUp>((int)M, mid, hidden, wgu, gate_up_scale, (int)(2 * I), (int)H, H,
+                                                H, I, 1, none_e, norm_w, norm_w_dtype, eps, none, st);
+    if (rc != FD_OK) return rc;
   } else {
     rc = act_dtype == FD_F16
              ? launch_mlp_fp8_m<f16>((int)M, mid, hidden, norm_w, norm_w_dtype, wgu,
@@ -1150,9 +1186,18 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
   e.srn = 1;
   e.ss = ss_out;
   const uint8_t* wd = static_cast<const uint8_t*>(w_down8);
-  rc = act_dtype == FD_F16
-           ? launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st)
-           : launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  if (!ss_out && fp8_px_takes((int)M, (int)H, (int)I)) {
+    const Rope none{};
+    rc = act_dtype == FD_F16
+             ? launch_fp8_px_m<f16, kPxGemv>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, nullptr,
+                                             FD_F32, 0.f, none, st)
+             : launch_fp8_px_m<bf16, kPxGemv>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e,
+                                              nullptr, FD_F32, 0.f, none, st);
+  } else {
+    rc = act_dtype == FD_F16
+             ? launch_gemv_fp8_m<f16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st)
+             : launch_gemv_fp8_m<bf16>((int)M, y, mid, wd, down_scale, (int)H, (int)I, I, I, H, 1, e, st);
+  }
   if (rc != FD_OK) return rc;
   return check_launch();
 }
@@ -1202,11 +1247,11 @@ int pre_attn_qkv_fp8_entry(void* y, void* normed, const void* hidden, const void
   if (H % 16 != 0) return set_error(FD_EUNSUPPORTED, "the fp8 QKV needs H %% 16 == 0");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint8_t* w = static_cast<const uint8_t*>(w_qkv8);
-  if (fp8_px_takes((int)M, (int)N, (int)H, true)) {
+  if (fp8_px_takes((int)M, (int)N, (int)H)) {
     const int rc = act_dtype == FD_F16
-                       ? launch_fp8_px_m<f16, true>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
+                       ? launch_fp8_px_m<f16, kPxQkv>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
                                                     norm_w, norm_w_dtype, eps, rp, st)
-                       : launch_fp8_px_m<bf16, true>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
+                       : launch_fp8_px_m<bf16, kPxQkv>((int)M, y, hidden, w, w_scale, (int)N, (int)H, H, H, N, 1, e,
                                                      norm_w, norm_w_dtype, eps, rp, st);
     if (rc != FD_OK) return rc;
   } else if (mfma) {  // one launch: the RMSNorm folded into the MFMA kernel
