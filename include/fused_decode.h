@@ -131,11 +131,13 @@ int fd_linear(void* y, const void* x, const void* w, const void* bias, int bias_
 /*
  * GEMV tiling: weight rows per workgroup, which also names the kernel (2, 4 or 8:
  * the SIMT kernel, 8 only up to M = 8; 16: the MFMA kernel, kind FD_KIND_DOT
- * only), waves per workgroup (SIMT 1..8; MFMA 2, 4 or 8) and, for the MFMA
- * kernel, K units of 128 each wave keeps in flight in its LDS ring (1..3; 2 by
- * default; waves x units must fit one CU's LDS). 0 = the library's default for
- * that field; with rows 0 the kernel is chosen as in fd_linear (MFMA for kind
- * FD_KIND_DOT from M = 5).
+ * only), waves per workgroup (SIMT 1..8; MFMA 2, 4 or 8) and stages: for the
+ * MFMA kernel, K units of 128 each wave keeps in flight in its LDS ring (1..3; 2
+ * by default; waves x units must fit one CU's LDS); for the SIMT kernel its form
+ * (0 the library's choice, 1 one workgroup per tile, 2 the persistent kernel that
+ * keeps the activations in registers, whose waves then set how many 512-element
+ * K chunks each lane holds). 0 = the library's default for that field; with rows
+ * 0 the kernel is chosen as in fd_linear (MFMA for kind FD_KIND_DOT from M = 5).
  */
 typedef struct fd_tile {
   int rows;
@@ -221,11 +223,13 @@ int fd_mlp_gate_up(void* mid, void* normed, const void* hidden, const void* norm
  * [M,N] are contiguous; bias ([N], bias_dtype) may be NULL. rope_cols is a
  * multiple of head_dim (0: no rotation); this build needs head_dim % 16 == 0 and
  * H % 8 == 0 (FD_EUNSUPPORTED otherwise: compose fd_rms_norm, fd_linear, fd_rope).
- * With kind FD_KIND_DOT from M = 5 the projection runs on MFMA with the RMSNorm
+ * With kind FD_KIND_DOT from M = 7 the projection runs on MFMA with the RMSNorm
  * folded into the kernel (any H when norm_w has act_dtype, which streams with
  * the weights; another norm_w dtype is staged in LDS as float32, which takes H
  * up to about 22,000, FD_EUNSUPPORTED beyond); below that, or with
- * FD_KIND_SIMT, a SIMT kernel normalises in its prologue. `normed` is unused at
+ * FD_KIND_SIMT, a SIMT kernel normalises in its prologue (up to 8 rows the
+ * persistent one, which holds the normalised rows in registers, where H fits
+ * eight waves of up to four 512-element chunks per lane). `normed` is unused at
  * every M and may be NULL (it stays in the signature for callers written against
  * earlier builds).
  * No reference counterpart as one call: it fuses the composition a caller of the
@@ -263,7 +267,8 @@ int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
  * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
  * rounding points as fd_post_attn_mlp. Two launches at every M (fused RMSNorm +
  * gate/up + SwiGLU, from M = 5 on MFMA with the norm weight staged in LDS, which
- * takes H up to about 38,000: FD_EUNSUPPORTED beyond, then down + residual);
+ * takes H up to about 38,000: FD_EUNSUPPORTED beyond, at 2-4 rows the persistent
+ * SIMT kernel; then down + residual);
  * `mid` is caller scratch of M*I activations. y, mid and hidden must not share
  * memory (FD_EINVAL). H % 16 == 0 and I % 16 == 0. No reference counterpart (see
  * fd_linear_fp8).
@@ -277,8 +282,9 @@ int fd_post_attn_mlp_fp8(void* y, void* mid, const void* hidden, const void* nor
  * fd_pre_attn_qkv with FP8 weights: w_qkv8 [N,H] E4M3 codes (contiguous) with
  * per-row float32 scales w_scale [N]; the projection is fd_linear_fp8's product
  * and everything else (RMSNorm, bias, rounding, RoPE of the first rope_cols
- * columns, cos/sin layout) is fd_pre_attn_qkv's. One launch at every M (from
- * M = 5 the MFMA form, with the RMSNorm folded in); `normed` is unused and may
+ * columns, cos/sin layout) is fd_pre_attn_qkv's. One launch at every M (at 2-4
+ * rows the persistent SIMT kernel, from M = 5 the MFMA form, each with the
+ * RMSNorm folded in); `normed` is unused and may
  * be NULL (kept for the fp16 entry point's signature). H % 16 == 0 and
  * head_dim % 16 == 0 (else FD_EUNSUPPORTED). No reference counterpart (see
  * fd_linear_fp8 and fd_pre_attn_qkv).
@@ -309,7 +315,9 @@ int fd_pre_attn_qkv_fp8(void* y, void* normed, const void* hidden, const void* n
  * fd_linear_sumsq: fd_linear plus ss_out (non-NULL).
  * fd_post_attn_mlp_sumsq: fd_post_attn_mlp; ss_in may be NULL (the MLP then
  *   normalises as in fd_post_attn_mlp), ss_out may be NULL.
- * fd_pre_attn_qkv_sumsq: fd_pre_attn_qkv without `normed`, ss_in non-NULL.
+ * fd_pre_attn_qkv_sumsq: fd_pre_attn_qkv without `normed`, ss_in non-NULL (at 5-6
+ *   rows the persistent SIMT QKV runs, which sums the squares of the rows it holds
+ *   in registers anyway and does not read ss_in).
  * The _fp8 forms are the same over fd_linear_fp8, fd_post_attn_mlp_fp8 and
  * fd_pre_attn_qkv_fp8.
  */
