@@ -173,6 +173,26 @@ def test_post_attn_mlp_fp8_wide_hidden_composes():
     torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(torch.float16))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("i_", [2064, 4096])
+def test_post_attn_mlp_fp8_resident_rows_form(dtype, i_):
+    """H a multiple of 512 and 5-8 rows: the E4M3 gate/up runs its persistent
+    form (row scales staged per tile iteration, the normalised rows resident
+    in LDS); I = 2064 splits the tiles unevenly, I = 4096 two per workgroup."""
+    import fused_decode as fd
+
+    h = 512
+    gq, gs, gqn, gsn = quant(rnd(2 * i_, h, seed=70, scale=h ** -0.5))
+    dq, ds, dqn, dsn = quant(rnd(h, i_, seed=71, scale=i_ ** -0.5))
+    for m in (5, 6, 7, 8):
+        for nw_dtype in (torch.float32, dtype):
+            hid = rnd(m, h, seed=72 + m, dtype=dtype)
+            nw = rnd(h, seed=80 + m, dtype=nw_dtype, scale=0.1, mean=1.0)
+            y = fd.post_attn_mlp_fp8(hid.to(DEV), nw.to(DEV), gq, gs, dq, ds, 1e-5)
+            ref = O.post_attn_mlp_fp8(npf(hid), npf(nw), gqn, gsn, dqn, dsn, 1e-5, tag(dtype))
+            torch.testing.assert_close(y.float().cpu(), torch.from_numpy(ref), **tol(dtype))
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_post_attn_mlp_fp8_several_tiles_per_workgroup(m):
     """I = 6144 with 4-row tiles: 1536 tiles over two workgroups per CU, so each
