@@ -127,20 +127,29 @@ __global__ __launch_bounds__(NW * kWave) void gate_up_res_kernel(T* mid, const T
     wrw[i] = row;
     wch[i] = ((lane % G.cpr) ^ (row % G.cpr)) * G.epc;
   }
-  auto wrow_of = [&](int t, int row) -> const W* {
-    const int64_t n = row < 8 ? (int64_t)8 * t + row : (int64_t)I + 8 * t + (row - 8);
-    return w + n * (int64_t)K;
+  // this lane's chunk of the issue tile's rows at the wave's first unit; a unit
+  // adds only its K offset (the row addresses change once per tile)
+  const W* wb[G.aops];
+  auto set_tile = [&](int itile) {
+    const int t = (int)blockIdx.x + itile * (int)gridDim.x;
+#pragma unroll
+    for (int i = 0; i < G.aops; ++i) {
+      const int row = wrw[i];
+      const int64_t n = row < 8 ? (int64_t)8 * t + row : (int64_t)I + 8 * t + (row - 8);
+      wb[i] = w + n * (int64_t)K + wave * kUnit + wch[i];
+    }
   };
-  int it = 0, iu = 0;  // issue cursor: tile iteration, unit of this wave
+  set_tile(0);
+  int it = 0, iu = 0, koff = 0;  // issue cursor: tile iteration, unit of this wave, its K offset
   auto issue = [&](int slot) {
-    const int t = (int)blockIdx.x + it * (int)gridDim.x;
-    const int k0 = (wave + iu * NW) * kUnit;
     u32x4* dst = ring[wave][slot];
 #pragma unroll
-    for (int i = 0; i < G.aops; ++i) dma16_nt(wrow_of(t, wrw[i]) + k0 + wch[i], dst + i * kWave);
+    for (int i = 0; i < G.aops; ++i) dma16_nt(wb[i] + koff, dst + i * kWave);
+    koff += NW * kUnit;
     if (++iu == mine) {
       iu = 0;
-      ++it;
+      koff = 0;
+      if (++it < ntw) set_tile(it);
     }
   };
 #pragma unroll

@@ -288,25 +288,38 @@ def bench_linear(dtype, roof, quick, cpu) -> list[dict]:
     return rows
 
 
-def one_gemv(m: int, n: int, kk: int, kind: str, dtype, replays: int = 20) -> dict:
+def one_gemv(m: int, n: int, kk: int, kind: str, dtype, replays: int = 20, fp8: bool = False) -> dict:
     """One decode GEMV alone: device time per call from a HIP graph over rotated
     weights (the ops block's `dev_us`), beside a read of the same bytes timed the
-    same way. A profiler run over it sees only this kernel and the read."""
+    same way. A profiler run over it sees only this kernel and the read. With
+    `fp8` the weights are E4M3 codes with float32 row scales (`linear_decode_fp8`)."""
     e = torch.empty((), dtype=dtype).element_size()
     g = torch.Generator(device="cuda").manual_seed(1)
-    k = copies_for(n * kk * e)
-    ws = [_gen((n, kk), dtype, g, kk ** -0.5) for _ in range(k)]
-    x = _gen((m, kk), dtype, g)
-    out = torch.empty(m, n, device="cuda", dtype=dtype)
-    dev = graph_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), k, replays)
+    if fp8:
+        from .fp8 import linear_decode_fp8, quantize_fp8
+
+        k = copies_for(n * kk)
+        ws = [quantize_fp8(_gen((n, kk), dtype, g, kk ** -0.5)) for _ in range(k)]
+        x = _gen((m, kk), dtype, g)
+        out = torch.empty(m, n, device="cuda", dtype=dtype)
+        dev = graph_us(lambda i: linear_decode_fp8(x, *ws[i % k], out=out), k, replays)
+        wbytes = n * kk + 4 * n
+    else:
+        k = copies_for(n * kk * e)
+        ws = [_gen((n, kk), dtype, g, kk ** -0.5) for _ in range(k)]
+        x = _gen((m, kk), dtype, g)
+        out = torch.empty(m, n, device="cuda", dtype=dtype)
+        dev = graph_us(lambda i: linear_decode(x, ws[i % k], out=out, kind=kind), k, replays)
+        wbytes = n * kk * e
     del ws
     torch.cuda.empty_cache()
-    nbytes = (m * kk + n * kk + m * n) * e
+    nbytes = wbytes + (m * kk + m * n) * e
     kr = copies_for(nbytes)
     srcs = [torch.zeros(nbytes // 16 * 16, dtype=torch.uint8, device="cuda") for _ in range(kr)]
     flag = torch.zeros(1, dtype=torch.int32, device="cuda")
     read = graph_us(lambda i: launch_read(srcs[i % kr], flag), kr, replays)
-    row = {"op": "linear_decode", "shape": [m, n, kk], "dtype": str(dtype).replace("torch.", ""), "kind": kind,
+    row = {"op": "linear_decode_fp8" if fp8 else "linear_decode", "shape": [m, n, kk],
+           "dtype": str(dtype).replace("torch.", ""), "kind": "e4m3" if fp8 else kind,
            "bytes": nbytes, "dev_us": round(dev, 3), "gbs": round(nbytes / dev / 1e3, 1),
            "same_size_read_us": round(read, 3), "pct_same_size": round(100 * read / dev, 1)}
     print(json.dumps(row), flush=True)
@@ -919,6 +932,7 @@ def main() -> None:
     ap.add_argument("--gemv", default=None, metavar="M,N,K",
                     help="time one GEMV (with --kind, --dtype, --replays) beside a same-size read and exit")
     ap.add_argument("--kind", choices=["dot", "simt"], default="dot")
+    ap.add_argument("--fp8", action="store_true", help="with --gemv: E4M3 weights (linear_decode_fp8)")
     ap.add_argument("--replays", type=int, default=20)
     ap.add_argument("--trace-gaps", default=None, metavar="CSV",
                     help="summarise a rocprofv3 kernel trace of --only graph and exit")
@@ -935,7 +949,8 @@ def main() -> None:
     torch.cuda.set_device(0)
     if args.gemv:
         m, n, kk = (int(v) for v in args.gemv.split(","))
-        one_gemv(m, n, kk, args.kind, torch.bfloat16 if args.dtype == "bf16" else torch.float16, args.replays)
+        one_gemv(m, n, kk, args.kind, torch.bfloat16 if args.dtype == "bf16" else torch.float16, args.replays,
+                 args.fp8)
         return
     if args.tune:
         tune(torch.float16 if args.dtype != "bf16" else torch.bfloat16, args.tune_out)
