@@ -267,8 +267,10 @@ int fd_linear_fp8(void* y, const void* x, const void* w8, const float* w_scale,
  * down_scale [H]; each projection is fd_linear_fp8's product, with the same four
  * rounding points as fd_post_attn_mlp. Two launches at every M (fused RMSNorm +
  * gate/up + SwiGLU, from M = 5 on MFMA with the norm weight staged in LDS, which
- * takes H up to about 38,000: FD_EUNSUPPORTED beyond, at 2-4 rows the persistent
- * SIMT kernel; then down + residual);
+ * takes H up to about 38,000: FD_EUNSUPPORTED beyond; at 5-8 rows with H a
+ * multiple of 512 and a float32 or activation-type norm weight the persistent
+ * MFMA form, one workgroup per CU with the normalised rows resident in LDS; at
+ * 2-4 rows the persistent SIMT kernel; then down + residual);
  * `mid` is caller scratch of M*I activations. y, mid and hidden must not share
  * memory (FD_EINVAL). H % 16 == 0 and I % 16 == 0. No reference counterpart (see
  * fd_linear_fp8).
