@@ -174,11 +174,12 @@ def test_post_attn_mlp_fp8_wide_hidden_composes():
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("i_", [2064, 4096])
+@pytest.mark.parametrize("i_", [64, 2064, 4096])
 def test_post_attn_mlp_fp8_resident_rows_form(dtype, i_):
     """H a multiple of 512 and 5-8 rows: the E4M3 gate/up runs its persistent
     form (row scales staged per tile iteration, the normalised rows resident
-    in LDS); I = 2064 splits the tiles unevenly, I = 4096 two per workgroup."""
+    in LDS); I = 64 has fewer tiles (8) than CUs, I = 2064 splits the tiles
+    unevenly, I = 4096 gives every workgroup two."""
     import fused_decode as fd
 
     h = 512
