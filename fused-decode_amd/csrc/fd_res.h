@@ -1,5 +1,7 @@
 // Persistent MFMA gate/up with resident activations, for 5-8 activation rows
-// (the MLP's fused RMSNorm + gate/up + SwiGLU; fp16/bf16 or E4M3 weights).
+// (the MLP's fused RMSNorm + gate/up + SwiGLU). Written for fp16/bf16 and E4M3
+// weights; the library launches it for E4M3 weights (with fp16/bf16 weights it
+// ties the relayout kernel).
 //
 // One workgroup per CU walks the tiles blockIdx.x, blockIdx.x + gridDim.x, ...
 // of the gate/up weights [2I, K]: tile t is gate rows 8t..8t+7 and up rows
@@ -11,13 +13,13 @@
 // stream running on across tile boundaries, and reads its B fragments from the
 // resident rows. At M = 8 the per-unit activation re-reads of the one-tile
 // workgroups are half (E4M3) or a third (fp16) of the L2 requests a CU keeps
-// outstanding, and those requests, not bytes or instructions, are what the
-// narrow-M MFMA GEMVs wait on; resident rows are read from L2 once per CU.
+// outstanding, which the weight stream then cannot use; resident rows are read
+// from L2 once per CU.
 //
 // Layout of the resident rows: row r holds its 16-byte chunks with chunk c at
 // slot c ^ (r & 7), so the 8 lanes of a B read (8 rows, one chunk) hit distinct
 // bank groups. Rows past M copy row 0 and get inv_rms 0 (zero B columns, never
-// stored); chunks past K are zero.
+// stored). K is a multiple of 512, so no unit or DMA instruction crosses it.
 //
 // At the end of a tile every wave leaves its partial sums in one of two LDS
 // buffers (consecutive tiles alternate; they take the norm weight's place once
