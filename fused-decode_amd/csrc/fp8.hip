@@ -894,11 +894,12 @@ int launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const 
   const Rope none{};
   const unsigned blocks =
       rp ? (unsigned)(rp->tiles + (N - rp->cols + 15) / 16) : (unsigned)((N + 15) / 16);
-  // The fused QKV at 5-8 rows: eight waves, two units in flight each, where K
-  // gives every wave a unit (Llama-3-8B widths with the producer's row sums,
-  // M = 5 / 8: 10.3 / 10.9 -> 10.1 / 10.6 us; with 16 rows the larger B tiles
-  // would leave one such workgroup per CU: 13.2 -> 16.9)
-  if (rp && fold && dma_rows(M) <= 8 && (K + kUnit - 1) / kUnit >= 8)
+  // The fused QKV at 5-8 rows with the producer's row sums: eight waves, two
+  // units in flight each, where K gives every wave a unit (Llama-3-8B widths,
+  // M = 5 / 8: 10.3 / 10.9 -> 10.1 / 10.6 us; in the decode step 11.6 -> 11.2).
+  // Not with 16 rows, whose larger B tiles would leave one such workgroup per
+  // CU (13.2 -> 16.9), nor where the prologue sums x itself (M = 8: 11.9 -> 13.0)
+  if (rp && fold && fold->sq.p && dma_rows(M) <= 8 && (K + kUnit - 1) / kUnit >= 8)
     return launch_dma_rows<T, uint8_t, 8, 2, EPI_ROPE, true>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn, e,
                                                              *rp, *fold, st);
   if (rp && fold)
