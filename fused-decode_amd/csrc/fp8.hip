@@ -916,7 +916,14 @@ int launch_gemv_fp8_mfma(int M, void* y, const void* x, const uint8_t* w, const 
   // flight; wider layers: four waves, two units (Llama-3-8B widths, M=8:
   // N=4096 K=14336 14.4 us against 14.9 for 4 x 3 and 17.0 for 4 x 2; N=6144
   // 9.5 with 4 x 3; N=28672 K=4096 26.6 against 27.6 for 4 x 3; the relayout
-  // kernel this replaced: 15.6, 11.0 and 29.8).
+  // kernel this replaced: 15.6, 11.0 and 29.8). A launch that also writes the
+  // row sums for the next norm (the decode step's O and down projections, with
+  // the residual as row_add) runs four waves with four units in flight there
+  // (M=8: N = K = 4096 7.0 -> 6.6 us, K = 14336 14.3 -> 13.8; without the sums
+  // the two shapes tie).
+  if (blocks <= (unsigned)device_cus() && e.ss && (K + kUnit - 1) / kUnit >= 16)
+    return launch_dma_rows<T, uint8_t, 4, 4, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
+                                                               e, none, nofold, st);
   if (blocks <= (unsigned)device_cus())
     return launch_dma_rows<T, uint8_t, 8, 2, EPI_PLAIN, false>(blocks, y, x, w, s, M, N, K, sxm, swn, sym, syn,
                                                                e, none, nofold, st);
