@@ -161,14 +161,22 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_kernel(
 // between tiles, so a wave whose loads arrive late delays no other. More chunks
 // per lane spread the per-tile butterfly over more products (the activations'
 // registers grow by M * 4 per chunk) and let K = 14336 run on seven waves.
+//
+// PH (K past what eight waves hold at CPL chunks per lane, e.g. 9-16 rows at
+// K = 14336): the K chunks split into `phases` runs of nw * CPL; the wave walks
+// its tiles once per phase (phase p: chunks p * nw * CPL + wave + c * nw) with
+// that phase's activation vectors in its registers, and adds each tile's folded
+// sums into its LDS slot: the activations are read once per phase per
+// workgroup instead of once per tile, at the cost of one exposed load latency
+// per phase (the registers hold one phase's activations, not two).
 __host__ __device__ constexpr size_t simt_px_lds(int tiles_per_wg, int nw, int V) {
   return sizeof(float) * (size_t)tiles_per_wg * nw * V;
 }
 
-template <typename T, int M, int R, int CPL, bool NTW>
+template <typename T, int M, int R, int CPL, bool NTW, bool PH = false>
 __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
     T* y, const T* x, const T* w, int N, int K, int64_t sxm, int64_t swn, int64_t sym,
-    int64_t syn, Epi e, int tiles) {
+    int64_t syn, Epi e, int tiles, int phases) {
   typedef typename Vec8<T>::type V8;
   constexpr int V = pow2_ceil(R * M);
   extern __shared__ __align__(16) float parts[];  // [my tile][wave][V]
@@ -177,20 +185,24 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
   const int nt = block_threads(), nw = nt / kWave;
   const int g = (int)gridDim.x;
   const int mine = ((int)blockIdx.x < tiles) ? (tiles - (int)blockIdx.x + g - 1) / g : 0;
-  // this lane's CPL K chunks: chunk wave + c * nw of the row (past K: a dummy
-  // address, never used)
+  // this lane's CPL K chunks in phase p: chunk p * nw * CPL + wave + c * nw of
+  // the row (past K: a dummy address, never used)
   int kc[CPL];
   bool kin[CPL];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int k = ((wave + c * nw) * kWave + lane) * 8;
-    kin[c] = k < K;
-    kc[c] = kin[c] ? k : 0;
-  }
   // every chunk of this wave inside K (every wave when the chunks fill the
   // waves evenly): its sums start from the first chunk's products, with no
   // masking and no separate zeroing
-  const bool whole = ((wave + (CPL - 1) * nw) * kWave + kWave - 1) * 8 < K;
+  bool whole;
+  auto set_phase = [&](int p) {
+    const int c0 = p * nw * CPL + wave;
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int k = ((c0 + c * nw) * kWave + lane) * 8;
+      kin[c] = k < K;
+      kc[c] = kin[c] ? k : 0;
+    }
+    whole = ((c0 + (CPL - 1) * nw) * kWave + kWave - 1) * 8 < K;
+  };
 
   struct Regs {
     V8 v[CPL][R];
@@ -208,12 +220,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
     }
   };
   Regs a, b;
-  if (mine > 0) issue(a, 0);
   V8 xv[CPL][M];
-#pragma unroll
-  for (int c = 0; c < CPL; ++c)
-#pragma unroll
-    for (int m = 0; m < M; ++m) xv[c][m] = load8<T>(x + m * sxm + kc[c]);
+  bool first = true;  // phase 0: the sums start the LDS slots
   auto consume = [&](const Regs& q, int i) {
     float acc[V];
     if (whole) {
@@ -243,9 +251,21 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void gemv_simt_px_kernel(
       }
     }
     butterfly_sum<V>(acc, lane);
-    if (butterfly_writer<V>(lane)) parts[(i * nw + wave) * V + butterfly_index<V>(lane)] = acc[0];
+    if (butterfly_writer<V>(lane)) {
+      float& slot = parts[(i * nw + wave) * V + butterfly_index<V>(lane)];
+      slot = first ? acc[0] : slot + acc[0];
+    }
   };
-  stream_steps(mine, a, b, issue, consume);
+  for (int p = 0; p < (PH ? phases : 1); ++p) {
+    set_phase(p);
+    if (mine > 0) issue(a, 0);
+#pragma unroll
+    for (int c = 0; c < CPL; ++c)
+#pragma unroll
+      for (int m = 0; m < M; ++m) xv[c][m] = load8<T>(x + m * sxm + kc[c]);
+    stream_steps(mine, a, b, issue, consume);
+    first = false;
+  }
   __syncthreads();
   for (int t = tid; t < mine * R * M; t += nt) {
     const int i = t / (R * M), rm = t % (R * M);
@@ -865,6 +885,18 @@ inline int simt_px_waves(int K, int cpl) {
   return (chunks + cpl - 1) / cpl;
 }
 
+// Phases of the persistent SIMT GEMV: the fewest runs of at most eight waves x
+// cpl chunks that cover K, and the waves that spread the chunks evenly over
+// them (K = 14336, cpl = 2: two phases of seven waves).
+struct PxPhases {
+  int phases, waves;
+};
+inline PxPhases simt_px_phases(int K, int cpl) {
+  const int chunks = (K + kChunk - 1) / kChunk;
+  const int ph = (chunks + kMaxWaves * cpl - 1) / (kMaxWaves * cpl);
+  return {ph, (chunks + ph * cpl - 1) / (ph * cpl)};
+}
+
 // Workgroups of the persistent SIMT GEMV. Each one reads all M activation rows
 // into registers (M*K elements from L2) before its first tile, so a second
 // workgroup per CU pays off only while the weight rows each one streams still
@@ -881,19 +913,20 @@ template <typename T, int M, int R, int CPL>
 int launch_simt_px_r(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
                      int64_t sym, int64_t syn, const Epi& e, hipStream_t st) {
   constexpr int V = pow2_ceil(R * M);
-  const int nw = simt_px_waves(K, CPL);
-  if (K <= 0 || nw > kMaxWaves)
-    return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV takes K up to %d with %d chunks per lane",
-                     kMaxWaves * kChunk * CPL, CPL);
+  if (K <= 0) return set_error(FD_EUNSUPPORTED, "the persistent SIMT GEMV needs K > 0");
+  const PxPhases ph = simt_px_phases(K, CPL);
+  const int nw = ph.waves;
   const int tiles = (N + R - 1) / R;
   const int grid = simt_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
   const size_t lds = simt_px_lds(per, nw, V);
   if (lds > kMaxLds / 2) return set_error(FD_EUNSUPPORTED, "too many tiles per workgroup for the LDS sums");
-  auto kernel = gemv_simt_px_kernel<T, M, R, CPL, kNtWeights>;
+  auto kernel = ph.phases > 1 ? gemv_simt_px_kernel<T, M, R, CPL, kNtWeights, true>
+                              : gemv_simt_px_kernel<T, M, R, CPL, kNtWeights, false>;
   if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
   hipLaunchKernelGGL(kernel, dim3(grid), dim3(nw * kWave), lds, st, static_cast<T*>(y),
-                     static_cast<const T*>(x), static_cast<const T*>(w), N, K, sxm, swn, sym, syn, e, tiles);
+                     static_cast<const T*>(x), static_cast<const T*>(w), N, K, sxm, swn, sym, syn, e, tiles,
+                     ph.phases);
   return FD_OK;
 }
 
@@ -917,13 +950,16 @@ __host__ __device__ constexpr bool simt_px_regs_ok(int M, int R, int cpl) {
   return cpl * M * 4 + 8 * R * cpl + pow2_ceil(R * M) <= 224;
 }
 
-// Can the persistent SIMT GEMV take this launch (R rows per tile, cpl chunks per lane)?
-inline bool simt_px_fits(int N, int K, int R, int M, int cpl) {
-  if (K <= 0 || simt_px_waves(K, cpl) > kMaxWaves || !simt_px_regs_ok(M, R, cpl)) return false;
+// Can the persistent SIMT GEMV take this launch (R rows per tile, cpl chunks
+// per lane; in one phase unless `phased`)?
+inline bool simt_px_fits(int N, int K, int R, int M, int cpl, bool phased = false) {
+  if (K <= 0 || !simt_px_regs_ok(M, R, cpl)) return false;
+  const PxPhases ph = simt_px_phases(K, cpl);
+  if (ph.phases > 1 && !phased) return false;
   const int tiles = (N + R - 1) / R;
   const int grid = simt_px_grid(N, M, tiles);
   const int per = (tiles + grid - 1) / grid;
-  return simt_px_lds(per, simt_px_waves(K, cpl), pow2_ceil(R * M)) <= kMaxLds / 2;
+  return simt_px_lds(per, ph.waves, pow2_ceil(R * M)) <= kMaxLds / 2;
 }
 
 // Default rows per tile of the persistent SIMT GEMV: up to 4 rows, 4; with
@@ -949,10 +985,10 @@ int launch_simt_px_c(int cpl, void* y, const void* x, const void* w, int N, int 
 }
 
 // Default: 4 rows, waves = one per 512-element K chunk up to 8; from 2 rows the
-// persistent kernel where K fits eight waves of up to four chunks per lane
-// (stages 0 or 2; with stages 2 the tile's waves set the chunks per lane), else
-// (or with stages 1) the per-tile kernel. Rows 8 exist up to M = 8 (R*M
-// accumulators per lane).
+// persistent kernel where its registers hold the rows (stages 0 or 2; with
+// stages 2 the tile's waves set the chunks per lane), in phases where K is past
+// eight waves of those chunks, else (or with stages 1) the per-tile kernel. Rows
+// 8 exist up to M = 8 (R*M accumulators per lane).
 template <typename T, int M>
 int launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm, int64_t swn,
                 int64_t sym, int64_t syn, const Epi& e, const Tile& t, hipStream_t st) {
@@ -961,12 +997,12 @@ int launch_simt(void* y, const void* x, const void* w, int N, int K, int64_t sxm
   const bool waves_set = t.stages == 2 && t.waves > 0;
   int cpl = simt_px_cpl(M, K, waves_set ? t.waves : 0);
   const int px_rows = t.rows ? t.rows : simt_px_rows<M>(N, cpl);
-  // defaulted chunks per lane step down until the registers hold them (never
-  // below what keeps K within eight waves)
-  while (!waves_set && cpl > 1 && !simt_px_regs_ok(M, px_rows, cpl) &&
-         simt_px_waves(K, cpl / 2) <= kMaxWaves)
-    cpl /= 2;
-  const bool px = t.stages == 2 || (t.stages == 0 && M >= 2 && simt_px_fits(N, K, px_rows, M, cpl));
+  // defaulted chunks per lane step down until the registers hold them; K past
+  // eight waves of them runs in phases (9-16 rows at K = 14336: two phases of
+  // seven waves x two chunks, which read the activations once per phase per
+  // workgroup where the per-tile kernel reads them once per tile)
+  while (!waves_set && cpl > 1 && !simt_px_regs_ok(M, px_rows, cpl)) cpl /= 2;
+  const bool px = t.stages == 2 || (t.stages == 0 && M >= 2 && simt_px_fits(N, K, px_rows, M, cpl, true));
   const int rows = t.rows ? t.rows : px ? px_rows : SimtRows<M>::R;
   const int r = rows == 2 ? 2 : rows == 8 && M <= 8 ? 8 : 4;
   constexpr int R8 = M <= 8 ? 8 : 4;

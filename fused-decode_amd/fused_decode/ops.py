@@ -59,9 +59,10 @@ from .kernels import (
 DECODE_LINEAR_MAX_M = 16
 # The same cutoff for the SIMT kernel, which the default dispatcher runs when
 # FUSED_DECODE_LINEAR_KIND selects kind "simt": from 9 rows its v_dot2 work on
-# the down projection (K = 14336, whose activations no longer fit the persistent
-# kernel's registers) makes it slower than F.linear (31.7 against 26.1 us at
-# M = 9), so the default stops at 8 there. A caller that names the kind still
+# the down projection (K = 14336, whose activations the persistent kernel then
+# holds in two phases) makes it no faster than F.linear (M = 9: 26.0 against
+# 25.9 us, M = 10: 27.1 against 25.8, M = 16: 32.2 against 26.4), so the default
+# stops at 8 there. A caller that names the kind still
 # gets the SIMT kernel up to 16 rows, as in the reference.
 SIMT_DECODE_LINEAR_MAX_M = 8
 _FORCED_LIMIT = 16  # rows the GEMV takes when the caller names a kind

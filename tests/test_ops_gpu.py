@@ -368,6 +368,21 @@ def test_linear_config_shapes(dtype, nk):
             check(fd().linear_decode(xd, wd, bd, row_add=rd, kind=kind), exp_epi, dtype, "linear")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", [(9, 4096, 14336), (16, 4096, 14336), (12, 300, 14336), (16, 70, 9000),
+                                   (2, 130, 16408), (4, 1000, 20480)])
+def test_linear_simt_phases(dtype, m, n, k):
+    """The persistent SIMT GEMV where K is past eight waves of the chunks per
+    lane its registers hold: two or three phases, even and ragged K (the last
+    phase's chunks partly or wholly past K), tiles past N and workgroups with
+    no tile; bias and row_add."""
+    x, w, b = _linear_case(m, n, k, dtype, 300 + m + n, bias=True)
+    ra = randn(m, n, dtype=dtype, seed=400 + m)
+    exp = O.linear(npf(x), npf(w), npf(b), npf(ra), dtype=tag(dtype))
+    y = fd().linear_decode(x.to(DEV), w.to(DEV), b.to(DEV), row_add=ra.to(DEV), kind="simt")
+    check(y, exp, dtype, "linear")
+
+
 # ---------------------------------------------------------------- post_attn_mlp
 
 
