@@ -54,17 +54,18 @@ from .kernels import (
 # ops.py:16-19); for MI355X it is the `decode_linear_max_m` of the tile search
 # (python -m fused_decode.bench --tune, table in tiles_gfx950.json): at every row
 # count up to 16 the four GEMVs of a Llama-3-8B layer run faster in sum than
-# hipBLASLt's F.linear, none of them more than 5% slower (each strictly faster
-# up to 14 rows), so the HIP GEMV is the default over the whole hand range.
+# hipBLASLt's F.linear, each of them strictly faster, so the HIP GEMV is the
+# default over the whole hand range.
 DECODE_LINEAR_MAX_M = 16
 # The same cutoff for the SIMT kernel, which the default dispatcher runs when
-# FUSED_DECODE_LINEAR_KIND selects kind "simt": from 9 rows its v_dot2 work on
-# the down projection (K = 14336, whose activations the persistent kernel then
-# holds in two phases) makes it no faster than F.linear (M = 9: 26.0 against
-# 25.9 us, M = 10: 27.1 against 25.8, M = 16: 32.2 against 26.4), so the default
-# stops at 8 there. A caller that names the kind still
-# gets the SIMT kernel up to 16 rows, as in the reference.
-SIMT_DECODE_LINEAR_MAX_M = 8
+# FUSED_DECODE_LINEAR_KIND selects kind "simt", by the same rule: from 9 rows its
+# v_dot2 work on the down projection (K = 14336, whose activations the
+# persistent kernel then holds in two phases) makes it no faster than F.linear
+# (M = 9: 26.07 against 26.06 us, M = 10: 26.99 against 26.06, within the 5%
+# band; M = 11: 28.12 against 26.16, beyond it), so the default stops at 10. A
+# caller that names the kind still gets the SIMT kernel up to 16 rows, as in the
+# reference.
+SIMT_DECODE_LINEAR_MAX_M = 10
 _FORCED_LIMIT = 16  # rows the GEMV takes when the caller names a kind
 _FP8_ROWS = 16  # rows the E4M3 kernels take
 
