@@ -214,6 +214,50 @@ def test_fp8_sumsq_chain_matches_oracle(dtype, m):
                            dtype=t)), **tol(dtype))
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m", [5, 8, 16])
+@pytest.mark.parametrize("h", [2048, 2064])
+def test_fp8_sumsq_wide_launch_shapes(dtype, m, h):
+    """The E4M3 row-sum launches at widths where their wide shapes run: the
+    O-proj-like GEMV writing sums (one tile per CU and 16 or more K units: four
+    waves with four units in flight each; H = 2064 ends in a partial unit), the
+    QKV taking its norm from those sums (from 8 K units at up to 8 rows: eight
+    waves), and the down projection at Llama-3-8B size (N = 4096, K = 14336)."""
+    from fused_decode.rowsq import linear_fp8_sumsq, pre_attn_qkv_fp8_sumsq, sumsq_buffer
+
+    d, heads, kv = 128, 16, 4
+    n = (heads + 2 * kv) * d
+    attn, x = rnd(m, h, seed=60 + m, dtype=dtype), rnd(m, h, seed=70 + m, dtype=dtype)
+    oq, os_, oqn, osn = quant(rnd(h, h, seed=61, scale=h ** -0.5))
+    qq, qs, qqn, qsn = quant(rnd(n, h, seed=62, scale=h ** -0.5))
+    nw = rnd(h, seed=63, dtype=dtype, scale=0.3, mean=1.0)
+    ang = torch.arange(d, dtype=torch.float32) * 0.37 + 1.0
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    hbuf = torch.empty(m, h, device=DEV, dtype=dtype)
+    y = torch.empty(m, n, device=DEV, dtype=dtype)
+    ss_h = sumsq_buffer(h, DEV)
+    linear_fp8_sumsq(attn.to(DEV), oq, os_, row_add=x.to(DEV), out=hbuf, ss_out=ss_h)
+    pre_attn_qkv_fp8_sumsq(hbuf, nw.to(DEV), qq, qs, cos.to(DEV), sin.to(DEV), 1e-5, rope_cols=(heads + kv) * d,
+                           ss_in=ss_h, out=y)
+    t = tag(dtype)
+    torch.testing.assert_close(hbuf.float().cpu(), torch.from_numpy(
+        O.linear_fp8(npf(attn), oqn, osn, row_add=npf(x), dtype=t)), **tol(dtype))
+    torch.testing.assert_close(ss_h.cpu(), tile_sums(hbuf), rtol=2e-6, atol=1e-6)
+    torch.testing.assert_close(y.float().cpu(), torch.from_numpy(
+        O.pre_attn_qkv_fp8(npf(hbuf), npf(nw), qqn, qsn, npf(cos), npf(sin), 1e-5, (heads + kv) * d,
+                           dtype=t)), **tol(dtype))
+    if h == 2048:  # the down projection's shape, its residual as row_add
+        k_d, n_d = 14336, 4096
+        mid, res = rnd(m, k_d, seed=64 + m, dtype=dtype), rnd(m, n_d, seed=65 + m, dtype=dtype)
+        dq, ds, dqn, dsn = quant(rnd(n_d, k_d, seed=66, scale=k_d ** -0.5))
+        out = torch.empty(m, n_d, device=DEV, dtype=dtype)
+        ss = sumsq_buffer(n_d, DEV)
+        linear_fp8_sumsq(mid.to(DEV), dq, ds, row_add=res.to(DEV), out=out, ss_out=ss)
+        torch.testing.assert_close(out.float().cpu(), torch.from_numpy(
+            O.linear_fp8(npf(mid), dqn, dsn, row_add=npf(res), dtype=t)), **tol(dtype))
+        torch.testing.assert_close(ss.cpu(), tile_sums(out), rtol=2e-6, atol=1e-6)
+
+
 @pytest.mark.parametrize("weights", ["fp16", "fp8"])
 @pytest.mark.parametrize("m", [5, 8, 16])
 def test_decode_step_rowsq_matches_row_kernel_form(weights, m):
