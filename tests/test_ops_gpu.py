@@ -414,6 +414,24 @@ def test_post_attn_mlp_wide_hidden_row_kernel_form(m):
     check(y, O.post_attn_mlp(npf(x), npf(nw), npf(w_gu), npf(w_d), 1e-5, "f16"), torch.float16, "linear")
 
 
+@pytest.mark.parametrize("m", [5, 8, 12, 16])
+@pytest.mark.parametrize("i", [4096, 4104, 14336])
+def test_post_attn_mlp_gate_up_tile_forms(m, i):
+    """The MFMA gate/up (tiles of 16 gate + 16 up rows) at tile counts that
+    divide over the CUs (I = 4096: 256 tiles) and that do not (I = 4104, whose
+    last tile is partial, and I = 14336: 896 tiles); the norm inside the kernel
+    up to 8 rows, a row kernel's normalised rows from 9; bf16 at 8 rows."""
+    h = 1024
+    dtype = torch.bfloat16 if m == 8 and i == 14336 else torch.float16
+    g = torch.Generator().manual_seed(i + m)
+    x = randn(m, h, dtype=dtype, gen=g)
+    nw = randn(h, dtype=dtype, gen=g, scale=0.1, mean=1.0)
+    w_gu = randn(2 * i, h, dtype=dtype, gen=g, scale=h ** -0.5)
+    w_d = randn(h, i, dtype=dtype, gen=g, scale=i ** -0.5)
+    y = fd().post_attn_mlp(x.to(DEV), nw.to(DEV), w_gu.to(DEV), w_d.to(DEV), 1e-5, kind="dot")
+    check(y, O.post_attn_mlp(npf(x), npf(nw), npf(w_gu), npf(w_d), 1e-5, tag(dtype)), dtype, "linear")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_post_attn_mlp_every_m_and_fp32_norm_weight(dtype):
     h, i = 256, 384
