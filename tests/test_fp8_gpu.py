@@ -355,6 +355,34 @@ def test_decode_step_fp8_matches_oracle_and_graph(m):
     assert ds.launches_per_layer == 4  # from 5 rows the MLP's norm runs inside its gate/up (row sums)
 
 
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_decode_step_fp8_llama3_8b_matches_oracle(m):
+    """Two E4M3 layers at full Llama-3-8B widths, the shapes of the 32-layer
+    benchmark step: one row (the one-row kernels), four (the persistent SIMT
+    forms) and eight (the resident gate/up, the QKV from the producer's row sums
+    in eight-wave workgroups, the O and down projections writing row sums with
+    four units in flight), against the oracle, then a graph replay."""
+    from fused_decode.decode_step import HEAD_DIM, DecodeStep
+
+    print(f"[fp8 decode step llama3-8b m={m}]", flush=True)
+    ds = DecodeStep(m=m, layers=2, seed=7, weights="fp8")
+    eager = ds.step().clone()
+    codes = lambda q: q.cpu().view(torch.uint8).numpy()  # noqa: E731
+    x = npf(ds.x_in)
+    cos, sin = npf(ds.cos), npf(ds.sin)
+    qk = ds.qk_heads * HEAD_DIM
+    for w in ds.w:
+        qkv = O.pre_attn_qkv_fp8(x, npf(w["attn_norm"]), codes(w["qkv"][0]), npf(w["qkv"][1]), cos, sin,
+                                 1e-5, qk, dtype="f16")
+        h = O.linear_fp8(npf(w["attn_out"]), codes(w["o"][0]), npf(w["o"][1]), row_add=x, dtype="f16")
+        x = O.post_attn_mlp_fp8(h, npf(w["mlp_norm"]), codes(w["gate_up"][0]), npf(w["gate_up"][1]),
+                                codes(w["down"][0]), npf(w["down"][1]), 1e-5, "f16")
+    torch.testing.assert_close(eager.float().cpu(), torch.from_numpy(x), **tol(torch.float16))
+    torch.testing.assert_close(ds.qkv.float().cpu(), torch.from_numpy(qkv), **tol(torch.float16))
+    ds.out.zero_()
+    torch.testing.assert_close(ds.replay(), eager, rtol=0, atol=0)
+
+
 # ---------------------------------------------------------------- fused QKV
 
 
