@@ -632,21 +632,22 @@ def test_decode_step_small_bf16_matches_oracle(m):
     torch.testing.assert_close(ds.replay(), eager, rtol=0, atol=0)
 
 
-@pytest.mark.parametrize("m", [1, 8])
-def test_decode_step_llama3_8b_matches_oracle(m):
+@pytest.mark.parametrize("m,dtype", [(1, torch.float16), (8, torch.float16), (1, torch.bfloat16),
+                                     (8, torch.bfloat16), (16, torch.float16)])
+def test_decode_step_llama3_8b_matches_oracle(m, dtype):
     """Two layers at full Llama-3-8B widths (H=4096, 32 q + 8 kv heads of 128,
     I=14336), the shapes the 32-layer benchmark step runs, against the oracle:
     the step's output and the last layer's q/k/v, then a graph replay."""
     from fused_decode.decode_step import DecodeStep
 
-    print(f"[decode step llama3-8b m={m}]", flush=True)
-    ds = DecodeStep(m=m, layers=2, seed=6)
+    print(f"[decode step llama3-8b m={m} {dtype}]", flush=True)
+    ds = DecodeStep(m=m, layers=2, seed=6, dtype=dtype)
     assert ds.weight_bytes == 2 * 436_207_616 + 2 * 2 * 4096 * 2
     eager = ds.step().clone()
     qkv = ds.qkv.clone()
-    ref, ref_qkv = _oracle_decode_step(ds, "f16")
-    check(eager, ref, torch.float16, "linear")
-    check(qkv, ref_qkv, torch.float16, "linear")
+    ref, ref_qkv = _oracle_decode_step(ds, tag(dtype))
+    check(eager, ref, dtype, "linear")
+    check(qkv, ref_qkv, dtype, "linear")
     ds.out.zero_()
     torch.testing.assert_close(ds.replay(), eager, rtol=0, atol=0)
 
