@@ -741,39 +741,49 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_px_kernel(
 // FX (with SS): no producer sums; the prologue derives the row sums from x
 // (up to 8 rows: every workgroup reads the rows from L2 once more, which costs
 // less than the row kernel's launch).
-template <typename T, bool NTW, bool SS, bool HALF, bool FX = false>
-__global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_relayout_kernel(
-    T* mid, const T* x, const T* wgu, int M, int H, int I, const void* nwp, int nw_dtype, float eps,
-    RowSq rq) {
+//
+// SPLIT: a tile of 8 gate rows (from j0) and their 8 up rows, one 16-row weight
+// set per unit (one relayout, four MFMAs); output rows 0-7 (gate) sit in lanes
+// 0-31 and their up rows 8-15 in lanes 32-63, so the epilogue pairs lane t
+// with t + 32. Each activation fragment then feeds half the MFMAs, so these
+// tiles only take the rows past the last whole round of 16 + 16 tiles over the
+// CUs (relayout_grid).
+template <typename T, bool NTW, bool SS, bool HALF, bool FX, bool SPLIT>
+__device__ __forceinline__ void gate_up_relayout_tile(f32x4* part, u32x4 (*tiles)[256], int64_t j0, T* mid,
+                                                      const T* x, const T* wgu, int M, int H, int I,
+                                                      const void* nwp, int nw_dtype, float eps, const RowSq& rq) {
   typedef typename Vec8<T>::type V8;
-  constexpr int LW = SS ? kSsWaves : kMaxWaves;
-  __shared__ f32x4 part[LW * kWave];
-  __shared__ u32x4 tiles[LW][256];
+  constexpr int S = SPLIT ? 1 : 2;  // weight sets per unit
   extern __shared__ float norm_lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t j0 = (int64_t)blockIdx.x * 16;
   const int hi = r >= 8, xrow = HALF ? half_b_row(r) : r;
   const T* xr = x + (xrow < M ? xrow : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 4, lchunk = lane & 15;
-  const T* wl[2][4];  // [gate, up][row 4i + lrow] bases
+  const T* wl[S][4];  // [gate, up][row 4i + lrow] bases; SPLIT: tile row 4i + lrow
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t j = j0 + 4 * i + lrow;
-    const int64_t jc = j < I ? j : 0;
-    wl[0][i] = wgu + jc * H;
-    wl[1][i] = wgu + (I + jc) * H;
+    if constexpr (SPLIT) {
+      const int64_t j = j0 + ((4 * i + lrow) & 7);
+      const int64_t jc = j < I ? j : 0;
+      wl[0][i] = wgu + (i < 2 ? jc : I + jc) * H;  // rows 0-7 gate, 8-15 up
+    } else {
+      const int64_t j = j0 + 4 * i + lrow;
+      const int64_t jc = j < I ? j : 0;
+      wl[0][i] = wgu + jc * H;
+      wl[S - 1][i] = wgu + (I + jc) * H;
+    }
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   const int off = sweep_offset(units);
-  auto issue = [&](UnitRegs16<T, 2>& q, int i) {
+  auto issue = [&](UnitRegs16<T, S>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
-    load_unit16<T, 2, NTW, !HALF>(q, wl, xr, u, lchunk, g, H);
+    load_unit16<T, S, NTW, !HALF>(q, wl, xr, u, lchunk, g, H);
     if constexpr (HALF) load_b_half<T>(q.b, xr, u, g, hi, H);
   };
   float rinv = 0.f;
@@ -788,31 +798,31 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
     }
     return unit_b(xb, u, s2, g, H);
   };
-  auto consume = [&](const UnitRegs16<T, 2>& q, int i) {
+  auto consume = [&](const UnitRegs16<T, S>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
     stage_unit16<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
-    stage_unit16<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
+    if constexpr (!SPLIT) stage_unit16<T>(q.v[S - 1], tile, lrow, lchunk, u, H, r, g, c);
     if constexpr (HALF) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const V8 own = frag(q.b[p], u, 2 * p + hi);
         const V8 oth = __builtin_bit_cast(V8, mirror16(__builtin_bit_cast(u32x4, own)));
         ag = mfma16(a[2 * p], own, ag);
-        au = mfma16(c[2 * p], own, au);
+        if constexpr (!SPLIT) au = mfma16(c[2 * p], own, au);
         ag = mfma16(a[2 * p + 1], oth, ag);
-        au = mfma16(c[2 * p + 1], oth, au);
+        if constexpr (!SPLIT) au = mfma16(c[2 * p + 1], oth, au);
       }
     } else {
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const V8 b = frag(q.b[s2], u, s2);
         ag = mfma16(a[s2], b, ag);
-        au = mfma16(c[s2], b, au);
+        if constexpr (!SPLIT) au = mfma16(c[s2], b, au);
       }
     }
   };
-  UnitRegs16<T, 2> qa, qb;
+  UnitRegs16<T, S> qa, qb;
   if constexpr (SS) {  // the first unit's loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
     norm_prologue<T, HALF ? 8 : 16, FX, kSsWaves * kWave>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H,
@@ -824,6 +834,27 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
     if (mine > 0) issue(qa, 0);
   }
   stream_steps(mine, qa, qb, issue, consume);
+  if constexpr (SPLIT) {  // one reduction: lane t < 32 adds the gate sums of t, the up sums of t + 32
+    part[wave * kWave + lane] = ag;
+    __syncthreads();
+    if (threadIdx.x < 32) {
+      f32x4 sg = part[threadIdx.x], su = part[threadIdx.x + 32];
+      for (int i = 1; i < nw; ++i) {
+        sg += part[i * kWave + threadIdx.x];
+        su += part[i * kWave + threadIdx.x + 32];
+      }
+      const int m = threadIdx.x & 15;
+      const int nb = (threadIdx.x >> 4) * 4;
+      if (m < M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t jj = j0 + nb + i;
+          if (jj < I) mid[m * (int64_t)I + jj] = swiglu_out<T>(sg[i], su[i]);
+        }
+      }
+    }
+    return;
+  }
   // two-phase reduction through one buffer: gate sums, then up sums
   part[wave * kWave + lane] = ag;
   __syncthreads();
@@ -846,6 +877,27 @@ __global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, 
       }
     }
   }
+}
+
+// The gate/up launch: workgroup b < big takes 16 gate + 16 up rows from 16 b;
+// with MIX the rest take 8 + 8 rows each after those (relayout_grid).
+template <typename T, bool NTW, bool SS, bool HALF, bool FX = false, bool MIX = false>
+__global__ __launch_bounds__(SS || HALF ? kSsWaves * kWave : kMaxWaves * kWave, SS || HALF ? 3 : 1) void mlp_gate_up_relayout_kernel(
+    T* mid, const T* x, const T* wgu, int M, int H, int I, const void* nwp, int nw_dtype, float eps,
+    RowSq rq, int big) {
+  constexpr int LW = SS ? kSsWaves : kMaxWaves;
+  __shared__ f32x4 part[LW * kWave];
+  __shared__ u32x4 tiles[LW][256];
+  const int b = (int)blockIdx.x;
+  if constexpr (MIX) {
+    if (b >= big) {
+      gate_up_relayout_tile<T, NTW, SS, HALF, FX, true>(part, tiles, (int64_t)big * 16 + (int64_t)(b - big) * 8, mid,
+                                                        x, wgu, M, H, I, nwp, nw_dtype, eps, rq);
+      return;
+    }
+  }
+  gate_up_relayout_tile<T, NTW, SS, HALF, FX, false>(part, tiles, (int64_t)b * 16, mid, x, wgu, M, H, I, nwp,
+                                                     nw_dtype, eps, rq);
 }
 
 // ---------------------------------------------------------------------------
@@ -1250,6 +1302,27 @@ int launch_qkv_simt_m(int M, void* y, const void* hidden, const void* nw, int nw
   }
 }
 
+// Workgroups of the relayout gate/up: tiles of 16 gate + 16 up rows, and where
+// their count is past a whole number of rounds over the CUs, the rows past the
+// last whole round as tiles of 8 + 8 (MIX), so every CU streams about the same
+// rows. At Llama-3-8B widths (I = 14336) 896 tiles of 16 + 16 put four on half
+// the CUs and three on the rest (timed alone at M = 8, H = 4096: 5.61 TB/s,
+// against 6.04-6.07 where they divide evenly, I = 12288 and 16384); 768 of
+// them and 256 of 8 + 8 put the same rows on every CU. Tiles of 8 + 8
+// throughout were slower: each activation fragment feeds half the MFMAs.
+struct GateUpGrid {
+  unsigned blocks;
+  int big;   // workgroups with 16 + 16 rows
+  bool mix;  // the rest with 8 + 8
+};
+inline GateUpGrid relayout_grid(int I) {
+  const int cus = device_cus();
+  const int t16 = (I + 15) / 16;
+  if (t16 <= cus || t16 % cus == 0) return {(unsigned)t16, t16, false};
+  const int big = t16 - t16 % cus;
+  return {(unsigned)(big + (I - big * 16 + 7) / 8), big, true};
+}
+
 template <typename T>
 int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, int H, int I,
                         hipStream_t st) {
@@ -1257,13 +1330,17 @@ int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, i
   // 39.3 us against 41.2 for eight waves and 39.8 for the one-unit loop).
   const int units = (H + kUnit - 1) / kUnit;
   const int nwv = units < 4 ? units : 4;
+  const GateUpGrid gg = relayout_grid(I);
   auto launch = [&](auto kernel) {
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
+    hipLaunchKernelGGL(kernel, dim3(gg.blocks), dim3(nwv * kWave), 0, st, static_cast<T*>(mid),
                        static_cast<const T*>(normed), static_cast<const T*>(wgu), M, H, I, nullptr, FD_F32, 0.f,
-                       RowSq{nullptr, 0});
+                       RowSq{nullptr, 0}, gg.big);
   };
   // (the half-B form would spill here: 168 VGPRs and 20 bytes of scratch)
-  launch(mlp_gate_up_relayout_kernel<T, true, false, false>);
+  if (gg.mix)
+    launch(mlp_gate_up_relayout_kernel<T, true, false, false, false, true>);
+  else
+    launch(mlp_gate_up_relayout_kernel<T, true, false, false>);
   return FD_OK;
 }
 
@@ -1278,13 +1355,21 @@ int launch_mlp_relayout_ss(int M, void* mid, const void* hidden, const void* nw,
   const size_t lds = relayout_ss_lds(H, kSsWaves);
   if (lds + (size_t)(kSsWaves * kWave + kSsWaves * 256) * 16 > kMaxLds)
     return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
+  const GateUpGrid gg = relayout_grid(I);
   auto launch = [&](auto kernel) {
     if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
-    hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
+    hipLaunchKernelGGL(kernel, dim3(gg.blocks), dim3(nwv * kWave), lds, st, static_cast<T*>(mid),
                        static_cast<const T*>(hidden), static_cast<const T*>(wgu), M, H, I, nw, nw_dtype, eps,
-                       rq ? *rq : RowSq{nullptr, 0});
+                       rq ? *rq : RowSq{nullptr, 0}, gg.big);
     return (int)FD_OK;
   };
+  if (gg.mix) {
+    if (rq)
+      return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true, false, true>)
+                    : launch(mlp_gate_up_relayout_kernel<T, true, true, false, false, true>);
+    return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true, true, true>)
+                  : launch(mlp_gate_up_relayout_kernel<T, true, true, false, true, true>);
+  }
   if (rq)
     return M <= 8 ? launch(mlp_gate_up_relayout_kernel<T, true, true, true>)
                   : launch(mlp_gate_up_relayout_kernel<T, true, true, false>);

@@ -417,10 +417,11 @@ def test_post_attn_mlp_wide_hidden_row_kernel_form(m):
 @pytest.mark.parametrize("m", [5, 8, 12, 16])
 @pytest.mark.parametrize("i", [4096, 4104, 14336])
 def test_post_attn_mlp_gate_up_tile_forms(m, i):
-    """The MFMA gate/up (tiles of 16 gate + 16 up rows) at tile counts that
-    divide over the CUs (I = 4096: 256 tiles) and that do not (I = 4104, whose
-    last tile is partial, and I = 14336: 896 tiles); the norm inside the kernel
-    up to 8 rows, a row kernel's normalised rows from 9; bf16 at 8 rows."""
+    """The MFMA gate/up with tiles of 16 gate + 16 up rows only (I = 4096: 256
+    tiles, one round over the CUs) and with the rows past the last whole round
+    in tiles of 8 + 8 (I = 4104: one such tile, 8 rows; I = 14336: 768 + 256
+    tiles); the norm inside the kernel up to 8 rows, a row kernel's normalised
+    rows from 9; bf16 at 8 rows."""
     h = 1024
     dtype = torch.bfloat16 if m == 8 and i == 14336 else torch.float16
     g = torch.Generator().manual_seed(i + m)
