@@ -645,41 +645,49 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void qkv_fp8_kernel(
 // per SIMD, so its 896 four-wave workgroups are all resident too and each CU
 // keeps twice the units in flight (M=8 step: 26.7 -> 26.2 us).
 // HALF (M <= 8): the activation fragments in the half-B form (load_b_half).
+// SPLIT: 8 gate rows and their 8 up rows in one 16-row set, paired in the
+// epilogue as in gemv.hip's gate_up_relayout_tile; these take the rows past the
+// last whole round of 16 + 16 tiles over the CUs (relayout_grid).
 template <bool HALF, bool FX>
 constexpr int fp8_ss_waves() { return HALF && !FX ? 4 : 2; }
-template <typename T, bool HALF, bool FX>
-__global__ __launch_bounds__((fp8_ss_waves<HALF, FX>() * kWave), 3) void mlp_gate_up_fp8_relayout_kernel(
-    T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I, const void* nwp,
-    int nw_dtype, float eps, RowSq rq) {
+template <typename T, bool HALF, bool FX, bool SPLIT>
+__device__ __forceinline__ void gate_up_fp8_relayout_tile(f32x4* part, u32x4 (*tiles)[256], int64_t j0, T* mid,
+                                                          const T* x, const uint8_t* wgu, const float* gu_scale,
+                                                          int M, int H, int I, const void* nwp, int nw_dtype,
+                                                          float eps, const RowSq& rq) {
   typedef typename Vec8<T>::type V8;
   constexpr int LW = fp8_ss_waves<HALF, FX>();
-  __shared__ f32x4 part[LW * kWave];
-  __shared__ u32x4 tiles[LW][256];
+  constexpr int S = SPLIT ? 1 : 2;  // weight sets per unit
   extern __shared__ float norm_lds[];
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int nw = block_threads() / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int64_t j0 = (int64_t)blockIdx.x * 16;
   const int hi = r >= 8, xrow = HALF ? half_b_row(r) : r;
   const T* xr = x + (xrow < M ? xrow : 0) * (int64_t)H;  // rows past M: columns never stored
   const int lrow = lane >> 3, lchunk = lane & 7;
-  const uint8_t* wl[2][2];  // [gate, up][row lrow, lrow + 8] bases
+  const uint8_t* wl[S][2];  // [gate, up][row lrow, lrow + 8] bases; SPLIT: gate row lrow, its up row
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int64_t j = j0 + 8 * i + lrow;
-    const int64_t jc = j < I ? j : 0;
-    wl[0][i] = wgu + jc * H;
-    wl[1][i] = wgu + (I + jc) * H;
+    if constexpr (SPLIT) {
+      const int64_t j = j0 + lrow;
+      const int64_t jc = j < I ? j : 0;
+      wl[0][i] = wgu + (i == 0 ? jc : I + jc) * H;
+    } else {
+      const int64_t j = j0 + 8 * i + lrow;
+      const int64_t jc = j < I ? j : 0;
+      wl[0][i] = wgu + jc * H;
+      wl[S - 1][i] = wgu + (I + jc) * H;
+    }
   }
   u32x4* tile = tiles[wave];
   f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
   const int units = (H + kUnit - 1) / kUnit;
   const int mine = wave < units ? (units - wave + nw - 1) / nw : 0;
   const int off = sweep_offset(units);
-  auto issue = [&](UnitRegs8<T, 2>& q, int i) {
+  auto issue = [&](UnitRegs8<T, S>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
-    load_unit8<T, 2, !HALF>(q, wl, xr, u, lchunk, g, H);
+    load_unit8<T, S, !HALF>(q, wl, xr, u, lchunk, g, H);
     if constexpr (HALF) load_b_half<T>(q.b, xr, u, g, hi, H);
   };
   float rinv = 0.f;
@@ -691,31 +699,31 @@ __global__ __launch_bounds__((fp8_ss_waves<HALF, FX>() * kWave), 3) void mlp_gat
                                                       __builtin_bit_cast(u32x4, wk[1])));
     return unit_b(xb, u, s2, g, H);
   };
-  auto consume = [&](const UnitRegs8<T, 2>& q, int i) {
+  auto consume = [&](const UnitRegs8<T, S>& q, int i) {
     const int u = sweep_unit(wave, i, nw, off, units);
     V8 a[4], c[4];
     stage_unit8<T>(q.v[0], tile, lrow, lchunk, u, H, r, g, a);
-    stage_unit8<T>(q.v[1], tile, lrow, lchunk, u, H, r, g, c);
+    if constexpr (!SPLIT) stage_unit8<T>(q.v[S - 1], tile, lrow, lchunk, u, H, r, g, c);
     if constexpr (HALF) {
 #pragma unroll
       for (int p = 0; p < 2; ++p) {
         const V8 own = frag(q.b[p], u, 2 * p + hi);
         const V8 oth = __builtin_bit_cast(V8, mirror16(__builtin_bit_cast(u32x4, own)));
         ag = mfma16(a[2 * p], own, ag);
-        au = mfma16(c[2 * p], own, au);
+        if constexpr (!SPLIT) au = mfma16(c[2 * p], own, au);
         ag = mfma16(a[2 * p + 1], oth, ag);
-        au = mfma16(c[2 * p + 1], oth, au);
+        if constexpr (!SPLIT) au = mfma16(c[2 * p + 1], oth, au);
       }
     } else {
 #pragma unroll
       for (int s2 = 0; s2 < 4; ++s2) {
         const V8 b = frag(q.b[s2], u, s2);
         ag = mfma16(a[s2], b, ag);
-        au = mfma16(c[s2], b, au);
+        if constexpr (!SPLIT) au = mfma16(c[s2], b, au);
       }
     }
   };
-  UnitRegs8<T, 2> qa, qb;
+  UnitRegs8<T, S> qa, qb;
   {  // the first two units' loads fly while the prologue runs
     float* inv = norm_lds + units * kUnit;
     norm_prologue<T, HALF ? 8 : 16, FX, LW * kWave>(norm_lds, inv, inv + 16, nwp, nw_dtype, x, H, M, H,
@@ -726,6 +734,28 @@ __global__ __launch_bounds__((fp8_ss_waves<HALF, FX>() * kWave), 3) void mlp_gat
     rinv = inv[xrow];
   }
   stream_steps_issued2(mine, qa, qb, issue, consume);
+  if constexpr (SPLIT) {  // one reduction: lane t < 32 adds the gate sums of t, the up sums of t + 32
+    part[wave * kWave + lane] = ag;
+    __syncthreads();
+    if (threadIdx.x < 32) {
+      f32x4 sg = part[threadIdx.x], su = part[threadIdx.x + 32];
+      for (int i = 1; i < nw; ++i) {
+        sg += part[i * kWave + threadIdx.x];
+        su += part[i * kWave + threadIdx.x + 32];
+      }
+      const int m = threadIdx.x & 15;
+      const int nb = (threadIdx.x >> 4) * 4;
+      if (m < M) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int64_t jj = j0 + nb + i;
+          if (jj < I)
+            mid[m * (int64_t)I + jj] = swiglu_out<T>(sg[i] * gu_scale[jj], su[i] * gu_scale[I + jj]);
+        }
+      }
+    }
+    return;
+  }
   part[wave * kWave + lane] = ag;
   __syncthreads();
   f32x4 sg = {0.f, 0.f, 0.f, 0.f};
@@ -749,6 +779,27 @@ __global__ __launch_bounds__((fp8_ss_waves<HALF, FX>() * kWave), 3) void mlp_gat
       }
     }
   }
+}
+
+// The gate/up launch: workgroup b < big takes 16 gate + 16 up rows from 16 b;
+// with MIX the rest take 8 + 8 rows each after those (relayout_grid).
+template <typename T, bool HALF, bool FX, bool MIX = false>
+__global__ __launch_bounds__((fp8_ss_waves<HALF, FX>() * kWave), 3) void mlp_gate_up_fp8_relayout_kernel(
+    T* mid, const T* x, const uint8_t* wgu, const float* gu_scale, int M, int H, int I, const void* nwp,
+    int nw_dtype, float eps, RowSq rq, int big) {
+  constexpr int LW = fp8_ss_waves<HALF, FX>();
+  __shared__ f32x4 part[LW * kWave];
+  __shared__ u32x4 tiles[LW][256];
+  const int b = (int)blockIdx.x;
+  if constexpr (MIX) {
+    if (b >= big) {
+      gate_up_fp8_relayout_tile<T, HALF, FX, true>(part, tiles, (int64_t)big * 16 + (int64_t)(b - big) * 8, mid, x,
+                                                   wgu, gu_scale, M, H, I, nwp, nw_dtype, eps, rq);
+      return;
+    }
+  }
+  gate_up_fp8_relayout_tile<T, HALF, FX, false>(part, tiles, (int64_t)b * 16, mid, x, wgu, gu_scale, M, H, I, nwp,
+                                                nw_dtype, eps, rq);
 }
 
 namespace {
@@ -1168,26 +1219,39 @@ int post_attn_mlp_fp8_entry(void* y, void* mid, const void* hidden, const void* 
     if (lds + (size_t)(waves * kWave + waves * 256) * 16 > kMaxLds)
       return set_error(FD_EUNSUPPORTED, "H too large for the norm weight's LDS stage");
     const RowSq sq = rq ? *rq : RowSq{nullptr, 0};
+    const GateUpGrid gg = relayout_grid((int)I);
     auto launch = [&](auto kernel, auto* out, auto* in) {
       if (!allow_lds(kernel, lds)) return set_error(FD_ELAUNCH, "cannot raise the LDS limit to %zu bytes", lds);
-      hipLaunchKernelGGL(kernel, dim3((unsigned)((I + 15) / 16)), dim3(nwv * kWave), lds, st, out, in, wgu,
-                         gate_up_scale, (int)M, (int)H, (int)I, norm_w, norm_w_dtype, eps, sq);
+      hipLaunchKernelGGL(kernel, dim3(gg.blocks), dim3(nwv * kWave), lds, st, out, in, wgu, gate_up_scale, (int)M,
+                         (int)H, (int)I, norm_w, norm_w_dtype, eps, sq, gg.big);
       return (int)FD_OK;
     };
     auto run = [&](auto k16, auto kb16) {
       return act_dtype == FD_F16 ? launch(k16, static_cast<f16*>(mid), static_cast<const f16*>(hidden))
                                  : launch(kb16, static_cast<bf16*>(mid), static_cast<const bf16*>(hidden));
     };
-    if (rq)
+    if (gg.mix) {
+      if (rq)
+        rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, false, true>,
+                          mlp_gate_up_fp8_relayout_kernel<bf16, true, false, true>)
+                    : run(mlp_gate_up_fp8_relayout_kernel<f16, false, false, true>,
+                          mlp_gate_up_fp8_relayout_kernel<bf16, false, false, true>);
+      else
+        rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, true, true>,
+                          mlp_gate_up_fp8_relayout_kernel<bf16, true, true, true>)
+                    : run(mlp_gate_up_fp8_relayout_kernel<f16, false, true, true>,
+                          mlp_gate_up_fp8_relayout_kernel<bf16, false, true, true>);
+    } else if (rq) {
       rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, false>,
                         mlp_gate_up_fp8_relayout_kernel<bf16, true, false>)
                   : run(mlp_gate_up_fp8_relayout_kernel<f16, false, false>,
                         mlp_gate_up_fp8_relayout_kernel<bf16, false, false>);
-    else
+    } else {
       rc = M <= 8 ? run(mlp_gate_up_fp8_relayout_kernel<f16, true, true>,
                         mlp_gate_up_fp8_relayout_kernel<bf16, true, true>)
                   : run(mlp_gate_up_fp8_relayout_kernel<f16, false, true>,
                         mlp_gate_up_fp8_relayout_kernel<bf16, false, true>);
+    }
     if (rc != FD_OK) return rc;
   } else if (fp8_px_takes((int)M, (int)(2 * I), (int)H)) {
     const Epi none_e{};

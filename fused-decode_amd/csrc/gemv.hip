@@ -1302,27 +1302,6 @@ int launch_qkv_simt_m(int M, void* y, const void* hidden, const void* nw, int nw
   }
 }
 
-// Workgroups of the relayout gate/up: tiles of 16 gate + 16 up rows, and where
-// their count is past a whole number of rounds over the CUs, the rows past the
-// last whole round as tiles of 8 + 8 (MIX), so every CU streams about the same
-// rows. At Llama-3-8B widths (I = 14336) 896 tiles of 16 + 16 put four on half
-// the CUs and three on the rest (timed alone at M = 8, H = 4096: 5.61 TB/s,
-// against 6.04-6.07 where they divide evenly, I = 12288 and 16384); 768 of
-// them and 256 of 8 + 8 put the same rows on every CU. Tiles of 8 + 8
-// throughout were slower: each activation fragment feeds half the MFMAs.
-struct GateUpGrid {
-  unsigned blocks;
-  int big;   // workgroups with 16 + 16 rows
-  bool mix;  // the rest with 8 + 8
-};
-inline GateUpGrid relayout_grid(int I) {
-  const int cus = device_cus();
-  const int t16 = (I + 15) / 16;
-  if (t16 <= cus || t16 % cus == 0) return {(unsigned)t16, t16, false};
-  const int big = t16 - t16 % cus;
-  return {(unsigned)(big + (I - big * 16 + 7) / 8), big, true};
-}
-
 template <typename T>
 int launch_mlp_relayout(int M, void* mid, const void* normed, const void* wgu, int H, int I,
                         hipStream_t st) {
