@@ -984,7 +984,10 @@ inline int fused_grid(int tiles, size_t lds, int per_cu) {
 // the CUs and three on the rest (timed alone at M = 8, H = 4096: 5.61 TB/s,
 // against 6.04-6.07 where they divide evenly, I = 12288 and 16384); 768 of
 // them and 256 of 8 + 8 put the same rows on every CU. Tiles of 8 + 8
-// throughout were slower: each activation fragment feeds half the MFMAs.
+// throughout were slower: each activation fragment feeds half the MFMAs. The
+// mix is taken only where it lowers the busiest CU's rows (in 16-row tiles:
+// rounds of big tiles plus half a tile per round of small ones), e.g. not at
+// I = 11008, whose leftover would put two small tiles on some CUs.
 struct GateUpGrid {
   unsigned blocks;
   int big;   // workgroups with 16 + 16 rows
@@ -993,9 +996,14 @@ struct GateUpGrid {
 inline GateUpGrid relayout_grid(int I) {
   const int cus = device_cus();
   const int t16 = (I + 15) / 16;
-  if (t16 <= cus || t16 % cus == 0) return {(unsigned)t16, t16, false};
+  const GateUpGrid plain{(unsigned)t16, t16, false};
+  if (t16 <= cus || t16 % cus == 0) return plain;
   const int big = t16 - t16 % cus;
-  return {(unsigned)(big + (I - big * 16 + 7) / 8), big, true};
+  const int small = (I - big * 16 + 7) / 8;
+  const int rounds16 = (t16 + cus - 1) / cus;                 // busiest CU, plain grid
+  const int halves = 2 * (big / cus) + (small + cus - 1) / cus;  // busiest CU, mixed, in 8 + 8 tiles
+  if (halves >= 2 * rounds16) return plain;
+  return {(unsigned)(big + small), big, true};
 }
 
 // Argument checks and operand set-up shared by the fused QKV entry points
